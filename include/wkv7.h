@@ -1,0 +1,111 @@
+/*
+ * wkv7.h -- C ABI of the MI355X (gfx950) WKV7 recurrence library, librwkv7_hip.so.
+ *
+ * Drop-in replacement for the WKV7 hot path of OpenMOSE/RWKV-Infer-Next.  In the reference every caller of the
+ * recurrence -- the functional op, the varlen prefill call and the in-place rollback replay -- ends in one
+ * launcher, `_launch(r, w, k, v, a, b, h0, ht, cu, nkeep, store_o, H, K)` (rwkv_next/kernels/wkv7.py:89-104),
+ * which runs the Triton program `_wkv7_raw` (rwkv_next/kernels/wkv7.py:38-79).  `wkv7_run` below takes the same
+ * arguments (plus the slot-pool, snapshot and workspace extensions) and is what a binding of that launcher
+ * calls.
+ *
+ * Math (rwkv_next/kernels/wkv7.py:4-7), per (sequence, head), state S = K x V fp32 with V contiguous:
+ *     S_t = diag(d_t) S_{t-1} + b_t (a_t^T S_{t-1}) + k_t v_t^T,   d_t = exp(-exp(w_t)),   o_t = S_t^T r_t
+ * with the RAW w (the decay is computed in fp32 inside the kernels).  Head size K = V = 64.
+ *
+ * Plain C: no HIP, CUDA or torch types.  Pointers are device pointers; `stream` is a hipStream_t passed as
+ * void*.  No function allocates device memory, synchronises the host, or keeps mutable global state, so every
+ * call is reentrant and can be recorded into a hipGraph (scratch memory comes from the caller's workspace).
+ */
+#ifndef RWKV_NEXT_AMD_WKV7_H
+#define RWKV_NEXT_AMD_WKV7_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WKV7_ABI_VERSION 1
+
+/* Return codes.  Negative: argument validation failed before anything was launched.  Positive: the hipError_t
+ * of a failed launch (the reference surfaces Triton/GPU errors as Python exceptions, engine.py:486-495). */
+#define WKV7_OK 0
+#define WKV7_ERR_NULL (-1)       /* a required pointer is NULL */
+#define WKV7_ERR_SHAPE (-2)      /* head_size != 64, H < 1, negative sizes, T too large */
+#define WKV7_ERR_ALIGN (-3)      /* operand/state pointers not 16-byte aligned, or strides not multiples of 8 */
+#define WKV7_ERR_WORKSPACE (-4)  /* workspace missing or smaller than wkv7_workspace_size() */
+#define WKV7_ERR_ARG (-5)        /* inconsistent arguments (snapshots on the chunked path, bad algo, ...) */
+
+/* Algorithm selection (wkv7_args.algo). */
+#define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens, chunked otherwise */
+#define WKV7_ALGO_RECURRENT 1  /* token-serial kernel for every row */
+#define WKV7_ALGO_CHUNKED 2    /* chunked MFMA prefill for every row */
+
+/*
+ * One call.  Operand element (token t, head h, channel i) is at ptr[t * in_tok_stride + h * 64 + i] (bf16 bit
+ * patterns); the reference's layout (B, T, H*K) contiguous has in_tok_stride = H * 64 and token index
+ * t = b * T + tau.
+ */
+typedef struct wkv7_args {
+    /* operands, bf16: r, w (raw log-log decay), k, v, a, b -- rwkv_next/kernels/wkv7.py:39, 60-73 */
+    const uint16_t *r, *w, *k, *v, *a, *b;
+    int64_t in_tok_stride;        /* elements between consecutive tokens (multiple of 8) */
+    uint16_t *o;                  /* output o, bf16, or NULL for STORE_O = False (wkv7.py:76-77, 93) */
+    int64_t o_tok_stride;         /* elements between consecutive output tokens (multiple of 8) */
+
+    /* states, fp32 [rows][H][64][64] -- h0 / ht of wkv7.py:62-64, 78-79 */
+    const float *h0;              /* initial states, or NULL for zeros (HAS_H0 = False) */
+    const int64_t *h0_idx;        /* NULL: sequence n reads h0 row n; else row h0_idx[n] (slot pool) */
+    int64_t h0_rows;              /* rows addressable through h0 (slot indices outside [0, h0_rows) read zeros) */
+    float *ht;                    /* final states, or NULL for final=False (STORE_HT, wkv7.py:78-79, 119) */
+    const int64_t *ht_idx;        /* NULL: row n; else row ht_idx[n].  ht == h0 with equal indices = in place */
+    int64_t ht_rows;              /* rows addressable through ht (indices outside are not written) */
+    const uint8_t *fresh;         /* NULL, or per sequence: nonzero = start from zeros (model.py:382-383) */
+
+    /* sequences -- wkv7.py:46-54 */
+    const int32_t *cu_seqlens;    /* NULL: dense, sequence n = tokens [n*T, (n+1)*T); else [num_seqs + 1] */
+    const int64_t *n_keep;        /* NULL, or per sequence: run only the first min(len, n_keep[n]) tokens */
+    float *snapshots;             /* NULL, or [num_seqs][T][H][64][64]: state after each token (recurrent) */
+
+    void *workspace;              /* device scratch for the chunked path (see wkv7_workspace_size) */
+    size_t workspace_bytes;
+
+    int32_t num_seqs;             /* N: B when dense, cu_seqlens entries - 1 when ragged */
+    int32_t T;                    /* dense: tokens per sequence.  Ragged: an upper bound on any row's length
+                                   * (0 = total_tokens); the snapshot time stride in both cases */
+    int64_t total_tokens;         /* operand rows: N*T dense, the packed length when ragged */
+    int32_t H;                    /* heads */
+    int32_t head_size;            /* must be 64 */
+    int32_t algo;                 /* WKV7_ALGO_* */
+    int32_t rec_max_len;          /* AUTO: rows of at most this many tokens run token-serial; -1 = default */
+} wkv7_args;
+
+/* Bytes of device workspace `wkv7_run` needs for these arguments (0 when only the token-serial kernel runs).
+ * Depends only on host-side sizes and flags, never on device data.  No reference counterpart: the reference's
+ * launcher allocates its outputs through the torch caching allocator (wkv7.py:93, 119, 135). */
+int wkv7_workspace_size(const wkv7_args *args, size_t *bytes);
+
+/* Run the recurrence for `args` on `stream` (a hipStream_t).  Replaces `_launch` + `_wkv7_raw`
+ * (rwkv_next/kernels/wkv7.py:89-104, 38-79), i.e. the bodies of
+ *   wkv7()          functional / varlen forward  (wkv7.py:126-138; torch op rwkv_next::wkv7_fwd, 113-123)
+ *   wkv7_replay()   in-place rollback over the first n_keep[b] tokens (wkv7.py:141-147)
+ * and the model's pool traffic around them (model.py:366-371 decode, 382-396 prefill gather/scatter,
+ * 485 verify with final=False) when h0/ht address the slot pool through h0_idx/ht_idx.
+ * Asynchronous; returns after launching. */
+int wkv7_run(const wkv7_args *args, void *stream);
+
+/* Static description of a return code. */
+const char *wkv7_strerror(int code);
+
+/* WKV7_ABI_VERSION of the loaded library. */
+int wkv7_abi_version(void);
+
+/* sizeof(wkv7_args) as compiled into the library, so a binding can check its struct layout. */
+size_t wkv7_args_size(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV_NEXT_AMD_WKV7_H */

@@ -1,0 +1,164 @@
+// wkv7_capi.hip -- the extern "C" entry points of include/wkv7.h: argument validation, the host-side choice
+// between the token-serial and the chunked kernels, and the launches.
+//
+// Everything here is decided from host-known sizes and flags (never from device data), so a call can be
+// recorded into a hipGraph and replayed with new device-side lengths, slots or n_keep values.
+#include <stdint.h>
+
+#include "wkv7.h"
+#include "wkv7_launch.h"
+
+namespace {
+
+using wkv7::Params;
+
+// AUTO threshold: rows of at most this many tokens run the token-serial kernel.  Below it one wavefront walking
+// the tokens beats the chunked path's fixed cost (a 64-token chunk transition built on MFMA per row).
+constexpr int kDefaultRecMaxLen = 32;
+
+struct Plan {
+    bool run_recurrent = false;
+    bool run_chunked = false;
+    int rec_len_rec = -1;    // Params.rec_max_len of the token-serial launch (-1: all rows)
+    int rec_len_chunk = -1;  // Params.rec_max_len of the chunked launch (-1: all rows)
+    wkv7::ChunkWorkspace ws{};
+};
+
+bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+int validate(const wkv7_args* a) {
+    if (a->head_size != wkv7::HS) return WKV7_ERR_SHAPE;
+    if (a->H < 1 || a->num_seqs < 0 || a->T < 0 || a->total_tokens < 0) return WKV7_ERR_SHAPE;
+    if (a->algo < WKV7_ALGO_AUTO || a->algo > WKV7_ALGO_CHUNKED) return WKV7_ERR_ARG;
+    if (a->rec_max_len < -1) return WKV7_ERR_ARG;
+    if ((int64_t)a->num_seqs * a->H > ((int64_t)1 << 31)) return WKV7_ERR_SHAPE;
+    if (!a->cu_seqlens && (int64_t)a->num_seqs * a->T > a->total_tokens) return WKV7_ERR_SHAPE;
+    if (a->T > (1 << 30) || a->total_tokens > ((int64_t)1 << 40)) return WKV7_ERR_SHAPE;
+    const bool has_tokens = a->num_seqs > 0 && a->total_tokens > 0;
+    if (has_tokens) {
+        const uint16_t* ops[6] = {a->r, a->w, a->k, a->v, a->a, a->b};
+        for (const uint16_t* p : ops) {
+            if (!p) return WKV7_ERR_NULL;
+            if (!aligned(p, 16)) return WKV7_ERR_ALIGN;
+        }
+        if (a->in_tok_stride < (int64_t)a->H * wkv7::HS || a->in_tok_stride % 8) return WKV7_ERR_ALIGN;
+        if (a->o) {
+            if (!aligned(a->o, 16)) return WKV7_ERR_ALIGN;
+            if (a->o_tok_stride < (int64_t)a->H * wkv7::HS || a->o_tok_stride % 8) return WKV7_ERR_ALIGN;
+        }
+    }
+    if (a->h0 && !aligned(a->h0, 16)) return WKV7_ERR_ALIGN;
+    if (a->ht && !aligned(a->ht, 16)) return WKV7_ERR_ALIGN;
+    if (a->h0_idx && !a->h0) return WKV7_ERR_ARG;
+    if (a->ht_idx && !a->ht) return WKV7_ERR_ARG;
+    if ((a->h0 && a->h0_rows < 0) || (a->ht && a->ht_rows < 0)) return WKV7_ERR_SHAPE;
+    if (a->snapshots) {
+        if (!aligned(a->snapshots, 16)) return WKV7_ERR_ALIGN;
+        if (a->T < 1) return WKV7_ERR_ARG;
+        if (a->algo == WKV7_ALGO_CHUNKED) return WKV7_ERR_ARG;
+    }
+    return WKV7_OK;
+}
+
+Plan make_plan(const wkv7_args* a) {
+    Plan pl;
+    const bool varlen = a->cu_seqlens != nullptr;
+    const int64_t bound = varlen ? (a->T > 0 ? a->T : a->total_tokens) : a->T;
+    const int thr = a->rec_max_len >= 0 ? a->rec_max_len : kDefaultRecMaxLen;
+    if (a->snapshots || a->algo == WKV7_ALGO_RECURRENT) {
+        pl.run_recurrent = true;
+    } else if (a->algo == WKV7_ALGO_CHUNKED) {
+        pl.run_chunked = true;
+    } else if (bound <= thr) {
+        pl.run_recurrent = true;
+    } else if (!varlen && !a->n_keep) {
+        pl.run_chunked = true;  // every row has exactly T > thr tokens
+    } else {
+        pl.run_recurrent = pl.run_chunked = true;  // row lengths are only known on the device: split by length
+        pl.rec_len_rec = thr;
+        pl.rec_len_chunk = thr;
+    }
+    if (pl.run_chunked)
+        pl.ws = wkv7::chunk_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen, pl.rec_len_chunk);
+    return pl;
+}
+
+Params to_params(const wkv7_args* a) {
+    Params p{};
+    p.r = a->r; p.w = a->w; p.k = a->k; p.v = a->v; p.a = a->a; p.b = a->b;
+    p.in_tok_stride = a->in_tok_stride;
+    p.o = a->o;
+    p.o_tok_stride = a->o_tok_stride;
+    p.h0 = a->h0;
+    p.h0_idx = a->h0_idx;
+    p.ht = a->ht;
+    p.ht_idx = a->ht_idx;
+    p.h0_rows = a->h0 ? (a->h0_idx ? a->h0_rows : (a->h0_rows > 0 ? a->h0_rows : a->num_seqs)) : 0;
+    p.ht_rows = a->ht ? (a->ht_idx ? a->ht_rows : (a->ht_rows > 0 ? a->ht_rows : a->num_seqs)) : 0;
+    p.fresh = a->fresh;
+    p.cu = a->cu_seqlens;
+    p.n_keep = a->n_keep;
+    p.snap = a->snapshots;
+    p.total_tokens = a->total_tokens;
+    p.num_seqs = a->num_seqs;
+    p.T = a->T;
+    p.H = a->H;
+    p.rec_max_len = -1;
+    return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wkv7_abi_version(void) { return WKV7_ABI_VERSION; }
+
+size_t wkv7_args_size(void) { return sizeof(wkv7_args); }
+
+const char* wkv7_strerror(int code) {
+    switch (code) {
+        case WKV7_OK: return "ok";
+        case WKV7_ERR_NULL: return "a required pointer is NULL";
+        case WKV7_ERR_SHAPE: return "invalid sizes (head_size must be 64, H >= 1, counts non-negative)";
+        case WKV7_ERR_ALIGN: return "pointers must be 16-byte aligned and token strides multiples of 8 elements";
+        case WKV7_ERR_WORKSPACE: return "workspace missing or smaller than wkv7_workspace_size()";
+        case WKV7_ERR_ARG: return "inconsistent arguments";
+        default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
+    }
+}
+
+int wkv7_workspace_size(const wkv7_args* args, size_t* bytes) {
+    if (!args || !bytes) return WKV7_ERR_NULL;
+    const int rc = validate(args);
+    if (rc != WKV7_OK) return rc;
+    const Plan pl = make_plan(args);
+    *bytes = pl.run_chunked ? pl.ws.total_bytes : 0;
+    return WKV7_OK;
+}
+
+int wkv7_run(const wkv7_args* args, void* stream) {
+    if (!args) return WKV7_ERR_NULL;
+    const int rc = validate(args);
+    if (rc != WKV7_OK) return rc;
+    const Plan pl = make_plan(args);
+    if (pl.run_chunked && pl.ws.total_bytes > 0) {
+        if (!args->workspace || args->workspace_bytes < pl.ws.total_bytes) return WKV7_ERR_WORKSPACE;
+        if (!aligned(args->workspace, 256)) return WKV7_ERR_ALIGN;
+    }
+    if (args->num_seqs == 0) return WKV7_OK;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    Params p = to_params(args);
+    if (pl.run_recurrent) {
+        p.rec_max_len = pl.rec_len_rec;
+        const hipError_t e = wkv7::launch_recurrent(p, s);
+        if (e != hipSuccess) return static_cast<int>(e);
+    }
+    if (pl.run_chunked) {
+        p.rec_max_len = pl.rec_len_chunk;
+        const hipError_t e = wkv7::launch_chunked(p, pl.ws, args->workspace, s);
+        if (e != hipSuccess) return static_cast<int>(e);
+    }
+    return WKV7_OK;
+}
+
+}  // extern "C"

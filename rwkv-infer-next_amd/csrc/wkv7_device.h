@@ -1,0 +1,120 @@
+// wkv7_device.h -- device-side building blocks shared by the WKV7 kernels (gfx950, wave64).
+//
+// Conventions (the reference's, rwkv_next/kernels/wkv7.py:4-7, 20):
+//   per (sequence, head) the state S is K x V = 64 x 64 fp32 stored row-major [k][v] (v contiguous);
+//   S_t = diag(d_t) S_{t-1} + b_t (a_t^T S_{t-1}) + k_t v_t^T,   d_t = exp(-exp(w_t)),   o_t = S_t^T r_t.
+//   Operands r, w, k, v, a, b and the output o are bf16 rows [token][head][64].
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wkv7 {
+
+constexpr int HS = 64;          // head size, K == V
+constexpr int HS2 = HS * HS;    // state elements per (sequence, head)
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Unpack two bf16 held in one 32-bit word (low half first).
+__device__ __forceinline__ void bf16x2_to_f32(uint32_t x, float& lo, float& hi) {
+    lo = __uint_as_float(x << 16);
+    hi = __uint_as_float(x & 0xffff0000u);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// log of the decay, log d = -exp(w), for the raw w (rwkv_next/kernels/wkv7.py:74).  Uses the device library's
+// full-precision expf.
+__device__ __forceinline__ float log_decay(float w) { return -expf(w); }
+__device__ __forceinline__ float decay(float w) { return expf(-expf(w)); }
+
+// Orders LDS traffic between the lanes of one wavefront: a wave's LDS instructions execute in issue order, so
+// only compiler reordering has to be prevented.
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Returns p as a wave-uniform (SGPR) value.  Loads through the result use a scalar base plus a 32-bit per-lane
+// offset; without it LLVM hoists `base + lane` out of token loops as one 64-bit VGPR pair per pointer.
+template <typename T>
+__device__ __forceinline__ T* uniform_ptr(T* p) {
+    const uint64_t x = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+
+// Kernel-side view of one call (filled by the C-ABI layer from wkv7_args after validation).
+struct Params {
+    const uint16_t *r, *w, *k, *v, *a, *b;
+    int64_t in_tok_stride;          // elements between tokens of the operands (head stride is 64)
+    uint16_t* o;                    // nullable output
+    int64_t o_tok_stride;
+    const float* h0;                // nullable initial states [h0_rows, H, 64, 64]
+    const int64_t* h0_idx;          // nullable: sequence n reads h0[h0_idx[n]]
+    float* ht;                      // nullable final states [ht_rows, H, 64, 64]
+    const int64_t* ht_idx;          // nullable: sequence n writes ht[ht_idx[n]]
+    int64_t h0_rows, ht_rows;       // state rows addressable through h0 / ht (indices outside are ignored)
+    const uint8_t* fresh;           // nullable: nonzero = sequence n starts from zeros
+    const int32_t* cu;              // nullable cu_seqlens [num_seqs + 1]
+    const int64_t* n_keep;          // nullable
+    float* snap;                    // nullable [num_seqs][T][H][64][64]
+    int64_t total_tokens;           // packed token count; ragged extents are clamped to it
+    int32_t num_seqs;
+    int32_t T;                      // dense tokens per sequence; snapshot time stride
+    int32_t H;
+    int32_t rec_max_len;            // chunked launches: rows this short run the recurrent path instead
+};
+
+// Extent of sequence n (rwkv_next/kernels/wkv7.py:46-54).
+__device__ __forceinline__ void seq_extent(const Params& p, int n, int64_t& bos, int& len) {
+    if (p.cu) {
+        // clamped to [0, total_tokens] so that a malformed cu_seqlens cannot index past the operands
+        int64_t s = p.cu[n], e = p.cu[n + 1];
+        s = s < 0 ? 0 : (s > p.total_tokens ? p.total_tokens : s);
+        e = e < s ? s : (e > p.total_tokens ? p.total_tokens : e);
+        bos = s;
+        len = (int)(e - s);
+    } else {
+        bos = (int64_t)n * p.T;
+        len = p.T;
+    }
+    if (p.n_keep) {
+        const int64_t nk = p.n_keep[n];
+        if (nk < len) len = (int)(nk < 0 ? 0 : nk);
+    }
+    if (len < 0) len = 0;
+}
+
+// Initial state of (sequence n, head h), or nullptr for a zero state (no h0, a fresh row, or a slot index
+// outside [0, h0_rows): such rows start from zeros instead of reading out of bounds).
+__device__ __forceinline__ const float* state_src(const Params& p, int n, int h) {
+    if (!p.h0 || (p.fresh && p.fresh[n])) return nullptr;
+    const int64_t s = p.h0_idx ? p.h0_idx[n] : n;
+    if (s < 0 || s >= p.h0_rows) return nullptr;
+    return p.h0 + (s * p.H + h) * (int64_t)HS2;
+}
+
+// Final-state destination, or nullptr when not stored (no ht, or a slot index outside [0, ht_rows)).
+__device__ __forceinline__ float* state_dst(const Params& p, int n, int h) {
+    if (!p.ht) return nullptr;
+    const int64_t s = p.ht_idx ? p.ht_idx[n] : n;
+    if (s < 0 || s >= p.ht_rows) return nullptr;
+    return p.ht + (s * p.H + h) * (int64_t)HS2;
+}
+
+}  // namespace wkv7

@@ -1,0 +1,37 @@
+// wkv7_launch.h -- host-side launchers of the WKV7 kernels (internal to the library; the public interface is
+// include/wkv7.h).  All launchers are asynchronous on `stream`, allocate nothing and never synchronise, so
+// every call can be recorded into a hipGraph.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "wkv7_device.h"
+
+namespace wkv7 {
+
+constexpr int kChunk = 64;                 // chunk length of the chunked prefill
+constexpr int kChunkFloats = 4 * HS2;      // per (chunk, head): A, H^T, Q, O_intra^T (fp32 64x64 each)
+
+// Token-serial kernel: every row, or only rows with len <= p.rec_max_len when p.rec_max_len >= 0.
+hipError_t launch_recurrent(const Params& p, hipStream_t stream);
+
+// Workspace of the chunked path for one call.  Layout (byte offsets, each 256-aligned):
+//   [plan]   int32 chunk_seq[max_chunks], chunk_idx[max_chunks], seq_off[num_seqs + 1], total   (varlen only)
+//   [chunks] float [max_chunks][H][4][64][64]
+struct ChunkWorkspace {
+    int64_t max_chunks;
+    size_t plan_bytes;
+    size_t chunk_bytes;
+    size_t total_bytes;
+};
+
+// max_len_bound: an upper bound on any row's length (dense: T).
+ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_t max_len_bound, bool varlen,
+                               int rec_max_len);
+
+// Chunked path over rows with len > p.rec_max_len (all rows when p.rec_max_len < 0): plan (varlen only), prep
+// (parallel over chunks), scan (sequential over chunks per (row, head, 16-column block)).
+hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* workspace, hipStream_t stream);
+
+}  // namespace wkv7

@@ -1,0 +1,112 @@
+"""ctypes binding of librwkv7_hip.so (the C ABI declared in include/wkv7.h).
+
+The library must have been built (rwkv_next_amd._build / __graft_entry__.build()).  There is no fallback: if the
+shared object is missing or does not match this binding, importing the kernels raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from ._build import LIB_PATH
+
+WKV7_ABI_VERSION = 1
+WKV7_OK = 0
+WKV7_ERR_NULL = -1
+WKV7_ERR_SHAPE = -2
+WKV7_ERR_ALIGN = -3
+WKV7_ERR_WORKSPACE = -4
+WKV7_ERR_ARG = -5
+
+ALGO_AUTO = 0
+ALGO_RECURRENT = 1
+ALGO_CHUNKED = 2
+
+EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size")
+
+_vp = ctypes.c_void_p
+
+
+class Wkv7Args(ctypes.Structure):
+    """Mirror of `wkv7_args` (include/wkv7.h); field order and types must match the header exactly."""
+    _fields_ = [
+        ("r", _vp), ("w", _vp), ("k", _vp), ("v", _vp), ("a", _vp), ("b", _vp),
+        ("in_tok_stride", ctypes.c_int64),
+        ("o", _vp),
+        ("o_tok_stride", ctypes.c_int64),
+        ("h0", _vp),
+        ("h0_idx", _vp),
+        ("h0_rows", ctypes.c_int64),
+        ("ht", _vp),
+        ("ht_idx", _vp),
+        ("ht_rows", ctypes.c_int64),
+        ("fresh", _vp),
+        ("cu_seqlens", _vp),
+        ("n_keep", _vp),
+        ("snapshots", _vp),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_size_t),
+        ("num_seqs", ctypes.c_int32),
+        ("T", ctypes.c_int32),
+        ("total_tokens", ctypes.c_int64),
+        ("H", ctypes.c_int32),
+        ("head_size", ctypes.c_int32),
+        ("algo", ctypes.c_int32),
+        ("rec_max_len", ctypes.c_int32),
+    ]
+
+
+class Wkv7Error(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"wkv7 error {code}: {msg}")
+        self.code = code
+
+
+_lib = None
+
+
+def load(path: str = LIB_PATH):
+    """Load the library (after torch, so that it binds to the HIP runtime torch loaded) and check its ABI."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build it with `python -m rwkv_next_amd._build` "
+                          "(or __graft_entry__.build()); there is no fallback implementation")
+    try:
+        import torch  # noqa: F401  -- load torch's libamdhip64 first
+    except ImportError:
+        pass
+    lib = ctypes.CDLL(path)
+    lib.wkv7_run.restype = ctypes.c_int
+    lib.wkv7_run.argtypes = [ctypes.POINTER(Wkv7Args), _vp]
+    lib.wkv7_workspace_size.restype = ctypes.c_int
+    lib.wkv7_workspace_size.argtypes = [ctypes.POINTER(Wkv7Args), ctypes.POINTER(ctypes.c_size_t)]
+    lib.wkv7_strerror.restype = ctypes.c_char_p
+    lib.wkv7_strerror.argtypes = [ctypes.c_int]
+    lib.wkv7_abi_version.restype = ctypes.c_int
+    lib.wkv7_args_size.restype = ctypes.c_size_t
+    if lib.wkv7_abi_version() != WKV7_ABI_VERSION:
+        raise ImportError(f"{path}: ABI version {lib.wkv7_abi_version()} != {WKV7_ABI_VERSION}")
+    if lib.wkv7_args_size() != ctypes.sizeof(Wkv7Args):
+        raise ImportError(f"{path}: sizeof(wkv7_args) {lib.wkv7_args_size()} != binding {ctypes.sizeof(Wkv7Args)}")
+    _lib = lib
+    return lib
+
+
+def strerror(code: int) -> str:
+    return load().wkv7_strerror(code).decode()
+
+
+def workspace_size(args: Wkv7Args) -> int:
+    n = ctypes.c_size_t(0)
+    rc = load().wkv7_workspace_size(ctypes.byref(args), ctypes.byref(n))
+    if rc != WKV7_OK:
+        raise Wkv7Error(rc, strerror(rc))
+    return int(n.value)
+
+
+def run(args: Wkv7Args, stream: int) -> None:
+    rc = load().wkv7_run(ctypes.byref(args), _vp(stream))
+    if rc != WKV7_OK:
+        raise Wkv7Error(rc, strerror(rc))

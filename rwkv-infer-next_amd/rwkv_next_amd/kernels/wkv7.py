@@ -1,0 +1,249 @@
+"""RWKV-7 WKV recurrence on MI355X: the reference's Python surface over the HIP library (include/wkv7.h).
+
+Per head the state S (K x V, fp32) evolves as
+
+    S_t = diag(d_t) S_{t-1} + b_t (a_t^T S_{t-1}) + k_t v_t^T          d_t = exp(-exp(w_t))
+    o_t = S_t^T r_t
+
+(rwkv_next/kernels/wkv7.py:4-7).  Same names, argument meanings and return values as the reference module
+rwkv_next/kernels/wkv7.py:
+    wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True) -> (o, ht | None)      (wkv7.py:126-138)
+    wkv7_replay(r, w, k, v, a, b, state, n_keep, H, K) -> state   (in place)                (wkv7.py:141-147)
+    torch op rwkv_next_amd::wkv7_fwd, functional, for torch.compile                          (wkv7.py:113-123)
+plus the slot-pool entry the reference builds around the op in the model (model.py:366-371, 382-396, 485):
+    wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, ...) -> o     (pool updated in place, optional snapshots)
+
+Layouts: r, w, k, v, a, b (B, T, H*K) bf16 (w RAW); states (N, H, K, K) fp32; o like v.  K must be 64.
+All work runs in HIP kernels on the current stream; nothing here synchronises, so every entry point can be
+captured in a CUDA/HIP graph.  There is no CPU or PyTorch fallback.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from .. import _lib
+
+HEAD_SIZE = 64
+OPERANDS = ("r", "w", "k", "v", "a", "b")
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else t.data_ptr()
+
+
+def _prep_operands(r, w, k, v, a, b, H, K):
+    if K != HEAD_SIZE:
+        raise ValueError(f"head size K={K} is not supported (the kernels are built for K = {HEAD_SIZE})")
+    ops = [r, w, k, v, a, b]
+    shape = r.shape
+    for name, t in zip(OPERANDS, ops):
+        if t.shape != shape:
+            raise ValueError(f"operand {name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"operand {name} must be bfloat16 (got {t.dtype})")
+        if t.device.type != "cuda":
+            raise ValueError(f"operand {name} must be on a GPU (got {t.device})")
+    if r.dim() == 4:
+        B, T = shape[0], shape[1]
+        if shape[2] != H or shape[3] != K:
+            raise ValueError(f"operands (B, T, H, K) = {tuple(shape)} do not match H={H}, K={K}")
+    elif r.dim() == 3:
+        B, T = shape[0], shape[1]
+        if shape[2] != H * K:
+            raise ValueError(f"operands (B, T, H*K) = {tuple(shape)} do not match H={H}, K={K}")
+    else:
+        raise ValueError(f"operands must be (B, T, H*K) or (B, T, H, K), got {tuple(shape)}")
+    ops = [t.contiguous() for t in ops]  # the reference does the same (wkv7.py:129, 144)
+    return ops, B, T
+
+
+def _state_arg(state, rows_expected, H, K, name="state"):
+    if state is None:
+        return None
+    if state.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32 (got {state.dtype})")
+    if tuple(state.shape[1:]) != (H, K, K):
+        raise ValueError(f"{name} must be (N, {H}, {K}, {K}), got {tuple(state.shape)}")
+    if rows_expected is not None and state.shape[0] != rows_expected:
+        raise ValueError(f"{name} has {state.shape[0]} rows, expected {rows_expected}")
+    return state.contiguous()
+
+
+def _launch(ops, *, H, num_seqs, T, total, o=None, h0=None, h0_idx=None, h0_rows=0, ht=None, ht_idx=None,
+            ht_rows=0, fresh=None, cu=None, n_keep=None, snap=None, algo=_lib.ALGO_AUTO, rec_max_len=-1):
+    dev = ops[0].device
+    args = _lib.Wkv7Args()
+    for name, t in zip(OPERANDS, ops):
+        setattr(args, name, t.data_ptr())
+    args.in_tok_stride = H * HEAD_SIZE
+    args.o = _ptr(o)
+    args.o_tok_stride = H * HEAD_SIZE
+    args.h0, args.h0_idx, args.h0_rows = _ptr(h0), _ptr(h0_idx), h0_rows
+    args.ht, args.ht_idx, args.ht_rows = _ptr(ht), _ptr(ht_idx), ht_rows
+    args.fresh = _ptr(fresh)
+    args.cu_seqlens = _ptr(cu)
+    args.n_keep = _ptr(n_keep)
+    args.snapshots = _ptr(snap)
+    args.num_seqs, args.T, args.total_tokens = num_seqs, T, total
+    args.H, args.head_size, args.algo, args.rec_max_len = H, HEAD_SIZE, algo, rec_max_len
+    nbytes = _lib.workspace_size(args)
+    ws = None
+    if nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)  # caching allocator (graph pool under capture)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+    with torch.cuda.device(dev):
+        _lib.run(args, torch.cuda.current_stream(dev).cuda_stream)
+    return ws
+
+
+def _index_tensor(x, dev, dtype, name):
+    if x is None:
+        return None
+    x = torch.as_tensor(x, device=dev)
+    if x.dtype != dtype:
+        x = x.to(dtype)
+    return x.contiguous()
+
+
+# --------------------------------------------------------------------------------------------------------------
+# functional forward (reference: _wkv7_op / wkv7)
+# --------------------------------------------------------------------------------------------------------------
+def _fwd_impl(r, w, k, v, a, b, h0, H: int, K: int, final: bool, algo: int = _lib.ALGO_AUTO):
+    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    h0 = _state_arg(h0 if (h0 is not None and h0.numel()) else None, B, H, K, "h0")
+    o = torch.empty_like(ops[3])
+    ht = torch.empty(B, H, K, K, device=r.device, dtype=torch.float32) if final else r.new_empty(0,
+                                                                                              dtype=torch.float32)
+    _launch(ops, H=H, num_seqs=B, T=T, total=B * T, o=o, h0=h0, h0_rows=B, ht=ht if final else None, ht_rows=B,
+            algo=algo)
+    return o, ht
+
+
+@torch.library.custom_op("rwkv_next_amd::wkv7_fwd", mutates_args=())
+def wkv7_fwd(r: torch.Tensor, w: torch.Tensor, k: torch.Tensor, v: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
+             h0: torch.Tensor, H: int, K: int, final: bool) -> tuple[torch.Tensor, torch.Tensor]:
+    """Functional form (fresh o and final state) with the schema of the reference's rwkv_next::wkv7_fwd
+    (rwkv_next/kernels/wkv7.py:113-123).  h0 may be empty (0 rows) for a zero initial state."""
+    return _fwd_impl(r, w, k, v, a, b, h0, H, K, final)
+
+
+@wkv7_fwd.register_fake
+def _(r, w, k, v, a, b, h0, H, K, final):
+    B = r.shape[0]
+    return torch.empty_like(v), (r.new_empty(B, H, K, K, dtype=torch.float32) if final
+                                 else r.new_empty(0, dtype=torch.float32))
+
+
+def wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True, *, algo: int = _lib.ALGO_AUTO):
+    """o, final_state = recurrence over (B, T, H*K) inputs from `state` (B|N, H, K, K) fp32 or None.
+    w is RAW (decay = exp(-exp(w))).  cu_seqlens (N+1,) int32: packed varlen (B must be 1).
+    Mirrors rwkv_next/kernels/wkv7.py:126-138."""
+    if cu_seqlens is None:
+        if algo == _lib.ALGO_AUTO:
+            h0 = state.contiguous() if state is not None else r.new_empty(0, dtype=torch.float32)
+            o, ht = wkv7_fwd(r, w, k, v, a, b, h0, H, K, final)
+        else:
+            o, ht = _fwd_impl(r, w, k, v, a, b, state, H, K, final, algo)
+        return o, (ht if final else None)
+    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    if B != 1:
+        raise ValueError("cu_seqlens requires B == 1 (packed varlen)")
+    cu = _index_tensor(cu_seqlens, r.device, torch.int32, "cu_seqlens")
+    N = cu.numel() - 1
+    h0 = _state_arg(state, N, H, K, "state")
+    o = torch.empty_like(ops[3])
+    ht = torch.empty(N, H, K, K, device=r.device, dtype=torch.float32) if final else None
+    _launch(ops, H=H, num_seqs=N, T=0, total=T, o=o, h0=h0, h0_rows=N, ht=ht, ht_rows=N, cu=cu, algo=algo)
+    return o, ht
+
+
+def wkv7_replay(r, w, k, v, a, b, state, n_keep, H, K):
+    """Rollback: state (B, H, K, K) fp32 := the recurrence over the first n_keep[b] steps of row b, IN PLACE.
+    No output is computed.  Mirrors rwkv_next/kernels/wkv7.py:141-147."""
+    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    if state.dtype != torch.float32 or not state.is_contiguous() or tuple(state.shape) != (B, H, K, K):
+        raise ValueError(f"state must be a contiguous float32 ({B}, {H}, {K}, {K}) tensor")
+    nk = _index_tensor(n_keep, r.device, torch.int64, "n_keep")
+    if nk.numel() != B:
+        raise ValueError(f"n_keep has {nk.numel()} entries, expected {B}")
+    _launch(ops, H=H, num_seqs=B, T=T, total=B * T, h0=state, h0_rows=B, ht=state, ht_rows=B, n_keep=nk,
+            algo=_lib.ALGO_RECURRENT)
+    return state
+
+
+# --------------------------------------------------------------------------------------------------------------
+# slot-pool entry (the model's decode / prefill / verify call sites, model.py:366-371, 382-396, 485)
+# --------------------------------------------------------------------------------------------------------------
+def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=None, fresh=None, final=True,
+               store_o=True, snapshots=None, max_len: int = 0, algo: int = _lib.ALGO_AUTO,
+               rec_max_len: int = -1, check_slots: bool = False):
+    """Recurrence for N sequences whose states live in `pool` (S, H, K, K) fp32, updated IN PLACE.
+
+    slots (N,) int64: pool row of each sequence (must be distinct).  Dense operands (N, T, H*K), or packed
+    (1, sumT, H*K) with cu_seqlens (N+1,) int32.  fresh (N,) bool: start those rows from zeros (the reference
+    zeroes them first, model.py:382-383).  n_keep (N,) int64: run only the first n_keep[n] tokens.
+    final=False reads the pool without writing it (speculative verify, model.py:475-496).
+    snapshots: optional (N, T, H, K, K) fp32 receiving the state after every token (dense only); rolling back to
+    an accepted prefix of n tokens is `restore_snapshots_(pool, slots, snapshots, n)`.
+    max_len: ragged calls may pass an upper bound on any row's length (sizes the workspace; 0 = sumT).
+    Returns o like v (or None when store_o=False)."""
+    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    dev = r.device
+    if pool.dtype != torch.float32 or not pool.is_contiguous() or tuple(pool.shape[1:]) != (H, K, K):
+        raise ValueError(f"pool must be a contiguous float32 (S, {H}, {K}, {K}) tensor")
+    sl = _index_tensor(slots, dev, torch.int64, "slots")
+    if cu_seqlens is not None:
+        if B != 1:
+            raise ValueError("cu_seqlens requires B == 1 (packed varlen)")
+        cu = _index_tensor(cu_seqlens, dev, torch.int32, "cu_seqlens")
+        N, Tn, total = cu.numel() - 1, int(max_len), T
+    else:
+        cu, N, Tn, total = None, B, T, B * T
+    if sl.numel() != N:
+        raise ValueError(f"slots has {sl.numel()} entries, expected {N}")
+    if check_slots:  # host sync: for tests and debugging, not for the graphed hot path
+        check_distinct_slots(sl, pool.shape[0])
+    nk = _index_tensor(n_keep, dev, torch.int64, "n_keep")
+    fr = None
+    if fresh is not None:
+        fr = torch.as_tensor(fresh, device=dev)
+        fr = (fr if fr.dtype == torch.uint8 else fr.to(torch.uint8)).contiguous()
+    if snapshots is not None:
+        if cu is not None:
+            raise ValueError("snapshots are supported for dense (N, T) calls only")
+        if snapshots.dtype != torch.float32 or not snapshots.is_contiguous() or \
+                tuple(snapshots.shape) != (N, T, H, K, K):
+            raise ValueError(f"snapshots must be a contiguous float32 ({N}, {T}, {H}, {K}, {K}) tensor")
+    o = torch.empty_like(ops[3]) if store_o else None
+    S = pool.shape[0]
+    _launch(ops, H=H, num_seqs=N, T=Tn, total=total, o=o, h0=pool, h0_idx=sl, h0_rows=S,
+            ht=pool if final else None, ht_idx=sl if final else None, ht_rows=S, fresh=fr, cu=cu, n_keep=nk,
+            snap=snapshots, algo=algo, rec_max_len=rec_max_len)
+    return o
+
+
+def check_distinct_slots(slots: torch.Tensor, num_slots: int) -> None:
+    """Raise if slot indices repeat or fall outside [0, num_slots).  Duplicate slots in one in-place call race
+    (the reference's index_copy_ is nondeterministic for them, model.py:396).  Synchronises the host."""
+    s = slots.detach().to("cpu")
+    if s.numel() and (int(s.min()) < 0 or int(s.max()) >= num_slots):
+        raise ValueError(f"slot index outside [0, {num_slots})")
+    if torch.unique(s).numel() != s.numel():
+        raise ValueError("duplicate slot indices in one call")
+
+
+def restore_snapshots_(pool, slots, snapshots, n):
+    """Rollback after a speculative verify: pool[slots[b]] := snapshots[b, n[b] - 1], the state after the first
+    n[b] tokens (1 <= n[b] <= T); rows with n[b] = 0 keep the pool's state (a verify with final=False does not
+    write the pool).  Replaces the reference's second recurrence pass, wkv7_replay (model.py:498-508).
+    Device-side gather + scatter, no host sync."""
+    N = snapshots.shape[0]
+    nn = torch.as_tensor(n, device=pool.device).long()
+    idx = (nn - 1).clamp(0, snapshots.shape[1] - 1)
+    sl = torch.as_tensor(slots, device=pool.device).long()
+    new = snapshots[torch.arange(N, device=pool.device), idx]
+    new = torch.where((nn > 0).view(-1, 1, 1, 1), new, pool.index_select(0, sl))
+    pool.index_copy_(0, sl, new)
+    return pool

@@ -1,0 +1,99 @@
+"""The C ABI (include/wkv7.h) without a GPU: the library loads, exports every function the header declares, its
+struct layout matches the ctypes binding, and invalid arguments are rejected on the host before any launch.
+No compute call is made here (wkv7_run only reaches a launch after validation succeeds)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from conftest import REPO
+
+from rwkv_next_amd import _lib
+
+HEADER = os.path.join(REPO, "include", "wkv7.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(wkv7_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    names = declared_functions()
+    assert set(names) == set(_lib.EXPORTED), names
+    for n in names:
+        assert hasattr(lib, n), n
+
+
+def test_abi_version_and_struct_layout():
+    lib = _lib.load()
+    assert lib.wkv7_abi_version() == _lib.WKV7_ABI_VERSION
+    assert lib.wkv7_args_size() == ctypes.sizeof(_lib.Wkv7Args)
+
+
+def base_args(**kw):
+    a = _lib.Wkv7Args()
+    fake = 0x10000  # 64 KiB-aligned non-null "device" address: never dereferenced by the host-side checks below
+    for n in ("r", "w", "k", "v", "a", "b"):
+        setattr(a, n, fake)
+    a.in_tok_stride = 2 * 64
+    a.o, a.o_tok_stride = fake, 2 * 64
+    a.num_seqs, a.T, a.total_tokens, a.H, a.head_size = 3, 5, 15, 2, 64
+    a.algo, a.rec_max_len = _lib.ALGO_AUTO, -1
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("field,value,code", [
+    ("head_size", 63, _lib.WKV7_ERR_SHAPE),
+    ("H", 0, _lib.WKV7_ERR_SHAPE),
+    ("num_seqs", -1, _lib.WKV7_ERR_SHAPE),
+    ("total_tokens", 14, _lib.WKV7_ERR_SHAPE),        # dense rows need num_seqs * T operand rows
+    ("algo", 7, _lib.WKV7_ERR_ARG),
+    ("rec_max_len", -2, _lib.WKV7_ERR_ARG),
+    ("r", None, _lib.WKV7_ERR_NULL),
+    ("w", 0x10002, _lib.WKV7_ERR_ALIGN),
+    ("in_tok_stride", 2 * 64 + 4, _lib.WKV7_ERR_ALIGN),
+    ("in_tok_stride", 64, _lib.WKV7_ERR_ALIGN),        # smaller than H * 64
+    ("o_tok_stride", 2 * 64 + 2, _lib.WKV7_ERR_ALIGN),
+    ("h0_idx", 0x10000, _lib.WKV7_ERR_ARG),            # an index without a state array
+])
+def test_validation_rejects_before_launch(field, value, code):
+    a = base_args(**{field: value})
+    n = ctypes.c_size_t(0)
+    lib = _lib.load()
+    assert lib.wkv7_workspace_size(ctypes.byref(a), ctypes.byref(n)) == code
+    assert lib.wkv7_run(ctypes.byref(a), None) == code
+    assert _lib.strerror(code) not in ("", "unknown error")
+
+
+def test_snapshots_force_the_token_serial_kernel():
+    a = base_args(snapshots=0x10000, T=40, total_tokens=120)
+    assert _lib.workspace_size(a) == 0                     # token-serial: no workspace
+    a.algo = _lib.ALGO_CHUNKED
+    with pytest.raises(_lib.Wkv7Error) as e:
+        _lib.workspace_size(a)
+    assert e.value.code == _lib.WKV7_ERR_ARG
+
+
+def test_workspace_sizing_follows_the_dispatch_rule():
+    # dense short rows: token-serial, no workspace
+    assert _lib.workspace_size(base_args(T=32, total_tokens=96)) == 0
+    # dense long rows: chunked; 3 rows x ceil(100/64) chunks x H=2 x 4 matrices of 64x64 fp32
+    n = _lib.workspace_size(base_args(T=100, total_tokens=300))
+    assert n >= 3 * 2 * 2 * 4 * 64 * 64 * 4
+    # ragged: bound by total_tokens, plus the chunk table
+    r = _lib.workspace_size(base_args(cu_seqlens=0x10000, T=0, total_tokens=1000))
+    assert r > 0
+    # a missing workspace is refused before launch
+    a = base_args(T=100, total_tokens=300)
+    assert _lib.load().wkv7_run(ctypes.byref(a), None) == _lib.WKV7_ERR_WORKSPACE
+
+
+def test_zero_sequences_is_a_no_op():
+    a = base_args(num_seqs=0, total_tokens=0)
+    assert _lib.load().wkv7_run(ctypes.byref(a), None) == _lib.WKV7_OK
