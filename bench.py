@@ -28,6 +28,7 @@ HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
 DECODE_BYTES_PER_PAIR = 16384 + 16384 + 6 * 64 * 2 + 64 * 2       # 33 664
 PREFILL_BYTES_PER_HEAD_TOKEN = 6 * 64 * 2 + 64 * 2                 # 896 (+ 32 KB state per (sequence, head))
+COPY_CALIB_BYTES = 1 << 30
 C = 64
 PREFILL_FLOPS_PER_HEAD_TOKEN = 18 * C * 64 + 8 * 64 * 64 + (2 * C * C) // 3   # chunked form at C = 64
 
@@ -157,6 +158,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--only", choices=["decode", "prefill", "verify"], default=None)
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="first run a plain device copy of 1 GiB (reference dispatch for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: the WKV7 recurrence has no cross-GPU exchange (heads and slots shard "
@@ -170,6 +173,13 @@ def main():
 
     dev = torch.device("cuda:0")
     res = {}
+    if args.copy_calib:
+        src = torch.ones(COPY_CALIB_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     if args.only in (None, "decode"):
         log("decode")
         res["decode"] = decode_bench(torch, kernels, synth, dev, args.steps, args.warmup)
