@@ -151,6 +151,17 @@ def cpu_baseline(synth):
                       f"(oracle fp32 loop, OpenMP); CPU: {model}"}
 
 
+def decode_traffic():
+    """HBM bytes per decode launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, each
+    scaled by what the same counter reads for a 1 GiB device copy), or None if absent."""
+    path = os.path.join(REPO, "profiles", "wkv7_recurrent_decode_B64_H64.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -215,7 +226,7 @@ def main():
     if d:
         achieved = d["bytes_per_launch"] / (d["us_per_launch"] * 1e-6) / 1e9
         out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": achieved / HBM_PEAK_GBS, "traffic": None,
+                           "frac": achieved / HBM_PEAK_GBS, "traffic": decode_traffic(),
                            "kernel": "wkv7_recurrent_kernel", "us_per_launch": d["us_per_launch"]}
     if "prefill" in res:
         out["prefill"] = res["prefill"]
