@@ -3,15 +3,20 @@
 //
 // Replaces the reference's fused recurrent Triton program _wkv7_raw (rwkv_next/kernels/wkv7.py:38-79) for
 // these cases.  Work decomposition (MI355X, wave64):
-//   * one wavefront per (sequence, head); a 256-thread workgroup holds 4 independent pairs;
-//   * lane L = 16 g + c owns state rows k = 16 g .. 16 g + 15 and columns v = 4 c .. 4 c + 3, i.e. 64 fp32 in
-//     VGPRs.  Each of the 16 row loads is one dwordx4 per lane, and one load instruction of the wave reads four
-//     full 256-byte state rows, so the 16 KB state arrives in 16 coalesced instructions;
-//   * the per-token k-side vectors (decay, a, b, k, r) are computed by lane i for channel i and broadcast
-//     through a 1.25 KB per-wave LDS slab; v is read per lane;
+//   * one wavefront per (sequence, head) pair at a time.  The grid holds at most two waves per SIMD; each wave
+//     walks pairs gw, gw + nwaves, ... and issues the next pair's state loads before working on the current
+//     pair, so state reads, the recurrence math and state writes of different pairs overlap (with one pair per
+//     wave all waves would read, then all compute, then all write);
+//   * lane L = 16 g + c owns state rows k = 4 i + g (i = 0..15) and columns v = 4 c .. 4 c + 3: 64 fp32 in VGPRs.
+//     Load instruction i of a wave reads rows 4i .. 4i+3, i.e. 1 KB contiguous, so a 16 KB state arrives in 16
+//     coalesced dwordx4 instructions.  State traffic is streamed with non-temporal loads and stores (each state
+//     is touched once per call);
+//   * the per-token k-side vectors (decay, a, b, k, r) are computed by lane i for channel i and broadcast through
+//     a per-wave LDS slab, stored permuted (channel 4 i + g at slot 16 g + i) so each lane group reads its 16
+//     channels with four ds_read_b128; v is read per lane;
 //   * sa = a^T S and y = S^T r are lane-local sums over the lane's 16 rows followed by a two-step xor butterfly
 //     over the four row groups.  Every lane ends with bitwise identical sums (fp add is commutative), so all
-//     lanes hold the same update.
+//     lanes hold the same update.  Updated rows are stored as soon as they are final.
 // Decode is HBM-bound: 16 KB state read + 16 KB written per pair, plus 896 B of operands and output.
 //
 // The per-token arithmetic is one fixed instruction sequence with explicit fmaf (the file is built with
@@ -23,12 +28,18 @@ namespace wkv7 {
 
 namespace {
 
-constexpr int kWaves = 4;
+constexpr int kWaves = 4;            // waves per workgroup
+constexpr int kWavesPerSimd = 2;     // residency target: two 16 KB states in flight per wave
 
 struct TokenIn {
     uint16_t w, a, b, k, r;
     uint2 v;  // 4 bf16: v[4c .. 4c+3]
 };
+
+__device__ __forceinline__ f4 load_nt(const float* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+}
+__device__ __forceinline__ void store_nt(float* p, f4 x) { __builtin_nontemporal_store(x, reinterpret_cast<f4*>(p)); }
 
 // The token/head offset is wave-uniform and kept apart from the per-lane offset, so the loads use a scalar base
 // address plus a 32-bit vector offset instead of one 64-bit address per lane and operand.
@@ -48,50 +59,60 @@ __device__ __forceinline__ float butterfly4(float x) {
     return x;
 }
 
-__global__ __launch_bounds__(256, 4) void wkv7_recurrent_kernel(const Params p) {
-    __shared__ __attribute__((aligned(16))) float vec[kWaves][5][HS];  // decay, a, b, k, r
-    const int lane = threadIdx.x & 63;
-    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: indices stay in SGPRs
-    const int64_t pair = (int64_t)blockIdx.x * kWaves + wv;
-    if (pair >= (int64_t)p.num_seqs * p.H) return;  // no workgroup barriers below: waves are independent
-    const int n = (int)(pair / p.H), h = (int)(pair % p.H);
+// Pair geometry: sequence, head, first token, length; `run` is false for pairs another launch owns.
+struct Pair {
+    int n, h, L;
     int64_t bos;
-    int L;
-    seq_extent(p, n, bos, L);
-    if (p.rec_max_len >= 0 && L > p.rec_max_len) return;  // a chunked launch owns this row
+    bool run;
+};
 
-    const int g = lane >> 4, c = lane & 15;
-    float S[16][4];
-    if (const float* src = state_src(p, n, h)) {
-        const float* s = src + (16 * g) * HS + 4 * c;
+__device__ __forceinline__ Pair pair_of(const Params& p, uint32_t pair) {
+    Pair q;
+    q.n = (int)(pair / (uint32_t)p.H);
+    q.h = (int)(pair % (uint32_t)p.H);
+    seq_extent(p, q.n, q.bos, q.L);
+    q.run = p.rec_max_len < 0 || q.L <= p.rec_max_len;  // else a chunked launch owns this row
+    return q;
+}
+
+// Issue the loads of a pair's initial state (rows 4 i + g) and of its first token's operands.
+__device__ __forceinline__ void prefetch_pair(const Params& p, const Pair& q, int lane, int g, int c, f4 (&S)[16],
+                                              TokenIn& x) {
+    if (!q.run) return;
+    if (const float* src = state_src(p, q.n, q.h)) {
+        const float* s = uniform_ptr(src);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const f4 x = *reinterpret_cast<const f4*>(s + i * HS);
-            S[i][0] = x[0]; S[i][1] = x[1]; S[i][2] = x[2]; S[i][3] = x[3];
-        }
+        for (int i = 0; i < 16; ++i) S[i] = load_nt(s + (4 * i + g) * HS + 4 * c);
     } else {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) S[i][0] = S[i][1] = S[i][2] = S[i][3] = 0.f;
+        for (int i = 0; i < 16; ++i) S[i] = f4{0.f, 0.f, 0.f, 0.f};
     }
+    if (q.L > 0) load_token(p, q.bos, q.h, lane, c, x);
+}
 
-    float* const dvec = vec[wv][0];
-    float* const avec = vec[wv][1];
-    float* const bvec = vec[wv][2];
-    float* const kvec = vec[wv][3];
-    float* const rvec = vec[wv][4];
-
-    TokenIn cur{}, nxt{};
-    if (L > 0) load_token(p, bos, h, lane, c, cur);
-    for (int t = 0; t < L; ++t) {
-        dvec[lane] = decay(bf16_to_f32(cur.w));
-        avec[lane] = bf16_to_f32(cur.a);
-        bvec[lane] = bf16_to_f32(cur.b);
-        kvec[lane] = bf16_to_f32(cur.k);
-        rvec[lane] = bf16_to_f32(cur.r);
+// The recurrence over one pair's tokens, state in S (rows 4 i + g, columns 4 c .. 4 c + 3).
+__device__ __forceinline__ void run_pair(const Params& p, const Pair& q, int lane, int g, int c, f4 (&S)[16],
+                                         TokenIn cur, float* slab) {
+    if (!q.run) return;
+    float* const dvec = slab;
+    float* const avec = slab + HS;
+    float* const bvec = slab + 2 * HS;
+    float* const kvec = slab + 3 * HS;
+    float* const rvec = slab + 4 * HS;
+    const int slot = (lane & 3) * 16 + (lane >> 2);  // LDS position of channel `lane`
+    float* const dst = state_dst(p, q.n, q.h);
+    float* const dst_u = dst ? uniform_ptr(dst) : nullptr;
+    TokenIn nxt = cur;
+    for (int t = 0; t < q.L; ++t) {
+        dvec[slot] = decay(bf16_to_f32(cur.w));
+        avec[slot] = bf16_to_f32(cur.a);
+        bvec[slot] = bf16_to_f32(cur.b);
+        kvec[slot] = bf16_to_f32(cur.k);
+        rvec[slot] = bf16_to_f32(cur.r);
         float vj[4];
         bf16x2_to_f32(cur.v.x, vj[0], vj[1]);
         bf16x2_to_f32(cur.v.y, vj[2], vj[3]);
-        if (t + 1 < L) load_token(p, bos + t + 1, h, lane, c, nxt);  // in flight during this token's math
+        if (t + 1 < q.L) load_token(p, q.bos + t + 1, q.h, lane, c, nxt);  // in flight during this token's math
         wave_lds_sync();
 
         // sa[j] = sum_k a_k S[k][j] over the old state (wkv7.py:75)
@@ -101,15 +122,18 @@ __global__ __launch_bounds__(256, 4) void wkv7_recurrent_kernel(const Params p) 
             const f4 av = *reinterpret_cast<const f4*>(avec + 16 * g + 4 * i4);
 #pragma unroll
             for (int ii = 0; ii < 4; ++ii) {
-                const int i = 4 * i4 + ii;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) sa[j] = fmaf(av[ii], S[i][j], sa[j]);
+                for (int j = 0; j < 4; ++j) sa[j] = fmaf(av[ii], S[4 * i4 + ii][j], sa[j]);
             }
         }
 #pragma unroll
         for (int j = 0; j < 4; ++j) sa[j] = butterfly4(sa[j]);
 
         // S[k][j] = d_k S[k][j] + b_k sa[j] + k_k v_j;  y[j] = sum_k r_k S[k][j] (updated state, wkv7.py:75-77)
+        const bool last = t + 1 == q.L;
+        float* const snap = (p.snap && t < p.T)
+                                ? uniform_ptr(p.snap + (((int64_t)q.n * p.T + t) * p.H + q.h) * (int64_t)HS2)
+                                : nullptr;
         float y[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int i4 = 0; i4 < 4; ++i4) {
@@ -126,7 +150,15 @@ __global__ __launch_bounds__(256, 4) void wkv7_recurrent_kernel(const Params p) 
                     y[j] = fmaf(rv[ii], S[i][j], y[j]);
                 }
             }
-            // keeps the scheduler from hoisting all 64 broadcast reads above the FMAs (VGPR budget: 4 waves/SIMD)
+            if (snap) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) store_nt(snap + (4 * (4 * i4 + ii) + g) * HS + 4 * c, S[4 * i4 + ii]);
+            }
+            if (last && dst_u) {
+#pragma unroll
+                for (int ii = 0; ii < 4; ++ii) store_nt(dst_u + (4 * (4 * i4 + ii) + g) * HS + 4 * c, S[4 * i4 + ii]);
+            }
+            // keeps the scheduler from hoisting all 64 broadcast reads above the FMAs (VGPR budget)
             __builtin_amdgcn_sched_barrier(0);
         }
 #pragma unroll
@@ -136,29 +168,50 @@ __global__ __launch_bounds__(256, 4) void wkv7_recurrent_kernel(const Params p) 
             uint2 pk;
             pk.x = pack_bf16x2(y[0], y[1]);
             pk.y = pack_bf16x2(y[2], y[3]);
-            uniform_ptr(reinterpret_cast<uint2*>(p.o + (bos + t) * p.o_tok_stride + (int64_t)h * HS))[c] = pk;
-        }
-        if (p.snap && t < p.T) {
-            f4* sp = uniform_ptr(reinterpret_cast<f4*>(p.snap + (((int64_t)n * p.T + t) * p.H + h) * (int64_t)HS2));
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                f4 x;
-                x[0] = S[i][0]; x[1] = S[i][1]; x[2] = S[i][2]; x[3] = S[i][3];
-                sp[(16 * g + i) * (HS / 4) + c] = x;
-            }
+            uniform_ptr(reinterpret_cast<uint2*>(p.o + (q.bos + t) * p.o_tok_stride + (int64_t)q.h * HS))[c] = pk;
         }
         cur = nxt;
         wave_lds_sync();  // this token's LDS reads precede the next token's writes
     }
-
-    if (float* dst = state_dst(p, n, h)) {
-        float* s = dst + (16 * g) * HS + 4 * c;
+    if (q.L == 0 && dst_u) {  // no tokens: the state passes through (wkv7.py:65-79 with L = 0)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            f4 x;
-            x[0] = S[i][0]; x[1] = S[i][1]; x[2] = S[i][2]; x[3] = S[i][3];
-            *reinterpret_cast<f4*>(s + i * HS) = x;
+        for (int i = 0; i < 16; ++i) store_nt(dst_u + (4 * i + g) * HS + 4 * c, S[i]);
+    }
+}
+
+__global__ __launch_bounds__(64 * kWaves, kWavesPerSimd) void wkv7_recurrent_kernel(const Params p) {
+    __shared__ __attribute__((aligned(16))) float slab[kWaves][5 * HS];  // decay, a, b, k, r (permuted)
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: indices stay in SGPRs
+    const int g = lane >> 4, c = lane & 15;
+    // pair indices fit 32 bits (wkv7_run validates num_seqs * H <= 2^31); 64-bit divisions are software-emulated
+    const uint32_t npairs = (uint32_t)p.num_seqs * (uint32_t)p.H;
+    const uint32_t nwaves = gridDim.x * kWaves;
+    uint32_t pa = blockIdx.x * kWaves + wv;
+    if (pa >= npairs) return;  // no workgroup barriers below: waves are independent
+
+    f4 SA[16], SB[16];
+    TokenIn xa{}, xb{};
+    Pair qa = pair_of(p, pa);
+    prefetch_pair(p, qa, lane, g, c, SA, xa);
+    // Wave w takes pairs w, w + nwaves, ...  Two buffers, unrolled by two so that the state arrays stay in
+    // registers: the next pair's loads are issued before the current pair runs.
+    while (true) {
+        const uint32_t pb = pa + nwaves;
+        Pair qb{};
+        if (pb < npairs) {
+            qb = pair_of(p, pb);
+            prefetch_pair(p, qb, lane, g, c, SB, xb);
         }
+        run_pair(p, qa, lane, g, c, SA, xa, slab[wv]);
+        if (pb >= npairs) break;
+        pa = pb + nwaves;
+        if (pa < npairs) {
+            qa = pair_of(p, pa);
+            prefetch_pair(p, qa, lane, g, c, SA, xa);
+        }
+        run_pair(p, qb, lane, g, c, SB, xb, slab[wv]);
+        if (pa >= npairs) break;
     }
 }
 
@@ -167,7 +220,14 @@ __global__ __launch_bounds__(256, 4) void wkv7_recurrent_kernel(const Params p) 
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
     if (pairs == 0) return hipSuccess;
-    const int64_t blocks = (pairs + kWaves - 1) / kWaves;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) {
+        int v = 0;
+        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    }
+    const int64_t max_waves = (int64_t)cus * 4 * kWavesPerSimd;  // 4 SIMDs per CU
+    const int64_t waves = pairs < max_waves ? pairs : max_waves;
+    const int64_t blocks = (waves + kWaves - 1) / kWaves;
     hipLaunchKernelGGL(wkv7_recurrent_kernel, dim3((unsigned)blocks), dim3(64 * kWaves), 0, stream, p);
     return hipGetLastError();
 }
