@@ -1,4 +1,4 @@
-// wkv7_chunked.hip -- chunked WKV7 prefill on fp32 MFMA (gfx950).
+// wkv7_chunked.hip -- chunked WKV7 prefill on bf16 MFMA (gfx950, v_mfma_f32_16x16x32_bf16).
 //
 // Replaces the reference's token-serial Triton program (rwkv_next/kernels/wkv7.py:65-77) for long rows: the
 // reference walks every token of a row in one program, so a B=1, T=4096, H=64 prefill has only
@@ -18,13 +18,18 @@
 // midpoint m: alpha = (a e^{g_{t-1}-m}) (b e^{m-g_s})^T etc.; for the model's decays (|log d| < 0.61 per token)
 // those factors stay below e^{20}.
 //
+// Precision.  Products feeding the state (alpha, beta, W, G, A, F, H and the scan's A S) run as three bf16 MFMAs
+// on a hi/lo split of each fp32 operand (x = hi + lo, hi = bf16(x), lo = bf16(x - hi); x*y ~ hi*hi + hi*lo +
+// lo*hi, relative error ~2^-16); products feeding only the output y (rho, sigma, Q, E, O_intra, the scan's Q S)
+// run as one bf16 MFMA.  T = (I - alpha)^{-1} is formed in fp32 (fp32 MFMA).  Accumulation is fp32 throughout.
+//
 // Kernels:
 //   plan  (ragged calls only): chunk table of the rows this launch owns;
-//   prep  one 256-thread workgroup per (chunk, head): everything above that does not depend on S0, written to
-//         the workspace as A (64x64), H = F V (stored transposed), Q (64x64), O_intra = E V (transposed);
+//   prep  one 512-thread workgroup per (chunk, head): everything above that does not depend on S0, written to
+//         the workspace as A (hi/lo bf16), H = F V (fp32, transposed), Q (bf16), O_intra = E V (bf16, transposed);
 //   scan  one workgroup per (row, head, 16-column block): S <- A S + H, y <- Q S + O_intra, chunk after
-//         chunk, S held in LDS as S^T.  The 4 column blocks of a (row, head) are placed on one XCD so that the
-//         chunk matrices they share are read from HBM once.
+//         chunk.  The chunks of a head and its 4 column blocks run on one XCD (block id = head mod 8 when H is a
+//         multiple of 8), so the scan reads the prep's records from that XCD's L2 / the Infinity Cache.
 #include <algorithm>
 
 #include "wkv7_device.h"
@@ -34,139 +39,102 @@ namespace wkv7 {
 
 namespace {
 
-constexpr int C = kChunk;       // 64
-constexpr int P = 68;           // LDS row pitch (floats): float4 rows land on distinct bank groups
-constexpr int MAT = 64 * P;     // floats per 64 x 64 LDS matrix
-constexpr int OFF_A = 0, OFF_HT = HS2, OFF_Q = 2 * HS2, OFF_OT = 3 * HS2;
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ f4 mfma(float a, float b, f4 c) {
+constexpr int C = kChunk;        // 64
+constexpr int PB = 72;           // LDS row pitch in bf16 (144 B: 16 rows of a ds_read_b128 hit distinct banks)
+constexpr int PF = 72;           // LDS row pitch in fp32 for the fp32 matrices (same bytes as a hi/lo pair)
+constexpr int SLOT = 64 * PB;    // bf16 elements of one 64 x 64 LDS matrix (9216 B)
+constexpr int NSLOT = 17;
+
+// Workspace record of one (chunk, head), byte offsets.
+constexpr int REC_AH = 0;                  // A hi, bf16 [k1][k2]
+constexpr int REC_AL = REC_AH + 2 * HS2;   // A lo
+constexpr int REC_HT = REC_AL + 2 * HS2;   // H^T fp32 [v][k]
+constexpr int REC_Q = REC_HT + 4 * HS2;    // Q bf16 [t][k]
+constexpr int REC_OT = REC_Q + 2 * HS2;    // O_intra^T bf16 [v][t]
+static_assert(REC_OT + 2 * HS2 == kChunkBytes, "workspace record size");
+
+__device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
+
+__device__ __forceinline__ f4 mfma_bf16(bf8 a, bf8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f4 mfma_f32(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-__device__ __forceinline__ f4 zero4() {
-    f4 z;
-    z[0] = z[1] = z[2] = z[3] = 0.f;
-    return z;
-}
+// An LDS matrix stored as bf16 rows of pitch PB: the high part and (for split fp32 values) the low part.
+struct BM {
+    __bf16* h;
+    __bf16* l;
+};
 
-// Contraction operand for one lane: elements (row, kk .. kk+3) of an LDS matrix M (pitch P).
-//   TR = false: element (row, kk) is M[row * P + kk]  (contraction index contiguous: one ds_read_b128)
-//   TR = true : element (row, kk) is M[kk * P + row]  (stored transposed: four ds_read_b32)
-template <bool TR>
-__device__ __forceinline__ f4 fetch4(const float* M, int row, int kk) {
-    if constexpr (!TR) {
-        return *reinterpret_cast<const f4*>(M + row * P + kk);
-    } else {
-        f4 r;
-        r[0] = M[(kk + 0) * P + row];
-        r[1] = M[(kk + 1) * P + row];
-        r[2] = M[(kk + 2) * P + row];
-        r[3] = M[(kk + 3) * P + row];
-        return r;
-    }
-}
+__device__ __forceinline__ bf8 ld8(const __bf16* p) { return *reinterpret_cast<const bf8*>(p); }
 
-// A 16-row strip of a product on MFMA 16x16x4 f32.  Tile tj covers rows x0..x0+15 and columns
-// 16 tj .. 16 tj + 15 and accumulates  D[x][y] += sum_kk X(x, kk) Y(y, kk)  over the contraction blocks
-// kb (16 indices each) with klo[tj] <= kb < khi[tj].  Lane (i = lane & 15, q = lane >> 4) feeds
-// X(x0 + i, 16 kb + 4 q + s) and Y(16 tj + i, 16 kb + 4 q + s) to MFMA step s, so the 16 x 4 A operand and the
-// 4 x 16 B operand of every step share one contraction index per lane quarter.  On return lane (i, q) holds
-// D[x0 + 4 q + v][16 tj + i] in acc[tj][v].
-template <bool XT, bool YT>
-__device__ __forceinline__ void strip4(f4 (&acc)[4], const float* X, int x0, const float* Y, const int (&klo)[4],
-                                       const int (&khi)[4]) {
+// One 16 x 16 tile of P[x][y] = sum_kappa X[x][kappa] Y[y][kappa], both operands stored with kappa contiguous.
+// Lane (i = lane & 15, q = lane >> 4) feeds X[x0 + i][32 kb + 8 q .. + 7] and Y[y0 + i][32 kb + 8 q .. + 7] to
+// MFMA block kb, so the 16 x 32 A operand and the 32 x 16 B operand share one contraction index per element.
+// On return lane (i, q) holds P[x0 + 4 q + v][y0 + i] in acc[v].
+// TERMS: 1 = X.h Y.h;  2 = X.h Y.h + X.l Y.h (Y exact in bf16);  3 = X.h Y.h + X.h Y.l + X.l Y.h.
+template <int TERMS>
+__device__ __forceinline__ f4 mma(f4 acc, BM X, int x0, BM Y, int y0, int kb0, int kb1) {
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-    int kbeg = 4, kend = 0;
-#pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-        if (klo[tj] < khi[tj]) {
-            kbeg = min(kbeg, klo[tj]);
-            kend = max(kend, khi[tj]);
-        }
+    for (int kb = kb0; kb < kb1; ++kb) {
+        const int xo = (x0 + i) * PB + 32 * kb + 8 * q;
+        const int yo = (y0 + i) * PB + 32 * kb + 8 * q;
+        const bf8 xh = ld8(X.h + xo), yh = ld8(Y.h + yo);
+        if constexpr (TERMS == 3) acc = mfma_bf16(xh, ld8(Y.l + yo), acc);
+        if constexpr (TERMS >= 2) acc = mfma_bf16(ld8(X.l + xo), yh, acc);
+        acc = mfma_bf16(xh, yh, acc);
     }
-    for (int kb = kbeg; kb < kend; ++kb) {
-        const int kk = 16 * kb + 4 * q;
-        const f4 xa = fetch4<XT>(X, x0 + i, kk);
-        f4 ya[4];
-        bool on[4];
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) {
-            on[tj] = kb >= klo[tj] && kb < khi[tj];  // wave-uniform
-            ya[tj] = on[tj] ? fetch4<YT>(Y, 16 * tj + i, kk) : zero4();
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-#pragma unroll
-            for (int tj = 0; tj < 4; ++tj)
-                if (on[tj]) acc[tj] = mfma(xa[s], ya[tj][s], acc[tj]);
-        }
-    }
+    return acc;
 }
 
-// Store a strip row-major into an LDS matrix (element (x, y) at M[x * P + y]); mask: 0 none, 1 keep y < x,
-// 2 keep y <= x (masked elements are written as 0).
-__device__ __forceinline__ void store_rows(float* M, int x0, const f4 (&acc)[4], int mask) {
+__device__ __forceinline__ void split(float x, __bf16& h, __bf16& l) {
+    h = (__bf16)x;
+    l = (__bf16)(x - (float)h);
+}
+
+// Natural stores of a tile (element (x0 + 4q + v, y0 + i) at M[(y0 + i) * pitch + x0 + 4q + v]): 4 consecutive
+// elements per lane.
+__device__ __forceinline__ void st_hi(__bf16* M, int pitch, int x0, int y0, f4 acc) {
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    bf4 hv;
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int x = x0 + 4 * q + v, y = 16 * tj + i;
-            float val = acc[tj][v];
-            if (mask == 1 && !(y < x)) val = 0.f;
-            if (mask == 2 && !(y <= x)) val = 0.f;
-            M[x * P + y] = val;
-        }
-    }
+    for (int v = 0; v < 4; ++v) hv[v] = (__bf16)acc[v];
+    *reinterpret_cast<bf4*>(M + (y0 + i) * pitch + x0 + 4 * q) = hv;
 }
-
-// Store a strip transposed into an LDS matrix (element (x, y) at M[y * P + x]): one float4 per lane per tile.
-__device__ __forceinline__ void store_cols(float* M, int x0, const f4 (&acc)[4]) {
+__device__ __forceinline__ void st_split(BM M, int pitch, int x0, int y0, f4 acc) {
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    bf4 hv, lv;
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) *reinterpret_cast<f4*>(M + (16 * tj + i) * P + x0 + 4 * q) = acc[tj];
+    for (int v = 0; v < 4; ++v) {
+        __bf16 h, l;
+        split(acc[v], h, l);
+        hv[v] = h;
+        lv[v] = l;
+    }
+    *reinterpret_cast<bf4*>(M.h + (y0 + i) * pitch + x0 + 4 * q) = hv;
+    *reinterpret_cast<bf4*>(M.l + (y0 + i) * pitch + x0 + 4 * q) = lv;
+}
+__device__ __forceinline__ void st_f32(float* M, int pitch, int x0, int y0, f4 acc) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    *reinterpret_cast<f4*>(M + (y0 + i) * pitch + x0 + 4 * q) = acc;
 }
 
-__device__ __forceinline__ void set_range(int (&klo)[4], int (&khi)[4], int lo0, int hi0, int lo1, int hi1, int lo2,
-                                          int hi2, int lo3, int hi3) {
-    klo[0] = lo0; khi[0] = hi0;
-    klo[1] = lo1; khi[1] = hi1;
-    klo[2] = lo2; khi[2] = hi2;
-    klo[3] = lo3; khi[3] = hi3;
-}
-
-// Contraction ranges of a strip of a product whose tile (bx, tj) needs blocks [lo(tj), hi(tj)).
-__device__ __forceinline__ void full_range(int (&klo)[4], int (&khi)[4], int hi) {
-    set_range(klo, khi, 0, hi, 0, hi, 0, hi, 0, hi);
-}
-// tiles tj <= bx use blocks [tj, bx]; tiles tj > bx are empty (strictly-lower products of lower factors)
-__device__ __forceinline__ void lower_range(int (&klo)[4], int (&khi)[4], int bx) {
+// mask: 1 keeps x < y, 2 keeps x <= y, 3 keeps y < x (others become 0)
+__device__ __forceinline__ f4 mask_tile(f4 acc, int x0, int y0, int mode) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int y = y0 + i;
 #pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-        klo[tj] = tj;
-        khi[tj] = tj <= bx ? bx + 1 : tj;
+    for (int v = 0; v < 4; ++v) {
+        const int x = x0 + 4 * q + v;
+        const bool keep = mode == 1 ? x < y : (mode == 2 ? x <= y : y < x);
+        if (!keep) acc[v] = 0.f;
     }
-}
-// tiles tj use blocks [tj, 4)
-__device__ __forceinline__ void upper_range(int (&klo)[4], int (&khi)[4]) {
-#pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-        klo[tj] = tj;
-        khi[tj] = 4;
-    }
-}
-// Gram strips: tiles tj <= bx over the full contraction, tiles above the diagonal empty
-__device__ __forceinline__ void gram_range(int (&klo)[4], int (&khi)[4], int bx) {
-#pragma unroll
-    for (int tj = 0; tj < 4; ++tj) {
-        klo[tj] = 0;
-        khi[tj] = tj <= bx ? 4 : 0;
-    }
-}
-
-__device__ __forceinline__ void zero_strip(f4 (&acc)[4]) {
-#pragma unroll
-    for (int tj = 0; tj < 4; ++tj) acc[tj] = zero4();
+    return acc;
 }
 
 // Chunk -> (row, chunk index) of the rows this launch owns.  Returns false if the workgroup has no chunk.
@@ -186,93 +154,141 @@ __device__ __forceinline__ bool chunk_of(const Params& p, const int32_t* plan, i
 
 __device__ __forceinline__ bool owns_row(const Params& p, int L) { return p.rec_max_len < 0 || L > p.rec_max_len; }
 
+// fp32 16 x 16 tile product on MFMA 16x16x4: acc += sum_{kappa < K} X(x0 + i, kappa) Y(y0 + i, kappa) with
+// X(x, kappa) = Xp[x * xs + kappa * xk] and Y(y, kappa) = Yp[y * ys + kappa * yk] (Xp, Yp already offset to the
+// tile).  Lane (i, q) feeds contraction index m + q to step m and ends with P[4 q + v][i] in acc[v].
+__device__ __forceinline__ f4 mm_f32(f4 acc, const float* Xp, int xs, int xk, const float* Yp, int ys, int yk, int K) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    for (int m = 0; m < K; m += 4) acc = mfma_f32(Xp[i * xs + (m + q) * xk], Yp[i * ys + (m + q) * yk], acc);
+    return acc;
+}
+// Row-major store of such a tile: D[(4 q + v) * pd + i] = acc[v].
+__device__ __forceinline__ void st_rows_f32(float* D, int pd, f4 acc) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) D[(4 * q + v) * pd + i] = acc[v];
+}
+
+// B operand of a scaled identity, built in registers: Y[y][kappa] = (kappa == y) ? s : 0 for lane row y and the
+// lane's 8 contraction indices 32 kb + 8 q .. + 7.  P = X diag(s) stored naturally ([y][x]) is the transpose of
+// X with its columns scaled: the LDS transposes below cost a few MFMAs instead of scattered 2-byte stores.
+__device__ __forceinline__ bf8 diag_operand(int y, int kb, __bf16 s) {
+    const int lane = threadIdx.x & 63, q = lane >> 4;
+    bf8 d;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[e] = (32 * kb + 8 * q + e == y) ? s : (__bf16)0.f;
+    return d;
+}
+
 struct PrepSmem {
-    float mat[8][MAT];
-    float m[HS], em[HS], eglm[HS], gam[HS];
-    float bsum[4][HS];
+    __bf16 slot[NSLOT][SLOT];
+    float m[HS], em[HS], eglm[HS], gam[HS];  // m, em, eglm, gam: base-2 midpoint and decay factors per channel
+    float bsum[8][HS];
 };
 
-__global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(const Params p, float* __restrict__ wsc,
-                                                              const int32_t* __restrict__ plan, int64_t max_chunks,
-                                                              int ncps) {
-    __shared__ __attribute__((aligned(16))) PrepSmem sm;
-    const int64_t j = blockIdx.x;
-    const int h = blockIdx.y;
+// Raw operands of one chunk for one thread (token row `row`, channels cb .. cb + 7), bf16 x 8 each.
+struct RawIn {
+    uint4 w, a, b, k, r, v;
+};
+
+// One work item (chunk, head) of the prep kernel.
+struct Item {
+    bool ok;
+    int h, Lc;
+    int64_t j, tok0;  // chunk slot, first token of the chunk
+};
+
+__device__ __forceinline__ Item describe_item(const Params& p, const int32_t* plan, int64_t max_chunks, int ncps,
+                                             int64_t item) {
+    Item it{};
+    it.j = item / p.H;
+    it.h = (int)(item % p.H);
     int n, c;
-    if (!chunk_of(p, plan, max_chunks, ncps, j, n, c)) return;
+    if (!chunk_of(p, plan, max_chunks, ncps, it.j, n, c)) return it;
     int64_t bos;
     int L;
     seq_extent(p, n, bos, L);
-    if (!owns_row(p, L)) return;
-    const int t0 = c * C;
-    if (t0 >= L) return;
-    const int Lc = min(C, L - t0);
+    if (!owns_row(p, L) || c * C >= L) return it;
+    it.ok = true;
+    it.Lc = min(C, L - c * C);
+    it.tok0 = bos + (int64_t)c * C;
+    return it;
+}
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), q = lane >> 4;
-    float* const A_ = sm.mat[0];  // a -> Aq -> A0 -> W^T
-    float* const R_ = sm.mat[1];  // r -> Rq -> R0
-    float* const B_ = sm.mat[2];  // b -> Bk -> Bh
-    float* const K_ = sm.mat[3];  // k -> Kk -> Kh
-    float* const T_ = sm.mat[4];  // log d -> g -> alpha -> T -> E
-    float* const BE = sm.mat[5];  // beta -> G^T
-    float* const RH = sm.mat[6];  // rho -> V
-    float* const SG = sm.mat[7];  // sigma -> F
-    float* const out = wsc + (j * p.H + h) * (int64_t)kChunkFloats;
+__device__ __forceinline__ RawIn load_item(const Params& p, const Item& it, int row, int cb) {
+    RawIn x;
+    x.w = x.a = x.b = x.k = x.r = x.v = make_uint4(0u, 0u, 0u, 0u);
+    if (it.ok && row < it.Lc) {
+        const int64_t off = (it.tok0 + row) * p.in_tok_stride + (int64_t)it.h * HS + cb;
+        x.w = *reinterpret_cast<const uint4*>(p.w + off);
+        x.a = *reinterpret_cast<const uint4*>(p.a + off);
+        x.b = *reinterpret_cast<const uint4*>(p.b + off);
+        x.k = *reinterpret_cast<const uint4*>(p.k + off);
+        x.r = *reinterpret_cast<const uint4*>(p.r + off);
+        x.v = *reinterpret_cast<const uint4*>(p.v + off);
+    }
+    return x;
+}
 
-    // ---- 1. operands of the chunk -> LDS (fp32); rows past the row's end are zero (identity steps)
-    const int row = tid >> 2, cb = (tid & 3) * 16;
-    const bool valid = row < Lc;
-    uint4 vraw[2];
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Slots (each 64 x 72 bf16 = 9 KB; an fp32 64 x 72 matrix takes two):
+//   0-1   log2 d -> g (fp32) -> alpha (fp32) -> T (fp32, in place) -> W hi/lo
+//   2-3   Aq hi/lo -> A0^T hi/lo -> F hi/lo
+//   4-5   Bk hi/lo -> Bh^T hi/lo
+//   6-7   Kk hi/lo -> Kh^T hi/lo
+//   8     Rq hi                     9  V^T (exact bf16)
+//   10-11 beta hi/lo -> G hi/lo     12 rho    13 sigma    14 E
+//   15-16 V (row-major) -> fp32 scratch of the inversion -> T hi/lo
+// Decays are handled in base 2 (g = cumulative log2 d), so every decay factor is one v_exp_f32.
+__device__ __forceinline__ void prep_item(const Params& p, const Item& it, const RawIn& raw, char* wsc,
+                                          PrepSmem& sm) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int li = lane & 15, lq = lane >> 4;
+    float* const F32 = reinterpret_cast<float*>(sm.slot[0]);   // slots 0-1 as fp32 [64][PF]
+    float* const SCR = reinterpret_cast<float*>(sm.slot[15]);  // slots 15-16 as fp32 scratch (4608 floats)
+    const BM Aq{sm.slot[2], sm.slot[3]};
+    const BM Bk{sm.slot[4], sm.slot[5]};
+    const BM Kk{sm.slot[6], sm.slot[7]};
+    const BM Rq{sm.slot[8], nullptr};
+    const BM Vt{sm.slot[9], nullptr};
+    const BM Be{sm.slot[10], sm.slot[11]};
+    const BM Rho{sm.slot[12], nullptr};
+    const BM Sig{sm.slot[13], nullptr};
+    const BM Em{sm.slot[14], nullptr};
+    const BM Vr{sm.slot[15], nullptr};
+    const BM Tm{sm.slot[15], sm.slot[16]};
+    const BM A0t = Aq, Bht = Bk, Kht = Kk;          // after step 6
+    const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 9
+    const BM Fm{sm.slot[2], sm.slot[3]};            // step 10 (A0^T is dead after step 9)
+    char* const rec = wsc + (it.j * p.H + it.h) * (int64_t)kChunkBytes;
+    const int row = tid >> 3, cb = (tid & 7) * 8;
+    const bool valid = row < it.Lc;
+    f4 rl[12];  // step 5 -> step 6: relayout tiles of waves 4-7
+
+    // ---- 1. log2-decay -> F32; V (row-major, exact) -> Vr
     {
-        const int64_t off = (bos + t0 + row) * p.in_tok_stride + (int64_t)h * HS + cb;
-        uint4 wr[2], ar[2], rr[2], br[2], kr[2];
+        const uint32_t ww[4] = {raw.w.x, raw.w.y, raw.w.z, raw.w.w};
+        float lam[8];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            if (valid) {
-                wr[u] = reinterpret_cast<const uint4*>(p.w + off)[u];
-                ar[u] = reinterpret_cast<const uint4*>(p.a + off)[u];
-                rr[u] = reinterpret_cast<const uint4*>(p.r + off)[u];
-                br[u] = reinterpret_cast<const uint4*>(p.b + off)[u];
-                kr[u] = reinterpret_cast<const uint4*>(p.k + off)[u];
-                vraw[u] = reinterpret_cast<const uint4*>(p.v + off)[u];
-            } else {
-                wr[u] = ar[u] = rr[u] = br[u] = kr[u] = vraw[u] = make_uint4(0u, 0u, 0u, 0u);
-            }
+        for (int e = 0; e < 4; ++e) {
+            float lo, hi;
+            bf16x2_to_f32(ww[e], lo, hi);
+            lam[2 * e] = valid ? log_decay(lo) * kLog2e : 0.f;
+            lam[2 * e + 1] = valid ? log_decay(hi) * kLog2e : 0.f;
         }
-        float* const trow = T_ + row * P + cb;
-        float* const arow = A_ + row * P + cb;
-        float* const rrow = R_ + row * P + cb;
-        float* const brow = B_ + row * P + cb;
-        float* const krow = K_ + row * P + cb;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const uint32_t wv32[4] = {wr[u].x, wr[u].y, wr[u].z, wr[u].w};
-            const uint32_t av32[4] = {ar[u].x, ar[u].y, ar[u].z, ar[u].w};
-            const uint32_t rv32[4] = {rr[u].x, rr[u].y, rr[u].z, rr[u].w};
-            const uint32_t bv32[4] = {br[u].x, br[u].y, br[u].z, br[u].w};
-            const uint32_t kv32[4] = {kr[u].x, kr[u].y, kr[u].z, kr[u].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int col = 8 * u + 2 * e;
-                float lo, hi;
-                bf16x2_to_f32(wv32[e], lo, hi);
-                trow[col] = valid ? log_decay(lo) : 0.f;
-                trow[col + 1] = valid ? log_decay(hi) : 0.f;
-                bf16x2_to_f32(av32[e], arow[col], arow[col + 1]);
-                bf16x2_to_f32(rv32[e], rrow[col], rrow[col + 1]);
-                bf16x2_to_f32(bv32[e], brow[col], brow[col + 1]);
-                bf16x2_to_f32(kv32[e], krow[col], krow[col + 1]);
-            }
-        }
+        *reinterpret_cast<f4*>(F32 + row * PF + cb) = f4{lam[0], lam[1], lam[2], lam[3]};
+        *reinterpret_cast<f4*>(F32 + row * PF + cb + 4) = f4{lam[4], lam[5], lam[6], lam[7]};
+        *reinterpret_cast<uint4*>(Vr.h + row * PB + cb) = raw.v;
     }
     __syncthreads();
 
-    // ---- 2. g = inclusive cumulative log-decay per channel (wave wv: rows 16 wv .. 16 wv + 15, lane = channel)
+    // ---- 2. g = inclusive cumulative log2-decay per channel (wave wv: rows 8 wv .. 8 wv + 7; lane = channel)
     {
         float run = 0.f;
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) {
-            float* e = T_ + (16 * wv + rr) * P + lane;
+        for (int r = 0; r < 8; ++r) {
+            float* e = F32 + (8 * wv + r) * PF + lane;
             run += *e;
             *e = run;
         }
@@ -282,222 +298,333 @@ __global__ __launch_bounds__(256) void wkv7_chunk_prep_kernel(const Params p, fl
             float offs = 0.f;
             for (int w2 = 0; w2 < wv; ++w2) offs += sm.bsum[w2][lane];
 #pragma unroll
-            for (int rr = 0; rr < 16; ++rr) T_[(16 * wv + rr) * P + lane] += offs;
+            for (int r = 0; r < 8; ++r) F32[(8 * wv + r) * PF + lane] += offs;
         }
         __syncthreads();
         if (tid < HS) {
-            const float m = T_[31 * P + tid], gl = T_[63 * P + tid];
+            const float m = F32[31 * PF + tid], gl = F32[63 * PF + tid];
             sm.m[tid] = m;
-            sm.em[tid] = expf(m);
-            sm.eglm[tid] = expf(gl - m);
-            sm.gam[tid] = expf(gl);
+            sm.em[tid] = __builtin_amdgcn_exp2f(m);
+            sm.eglm[tid] = __builtin_amdgcn_exp2f(gl - m);
+            sm.gam[tid] = __builtin_amdgcn_exp2f(gl);
         }
         __syncthreads();
     }
 
-    // ---- 3. Gram operands referenced to the chunk midpoint: Aq = a e^{g_{t-1}-m}, Rq = r e^{g_t-m},
-    //         Bk = b e^{m-g_t}, Kk = k e^{m-g_t}
-#pragma unroll 4
-    for (int e = 0; e < 16; ++e) {
-        const int col = cb + e;
-        const float gi = T_[row * P + col];
-        const float ge = row > 0 ? T_[(row - 1) * P + col] : 0.f;
-        const float mk = sm.m[col];
-        const float up = expf(mk - gi);
-        A_[row * P + col] = valid ? A_[row * P + col] * expf(ge - mk) : 0.f;
-        R_[row * P + col] = valid ? R_[row * P + col] * expf(gi - mk) : 0.f;
-        B_[row * P + col] = valid ? B_[row * P + col] * up : 0.f;
-        K_[row * P + col] = valid ? K_[row * P + col] * up : 0.f;
+    // ---- 3. Gram operands referenced to the chunk midpoint: Aq = a 2^{g_{t-1}-m}, Rq = r 2^{g_t-m},
+    //         Bk = b 2^{m-g_t}, Kk = k 2^{m-g_t} (split hi/lo)
+    {
+        const uint32_t aw[4] = {raw.a.x, raw.a.y, raw.a.z, raw.a.w}, bw[4] = {raw.b.x, raw.b.y, raw.b.z, raw.b.w};
+        const uint32_t kw[4] = {raw.k.x, raw.k.y, raw.k.z, raw.k.w}, rw[4] = {raw.r.x, raw.r.y, raw.r.z, raw.r.w};
+        bf8 aqh, aql, bkh, bkl, kkh, kkl, rqh;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            float a2[2], b2[2], k2[2], r2[2];
+            bf16x2_to_f32(aw[e2], a2[0], a2[1]);
+            bf16x2_to_f32(bw[e2], b2[0], b2[1]);
+            bf16x2_to_f32(kw[e2], k2[0], k2[1]);
+            bf16x2_to_f32(rw[e2], r2[0], r2[1]);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int e = 2 * e2 + u, col = cb + e;
+                const float gi = F32[row * PF + col];
+                const float ge = row > 0 ? F32[(row - 1) * PF + col] : 0.f;
+                const float mk = sm.m[col];
+                const float fa = __builtin_amdgcn_exp2f(ge - mk), fr = __builtin_amdgcn_exp2f(gi - mk);
+                const float fb = __builtin_amdgcn_exp2f(mk - gi);
+                const float aq = valid ? a2[u] * fa : 0.f, rq = valid ? r2[u] * fr : 0.f;
+                const float bk = valid ? b2[u] * fb : 0.f, kq = valid ? k2[u] * fb : 0.f;
+                __bf16 h, l;
+                split(aq, h, l);
+                aqh[e] = h;
+                aql[e] = l;
+                split(bk, h, l);
+                bkh[e] = h;
+                bkl[e] = l;
+                split(kq, h, l);
+                kkh[e] = h;
+                kkl[e] = l;
+                rqh[e] = (__bf16)rq;
+            }
+        }
+        const int o = row * PB + cb;
+        *reinterpret_cast<bf8*>(Aq.h + o) = aqh;
+        *reinterpret_cast<bf8*>(Aq.l + o) = aql;
+        *reinterpret_cast<bf8*>(Bk.h + o) = bkh;
+        *reinterpret_cast<bf8*>(Bk.l + o) = bkl;
+        *reinterpret_cast<bf8*>(Kk.h + o) = kkh;
+        *reinterpret_cast<bf8*>(Kk.l + o) = kkl;
+        *reinterpret_cast<bf8*>(Rq.h + o) = rqh;
     }
     __syncthreads();
 
-    // ---- 4. Grams: alpha = tril_strict(Aq Bk^T) -> T_, beta -> BE, rho = tril(Rq Bk^T) -> RH, sigma -> SG
+    // ---- 4. Grams (natural store of P(x, y) is [y][x]) and V^T:
+    //   alpha: x = s, y = t  (X = Bk, Y = Aq, 3 terms), keep s < t, fp32 -> F32 as alpha[t][s]
+    //   beta : x = s, y = s' (X = Aq, Y = Kk, 3 terms), keep s' < s, hi/lo -> Be as beta[s][s'] at [s'][s]
+    //   rho  : x = s, y = t  (X = Bk, Y = Rq),            keep s <= t, -> Rho as rho[t][s]
+    //   sigma: x = s', y = t (X = Kk, Y = Rq),            keep s' <= t, -> Sig as sigma[t][s']
+    //   V^T  : x = s, y = v  (X = V, Y = I, exact)        -> Vt as V^T[v][s]
+    for (int idx = wv; idx < 80; idx += 8) {
+        const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+        const int x0 = 16 * bx, y0 = 16 * by;
+        f4 acc = zero4();
+        if (prod == 0) {
+            if (bx <= by) acc = mask_tile(mma<3>(acc, Bk, x0, Aq, y0, 0, 2), x0, y0, 1);
+            st_f32(F32, PF, x0, y0, acc);
+        } else if (prod == 1) {
+            if (by <= bx) acc = mask_tile(mma<3>(acc, Aq, x0, Kk, y0, 0, 2), x0, y0, 3);
+            st_split(Be, PB, x0, y0, acc);
+        } else if (prod == 2) {
+            if (bx <= by) acc = mask_tile(mma<1>(acc, Bk, x0, Rq, y0, 0, 2), x0, y0, 2);
+            st_hi(Rho.h, PB, x0, y0, acc);
+        } else if (prod == 3) {
+            if (bx <= by) acc = mask_tile(mma<1>(acc, Kk, x0, Rq, y0, 0, 2), x0, y0, 2);
+            st_hi(Sig.h, PB, x0, y0, acc);
+        } else {
+            const int kb = by >> 1;
+            acc = mfma_bf16(ld8(Vr.h + (x0 + li) * PB + 32 * kb + 8 * lq), diag_operand(y0 + li, kb, (__bf16)1.f), acc);
+            st_hi(Vt.h, PB, x0, y0, acc);
+        }
+    }
+    __syncthreads();
+
+    // ---- 5. waves 0-3: inverses of the diagonal 16 x 16 blocks of I - alpha by doubling,
+    //         (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8) for strictly lower L, in fp32, written over alpha;
+    //         waves 4-7: A0^T = (Aq diag(2^m))^T, Bh^T = (Bk diag(2^{g_C-m}))^T, Kh^T = (Kk diag(2^{g_C-m}))^T as
+    //         MFMA products with a scaled identity, kept in registers until step 6.
+    if (wv < 4) {
+        float* const Lb = F32 + (16 * wv) * PF + 16 * wv;
+        float* const S1 = SCR + wv * 768;
+        float* const S2 = S1 + 256;
+        float* const S3 = S2 + 256;
+        const f4 l2 = mm_f32(zero4(), Lb, PF, 1, Lb, 1, PF, 16);                     // L^2
+        st_rows_f32(S1, 16, l2);
+        wave_lds_sync();
+        const f4 l4 = mm_f32(zero4(), S1, 16, 1, S1, 1, 16, 16);                     // L^4
+        const f4 pl = mm_f32(zero4(), Lb, PF, 1, S1, 1, 16, 16);                     // L^3
+        f4 aa;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int x = 4 * lq + v;
+            aa[v] = (x == li ? 1.f : 0.f) + Lb[x * PF + li] + l2[v] + pl[v];  // A = I + L + L^2 + L^3
+        }
+        st_rows_f32(S2, 16, l4);
+        st_rows_f32(S3, 16, aa);
+        wave_lds_sync();
+        const f4 l8 = mm_f32(zero4(), S2, 16, 1, S2, 1, 16, 16);                     // L^8
+        st_rows_f32(S1, 16, l8);
+        wave_lds_sync();
+        const f4 l12 = mm_f32(zero4(), S2, 16, 1, S1, 1, 16, 16);                    // L^12
+        f4 bb;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int x = 4 * lq + v;
+            bb[v] = (x == li ? 1.f : 0.f) + l4[v] + l8[v] + l12[v];  // B = I + L^4 + L^8 + L^12
+        }
+        wave_lds_sync();
+        st_rows_f32(S2, 16, bb);
+        wave_lds_sync();
+        st_rows_f32(Lb, PF, mm_f32(zero4(), S3, 16, 1, S2, 1, 16, 16));             // T_dd = A B
+    } else {
+#pragma unroll
+        for (int u = 0; u < 12; ++u) {
+            const int idx = (wv - 4) + 4 * u;
+            const int mat = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            const BM X = mat == 0 ? Aq : (mat == 1 ? Bk : Kk);
+            const int y = 16 * by + li, kb = by >> 1;
+            const float sc = mat == 0 ? sm.em[y] : sm.eglm[y];
+            __bf16 sh, sl;
+            split(sc, sh, sl);
+            const int xo = (16 * bx + li) * PB + 32 * kb + 8 * lq;
+            const bf8 xh = ld8(X.h + xo), xl = ld8(X.l + xo);
+            const bf8 dh = diag_operand(y, kb, sh), dl = diag_operand(y, kb, sl);
+            f4 a = mfma_bf16(xh, dl, zero4());
+            a = mfma_bf16(xl, dh, a);
+            rl[u] = mfma_bf16(xh, dh, a);
+        }
+    }
+    __syncthreads();
+
+    // ---- 6. waves 4-7: store A0^T, Bh^T, Kh^T over their sources;
+    //         waves 0-1: 32 x 32 diagonal blocks, T_10 = T_11 (alpha_10 T_00) and T_32 = T_33 (alpha_32 T_22)
+    if (wv >= 4) {
+#pragma unroll
+        for (int u = 0; u < 12; ++u) {
+            const int idx = (wv - 4) + 4 * u;
+            const int mat = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            st_split(mat == 0 ? Aq : (mat == 1 ? Bk : Kk), PB, 16 * bx, 16 * by, rl[u]);
+        }
+    } else if (wv < 2) {
+        const int bi = 2 * wv + 1, bj = 2 * wv;
+        float* const Z = SCR + wv * 256;
+        st_rows_f32(Z, 16, mm_f32(zero4(), F32 + (16 * bi) * PF + 16 * bj, PF, 1, F32 + (16 * bj) * PF + 16 * bj, 1,
+                                  PF, 16));
+        wave_lds_sync();
+        st_rows_f32(F32 + (16 * bi) * PF + 16 * bj,
+                    PF, mm_f32(zero4(), F32 + (16 * bi) * PF + 16 * bi, PF, 1, Z, 1, 16, 16));
+    }
+    __syncthreads();
+
+    // ---- 7. 64 x 64: T_BA = T_B (alpha_BA T_A) with A = rows/cols 0-31, B = rows/cols 32-63 (waves 0-3, one
+    //         16 x 16 tile (tx, ty) of the 32 x 32 result each; the intermediate lives in the scratch)
+    if (wv < 4) {
+        const int tx = wv >> 1, ty = wv & 1;
+        st_rows_f32(SCR + (16 * tx) * 32 + 16 * ty, 32,
+                    mm_f32(zero4(), F32 + (32 + 16 * tx) * PF, PF, 1, F32 + 16 * ty, 1, PF, 32));
+    }
+    __syncthreads();
+    if (wv < 4) {
+        const int tx = wv >> 1, ty = wv & 1;
+        st_rows_f32(F32 + (32 + 16 * tx) * PF + 16 * ty, PF,
+                    mm_f32(zero4(), F32 + (32 + 16 * tx) * PF + 32, PF, 1, SCR + 16 * ty, 1, 32, 32));
+    }
+    __syncthreads();
+
+    // ---- 8. T hi/lo [t][s] -> slots 15-16 (T is lower triangular; the upper part of F32 holds zeros)
     {
-        int klo[4], khi[4];
+        bf8 th, tl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int col = cb + e;
+            __bf16 h, l;
+            split(col <= row ? F32[row * PF + col] : 0.f, h, l);
+            th[e] = h;
+            tl[e] = l;
+        }
+        *reinterpret_cast<bf8*>(Tm.h + row * PB + cb) = th;
+        *reinterpret_cast<bf8*>(Tm.l + row * PB + cb) = tl;
+    }
+    __syncthreads();
+
+    // ---- 9. W = T A0 (x = t, y = k: stored [k][s]) and G = T beta (x = t, y = s': stored [s'][s]), 3 terms each;
+    //         W over F32 (slots 0-1), G computed into registers and written over beta.
+    {
         f4 acc[4];
-        const int bx0 = wv, bx1 = 3 - wv;
-        gram_range(klo, khi, bx0);
-        zero_strip(acc);
-        strip4<false, false>(acc, A_, 16 * bx0, B_, klo, khi);
-        store_rows(T_, 16 * bx0, acc, 1);
-        gram_range(klo, khi, bx1);
-        zero_strip(acc);
-        strip4<false, false>(acc, A_, 16 * bx1, K_, klo, khi);
-        store_rows(BE, 16 * bx1, acc, 1);
-        gram_range(klo, khi, bx0);
-        zero_strip(acc);
-        strip4<false, false>(acc, R_, 16 * bx0, B_, klo, khi);
-        store_rows(RH, 16 * bx0, acc, 2);
-        gram_range(klo, khi, bx1);
-        zero_strip(acc);
-        strip4<false, false>(acc, R_, 16 * bx1, K_, klo, khi);
-        store_rows(SG, 16 * bx1, acc, 2);
-    }
-    __syncthreads();
-
-    // ---- 5. absolute decays for everything after the Grams: A0 = Aq e^m, R0 = Rq e^m, Bh = Bk e^{g_C-m},
-    //         Kh = Kk e^{g_C-m};  and T = (I - alpha)^{-1} in place of alpha
-#pragma unroll 4
-    for (int e = 0; e < 16; ++e) {
-        const int col = cb + e;
-        const float em = sm.em[col], eg = sm.eglm[col];
-        A_[row * P + col] *= em;
-        R_[row * P + col] *= em;
-        B_[row * P + col] *= eg;
-        K_[row * P + col] *= eg;
-    }
-    {
-        // 5a. diagonal 16x16 blocks by forward substitution: T[r][c] = alpha[r][c] + sum_{c<k<r} alpha[r][k] T[k][c]
-        float* const D = T_ + (16 * wv) * P + 16 * wv;
-        const int cc = lane & 15, part = lane >> 4;
-        for (int r = 0; r < 16; ++r) {
-            float s = 0.f;
-            for (int k = part; k < r; k += 4)
-                if (k > cc) s = fmaf(D[r * P + k], D[k * P + cc], s);
-            s += __shfl_xor(s, 16);
-            s += __shfl_xor(s, 32);
-            const float val = cc < r ? D[r * P + cc] + s : (cc == r ? 1.f : 0.f);
-            wave_lds_sync();
-            if (part == 0) D[r * P + cc] = val;
-            wave_lds_sync();
-        }
-    }
-    __syncthreads();
-    // 5b. off-diagonal blocks, block row by block row: T_ij = T_ii (sum_{j<=k<i} alpha_ik T_kj).  The sum Z_ij is
-    //     parked in the unused upper block (j, i).
-    for (int bi = 1; bi < 4; ++bi) {
-        const int i = lane & 15;
-        if (wv < bi) {
-            f4 z = zero4();
-            for (int kb = wv; kb < bi; ++kb) {
-                const f4 xa = fetch4<false>(T_, 16 * bi + i, 16 * kb + 4 * q);
-                const f4 ya = fetch4<true>(T_, 16 * wv + i, 16 * kb + 4 * q);
 #pragma unroll
-                for (int s = 0; s < 4; ++s) z = mfma(xa[s], ya[s], z);
+        for (int u = 0; u < 4; ++u) {
+            const int idx = wv + 8 * u;
+            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            f4 a = zero4();
+            if (prod == 0) {
+                a = mma<3>(a, Tm, 16 * bx, A0t, 16 * by, 0, (bx >> 1) + 1);       // s <= t
+            } else if (by <= bx) {
+                a = mma<3>(a, Tm, 16 * bx, Be, 16 * by, by >> 1, (bx >> 1) + 1);  // s' < s <= t
             }
-            float* Z = T_ + (16 * wv) * P + 16 * bi;
-#pragma unroll
-            for (int v = 0; v < 4; ++v) Z[(4 * q + v) * P + i] = z[v];
+            acc[u] = a;
         }
         __syncthreads();
-        if (wv < bi) {
-            const float* Z = T_ + (16 * wv) * P + 16 * bi;
-            const float* Tii = T_ + (16 * bi) * P + 16 * bi;
-            const f4 xa = fetch4<false>(Tii, i, 4 * q);
-            const f4 ya = fetch4<true>(Z, i, 4 * q);
-            f4 t = zero4();
 #pragma unroll
-            for (int s = 0; s < 4; ++s) t = mfma(xa[s], ya[s], t);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) T_[(16 * bi + 4 * q + v) * P + 16 * wv + i] = t[v];
+        for (int u = 0; u < 4; ++u) {
+            const int idx = wv + 8 * u;
+            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            st_split(prod == 0 ? Wm : Gm, PB, 16 * bx, 16 * by, acc[u]);
         }
-        __syncthreads();
-    }
-
-    // ---- 6. W = T A0 (strip wv) and G = T beta (strip 3 - wv), then W^T over A_ and G^T over BE
-    {
-        int klo[4], khi[4];
-        f4 accW[4], accG[4];
-        const int bxw = wv, bxg = 3 - wv;
-        full_range(klo, khi, bxw + 1);
-        zero_strip(accW);
-        strip4<false, true>(accW, T_, 16 * bxw, A_, klo, khi);
-        lower_range(klo, khi, bxg);
-        zero_strip(accG);
-        strip4<false, true>(accG, T_, 16 * bxg, BE, klo, khi);
-        __syncthreads();
-        store_cols(A_, 16 * bxw, accW);
-        store_cols(BE, 16 * bxg, accG);
     }
     __syncthreads();
 
-    // ---- 7. Q = R0 + rho W (strip wv) -> workspace; E = sigma + rho G (strip 3 - wv) -> T_
+    // ---- 10. Q = R0 + rho W  (x = k, y = t; bf16 -> workspace [t][k])
+    //          E = sigma + rho G (x = s', y = t; bf16 -> Em [t][s'], keep s' <= t)
+    //          A = Gamma + Bh^T W (x = k2, y = k1; 3 terms -> workspace hi/lo [k1][k2])
+    //          F = Kh^T + Bh^T G (x = s', y = k; 3 terms -> slots 2-3 as F[k][s'])
     {
-        const int i = lane & 15;
-        int klo[4], khi[4];
-        f4 accQ[4], accE[4];
-        const int bxq = wv, bxe = 3 - wv;
+        __bf16* const gQ = reinterpret_cast<__bf16*>(rec + REC_Q);
+        __bf16* const gAh = reinterpret_cast<__bf16*>(rec + REC_AH);
+        __bf16* const gAl = reinterpret_cast<__bf16*>(rec + REC_AL);
+        for (int idx = wv; idx < 64; idx += 8) {
+            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            const int x0 = 16 * bx, y0 = 16 * by;
+            f4 acc;
+            if (prod == 0) {
+                const bf4 r4 = *reinterpret_cast<const bf4*>(Rq.h + (y0 + li) * PB + x0 + 4 * lq);
 #pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
+                for (int v = 0; v < 4; ++v) acc[v] = (float)r4[v] * sm.em[x0 + 4 * lq + v];
+                acc = mma<1>(acc, Wm, x0, Rho, y0, 0, (by >> 1) + 1);                 // s <= t
+                st_hi(gQ, HS, x0, y0, acc);
+            } else if (prod == 1) {
+                acc = zero4();
+                if (bx <= by) {
+                    const bf4 s4 = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                accQ[tj][v] = R_[(16 * bxq + 4 * q + v) * P + 16 * tj + i];
-                accE[tj][v] = SG[(16 * bxe + 4 * q + v) * P + 16 * tj + i];
+                    for (int v = 0; v < 4; ++v) acc[v] = (float)s4[v];
+                    acc = mask_tile(mma<1>(acc, Gm, x0, Rho, y0, bx >> 1, (by >> 1) + 1), x0, y0, 2);
+                }
+                st_hi(Em.h, PB, x0, y0, acc);
+            } else if (prod == 2) {
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[v] = (x0 + 4 * lq + v == y0 + li) ? sm.gam[y0 + li] : 0.f;
+                acc = mma<3>(acc, Wm, x0, Bht, y0, 0, 2);
+                bf4 hv, lv;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    __bf16 hh, ll;
+                    split(acc[v], hh, ll);
+                    hv[v] = hh;
+                    lv[v] = ll;
+                }
+                *reinterpret_cast<bf4*>(gAh + (y0 + li) * HS + x0 + 4 * lq) = hv;
+                *reinterpret_cast<bf4*>(gAl + (y0 + li) * HS + x0 + 4 * lq) = lv;
+            } else {
+                const bf4 kh4 = *reinterpret_cast<const bf4*>(Kht.h + (y0 + li) * PB + x0 + 4 * lq);
+                const bf4 kl4 = *reinterpret_cast<const bf4*>(Kht.l + (y0 + li) * PB + x0 + 4 * lq);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) acc[v] = (float)kh4[v] + (float)kl4[v];
+                acc = mma<3>(acc, Gm, x0, Bht, y0, bx >> 1, 2);                     // s > s'
+                st_split(Fm, PB, x0, y0, acc);
             }
-        full_range(klo, khi, bxq + 1);
-        strip4<false, false>(accQ, RH, 16 * bxq, A_, klo, khi);
-        lower_range(klo, khi, bxe);
-        strip4<false, false>(accE, RH, 16 * bxe, BE, klo, khi);
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) out[OFF_Q + (16 * bxq + 4 * q + v) * HS + 16 * tj + i] = accQ[tj][v];
-        store_rows(T_, 16 * bxe, accE, 0);
-    }
-    __syncthreads();
-    // V (kept in registers since step 1) -> RH
-    {
-        float* const vrow = RH + row * P + cb;
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const uint32_t vv32[4] = {vraw[u].x, vraw[u].y, vraw[u].z, vraw[u].w};
-#pragma unroll
-            for (int e = 0; e < 4; ++e) bf16x2_to_f32(vv32[e], vrow[8 * u + 2 * e], vrow[8 * u + 2 * e + 1]);
         }
     }
+    __syncthreads();
 
-    // ---- 8. A = Gamma + Bh^T W (strip wv) -> workspace; F = Bh^T G + Kh^T (strip wv) -> SG
+    // ---- 11. H = F V (x = k, y = v; X split, V exact -> workspace fp32 [v][k]);
+    //          O_intra = E V (x = t, y = v -> workspace bf16 [v][t])
     {
-        const int i = lane & 15;
-        int klo[4], khi[4];
-        f4 accA[4], accF[4];
-        const int bx = wv;
-        zero_strip(accA);
-        full_range(klo, khi, 4);
-        strip4<true, false>(accA, B_, 16 * bx, A_, klo, khi);
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) accF[tj][v] = K_[(16 * tj + i) * P + 16 * bx + 4 * q + v];
-        upper_range(klo, khi);
-        strip4<true, false>(accF, B_, 16 * bx, BE, klo, khi);
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj)
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                const int x = 16 * bx + 4 * q + v, y = 16 * tj + i;
-                out[OFF_A + x * HS + y] = accA[tj][v] + (x == y ? sm.gam[x] : 0.f);
+        float* const gH = reinterpret_cast<float*>(rec + REC_HT);
+        __bf16* const gO = reinterpret_cast<__bf16*>(rec + REC_OT);
+        for (int idx = wv; idx < 32; idx += 8) {
+            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            const int x0 = 16 * bx, y0 = 16 * by;
+            if (prod == 0) {
+                st_f32(gH, HS, x0, y0, mma<2>(zero4(), Fm, x0, Vt, y0, 0, 2));
+            } else {
+                st_hi(gO, HS, x0, y0, mma<1>(zero4(), Em, x0, Vt, y0, 0, (bx >> 1) + 1));  // s' <= t
             }
-        store_rows(SG, 16 * bx, accF, 0);
-    }
-    __syncthreads();
-
-    // ---- 9. H = F V -> workspace as H^T; O_intra = E V -> workspace as O^T
-    {
-        const int i = lane & 15;
-        int klo[4], khi[4];
-        f4 accH[4], accO[4];
-        const int bx = wv;
-        zero_strip(accH);
-        full_range(klo, khi, 4);
-        strip4<false, true>(accH, SG, 16 * bx, RH, klo, khi);
-        zero_strip(accO);
-        full_range(klo, khi, bx + 1);
-        strip4<false, true>(accO, T_, 16 * bx, RH, klo, khi);
-#pragma unroll
-        for (int tj = 0; tj < 4; ++tj) {
-            *reinterpret_cast<f4*>(out + OFF_HT + (16 * tj + i) * HS + 16 * bx + 4 * q) = accH[tj];
-            *reinterpret_cast<f4*>(out + OFF_OT + (16 * tj + i) * HS + 16 * bx + 4 * q) = accO[tj];
         }
+    }
+    __syncthreads();  // LDS is reused by the next item
+}
+
+// Persistent: a grid of about one workgroup per CU walks the (chunk, head) items item = blockIdx.x + k gridDim.x
+// (chunk-major, head fastest, so with 8 | H and 8 | gridDim.x a head stays on one XCD) and prefetches the next
+// item's operands into registers while the current one is processed.
+__global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, char* __restrict__ wsc,
+                                                              const int32_t* __restrict__ plan, int64_t max_chunks,
+                                                              int ncps) {
+    __shared__ __attribute__((aligned(16))) PrepSmem sm;
+    const int tid = threadIdx.x;
+    const int row = tid >> 3, cb = (tid & 7) * 8;
+    const int64_t nitems = max_chunks * p.H;
+    int64_t item = blockIdx.x;
+    if (item >= nitems) return;
+    Item cur = describe_item(p, plan, max_chunks, ncps, item);
+    RawIn rc = load_item(p, cur, row, cb);
+    for (; item < nitems; item += gridDim.x) {
+        const int64_t nx = item + gridDim.x;
+        Item nxt{};
+        if (nx < nitems) nxt = describe_item(p, plan, max_chunks, ncps, nx);
+        const RawIn rn = load_item(p, nxt, row, cb);  // in flight while `cur` is processed
+        if (cur.ok) prep_item(p, cur, rc, wsc, sm);
+        cur = nxt;
+        rc = rn;
     }
 }
 
 // One workgroup per (row, head, 16-column block).  Block b -> XCD b % 8; the 4 column blocks of a (row, head)
-// pair share an XCD.
-__global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, const float* __restrict__ wsc,
+// pair share an XCD.  S is carried exactly in fp32 accumulators (wave w: rows 16 w .. 16 w + 15) and mirrored in
+// LDS as a hi/lo bf16 split S^T[v][k] for the next chunk's MFMAs.
+__global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, const char* __restrict__ wsc,
                                                               const int32_t* __restrict__ plan, int64_t max_chunks,
                                                               int ncps) {
-    __shared__ __attribute__((aligned(16))) float St[16 * P];  // S^T of this block's 16 columns: St[v][k]
+    __shared__ __attribute__((aligned(16))) __bf16 sth[16 * PB], stl[16 * PB];
     const int b = blockIdx.x;
     const int xcd = b & 7, rsl = b >> 3, vb = rsl & 3;
     const int64_t pair = (int64_t)(rsl >> 2) * 8 + xcd;
@@ -508,52 +635,71 @@ __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, co
     seq_extent(p, n, bos, L);
     if (!owns_row(p, L)) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6), i = lane & 15, q = lane >> 4;
-    const int krow = tid >> 2, c4 = (tid & 3) * 4;
-    {
-        const float* src = state_src(p, n, h);
-        f4 x = src ? *reinterpret_cast<const f4*>(src + krow * HS + 16 * vb + c4) : zero4();
-#pragma unroll
-        for (int e = 0; e < 4; ++e) St[(c4 + e) * P + krow] = x[e];
-    }
-    __syncthreads();
-
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, q = lane >> 4;
     const int64_t j0 = p.cu ? (int64_t)plan[2 * max_chunks + n] : (int64_t)n * ncps;
     // the chunk table never exceeds max_chunks for valid cu_seqlens; the clamp keeps invalid ones in bounds
     const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((L + C - 1) / C, max_chunks - j0));
+    const float* src = state_src(p, n, h);
+    float* dst = state_dst(p, n, h);
+
+    // initial state: thread (krow, c4) holds S0[krow][16 vb + c4 .. + 3]
+    {
+        const int krow = tid >> 2, c4 = (tid & 3) * 4;
+        const f4 x = src ? *reinterpret_cast<const f4*>(src + krow * HS + 16 * vb + c4) : zero4();
+        if (nch == 0) {  // no chunks (length 0): the state passes through
+            if (dst) *reinterpret_cast<f4*>(dst + krow * HS + 16 * vb + c4) = x;
+            return;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            __bf16 hh, ll;
+            split(x[e], hh, ll);
+            sth[(c4 + e) * PB + krow] = hh;
+            stl[(c4 + e) * PB + krow] = ll;
+        }
+    }
+    __syncthreads();
+
     const int xr = 16 * wv + i;          // operand row of A / Q this lane feeds
     const int orow = 16 * wv + 4 * q;    // first output row this lane holds
     const int col = 16 * vb + i;         // output column this lane holds
-
-    f4 xa[4], xq[4], hS, hO;
+    bf8 xah[2], xal[2], xq[2];
+    f4 hS;
+    bf4 hO;
     auto load_chunk = [&](int cc) {
-        const float* ws = wsc + ((j0 + cc) * p.H + h) * (int64_t)kChunkFloats;
+        const char* rec = wsc + ((j0 + cc) * p.H + h) * (int64_t)kChunkBytes;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            xa[kb] = *reinterpret_cast<const f4*>(ws + OFF_A + xr * HS + 16 * kb + 4 * q);
-            xq[kb] = *reinterpret_cast<const f4*>(ws + OFF_Q + xr * HS + 16 * kb + 4 * q);
+        for (int kb = 0; kb < 2; ++kb) {
+            xah[kb] = ld8(reinterpret_cast<const __bf16*>(rec + REC_AH) + xr * HS + 32 * kb + 8 * q);
+            xal[kb] = ld8(reinterpret_cast<const __bf16*>(rec + REC_AL) + xr * HS + 32 * kb + 8 * q);
+            xq[kb] = ld8(reinterpret_cast<const __bf16*>(rec + REC_Q) + xr * HS + 32 * kb + 8 * q);
         }
-        hS = *reinterpret_cast<const f4*>(ws + OFF_HT + col * HS + orow);
-        hO = *reinterpret_cast<const f4*>(ws + OFF_OT + col * HS + orow);
+        hS = *reinterpret_cast<const f4*>(reinterpret_cast<const float*>(rec + REC_HT) + col * HS + orow);
+        hO = *reinterpret_cast<const bf4*>(reinterpret_cast<const __bf16*>(rec + REC_OT) + col * HS + orow);
     };
-    if (nch > 0) load_chunk(0);
+    load_chunk(0);
+    f4 accS = zero4();
     for (int cc = 0; cc < nch; ++cc) {
-        f4 accS = hS, accO = hO;
-        f4 ca[4], cq[4];
+        accS = hS;
+        f4 accO;
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            ca[kb] = xa[kb];
+        for (int v = 0; v < 4; ++v) accO[v] = (float)hO[v];
+        bf8 cah[2], cal[2], cq[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            cah[kb] = xah[kb];
+            cal[kb] = xal[kb];
             cq[kb] = xq[kb];
         }
         if (cc + 1 < nch) load_chunk(cc + 1);  // next chunk's operands in flight during this chunk
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-            const f4 ys = *reinterpret_cast<const f4*>(St + i * P + 16 * kb + 4 * q);
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                accS = mfma(ca[kb][s], ys[s], accS);
-                accO = mfma(cq[kb][s], ys[s], accO);
-            }
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf8 ysh = ld8(sth + i * PB + 32 * kb + 8 * q), ysl = ld8(stl + i * PB + 32 * kb + 8 * q);
+            accS = mfma_bf16(cah[kb], ysl, accS);
+            accS = mfma_bf16(cal[kb], ysh, accS);
+            accS = mfma_bf16(cah[kb], ysh, accS);
+            accO = mfma_bf16(cq[kb], ysh, accO);
         }
         if (p.o) {
 #pragma unroll
@@ -563,15 +709,21 @@ __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, co
             }
         }
         __syncthreads();
-        *reinterpret_cast<f4*>(St + i * P + orow) = accS;
+        bf4 sh, sl;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            __bf16 hh, ll;
+            split(accS[v], hh, ll);
+            sh[v] = hh;
+            sl[v] = ll;
+        }
+        *reinterpret_cast<bf4*>(sth + i * PB + orow) = sh;
+        *reinterpret_cast<bf4*>(stl + i * PB + orow) = sl;
         __syncthreads();
     }
-
-    if (float* dst = state_dst(p, n, h)) {
-        f4 x;
+    if (dst) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) x[e] = St[(c4 + e) * P + krow];
-        *reinterpret_cast<f4*>(dst + krow * HS + 16 * vb + c4) = x;
+        for (int v = 0; v < 4; ++v) dst[(orow + v) * HS + col] = accS[v];
     }
 }
 
@@ -639,7 +791,7 @@ ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_
     }
     ws.max_chunks = maxc;
     ws.plan_bytes = varlen ? align256(sizeof(int32_t) * (size_t)(2 * maxc + num_seqs + 2)) : 0;
-    ws.chunk_bytes = align256(sizeof(float) * (size_t)maxc * (size_t)H * kChunkFloats);
+    ws.chunk_bytes = align256((size_t)maxc * (size_t)H * kChunkBytes);
     ws.total_bytes = ws.plan_bytes + ws.chunk_bytes;
     return ws;
 }
@@ -647,12 +799,20 @@ ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_
 hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* workspace, hipStream_t stream) {
     if (p.num_seqs == 0) return hipSuccess;
     int32_t* plan = reinterpret_cast<int32_t*>(workspace);
-    float* wsc = reinterpret_cast<float*>(static_cast<char*>(workspace) + ws.plan_bytes);
+    char* wsc = static_cast<char*>(workspace) + ws.plan_bytes;
     const int ncps = (int)std::max<int64_t>(1, (p.T + C - 1) / C);
     if (p.cu) hipLaunchKernelGGL(wkv7_chunk_plan_kernel, dim3(1), dim3(1024), 0, stream, p, plan, ws.max_chunks);
-    if (ws.max_chunks > 0)
-        hipLaunchKernelGGL(wkv7_chunk_prep_kernel, dim3((unsigned)ws.max_chunks, (unsigned)p.H), dim3(256), 0, stream,
-                           p, wsc, plan, ws.max_chunks, ncps);
+    if (ws.max_chunks > 0) {
+        int dev = 0, cus = 256;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            int v = 0;
+            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+        }
+        const int64_t items = ws.max_chunks * p.H;
+        const int64_t grid = std::min<int64_t>(items, cus);  // one 157 KB-LDS workgroup per CU
+        hipLaunchKernelGGL(wkv7_chunk_prep_kernel, dim3((unsigned)grid), dim3(512), 0, stream, p, wsc, plan,
+                           ws.max_chunks, ncps);
+    }
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
     const int64_t blocks = ((pairs + 7) / 8) * 8 * 4;
     hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, wsc, plan,

@@ -11,14 +11,15 @@
 namespace wkv7 {
 
 constexpr int kChunk = 64;                 // chunk length of the chunked prefill
-constexpr int kChunkFloats = 4 * HS2;      // per (chunk, head): A, H^T, Q, O_intra^T (fp32 64x64 each)
+// Workspace record per (chunk, head): A hi/lo (bf16), H^T (fp32), Q (bf16), O_intra^T (bf16), 64 x 64 each.
+constexpr int kChunkBytes = 2 * 2 * HS2 + 4 * HS2 + 2 * HS2 + 2 * HS2;
 
 // Token-serial kernel: every row, or only rows with len <= p.rec_max_len when p.rec_max_len >= 0.
 hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 
 // Workspace of the chunked path for one call.  Layout (byte offsets, each 256-aligned):
 //   [plan]   int32 chunk_seq[max_chunks], chunk_idx[max_chunks], seq_off[num_seqs + 1], total   (varlen only)
-//   [chunks] float [max_chunks][H][4][64][64]
+//   [chunks] [max_chunks][H] records of kChunkBytes
 struct ChunkWorkspace {
     int64_t max_chunks;
     size_t plan_bytes;
