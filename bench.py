@@ -9,9 +9,10 @@ value = algorithmic bytes / time: 33 664 B per (slot, head) per layer (16 KB sta
 768 B operands + 128 B output).
 
 Secondary (same line): chunked prefill B = 1, T = 4096, H = 64 (tok/s and fraction of its roofline), the
-speculative verify with snapshots (config 4) and the CPU baseline (the oracle's fp32 loop on the host cores).
+speculative verify with snapshots (config 4), the mixed continuous-batching step in a HIP graph (config 3) and the
+CPU baseline (the oracle's fp32 loop on the host cores).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu] [--only decode|prefill|verify]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu] [--only decode|prefill|verify|mixed]
 """
 import argparse
 import json
@@ -26,11 +27,20 @@ sys.path.insert(0, os.path.join(REPO, "rwkv-infer-next_amd"))
 METRIC = "WKV7 decode GB/s (%HBM peak) @B=64,H=64; prefill tok/s (%roofline) @T=4096"
 HBM_PEAK_GBS = 8000.0
 FP32_PEAK_TFLOPS = 157.3
+BF16_PEAK_TFLOPS = 2516.6
 DECODE_BYTES_PER_PAIR = 16384 + 16384 + 6 * 64 * 2 + 64 * 2       # 33 664
 PREFILL_BYTES_PER_HEAD_TOKEN = 6 * 64 * 2 + 64 * 2                 # 896 (+ 32 KB state per (sequence, head))
 COPY_CALIB_BYTES = 1 << 30
 C = 64
-PREFILL_FLOPS_PER_HEAD_TOKEN = 18 * C * 64 + 8 * 64 * 64 + (2 * C * C) // 3   # chunked form at C = 64
+N = 64
+# Chunked (WY) form at chunk C, per (chunk, head): the state path (Grams alpha/beta, the triangular solve, W, G, A,
+# F, H) and the output path (rho, sigma, Q, E, O_intra).  Together 18 C N + 8 N^2 + 2/3 C^2 per head-token.
+PREFILL_STATE_FLOPS_PER_CHUNK = 10 * C * C * N + 6 * C * N * N + (2 * C ** 3) // 3
+PREFILL_OUTPUT_FLOPS_PER_CHUNK = 8 * C * C * N + 2 * C * N * N
+PREFILL_FLOPS_PER_HEAD_TOKEN = (PREFILL_STATE_FLOPS_PER_CHUNK + PREFILL_OUTPUT_FLOPS_PER_CHUNK) / C
+# The kernels run state-path products as three bf16 MFMAs on a hi/lo split of each fp32 operand and output-path
+# products as one bf16 MFMA, so the compute roofline prices the state path at 3x the bf16 rate.
+STATE_PATH_BF16_PASSES = 3
 
 
 def log(*a):
@@ -89,14 +99,55 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
+    chunks = T // C
     bytes_ = PREFILL_BYTES_PER_HEAD_TOKEN * T * H + 2 * 16384 * H
-    flops = PREFILL_FLOPS_PER_HEAD_TOKEN * T * H
     t_hbm = bytes_ / (HBM_PEAK_GBS * 1e9)
-    t_fp32 = flops / (FP32_PEAK_TFLOPS * 1e12)   # every contraction currently runs on fp32 MFMA
-    t_roof = max(t_hbm, t_fp32)
-    return {"ms": ms, "tok_s": T / (ms * 1e-3), "roofline_bound": "mfma_fp32" if t_fp32 >= t_hbm else "hbm",
-            "t_roof_us": t_roof * 1e6, "frac": t_roof / (ms * 1e-3), "flops_chunked": flops,
+    f_state = PREFILL_STATE_FLOPS_PER_CHUNK * chunks * H
+    f_out = PREFILL_OUTPUT_FLOPS_PER_CHUNK * chunks * H
+    t_mfma = (STATE_PATH_BF16_PASSES * f_state + f_out) / (BF16_PEAK_TFLOPS * 1e12)
+    t_roof = max(t_hbm, t_mfma)
+    return {"ms": ms, "tok_s": T / (ms * 1e-3), "head_tok_s": T * H / (ms * 1e-3),
+            "roofline": {"bound": "hbm" if t_hbm >= t_mfma else "mfma", "t_roof_us": t_roof * 1e6,
+                         "t_hbm_us": t_hbm * 1e6, "t_mfma_us": t_mfma * 1e6, "frac": t_roof / (ms * 1e-3),
+                         "algorithmic_bytes": bytes_, "flops_state_path": f_state, "flops_output_path": f_out},
             "recurrence_equiv_TFLOPs": 9 * 64 * 64 * T * H / (ms * 1e-3) / 1e12}
+
+
+def mixed_bench(torch, kernels, synth, dev, steps, warmup):
+    """Config 3: one continuous-batching step over a 256-slot pool, H = 64: 8 prefill rows of U[1, 2048] tokens and
+    120 decode rows, packed varlen, random distinct slots, captured in one HIP graph and replayed."""
+    import numpy as np
+    H, S = 64, 256
+    rng = np.random.default_rng(1003)
+    lens = [int(v) for v in rng.integers(1, 2049, size=8)] + [1] * 120
+    lens = [lens[i] for i in rng.permutation(len(lens))]
+    total = int(sum(lens))
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=dev)
+    slots = torch.from_numpy(rng.permutation(S)[:len(lens)].astype(np.int64)).to(dev)
+    ops = synth.operands_torch((1, total, H, 64), seed=1003, device=dev)
+    x = [ops[n].reshape(1, total, H * 64).contiguous() for n in synth.OPERAND_NAMES]
+    pool = 0.1 * torch.randn(S, H, 64, 64, device=dev)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        kernels.wkv7_pool_(*x, pool, slots, H, 64, cu_seqlens=cu, max_len=2048)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        kernels.wkv7_pool_(*x, pool, slots, H, 64, cu_seqlens=cu, max_len=2048)
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    return {"ms": ms, "tokens": total, "tok_s": total / (ms * 1e-3), "prefill_lens": sorted(v for v in lens if v > 1)}
 
 
 def verify_bench(torch, kernels, synth, dev, steps, warmup):
@@ -168,7 +219,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "verify"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed"], default=None)
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain device copy of 1 GiB (reference dispatch for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -200,6 +251,9 @@ def main():
     if args.only in (None, "verify"):
         log("verify")
         res["verify"] = verify_bench(torch, kernels, synth, dev, args.steps, args.warmup)
+    if args.only in (None, "mixed"):
+        log("mixed")
+        res["mixed"] = mixed_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
     cpu = None
     if not args.skip_cpu and args.only is None:
         log("cpu baseline")
@@ -232,6 +286,8 @@ def main():
         out["prefill"] = res["prefill"]
     if "verify" in res:
         out["verify"] = res["verify"]
+    if "mixed" in res:
+        out["mixed"] = res["mixed"]
     if cpu:
         out["cpu_baseline"] = cpu
     print(json.dumps(out))

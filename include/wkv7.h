@@ -95,6 +95,30 @@ int wkv7_workspace_size(const wkv7_args *args, size_t *bytes);
  * Asynchronous; returns after launching. */
 int wkv7_run(const wkv7_args *args, void *stream);
 
+/*
+ * Slot-pool maintenance on a pool of `layers` consecutive fp32 [rows][H][64][64] arrays (a model's per-layer state
+ * pools, the reference's `wkv (L, S, Hl, 64, 64)`, rwkv_next/model.py:302).  Slot indices outside [0, rows) are
+ * ignored.  Asynchronous on `stream`; no allocation, no memset, so they can be recorded into a hipGraph.
+ */
+
+/* pool[l][idx[i]] := 0 for every layer l and i < n.  Replaces the WKV part of `reset_slots`
+ * (rwkv_next/model.py:310-311). */
+int wkv7_pool_reset(float *pool, int32_t layers, int64_t rows, int32_t H, const int64_t *idx, int32_t n,
+                    void *stream);
+
+/* pool[l][dst[i]] := pool[l][src[i]] for every layer l and i < n, with gather-then-scatter semantics: every source
+ * is read before any destination is written, so swaps and chains are exact.  dst entries must be distinct.
+ * n <= 1024.  Replaces the WKV part of `move_slots` (rwkv_next/model.py:313-316). */
+int wkv7_pool_move(float *pool, int32_t layers, int64_t rows, int32_t H, const int64_t *src, const int64_t *dst,
+                   int32_t n, void *stream);
+
+/* Rollback after a speculative verify that wrote per-token snapshots [num_seqs][T][H][64][64]:
+ * pool[slots[b]] := snapshots[b][n_accepted[b] - 1] for n_accepted[b] in [1, T]; other rows keep the pool's state.
+ * One layer.  Replaces the per-layer `wkv7_replay` pass of `rollback` (rwkv_next/model.py:498-508;
+ * rwkv_next/kernels/wkv7.py:141-147) with a copy. */
+int wkv7_snapshot_restore(float *pool, int64_t rows, int32_t H, const int64_t *slots, const float *snapshots,
+                          int32_t T, const int64_t *n_accepted, int32_t num_seqs, void *stream);
+
 /* Static description of a return code. */
 const char *wkv7_strerror(int code);
 

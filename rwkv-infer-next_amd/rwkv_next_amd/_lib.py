@@ -22,7 +22,9 @@ ALGO_AUTO = 0
 ALGO_RECURRENT = 1
 ALGO_CHUNKED = 2
 
-EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size")
+EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
+            "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore")
+MAX_MOVES = 1024
 
 _vp = ctypes.c_void_p
 
@@ -86,6 +88,13 @@ def load(path: str = LIB_PATH):
     lib.wkv7_strerror.argtypes = [ctypes.c_int]
     lib.wkv7_abi_version.restype = ctypes.c_int
     lib.wkv7_args_size.restype = ctypes.c_size_t
+    i32, i64 = ctypes.c_int32, ctypes.c_int64
+    lib.wkv7_pool_reset.restype = ctypes.c_int
+    lib.wkv7_pool_reset.argtypes = [_vp, i32, i64, i32, _vp, i32, _vp]
+    lib.wkv7_pool_move.restype = ctypes.c_int
+    lib.wkv7_pool_move.argtypes = [_vp, i32, i64, i32, _vp, _vp, i32, _vp]
+    lib.wkv7_snapshot_restore.restype = ctypes.c_int
+    lib.wkv7_snapshot_restore.argtypes = [_vp, i64, i32, _vp, _vp, i32, _vp, i32, _vp]
     if lib.wkv7_abi_version() != WKV7_ABI_VERSION:
         raise ImportError(f"{path}: ABI version {lib.wkv7_abi_version()} != {WKV7_ABI_VERSION}")
     if lib.wkv7_args_size() != ctypes.sizeof(Wkv7Args):
@@ -108,5 +117,11 @@ def workspace_size(args: Wkv7Args) -> int:
 
 def run(args: Wkv7Args, stream: int) -> None:
     rc = load().wkv7_run(ctypes.byref(args), _vp(stream))
+    if rc != WKV7_OK:
+        raise Wkv7Error(rc, strerror(rc))
+
+
+def check(rc: int) -> None:
+    """Raise Wkv7Error for a non-zero return code of the library."""
     if rc != WKV7_OK:
         raise Wkv7Error(rc, strerror(rc))

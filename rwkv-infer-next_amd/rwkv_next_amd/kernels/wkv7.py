@@ -234,16 +234,80 @@ def check_distinct_slots(slots: torch.Tensor, num_slots: int) -> None:
         raise ValueError("duplicate slot indices in one call")
 
 
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
 def restore_snapshots_(pool, slots, snapshots, n):
     """Rollback after a speculative verify: pool[slots[b]] := snapshots[b, n[b] - 1], the state after the first
     n[b] tokens (1 <= n[b] <= T); rows with n[b] = 0 keep the pool's state (a verify with final=False does not
-    write the pool).  Replaces the reference's second recurrence pass, wkv7_replay (model.py:498-508).
-    Device-side gather + scatter, no host sync."""
-    N = snapshots.shape[0]
-    nn = torch.as_tensor(n, device=pool.device).long()
-    idx = (nn - 1).clamp(0, snapshots.shape[1] - 1)
-    sl = torch.as_tensor(slots, device=pool.device).long()
-    new = snapshots[torch.arange(N, device=pool.device), idx]
-    new = torch.where((nn > 0).view(-1, 1, 1, 1), new, pool.index_select(0, sl))
-    pool.index_copy_(0, sl, new)
+    write the pool).  Replaces the reference's second recurrence pass, wkv7_replay (model.py:498-508), with one
+    HIP copy kernel (16 KB read + 16 KB written per (row, head)); no host sync.  slots must be distinct."""
+    if pool.dtype != torch.float32 or not pool.is_contiguous() or pool.dim() != 4 or pool.shape[2:] != (64, 64):
+        raise ValueError("pool must be a contiguous float32 (S, H, 64, 64) tensor")
+    N, T, H = snapshots.shape[0], snapshots.shape[1], pool.shape[1]
+    if snapshots.dtype != torch.float32 or not snapshots.is_contiguous() or \
+            tuple(snapshots.shape) != (N, T, H, 64, 64):
+        raise ValueError(f"snapshots must be a contiguous float32 (N, T, {H}, 64, 64) tensor")
+    dev = pool.device
+    sl = _index_tensor(slots, dev, torch.int64, "slots")
+    nn = _index_tensor(n, dev, torch.int64, "n")
+    if sl.numel() != N or nn.numel() != N:
+        raise ValueError(f"slots and n must have {N} entries")
+    with torch.cuda.device(dev):
+        _lib.check(_lib.load().wkv7_snapshot_restore(pool.data_ptr(), pool.shape[0], H, sl.data_ptr(),
+                                                     snapshots.data_ptr(), T, nn.data_ptr(), N, _stream(dev)))
     return pool
+
+
+# --------------------------------------------------------------------------------------------------------------
+# model-level wrapper and the per-model state pool (model.py:77-83, 298-316)
+# --------------------------------------------------------------------------------------------------------------
+def model_wkv7(r, w, k, v, a, b, state, H, N, cu_seqlens=None, final=True):
+    """RWKV-7 recurrence for (B, T, H*N) inputs of any float dtype (cast to bf16); `w` is the raw log-decay.
+    Returns (o (B, T, C) bf16, new_state fp32 | None).  Mirrors the model's wrapper, rwkv_next/model.py:77-83."""
+    B, T, C = r.shape
+    bf = lambda t: t if t.dtype == torch.bfloat16 else t.bfloat16()
+    o, s = wkv7(bf(r), bf(w), bf(k), bf(v), bf(a), bf(b), state, H, N, cu_seqlens, final)
+    return o.view(B, T, C), s
+
+
+class StatePool:
+    """fp32 WKV state for `layers` layers x `slots` slots x H heads, (L, S, H, 64, 64) -- the WKV part of the
+    reference model's slot pool (alloc_slots / state_bytes_per_slot / reset_slots / move_slots,
+    rwkv_next/model.py:298-316).  Layer i's pool `pool.layer(i)` (S, H, 64, 64) is what `wkv7_pool_` updates in
+    place; reset and move run as HIP kernels on the current stream (graph-capturable, no host sync)."""
+
+    def __init__(self, layers: int, slots: int, H: int, device, N: int = HEAD_SIZE):
+        if N != HEAD_SIZE:
+            raise ValueError(f"head size {N} is not supported (K = {HEAD_SIZE})")
+        self.L, self.S, self.H = int(layers), int(slots), int(H)
+        self.device = torch.device(device)
+        self.wkv = torch.zeros(self.L, self.S, self.H, N, N, device=self.device, dtype=torch.float32)
+
+    def layer(self, i: int) -> torch.Tensor:
+        return self.wkv[i]
+
+    def state_bytes_per_slot(self) -> int:
+        """WKV bytes per slot over all layers (the reference adds the two token-shift rows, model.py:307-308)."""
+        return self.L * self.H * HEAD_SIZE * HEAD_SIZE * 4
+
+    def reset_slots(self, idx) -> None:
+        """wkv[:, idx] = 0 (model.py:310-311)."""
+        i = _index_tensor(idx, self.device, torch.int64, "idx")
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.load().wkv7_pool_reset(self.wkv.data_ptr(), self.L, self.S, self.H, i.data_ptr(),
+                                                   i.numel(), _stream(self.device)))
+
+    def move_slots(self, src, dst) -> None:
+        """wkv[:, dst] = wkv[:, src] with gather-then-scatter semantics (swaps are exact); dst must be distinct
+        (model.py:313-316)."""
+        s = _index_tensor(src, self.device, torch.int64, "src")
+        d = _index_tensor(dst, self.device, torch.int64, "dst")
+        if s.numel() != d.numel():
+            raise ValueError("src and dst must have the same length")
+        if s.numel() > _lib.MAX_MOVES:
+            raise ValueError(f"at most {_lib.MAX_MOVES} moves per call")
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.load().wkv7_pool_move(self.wkv.data_ptr(), self.L, self.S, self.H, s.data_ptr(),
+                                                  d.data_ptr(), s.numel(), _stream(self.device)))

@@ -98,3 +98,28 @@ def test_workspace_sizing_follows_the_dispatch_rule():
 def test_zero_sequences_is_a_no_op():
     a = base_args(num_seqs=0, total_tokens=0)
     assert _lib.load().wkv7_run(ctypes.byref(a), None) == _lib.WKV7_OK
+
+
+def test_pool_entry_points_validate_before_launch():
+    """The slot-pool entry points reject bad sizes, NULL pointers and misalignment on the host; empty work is a
+    no-op (nothing is launched, so no GPU is needed)."""
+    lib = _lib.load()
+    fake = 0x10000
+    E = _lib
+    # reset: pool, layers, rows, H, idx, n, stream
+    assert lib.wkv7_pool_reset(fake, 2, 4, 0, fake, 1, None) == E.WKV7_ERR_SHAPE
+    assert lib.wkv7_pool_reset(fake, 2, 4, 2, fake, -1, None) == E.WKV7_ERR_SHAPE
+    assert lib.wkv7_pool_reset(None, 2, 4, 2, fake, 1, None) == E.WKV7_ERR_NULL
+    assert lib.wkv7_pool_reset(fake, 2, 4, 2, None, 1, None) == E.WKV7_ERR_NULL
+    assert lib.wkv7_pool_reset(fake + 4, 2, 4, 2, fake, 1, None) == E.WKV7_ERR_ALIGN
+    assert lib.wkv7_pool_reset(None, 2, 4, 2, None, 0, None) == E.WKV7_OK
+    # move: pool, layers, rows, H, src, dst, n, stream
+    assert lib.wkv7_pool_move(fake, 1, 4, 2, fake, None, 1, None) == E.WKV7_ERR_NULL
+    assert lib.wkv7_pool_move(fake, 1, 4, 2, fake, fake, E.MAX_MOVES + 1, None) == E.WKV7_ERR_SHAPE
+    assert lib.wkv7_pool_move(fake + 8, 1, 4, 2, fake, fake, 1, None) == E.WKV7_ERR_ALIGN
+    assert lib.wkv7_pool_move(None, 1, 4, 2, None, None, 0, None) == E.WKV7_OK
+    # restore: pool, rows, H, slots, snapshots, T, n_accepted, num_seqs, stream
+    assert lib.wkv7_snapshot_restore(fake, 4, 2, fake, fake, 0, fake, 1, None) == E.WKV7_ERR_SHAPE
+    assert lib.wkv7_snapshot_restore(fake, 4, 2, fake, None, 5, fake, 1, None) == E.WKV7_ERR_NULL
+    assert lib.wkv7_snapshot_restore(fake, 4, 2, fake, fake + 4, 5, fake, 1, None) == E.WKV7_ERR_ALIGN
+    assert lib.wkv7_snapshot_restore(None, 4, 2, None, None, 5, None, 0, None) == E.WKV7_OK
