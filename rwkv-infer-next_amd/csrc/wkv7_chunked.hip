@@ -26,7 +26,7 @@
 // Kernels:
 //   plan  (ragged calls only): chunk table of the rows this launch owns;
 //   prep  one 512-thread workgroup per (chunk, head): everything above that does not depend on S0, written to
-//         the workspace as A (hi/lo bf16), H = F V (fp32, transposed), Q (bf16), O_intra = E V (bf16, transposed);
+//         the workspace as A (hi/lo bf16), H = F V (fp32, transposed), Q (bf16), O_intra = E V (bf16);
 //   scan  one workgroup per (row, head, 16-column block): S <- A S + H, y <- Q S + O_intra, chunk after
 //         chunk.  The chunks of a head and its 4 column blocks run on one XCD (block id = head mod 8 when H is a
 //         multiple of 8), so the scan reads the prep's records from that XCD's L2 / the Infinity Cache.
@@ -53,10 +53,21 @@ constexpr int REC_AH = 0;                  // A hi, bf16 [k1][k2]
 constexpr int REC_AL = REC_AH + 2 * HS2;   // A lo
 constexpr int REC_HT = REC_AL + 2 * HS2;   // H^T fp32 [v][k]
 constexpr int REC_Q = REC_HT + 4 * HS2;    // Q bf16 [t][k]
-constexpr int REC_OT = REC_Q + 2 * HS2;    // O_intra^T bf16 [v][t]
+constexpr int REC_OT = REC_Q + 2 * HS2;    // O_intra bf16 [t][v]
 static_assert(REC_OT + 2 * HS2 == kChunkBytes, "workspace record size");
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
+
+// Makes the compiler complete the loads that produced `x` here (an empty asm reading the registers).  Used after a
+// loop's prologue loads: with nothing in flight from the prologue, the loop header's wait bookkeeping only carries
+// the loop's own prefetches, which it counts exactly, instead of falling back to waiting for every memory operation.
+template <typename T>
+__device__ __forceinline__ void settle(const T& x) {
+    static_assert(sizeof(T) % 4 == 0, "settle: 32-bit words");
+    const uint32_t* w = reinterpret_cast<const uint32_t*>(&x);
+#pragma unroll
+    for (int e = 0; e < (int)(sizeof(T) / 4); ++e) asm volatile("" ::"v"(w[e]));
+}
 
 __device__ __forceinline__ f4 mfma_bf16(bf8 a, bf8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -194,8 +205,9 @@ struct RawIn {
 // One work item (chunk, head) of the prep kernel.
 struct Item {
     bool ok;
-    int h, Lc;
+    int h, Lc;        // Lc = 0 for items without a chunk
     int64_t j, tok0;  // chunk slot, first token of the chunk
+    int64_t rec;      // workspace record: (j, h), or the trash record after the last one for items without a chunk
 };
 
 __device__ __forceinline__ Item describe_item(const Params& p, const int32_t* plan, int64_t max_chunks, int ncps,
@@ -203,6 +215,7 @@ __device__ __forceinline__ Item describe_item(const Params& p, const int32_t* pl
     Item it{};
     it.j = item / p.H;
     it.h = (int)(item % p.H);
+    it.rec = max_chunks * p.H;  // trash
     int n, c;
     if (!chunk_of(p, plan, max_chunks, ncps, it.j, n, c)) return it;
     int64_t bos;
@@ -212,21 +225,23 @@ __device__ __forceinline__ Item describe_item(const Params& p, const int32_t* pl
     it.ok = true;
     it.Lc = min(C, L - c * C);
     it.tok0 = bos + (int64_t)c * C;
+    it.rec = it.j * p.H + it.h;
     return it;
 }
 
+// The six loads are issued for every thread and item: rows outside the chunk (and items without a chunk) read token
+// 0, which always exists, and prep_item zeroes them.  A fixed number of loads per item lets the compiler count the
+// outstanding prefetch exactly; with conditional loads it falls back to waiting for all of them at first use.
 __device__ __forceinline__ RawIn load_item(const Params& p, const Item& it, int row, int cb) {
+    const bool valid = row < it.Lc;
+    const int64_t off = valid ? (it.tok0 + row) * p.in_tok_stride + (int64_t)it.h * HS + cb : (int64_t)cb;
     RawIn x;
-    x.w = x.a = x.b = x.k = x.r = x.v = make_uint4(0u, 0u, 0u, 0u);
-    if (it.ok && row < it.Lc) {
-        const int64_t off = (it.tok0 + row) * p.in_tok_stride + (int64_t)it.h * HS + cb;
-        x.w = *reinterpret_cast<const uint4*>(p.w + off);
-        x.a = *reinterpret_cast<const uint4*>(p.a + off);
-        x.b = *reinterpret_cast<const uint4*>(p.b + off);
-        x.k = *reinterpret_cast<const uint4*>(p.k + off);
-        x.r = *reinterpret_cast<const uint4*>(p.r + off);
-        x.v = *reinterpret_cast<const uint4*>(p.v + off);
-    }
+    x.w = *reinterpret_cast<const uint4*>(p.w + off);
+    x.a = *reinterpret_cast<const uint4*>(p.a + off);
+    x.b = *reinterpret_cast<const uint4*>(p.b + off);
+    x.k = *reinterpret_cast<const uint4*>(p.k + off);
+    x.r = *reinterpret_cast<const uint4*>(p.r + off);
+    x.v = *reinterpret_cast<const uint4*>(p.v + off);
     return x;
 }
 
@@ -261,7 +276,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const BM A0t = Aq, Bht = Bk, Kht = Kk;          // after step 6
     const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 9
     const BM Fm{sm.slot[2], sm.slot[3]};            // step 10 (A0^T is dead after step 9)
-    char* const rec = wsc + (it.j * p.H + it.h) * (int64_t)kChunkBytes;
+    char* const rec = wsc + it.rec * (int64_t)kChunkBytes;
     const int row = tid >> 3, cb = (tid & 7) * 8;
     const bool valid = row < it.Lc;
     f4 rl[12];  // step 5 -> step 6: relayout tiles of waves 4-7
@@ -279,7 +294,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         }
         *reinterpret_cast<f4*>(F32 + row * PF + cb) = f4{lam[0], lam[1], lam[2], lam[3]};
         *reinterpret_cast<f4*>(F32 + row * PF + cb + 4) = f4{lam[4], lam[5], lam[6], lam[7]};
-        *reinterpret_cast<uint4*>(Vr.h + row * PB + cb) = raw.v;
+        *reinterpret_cast<uint4*>(Vr.h + row * PB + cb) = valid ? raw.v : make_uint4(0u, 0u, 0u, 0u);
     }
     __syncthreads();
 
@@ -530,7 +545,9 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         __bf16* const gQ = reinterpret_cast<__bf16*>(rec + REC_Q);
         __bf16* const gAh = reinterpret_cast<__bf16*>(rec + REC_AH);
         __bf16* const gAl = reinterpret_cast<__bf16*>(rec + REC_AL);
-        for (int idx = wv; idx < 64; idx += 8) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int idx = wv + 8 * u;
             const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
             const int x0 = 16 * bx, y0 = 16 * by;
             f4 acc;
@@ -576,17 +593,19 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     __syncthreads();
 
     // ---- 11. H = F V (x = k, y = v; X split, V exact -> workspace fp32 [v][k]);
-    //          O_intra = E V (x = t, y = v -> workspace bf16 [v][t])
+    //          O_intra = E V (x = v, y = t -> workspace bf16 [t][v])
     {
         float* const gH = reinterpret_cast<float*>(rec + REC_HT);
         __bf16* const gO = reinterpret_cast<__bf16*>(rec + REC_OT);
-        for (int idx = wv; idx < 32; idx += 8) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int idx = wv + 8 * u;
             const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
             const int x0 = 16 * bx, y0 = 16 * by;
             if (prod == 0) {
                 st_f32(gH, HS, x0, y0, mma<2>(zero4(), Fm, x0, Vt, y0, 0, 2));
             } else {
-                st_hi(gO, HS, x0, y0, mma<1>(zero4(), Em, x0, Vt, y0, 0, (bx >> 1) + 1));  // s' <= t
+                st_hi(gO, HS, x0, y0, mma<1>(zero4(), Vt, x0, Em, y0, 0, (by >> 1) + 1));  // s' <= t
             }
         }
     }
@@ -602,26 +621,72 @@ __global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, ch
     __shared__ __attribute__((aligned(16))) PrepSmem sm;
     const int tid = threadIdx.x;
     const int row = tid >> 3, cb = (tid & 7) * 8;
-    const int64_t nitems = max_chunks * p.H;
+    // ragged calls: only the chunk slots the plan filled (the table size is an upper bound); items without a chunk
+    // would all write the one trash record at the same time
+    int64_t nitems = max_chunks * p.H;
+    if (p.cu) {
+        const int64_t used = plan[2 * max_chunks + p.num_seqs + 1];
+        nitems = std::max<int64_t>(0, std::min<int64_t>(used, max_chunks)) * p.H;
+    }
     int64_t item = blockIdx.x;
     if (item >= nitems) return;
     Item cur = describe_item(p, plan, max_chunks, ncps, item);
     RawIn rc = load_item(p, cur, row, cb);
+    settle(rc);
     for (; item < nitems; item += gridDim.x) {
         const int64_t nx = item + gridDim.x;
         Item nxt{};
+        nxt.rec = max_chunks * p.H;
         if (nx < nitems) nxt = describe_item(p, plan, max_chunks, ncps, nx);
         const RawIn rn = load_item(p, nxt, row, cb);  // in flight while `cur` is processed
-        if (cur.ok) prep_item(p, cur, rc, wsc, sm);
+        // every item runs the same instruction stream (an item without a chunk computes on zeros and writes the
+        // trash record), so the number of vector memory operations between a prefetch and its use is fixed
+        prep_item(p, cur, rc, wsc, sm);
         cur = nxt;
         rc = rn;
     }
 }
 
+// One chunk record's share of one scan lane: A hi/lo and Q rows (MFMA operands), H and O_intra entries.
+struct ScanRec {
+    bf8 ah[2], al[2], q[2];
+    f4 hS;
+    uint2 hO;  // 4 bf16
+};
+
+// Per-lane byte offsets inside a record (the same for every chunk).
+struct ScanOffs {
+    uint32_t a, s, o;  // A / Q row segment, H^T entry, O_intra entry
+};
+
+// `rec` is wave-uniform, so the loads address it as a scalar base plus the lane's 32-bit offset (no per-lane
+// 64-bit address registers to carry from one chunk to the next).
+__device__ __forceinline__ void scan_load(ScanRec& r, const char* rec, const ScanOffs& off) {
+    const char* const b = uniform_ptr(rec);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        r.ah[kb] = *reinterpret_cast<const bf8*>(b + REC_AH + off.a + 64 * kb);
+        r.al[kb] = *reinterpret_cast<const bf8*>(b + REC_AL + off.a + 64 * kb);
+        r.q[kb] = *reinterpret_cast<const bf8*>(b + REC_Q + off.a + 64 * kb);
+    }
+    r.hS = *reinterpret_cast<const f4*>(b + REC_HT + off.s);
+    r.hO = *reinterpret_cast<const uint2*>(b + REC_OT + off.o);
+}
+
+constexpr int kScanDepth = 4;  // chunk records in flight per lane (register ring)
+
 // One workgroup per (row, head, 16-column block).  Block b -> XCD b % 8; the 4 column blocks of a (row, head)
-// pair share an XCD.  S is carried exactly in fp32 accumulators (wave w: rows 16 w .. 16 w + 15) and mirrored in
-// LDS as a hi/lo bf16 split S^T[v][k] for the next chunk's MFMAs.
-__global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, const char* __restrict__ wsc,
+// pair share an XCD.  Wave w owns state rows (and output tokens) 16 w .. 16 w + 15.  S is carried exactly in fp32
+// accumulators and mirrored in LDS as a hi/lo bf16 split S^T[v][k] that feeds the next chunk's MFMAs; the output
+// tile is computed transposed (O^T = S^T Q^T), so each lane holds 4 consecutive columns of one token and writes
+// them with one 8-byte store.
+//
+// Chunk records stream through a ring of kScanDepth register sets: after a chunk is consumed its set is refilled
+// with the record kScanDepth chunks ahead.  Every step issues the same memory operations -- the refill index is
+// clamped to the last chunk, steps past the end compute without effect, and stores that must not land (tokens
+// past the row's end, no output requested) go to the workspace's trash record -- so the compiler can count the
+// outstanding loads exactly and waits only for the record about to be used.
+__global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
                                                               const int32_t* __restrict__ plan, int64_t max_chunks,
                                                               int ncps) {
     __shared__ __attribute__((aligned(16))) __bf16 sth[16 * PB], stl[16 * PB];
@@ -661,65 +726,72 @@ __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, co
     }
     __syncthreads();
 
-    const int xr = 16 * wv + i;          // operand row of A / Q this lane feeds
-    const int orow = 16 * wv + 4 * q;    // first output row this lane holds
-    const int col = 16 * vb + i;         // output column this lane holds
-    bf8 xah[2], xal[2], xq[2];
-    f4 hS;
-    bf4 hO;
-    auto load_chunk = [&](int cc) {
-        const char* rec = wsc + ((j0 + cc) * p.H + h) * (int64_t)kChunkBytes;
+    const int xr = 16 * wv + i;          // operand row of A / Q this lane feeds; also its output token in a chunk
+    const int orow = 16 * wv + 4 * q;    // first state row this lane holds
+    const int col = 16 * vb + i;         // state column this lane holds
+    const int ocol = 16 * vb + 4 * q;    // first output column this lane holds
+    const char* const rec0 = wsc + (j0 * p.H + h) * (int64_t)kChunkBytes;
+    const int64_t rec_stride = (int64_t)p.H * kChunkBytes;
+    // stores that must not land go to the trash record, 2 KB per workgroup slot (24 slots) so that workgroups do not
+    // all hit the same lines
+    uint2* const trash =
+        reinterpret_cast<uint2*>(wsc + max_chunks * p.H * (int64_t)kChunkBytes) + (b % 24) * 256 + tid;
+    ScanRec ring[kScanDepth];
+    const ScanOffs offs{(uint32_t)(xr * HS + 8 * q) * 2u, (uint32_t)(col * HS + orow) * 4u, (uint32_t)(xr * HS + ocol) * 2u};
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            xah[kb] = ld8(reinterpret_cast<const __bf16*>(rec + REC_AH) + xr * HS + 32 * kb + 8 * q);
-            xal[kb] = ld8(reinterpret_cast<const __bf16*>(rec + REC_AL) + xr * HS + 32 * kb + 8 * q);
-            xq[kb] = ld8(reinterpret_cast<const __bf16*>(rec + REC_Q) + xr * HS + 32 * kb + 8 * q);
-        }
-        hS = *reinterpret_cast<const f4*>(reinterpret_cast<const float*>(rec + REC_HT) + col * HS + orow);
-        hO = *reinterpret_cast<const bf4*>(reinterpret_cast<const __bf16*>(rec + REC_OT) + col * HS + orow);
-    };
-    load_chunk(0);
+    for (int d = 0; d < kScanDepth; ++d) scan_load(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, offs);
+#pragma unroll
+    for (int d = 0; d < kScanDepth; ++d) settle(ring[d]);
     f4 accS = zero4();
-    for (int cc = 0; cc < nch; ++cc) {
-        accS = hS;
-        f4 accO;
+    for (int c0 = 0; c0 < nch; c0 += kScanDepth) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) accO[v] = (float)hO[v];
-        bf8 cah[2], cal[2], cq[2];
+        for (int d = 0; d < kScanDepth; ++d) {
+            const int cc = c0 + d;
+            const bool live = cc < nch;  // wave-uniform
+            ScanRec& r = ring[d];
+            f4 newS = r.hS, accO;
+            {
+                float o0, o1, o2, o3;
+                bf16x2_to_f32(r.hO.x, o0, o1);
+                bf16x2_to_f32(r.hO.y, o2, o3);
+                accO = f4{o0, o1, o2, o3};
+            }
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            cah[kb] = xah[kb];
-            cal[kb] = xal[kb];
-            cq[kb] = xq[kb];
-        }
-        if (cc + 1 < nch) load_chunk(cc + 1);  // next chunk's operands in flight during this chunk
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const bf8 ysh = ld8(sth + i * PB + 32 * kb + 8 * q), ysl = ld8(stl + i * PB + 32 * kb + 8 * q);
-            accS = mfma_bf16(cah[kb], ysl, accS);
-            accS = mfma_bf16(cal[kb], ysh, accS);
-            accS = mfma_bf16(cah[kb], ysh, accS);
-            accO = mfma_bf16(cq[kb], ysh, accO);
-        }
-        if (p.o) {
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf8 ysh = ld8(sth + i * PB + 32 * kb + 8 * q), ysl = ld8(stl + i * PB + 32 * kb + 8 * q);
+                newS = mfma_bf16(r.ah[kb], ysl, newS);
+                newS = mfma_bf16(r.al[kb], ysh, newS);
+                newS = mfma_bf16(r.ah[kb], ysh, newS);
+                accO = mfma_bf16(ysh, r.q[kb], accO);  // O^T: lane (i, q) gets token xr, columns ocol .. + 3
+            }
+            // the refill reuses the slot's registers only if it is not scheduled above the slot's last use;
+            // otherwise the ring rotates through copies that wait for the newest loads
+            __builtin_amdgcn_sched_barrier(0);
+            scan_load(r, rec0 + std::min(cc + kScanDepth, nch - 1) * rec_stride, offs);
+            {
+                const int t = cc * C + xr;
+                uint2 pk;
+                pk.x = pack_bf16x2(accO[0], accO[1]);
+                pk.y = pack_bf16x2(accO[2], accO[3]);
+                uint2* const out = (live && t < L && p.o)
+                                       ? reinterpret_cast<uint2*>(p.o + (bos + t) * p.o_tok_stride + (int64_t)h * HS + ocol)
+                                       : trash;
+                *out = pk;
+            }
+            if (live) accS = newS;
+            __syncthreads();
+            bf4 sh, sl;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const int t = cc * C + orow + v;
-                if (t < L) p.o[(bos + t) * p.o_tok_stride + (int64_t)h * HS + col] = f32_to_bf16(accO[v]);
+                __bf16 hh, ll;
+                split(accS[v], hh, ll);
+                sh[v] = hh;
+                sl[v] = ll;
             }
+            *reinterpret_cast<bf4*>(sth + i * PB + orow) = sh;
+            *reinterpret_cast<bf4*>(stl + i * PB + orow) = sl;
+            __syncthreads();
         }
-        __syncthreads();
-        bf4 sh, sl;
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            __bf16 hh, ll;
-            split(accS[v], hh, ll);
-            sh[v] = hh;
-            sl[v] = ll;
-        }
-        *reinterpret_cast<bf4*>(sth + i * PB + orow) = sh;
-        *reinterpret_cast<bf4*>(stl + i * PB + orow) = sl;
-        __syncthreads();
     }
     if (dst) {
 #pragma unroll
@@ -791,7 +863,7 @@ ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_
     }
     ws.max_chunks = maxc;
     ws.plan_bytes = varlen ? align256(sizeof(int32_t) * (size_t)(2 * maxc + num_seqs + 2)) : 0;
-    ws.chunk_bytes = align256((size_t)maxc * (size_t)H * kChunkBytes);
+    ws.chunk_bytes = align256(((size_t)maxc * (size_t)H + 1) * kChunkBytes);  // + the trash record
     ws.total_bytes = ws.plan_bytes + ws.chunk_bytes;
     return ws;
 }

@@ -48,14 +48,19 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Returns p as a wave-uniform (SGPR) value.  Loads through the result use a scalar base plus a 32-bit per-lane
-// offset; without it LLVM hoists `base + lane` out of token loops as one 64-bit VGPR pair per pointer.
+// Returns p (a pointer to global memory) as a wave-uniform (SGPR) value.  Loads through the result use a scalar
+// base plus a 32-bit per-lane offset; without it LLVM hoists `base + lane` out of token loops as one 64-bit VGPR
+// pair per pointer.  The value is rebuilt as a global-address-space pointer: rebuilt as a generic pointer the
+// accesses would compile to flat instructions, which also count on lgkmcnt, so every LDS wait would then wait
+// for outstanding global loads as well.
 template <typename T>
 __device__ __forceinline__ T* uniform_ptr(T* p) {
+    typedef __attribute__((address_space(1))) T GT;
     const uint64_t x = reinterpret_cast<uint64_t>(p);
     const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)x);
     const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(x >> 32));
-    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+    GT* const g = (GT*)(((uint64_t)hi << 32) | lo);
+    return (T*)g;
 }
 
 // Kernel-side view of one call (filled by the C-ABI layer from wkv7_args after validation).

@@ -19,7 +19,7 @@ hipError_t launch_recurrent(const Params& p, hipStream_t stream);
 
 // Workspace of the chunked path for one call.  Layout (byte offsets, each 256-aligned):
 //   [plan]   int32 chunk_seq[max_chunks], chunk_idx[max_chunks], seq_off[num_seqs + 1], total   (varlen only)
-//   [chunks] [max_chunks][H] records of kChunkBytes
+//   [chunks] [max_chunks][H] records of kChunkBytes, then one trash record (stores that must not land)
 struct ChunkWorkspace {
     int64_t max_chunks;
     size_t plan_bytes;
