@@ -45,6 +45,8 @@ typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 constexpr int C = kChunk;        // 64
 constexpr int PB = 72;           // LDS row pitch in bf16 (144 B: 16 rows of a ds_read_b128 hit distinct banks)
 constexpr int PF = 72;           // LDS row pitch in fp32 for the fp32 matrices (same bytes as a hi/lo pair)
+constexpr int PG = 68;           // LDS row pitch of the cumulative log-decay g (fp32): the 128-bit row-segment reads
+                                 // and writes of steps 1 and 3 (two rows per 16 lanes) hit distinct banks
 constexpr int SLOT = 64 * PB;    // bf16 elements of one 64 x 64 LDS matrix (9216 B)
 constexpr int NSLOT = 17;
 
@@ -261,6 +263,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lq = lane >> 4;
     float* const F32 = reinterpret_cast<float*>(sm.slot[0]);   // slots 0-1 as fp32 [64][PF]
+    float* const G32 = F32;                                     // steps 1-3: g as fp32 [64][PG] in slots 0-1
     float* const SCR = reinterpret_cast<float*>(sm.slot[15]);  // slots 15-16 as fp32 scratch (4608 floats)
     const BM Aq{sm.slot[2], sm.slot[3]};
     const BM Bk{sm.slot[4], sm.slot[5]};
@@ -281,7 +284,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const bool valid = row < it.Lc;
     f4 rl[12];  // step 5 -> step 6: relayout tiles of waves 4-7
 
-    // ---- 1. log2-decay -> F32; V (row-major, exact) -> Vr
+    // ---- 1. log2-decay -> G32; V (row-major, exact) -> Vr.  log2 d = -e^w log2(e) = -2^{w log2(e)} log2(e).
     {
         const uint32_t ww[4] = {raw.w.x, raw.w.y, raw.w.z, raw.w.w};
         float lam[8];
@@ -289,11 +292,11 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         for (int e = 0; e < 4; ++e) {
             float lo, hi;
             bf16x2_to_f32(ww[e], lo, hi);
-            lam[2 * e] = valid ? log_decay(lo) * kLog2e : 0.f;
-            lam[2 * e + 1] = valid ? log_decay(hi) * kLog2e : 0.f;
+            lam[2 * e] = valid ? -__builtin_amdgcn_exp2f(lo * kLog2e) * kLog2e : 0.f;
+            lam[2 * e + 1] = valid ? -__builtin_amdgcn_exp2f(hi * kLog2e) * kLog2e : 0.f;
         }
-        *reinterpret_cast<f4*>(F32 + row * PF + cb) = f4{lam[0], lam[1], lam[2], lam[3]};
-        *reinterpret_cast<f4*>(F32 + row * PF + cb + 4) = f4{lam[4], lam[5], lam[6], lam[7]};
+        *reinterpret_cast<f4*>(G32 + row * PG + cb) = f4{lam[0], lam[1], lam[2], lam[3]};
+        *reinterpret_cast<f4*>(G32 + row * PG + cb + 4) = f4{lam[4], lam[5], lam[6], lam[7]};
         *reinterpret_cast<uint4*>(Vr.h + row * PB + cb) = valid ? raw.v : make_uint4(0u, 0u, 0u, 0u);
     }
     __syncthreads();
@@ -303,7 +306,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         float run = 0.f;
 #pragma unroll
         for (int r = 0; r < 8; ++r) {
-            float* e = F32 + (8 * wv + r) * PF + lane;
+            float* e = G32 + (8 * wv + r) * PG + lane;
             run += *e;
             *e = run;
         }
@@ -313,11 +316,11 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             float offs = 0.f;
             for (int w2 = 0; w2 < wv; ++w2) offs += sm.bsum[w2][lane];
 #pragma unroll
-            for (int r = 0; r < 8; ++r) F32[(8 * wv + r) * PF + lane] += offs;
+            for (int r = 0; r < 8; ++r) G32[(8 * wv + r) * PG + lane] += offs;
         }
         __syncthreads();
         if (tid < HS) {
-            const float m = F32[31 * PF + tid], gl = F32[63 * PF + tid];
+            const float m = G32[31 * PG + tid], gl = G32[63 * PG + tid];
             sm.m[tid] = m;
             sm.em[tid] = __builtin_amdgcn_exp2f(m);
             sm.eglm[tid] = __builtin_amdgcn_exp2f(gl - m);
@@ -331,6 +334,13 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     {
         const uint32_t aw[4] = {raw.a.x, raw.a.y, raw.a.z, raw.a.w}, bw[4] = {raw.b.x, raw.b.y, raw.b.z, raw.b.w};
         const uint32_t kw[4] = {raw.k.x, raw.k.y, raw.k.z, raw.k.w}, rw[4] = {raw.r.x, raw.r.y, raw.r.z, raw.r.w};
+        // g of this row and the previous one, and the midpoints, as 128-bit reads (row 0 reads itself and zeroes)
+        const int prow = row > 0 ? row - 1 : 0;
+        const f4 gi4[2] = {*reinterpret_cast<const f4*>(G32 + row * PG + cb),
+                           *reinterpret_cast<const f4*>(G32 + row * PG + cb + 4)};
+        const f4 ge4[2] = {*reinterpret_cast<const f4*>(G32 + prow * PG + cb),
+                           *reinterpret_cast<const f4*>(G32 + prow * PG + cb + 4)};
+        const f4 m4[2] = {*reinterpret_cast<const f4*>(sm.m + cb), *reinterpret_cast<const f4*>(sm.m + cb + 4)};
         bf8 aqh, aql, bkh, bkl, kkh, kkl, rqh;
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
@@ -341,10 +351,10 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             bf16x2_to_f32(rw[e2], r2[0], r2[1]);
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
-                const int e = 2 * e2 + u, col = cb + e;
-                const float gi = F32[row * PF + col];
-                const float ge = row > 0 ? F32[(row - 1) * PF + col] : 0.f;
-                const float mk = sm.m[col];
+                const int e = 2 * e2 + u;
+                const float gi = gi4[e >> 2][e & 3];
+                const float ge = row > 0 ? ge4[e >> 2][e & 3] : 0.f;
+                const float mk = m4[e >> 2][e & 3];
                 const float fa = __builtin_amdgcn_exp2f(ge - mk), fr = __builtin_amdgcn_exp2f(gi - mk);
                 const float fb = __builtin_amdgcn_exp2f(mk - gi);
                 const float aq = valid ? a2[u] * fa : 0.f, rq = valid ? r2[u] * fr : 0.f;
@@ -379,21 +389,25 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     //   rho  : x = s, y = t  (X = Bk, Y = Rq),            keep s <= t, -> Rho as rho[t][s]
     //   sigma: x = s', y = t (X = Kk, Y = Rq),            keep s' <= t, -> Sig as sigma[t][s']
     //   V^T  : x = s, y = v  (X = V, Y = I, exact)        -> Vt as V^T[v][s]
-    for (int idx = wv; idx < 80; idx += 8) {
-        const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+    // Wave wv computes tiles wv and wv + 8 of every product (prod = u >> 1 is a compile-time constant), each over
+    // the full contraction and masked afterwards: straight-line code whose independent MFMA chains the scheduler
+    // interleaves (fully masked tiles cost MFMAs but no branches).
+#pragma unroll
+    for (int u = 0; u < 10; ++u) {
+        const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
         const int x0 = 16 * bx, y0 = 16 * by;
         f4 acc = zero4();
         if (prod == 0) {
-            if (bx <= by) acc = mask_tile(mma<3>(acc, Bk, x0, Aq, y0, 0, 2), x0, y0, 1);
+            acc = mask_tile(mma<3>(acc, Bk, x0, Aq, y0, 0, 2), x0, y0, 1);
             st_f32(F32, PF, x0, y0, acc);
         } else if (prod == 1) {
-            if (by <= bx) acc = mask_tile(mma<3>(acc, Aq, x0, Kk, y0, 0, 2), x0, y0, 3);
+            acc = mask_tile(mma<3>(acc, Aq, x0, Kk, y0, 0, 2), x0, y0, 3);
             st_split(Be, PB, x0, y0, acc);
         } else if (prod == 2) {
-            if (bx <= by) acc = mask_tile(mma<1>(acc, Bk, x0, Rq, y0, 0, 2), x0, y0, 2);
+            acc = mask_tile(mma<1>(acc, Bk, x0, Rq, y0, 0, 2), x0, y0, 2);
             st_hi(Rho.h, PB, x0, y0, acc);
         } else if (prod == 3) {
-            if (bx <= by) acc = mask_tile(mma<1>(acc, Kk, x0, Rq, y0, 0, 2), x0, y0, 2);
+            acc = mask_tile(mma<1>(acc, Kk, x0, Rq, y0, 0, 2), x0, y0, 2);
             st_hi(Sig.h, PB, x0, y0, acc);
         } else {
             const int kb = by >> 1;
@@ -515,23 +529,17 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     //         W over F32 (slots 0-1), G computed into registers and written over beta.
     {
         f4 acc[4];
+        // full contractions: T is exactly zero above its diagonal and beta on and above its own, so the extra
+        // terms are exact zeros (and G's tiles above the diagonal come out exactly zero)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int idx = wv + 8 * u;
-            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
-            f4 a = zero4();
-            if (prod == 0) {
-                a = mma<3>(a, Tm, 16 * bx, A0t, 16 * by, 0, (bx >> 1) + 1);       // s <= t
-            } else if (by <= bx) {
-                a = mma<3>(a, Tm, 16 * bx, Be, 16 * by, by >> 1, (bx >> 1) + 1);  // s' < s <= t
-            }
-            acc[u] = a;
+            const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
+            acc[u] = mma<3>(zero4(), Tm, 16 * bx, prod == 0 ? A0t : Be, 16 * by, 0, 2);
         }
         __syncthreads();
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int idx = wv + 8 * u;
-            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
             st_split(prod == 0 ? Wm : Gm, PB, 16 * bx, 16 * by, acc[u]);
         }
     }
@@ -545,26 +553,23 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         __bf16* const gQ = reinterpret_cast<__bf16*>(rec + REC_Q);
         __bf16* const gAh = reinterpret_cast<__bf16*>(rec + REC_AH);
         __bf16* const gAl = reinterpret_cast<__bf16*>(rec + REC_AL);
+        // full contractions again: rho and G are exactly zero where the causal ranges end
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            const int idx = wv + 8 * u;
-            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
             const int x0 = 16 * bx, y0 = 16 * by;
             f4 acc;
             if (prod == 0) {
                 const bf4 r4 = *reinterpret_cast<const bf4*>(Rq.h + (y0 + li) * PB + x0 + 4 * lq);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[v] = (float)r4[v] * sm.em[x0 + 4 * lq + v];
-                acc = mma<1>(acc, Wm, x0, Rho, y0, 0, (by >> 1) + 1);                 // s <= t
+                acc = mma<1>(acc, Wm, x0, Rho, y0, 0, 2);
                 st_hi(gQ, HS, x0, y0, acc);
             } else if (prod == 1) {
-                acc = zero4();
-                if (bx <= by) {
-                    const bf4 s4 = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
+                const bf4 s4 = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
 #pragma unroll
-                    for (int v = 0; v < 4; ++v) acc[v] = (float)s4[v];
-                    acc = mask_tile(mma<1>(acc, Gm, x0, Rho, y0, bx >> 1, (by >> 1) + 1), x0, y0, 2);
-                }
+                for (int v = 0; v < 4; ++v) acc[v] = (float)s4[v];
+                acc = mask_tile(mma<1>(acc, Gm, x0, Rho, y0, 0, 2), x0, y0, 2);
                 st_hi(Em.h, PB, x0, y0, acc);
             } else if (prod == 2) {
 #pragma unroll
@@ -585,7 +590,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
                 const bf4 kl4 = *reinterpret_cast<const bf4*>(Kht.l + (y0 + li) * PB + x0 + 4 * lq);
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[v] = (float)kh4[v] + (float)kl4[v];
-                acc = mma<3>(acc, Gm, x0, Bht, y0, bx >> 1, 2);                     // s > s'
+                acc = mma<3>(acc, Gm, x0, Bht, y0, 0, 2);
                 st_split(Fm, PB, x0, y0, acc);
             }
         }
@@ -599,13 +604,12 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         __bf16* const gO = reinterpret_cast<__bf16*>(rec + REC_OT);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const int idx = wv + 8 * u;
-            const int prod = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
+            const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
             const int x0 = 16 * bx, y0 = 16 * by;
             if (prod == 0) {
                 st_f32(gH, HS, x0, y0, mma<2>(zero4(), Fm, x0, Vt, y0, 0, 2));
             } else {
-                st_hi(gO, HS, x0, y0, mma<1>(zero4(), Vt, x0, Em, y0, 0, (by >> 1) + 1));  // s' <= t
+                st_hi(gO, HS, x0, y0, mma<1>(zero4(), Vt, x0, Em, y0, 0, 2));  // E is zero for s' > t
             }
         }
     }

@@ -35,9 +35,8 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
 }
 
-// log of the decay, log d = -exp(w), for the raw w (rwkv_next/kernels/wkv7.py:74).  Uses the device library's
-// full-precision expf.
-__device__ __forceinline__ float log_decay(float w) { return -expf(w); }
+// Decay d = exp(-exp(w)) of the raw w (rwkv_next/kernels/wkv7.py:74), with the device library's full-precision
+// expf.
 __device__ __forceinline__ float decay(float w) { return expf(-expf(w)); }
 
 // Orders LDS traffic between the lanes of one wavefront: a wave's LDS instructions execute in issue order, so
