@@ -651,21 +651,27 @@ __global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, ch
     }
 }
 
-// One chunk record's share of one scan lane: A hi/lo and Q rows (MFMA operands), H and O_intra entries.
+// One chunk record's share of one scan lane: A hi/lo and Q rows (MFMA operands, shared by the workgroup's column
+// tiles), and per column tile the H^T and O_intra entries.
+template <int NT>
 struct ScanRec {
     bf8 ah[2], al[2], q[2];
-    f4 hS;
-    uint2 hO;  // 4 bf16
+    f4 hS[NT];
+    uint2 hO[NT];  // 4 bf16 each
 };
 
 // Per-lane byte offsets inside a record (the same for every chunk).
+template <int NT>
 struct ScanOffs {
-    uint32_t a, s, o;  // A / Q row segment, H^T entry, O_intra entry
+    uint32_t a;      // A / Q row segment
+    uint32_t s[NT];  // H^T entry per column tile
+    uint32_t o[NT];  // O_intra entry per column tile
 };
 
 // `rec` is wave-uniform, so the loads address it as a scalar base plus the lane's 32-bit offset (no per-lane
 // 64-bit address registers to carry from one chunk to the next).
-__device__ __forceinline__ void scan_load(ScanRec& r, const char* rec, const ScanOffs& off) {
+template <int NT>
+__device__ __forceinline__ void scan_load(ScanRec<NT>& r, const char* rec, const ScanOffs<NT>& off) {
     const char* const b = uniform_ptr(rec);
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
@@ -673,30 +679,40 @@ __device__ __forceinline__ void scan_load(ScanRec& r, const char* rec, const Sca
         r.al[kb] = *reinterpret_cast<const bf8*>(b + REC_AL + off.a + 64 * kb);
         r.q[kb] = *reinterpret_cast<const bf8*>(b + REC_Q + off.a + 64 * kb);
     }
-    r.hS = *reinterpret_cast<const f4*>(b + REC_HT + off.s);
-    r.hO = *reinterpret_cast<const uint2*>(b + REC_OT + off.o);
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+        r.hS[c] = *reinterpret_cast<const f4*>(b + REC_HT + off.s[c]);
+        r.hO[c] = *reinterpret_cast<const uint2*>(b + REC_OT + off.o[c]);
+    }
 }
 
 constexpr int kScanDepth = 4;  // chunk records in flight per lane (register ring)
+// 16-column tiles per scan workgroup (the kernel supports 1, 2 or 4).  One is fastest on MI355X at T = 4096,
+// H = 64 (scan 76 us vs 100 us with 2 and 155 us with 4): the scan is bound by each workgroup's serial per-chunk
+// chain, so more, smaller workgroups win even though the 4 column groups of a head each read the chunk's A and Q.
+constexpr int kScanTiles = 1;
 
-// One workgroup per (row, head, 16-column block).  Block b -> XCD b % 8; the 4 column blocks of a (row, head)
-// pair share an XCD.  Wave w owns state rows (and output tokens) 16 w .. 16 w + 15.  S is carried exactly in fp32
-// accumulators and mirrored in LDS as a hi/lo bf16 split S^T[v][k] that feeds the next chunk's MFMAs; the output
-// tile is computed transposed (O^T = S^T Q^T), so each lane holds 4 consecutive columns of one token and writes
-// them with one 8-byte store.
+// One workgroup per (row, head, group of NT 16-column blocks); 4 / NT groups per (row, head).  Block b -> XCD
+// b % 8, and the groups of a (row, head) pair share an XCD.  Wave w owns state rows (and output tokens)
+// 16 w .. 16 w + 15 of all the group's columns.  S is carried exactly in fp32 accumulators and mirrored in LDS as a
+// hi/lo bf16 split S^T[v][k] that feeds the next chunk's MFMAs; the output tiles are computed transposed
+// (O^T = S^T Q^T), so each lane holds 4 consecutive columns of one token per tile and writes them with one 8-byte
+// store.  A workgroup owning more columns reads the chunk's A and Q rows once for all of them.
 //
 // Chunk records stream through a ring of kScanDepth register sets: after a chunk is consumed its set is refilled
 // with the record kScanDepth chunks ahead.  Every step issues the same memory operations -- the refill index is
 // clamped to the last chunk, steps past the end compute without effect, and stores that must not land (tokens
 // past the row's end, no output requested) go to the workspace's trash record -- so the compiler can count the
 // outstanding loads exactly and waits only for the record about to be used.
+template <int NT>
 __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
                                                               const int32_t* __restrict__ plan, int64_t max_chunks,
                                                               int ncps) {
-    __shared__ __attribute__((aligned(16))) __bf16 sth[16 * PB], stl[16 * PB];
+    constexpr int NG = 4 / NT;  // column groups per (row, head)
+    __shared__ __attribute__((aligned(16))) __bf16 sth[NT * 16 * PB], stl[NT * 16 * PB];
     const int b = blockIdx.x;
-    const int xcd = b & 7, rsl = b >> 3, vb = rsl & 3;
-    const int64_t pair = (int64_t)(rsl >> 2) * 8 + xcd;
+    const int xcd = b & 7, rsl = b >> 3, vg = rsl % NG;
+    const int64_t pair = (int64_t)(rsl / NG) * 8 + xcd;
     if (pair >= (int64_t)p.num_seqs * p.H) return;
     const int n = (int)(pair / p.H), h = (int)(pair % p.H);
     int64_t bos;
@@ -711,62 +727,84 @@ __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, ch
     const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((L + C - 1) / C, max_chunks - j0));
     const float* src = state_src(p, n, h);
     float* dst = state_dst(p, n, h);
+    const int vcol0 = 16 * NT * vg;  // first state column of this workgroup
 
-    // initial state: thread (krow, c4) holds S0[krow][16 vb + c4 .. + 3]
+    // initial state: thread (krow, c4) holds S0[krow][vcol0 + 16 c + c4 .. + 3] for each tile c
     {
         const int krow = tid >> 2, c4 = (tid & 3) * 4;
-        const f4 x = src ? *reinterpret_cast<const f4*>(src + krow * HS + 16 * vb + c4) : zero4();
+        f4 x[NT];
+#pragma unroll
+        for (int c = 0; c < NT; ++c)
+            x[c] = src ? *reinterpret_cast<const f4*>(src + krow * HS + vcol0 + 16 * c + c4) : zero4();
         if (nch == 0) {  // no chunks (length 0): the state passes through
-            if (dst) *reinterpret_cast<f4*>(dst + krow * HS + 16 * vb + c4) = x;
+            if (dst) {
+#pragma unroll
+                for (int c = 0; c < NT; ++c) *reinterpret_cast<f4*>(dst + krow * HS + vcol0 + 16 * c + c4) = x[c];
+            }
             return;
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            __bf16 hh, ll;
-            split(x[e], hh, ll);
-            sth[(c4 + e) * PB + krow] = hh;
-            stl[(c4 + e) * PB + krow] = ll;
+        for (int c = 0; c < NT; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                __bf16 hh, ll;
+                split(x[c][e], hh, ll);
+                sth[(16 * c + c4 + e) * PB + krow] = hh;
+                stl[(16 * c + c4 + e) * PB + krow] = ll;
+            }
         }
     }
     __syncthreads();
 
     const int xr = 16 * wv + i;          // operand row of A / Q this lane feeds; also its output token in a chunk
     const int orow = 16 * wv + 4 * q;    // first state row this lane holds
-    const int col = 16 * vb + i;         // state column this lane holds
-    const int ocol = 16 * vb + 4 * q;    // first output column this lane holds
     const char* const rec0 = wsc + (j0 * p.H + h) * (int64_t)kChunkBytes;
     const int64_t rec_stride = (int64_t)p.H * kChunkBytes;
     // stores that must not land go to the trash record, 2 KB per workgroup slot (24 slots) so that workgroups do not
     // all hit the same lines
     uint2* const trash =
         reinterpret_cast<uint2*>(wsc + max_chunks * p.H * (int64_t)kChunkBytes) + (b % 24) * 256 + tid;
-    ScanRec ring[kScanDepth];
-    const ScanOffs offs{(uint32_t)(xr * HS + 8 * q) * 2u, (uint32_t)(col * HS + orow) * 4u, (uint32_t)(xr * HS + ocol) * 2u};
+    ScanOffs<NT> offs;
+    offs.a = (uint32_t)(xr * HS + 8 * q) * 2u;
+#pragma unroll
+    for (int c = 0; c < NT; ++c) {
+        offs.s[c] = (uint32_t)((vcol0 + 16 * c + i) * HS + orow) * 4u;
+        offs.o[c] = (uint32_t)(xr * HS + vcol0 + 16 * c + 4 * q) * 2u;
+    }
+    ScanRec<NT> ring[kScanDepth];
 #pragma unroll
     for (int d = 0; d < kScanDepth; ++d) scan_load(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, offs);
 #pragma unroll
     for (int d = 0; d < kScanDepth; ++d) settle(ring[d]);
-    f4 accS = zero4();
+    f4 accS[NT];
+#pragma unroll
+    for (int c = 0; c < NT; ++c) accS[c] = zero4();
     for (int c0 = 0; c0 < nch; c0 += kScanDepth) {
 #pragma unroll
         for (int d = 0; d < kScanDepth; ++d) {
             const int cc = c0 + d;
             const bool live = cc < nch;  // wave-uniform
-            ScanRec& r = ring[d];
-            f4 newS = r.hS, accO;
-            {
+            ScanRec<NT>& r = ring[d];
+            f4 newS[NT], accO[NT];
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+                newS[c] = r.hS[c];
                 float o0, o1, o2, o3;
-                bf16x2_to_f32(r.hO.x, o0, o1);
-                bf16x2_to_f32(r.hO.y, o2, o3);
-                accO = f4{o0, o1, o2, o3};
+                bf16x2_to_f32(r.hO[c].x, o0, o1);
+                bf16x2_to_f32(r.hO[c].y, o2, o3);
+                accO[c] = f4{o0, o1, o2, o3};
             }
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                const bf8 ysh = ld8(sth + i * PB + 32 * kb + 8 * q), ysl = ld8(stl + i * PB + 32 * kb + 8 * q);
-                newS = mfma_bf16(r.ah[kb], ysl, newS);
-                newS = mfma_bf16(r.al[kb], ysh, newS);
-                newS = mfma_bf16(r.ah[kb], ysh, newS);
-                accO = mfma_bf16(ysh, r.q[kb], accO);  // O^T: lane (i, q) gets token xr, columns ocol .. + 3
+#pragma unroll
+                for (int c = 0; c < NT; ++c) {
+                    const int so = (16 * c + i) * PB + 32 * kb + 8 * q;
+                    const bf8 ysh = ld8(sth + so), ysl = ld8(stl + so);
+                    newS[c] = mfma_bf16(r.ah[kb], ysl, newS[c]);
+                    newS[c] = mfma_bf16(r.al[kb], ysh, newS[c]);
+                    newS[c] = mfma_bf16(r.ah[kb], ysh, newS[c]);
+                    accO[c] = mfma_bf16(ysh, r.q[kb], accO[c]);  // O^T: lane (i, q): token xr, 4 columns
+                }
             }
             // the refill reuses the slot's registers only if it is not scheduled above the slot's last use;
             // otherwise the ring rotates through copies that wait for the newest loads
@@ -774,32 +812,46 @@ __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, ch
             scan_load(r, rec0 + std::min(cc + kScanDepth, nch - 1) * rec_stride, offs);
             {
                 const int t = cc * C + xr;
-                uint2 pk;
-                pk.x = pack_bf16x2(accO[0], accO[1]);
-                pk.y = pack_bf16x2(accO[2], accO[3]);
-                uint2* const out = (live && t < L && p.o)
-                                       ? reinterpret_cast<uint2*>(p.o + (bos + t) * p.o_tok_stride + (int64_t)h * HS + ocol)
-                                       : trash;
-                *out = pk;
-            }
-            if (live) accS = newS;
-            __syncthreads();
-            bf4 sh, sl;
+                const bool st = live && t < L && p.o;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                __bf16 hh, ll;
-                split(accS[v], hh, ll);
-                sh[v] = hh;
-                sl[v] = ll;
+                for (int c = 0; c < NT; ++c) {
+                    uint2 pk;
+                    pk.x = pack_bf16x2(accO[c][0], accO[c][1]);
+                    pk.y = pack_bf16x2(accO[c][2], accO[c][3]);
+                    uint2* const out =
+                        st ? reinterpret_cast<uint2*>(p.o + (bos + t) * p.o_tok_stride + (int64_t)h * HS + vcol0 +
+                                                      16 * c + 4 * q)
+                           : trash;
+                    *out = pk;
+                }
             }
-            *reinterpret_cast<bf4*>(sth + i * PB + orow) = sh;
-            *reinterpret_cast<bf4*>(stl + i * PB + orow) = sl;
+            if (live) {
+#pragma unroll
+                for (int c = 0; c < NT; ++c) accS[c] = newS[c];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int c = 0; c < NT; ++c) {
+                bf4 sh, sl;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    __bf16 hh, ll;
+                    split(accS[c][v], hh, ll);
+                    sh[v] = hh;
+                    sl[v] = ll;
+                }
+                *reinterpret_cast<bf4*>(sth + (16 * c + i) * PB + orow) = sh;
+                *reinterpret_cast<bf4*>(stl + (16 * c + i) * PB + orow) = sl;
+            }
             __syncthreads();
         }
     }
     if (dst) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) dst[(orow + v) * HS + col] = accS[v];
+        for (int c = 0; c < NT; ++c) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) dst[(orow + v) * HS + vcol0 + 16 * c + i] = accS[c][v];
+        }
     }
 }
 
@@ -890,8 +942,8 @@ hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* works
                            ws.max_chunks, ncps);
     }
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
-    const int64_t blocks = ((pairs + 7) / 8) * 8 * 4;
-    hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, wsc, plan,
+    const int64_t blocks = ((pairs + 7) / 8) * 8 * (4 / kScanTiles);
+    hipLaunchKernelGGL(wkv7_chunk_scan_kernel<kScanTiles>, dim3((unsigned)blocks), dim3(256), 0, stream, p, wsc, plan,
                        ws.max_chunks, ncps);
     return hipGetLastError();
 }
