@@ -78,6 +78,14 @@ __device__ __forceinline__ f4 mfma_f32(float a, float b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+typedef short s4 __attribute__((ext_vector_type(4)));  // 4 bf16 bit patterns, the 16x16x16 MFMA operand
+
+// 16x16x16 bf16 MFMA.  Lane (i = lane & 15, q = lane >> 4) feeds A[i][4q .. 4q+3] and B[4q .. 4q+3][i] and receives
+// D[4q + v][i] in acc[v]: a result tile is already laid out as a B operand.
+__device__ __forceinline__ f4 mfma16(s4 a, s4 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
 // An LDS matrix stored as bf16 rows of pitch PB: the high part and (for split fp32 values) the low part.
 struct BM {
     __bf16* h;
@@ -108,6 +116,17 @@ __device__ __forceinline__ f4 mma(f4 acc, BM X, int x0, BM Y, int y0, int kb0, i
 __device__ __forceinline__ void split(float x, __bf16& h, __bf16& l) {
     h = (__bf16)x;
     l = (__bf16)(x - (float)h);
+}
+
+// Four fp32 values as hi/lo bf16 operands of mfma16.
+__device__ __forceinline__ void split4(f4 x, s4& h, s4& l) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        __bf16 hh, ll;
+        split(x[v], hh, ll);
+        h[v] = __builtin_bit_cast(short, hh);
+        l[v] = __builtin_bit_cast(short, ll);
+    }
 }
 
 // Natural stores of a tile (element (x0 + 4q + v, y0 + i) at M[(y0 + i) * pitch + x0 + 4q + v]): 4 consecutive
@@ -250,13 +269,13 @@ __device__ __forceinline__ RawIn load_item(const Params& p, const Item& it, int 
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Slots (each 64 x 72 bf16 = 9 KB; an fp32 64 x 72 matrix takes two):
-//   0-1   log2 d -> g (fp32) -> alpha (fp32) -> T (fp32, in place) -> W hi/lo
+//   0-1   log2 d -> g (fp32) -> alpha (fp32, diagonal blocks replaced by their inverses T_ii) -> W hi/lo
 //   2-3   Aq hi/lo -> A0^T hi/lo -> F hi/lo
 //   4-5   Bk hi/lo -> Bh^T hi/lo
 //   6-7   Kk hi/lo -> Kh^T hi/lo
 //   8     Rq hi                     9  V^T (exact bf16)
 //   10-11 beta hi/lo -> G hi/lo     12 rho    13 sigma    14 E
-//   15-16 V (row-major) -> fp32 scratch of the inversion -> T hi/lo
+//   15-16 V (row-major) -> fp32 scratch of the diagonal-block inversion
 // Decays are handled in base 2 (g = cumulative log2 d), so every decay factor is one v_exp_f32.
 __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const RawIn& raw, char* wsc,
                                           PrepSmem& sm) {
@@ -275,10 +294,9 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const BM Sig{sm.slot[13], nullptr};
     const BM Em{sm.slot[14], nullptr};
     const BM Vr{sm.slot[15], nullptr};
-    const BM Tm{sm.slot[15], sm.slot[16]};
     const BM A0t = Aq, Bht = Bk, Kht = Kk;          // after step 6
-    const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 9
-    const BM Fm{sm.slot[2], sm.slot[3]};            // step 10 (A0^T is dead after step 9)
+    const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 7
+    const BM Fm{sm.slot[2], sm.slot[3]};            // step 8 (A0^T is dead after step 7)
     char* const rec = wsc + it.rec * (int64_t)kChunkBytes;
     const int row = tid >> 3, cb = (tid & 7) * 8;
     const bool valid = row < it.Lc;
@@ -474,8 +492,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     }
     __syncthreads();
 
-    // ---- 6. waves 4-7: store A0^T, Bh^T, Kh^T over their sources;
-    //         waves 0-1: 32 x 32 diagonal blocks, T_10 = T_11 (alpha_10 T_00) and T_32 = T_33 (alpha_32 T_22)
+    // ---- 6. waves 4-7: store A0^T, Bh^T, Kh^T over their sources
     if (wv >= 4) {
 #pragma unroll
         for (int u = 0; u < 12; ++u) {
@@ -483,69 +500,52 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             const int mat = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
             st_split(mat == 0 ? Aq : (mat == 1 ? Bk : Kk), PB, 16 * bx, 16 * by, rl[u]);
         }
-    } else if (wv < 2) {
-        const int bi = 2 * wv + 1, bj = 2 * wv;
-        float* const Z = SCR + wv * 256;
-        st_rows_f32(Z, 16, mm_f32(zero4(), F32 + (16 * bi) * PF + 16 * bj, PF, 1, F32 + (16 * bj) * PF + 16 * bj, 1,
-                                  PF, 16));
-        wave_lds_sync();
-        st_rows_f32(F32 + (16 * bi) * PF + 16 * bj,
-                    PF, mm_f32(zero4(), F32 + (16 * bi) * PF + 16 * bi, PF, 1, Z, 1, 16, 16));
     }
     __syncthreads();
 
-    // ---- 7. 64 x 64: T_BA = T_B (alpha_BA T_A) with A = rows/cols 0-31, B = rows/cols 32-63 (waves 0-3, one
-    //         16 x 16 tile (tx, ty) of the 32 x 32 result each; the intermediate lives in the scratch)
-    if (wv < 4) {
-        const int tx = wv >> 1, ty = wv & 1;
-        st_rows_f32(SCR + (16 * tx) * 32 + 16 * ty, 32,
-                    mm_f32(zero4(), F32 + (32 + 16 * tx) * PF, PF, 1, F32 + 16 * ty, 1, PF, 32));
-    }
-    __syncthreads();
-    if (wv < 4) {
-        const int tx = wv >> 1, ty = wv & 1;
-        st_rows_f32(F32 + (32 + 16 * tx) * PF + 16 * ty, PF,
-                    mm_f32(zero4(), F32 + (32 + 16 * tx) * PF + 32, PF, 1, SCR + 16 * ty, 1, 32, 32));
-    }
-    __syncthreads();
-
-    // ---- 8. T hi/lo [t][s] -> slots 15-16 (T is lower triangular; the upper part of F32 holds zeros)
+    // ---- 7. W = T A0 and G = T beta without forming T: block forward substitution of (I - alpha) X = [A0 | beta]
+    //         over the four 16-row blocks, X_i = T_ii (B_i + sum_{j<i} alpha_ij X_j), with the diagonal-block
+    //         inverses T_ii from step 5.  Wave w owns one 16-column tile of X (w < 4: W columns 16 w ..; w >= 4: G
+    //         columns 16 (w - 4) ..) and keeps its X_j in registers: the 16x16x16 MFMA returns a tile in exactly the
+    //         layout it takes as its B operand.  3-term hi/lo products throughout (state path).
     {
-        bf8 th, tl;
+        const bool is_w = wv < 4;
+        const int col0 = 16 * (wv & 3);
+        const BM rhs = is_w ? A0t : Be;  // A0^T [k][t] / beta stored [s'][s]: column-major right-hand side
+        f4 X[4];
+        s4 Xh[4], Xl[4];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int col = cb + e;
-            __bf16 h, l;
-            split(col <= row ? F32[row * PF + col] : 0.f, h, l);
-            th[e] = h;
-            tl[e] = l;
+        for (int bi = 0; bi < 4; ++bi) {
+            const int o = (col0 + li) * PB + 16 * bi + 4 * lq;
+            const bf4 bh = *reinterpret_cast<const bf4*>(rhs.h + o), bl = *reinterpret_cast<const bf4*>(rhs.l + o);
+            f4 acc;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[v] = (float)bh[v] + (float)bl[v];
+#pragma unroll
+            for (int bj = 0; bj < bi; ++bj) {
+                const f4 al = *reinterpret_cast<const f4*>(F32 + (16 * bi + li) * PF + 16 * bj + 4 * lq);
+                s4 ah4, al4;
+                split4(al, ah4, al4);
+                acc = mfma16(ah4, Xl[bj], acc);
+                acc = mfma16(al4, Xh[bj], acc);
+                acc = mfma16(ah4, Xh[bj], acc);
+            }
+            const f4 tt = *reinterpret_cast<const f4*>(F32 + (16 * bi + li) * PF + 16 * bi + 4 * lq);
+            s4 th4, tl4, ch4, cl4;
+            split4(tt, th4, tl4);
+            split4(acc, ch4, cl4);
+            f4 x = mfma16(th4, cl4, zero4());
+            x = mfma16(tl4, ch4, x);
+            X[bi] = mfma16(th4, ch4, x);
+            split4(X[bi], Xh[bi], Xl[bi]);
         }
-        *reinterpret_cast<bf8*>(Tm.h + row * PB + cb) = th;
-        *reinterpret_cast<bf8*>(Tm.l + row * PB + cb) = tl;
+        __syncthreads();  // alpha / T_ii (slots 0-1) and beta are read above; W and G are written over them
+#pragma unroll
+        for (int bi = 0; bi < 4; ++bi) st_split(is_w ? Wm : Gm, PB, 16 * bi, col0, X[bi]);
     }
     __syncthreads();
 
-    // ---- 9. W = T A0 (x = t, y = k: stored [k][s]) and G = T beta (x = t, y = s': stored [s'][s]), 3 terms each;
-    //         W over F32 (slots 0-1), G computed into registers and written over beta.
-    {
-        f4 acc[4];
-        // full contractions: T is exactly zero above its diagonal and beta on and above its own, so the extra
-        // terms are exact zeros (and G's tiles above the diagonal come out exactly zero)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
-            acc[u] = mma<3>(zero4(), Tm, 16 * bx, prod == 0 ? A0t : Be, 16 * by, 0, 2);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
-            st_split(prod == 0 ? Wm : Gm, PB, 16 * bx, 16 * by, acc[u]);
-        }
-    }
-    __syncthreads();
-
-    // ---- 10. Q = R0 + rho W  (x = k, y = t; bf16 -> workspace [t][k])
+    // ---- 8. Q = R0 + rho W  (x = k, y = t; bf16 -> workspace [t][k])
     //          E = sigma + rho G (x = s', y = t; bf16 -> Em [t][s'], keep s' <= t)
     //          A = Gamma + Bh^T W (x = k2, y = k1; 3 terms -> workspace hi/lo [k1][k2])
     //          F = Kh^T + Bh^T G (x = s', y = k; 3 terms -> slots 2-3 as F[k][s'])
@@ -597,7 +597,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     }
     __syncthreads();
 
-    // ---- 11. H = F V (x = k, y = v; X split, V exact -> workspace fp32 [v][k]);
+    // ---- 9. H = F V (x = k, y = v; X split, V exact -> workspace fp32 [v][k]);
     //          O_intra = E V (x = v, y = t -> workspace bf16 [t][v])
     {
         float* const gH = reinterpret_cast<float*>(rec + REC_HT);

@@ -4,8 +4,8 @@ decay references, which masks, the blocked triangular inverse) independently of 
 tests then only have to show the HIP kernels compute these same products.
 
 Per chunk (C tokens, initial state S0):  S_C = A S0 + F V,  O = Q S0 + E V  with
-  A = Gamma + Bh^T W,  F = Bh^T G + Kh^T,  Q = R0 + rho W,  E = sigma + rho G,  W = T A0,  G = T beta,
-  T = (I - alpha)^{-1}.
+  A = Gamma + Bh^T W,  F = Bh^T G + Kh^T,  Q = R0 + rho W,  E = sigma + rho G,  [W | G] = (I - alpha)^{-1} [A0 | beta],
+the last solved block by block (forward substitution with the inverses of the 16 x 16 diagonal blocks).
 """
 import numpy as np
 
@@ -35,6 +35,19 @@ def blocked_unit_lower_inverse(alpha):
     return T
 
 
+def block_forward_substitution(alpha, B):
+    """X = (I - alpha)^{-1} B for strictly lower alpha (64 x 64) the way the prep kernel solves for W and G: 16-row
+    blocks in order, X_i = T_ii (B_i + sum_{j<i} alpha_ij X_j), with T_ii the inverse of the diagonal block."""
+    X = np.zeros_like(B)
+    for bi in range(4):
+        rows = slice(16 * bi, 16 * bi + 16)
+        acc = B[rows].copy()
+        for bj in range(bi):
+            acc += alpha[rows, 16 * bj:16 * bj + 16] @ X[16 * bj:16 * bj + 16]
+        X[rows] = np.linalg.inv(np.eye(16) - alpha[rows, rows]) @ acc
+    return X
+
+
 def chunk_prep(r, w, k, v, a, b):
     """One chunk of one head; inputs [L, 64] (L <= C) -> (A, H = F V, Q, O_intra = E V)."""
     L = r.shape[0]
@@ -50,8 +63,8 @@ def chunk_prep(r, w, k, v, a, b):
     rho, sigma = np.tril(Rq @ Bk.T), np.tril(Rq @ Kk.T)
     A0, R0 = Aq * np.exp(m), Rq * np.exp(m)
     Bh, Kh = Bk * np.exp(gL - m), Kk * np.exp(gL - m)
-    T = blocked_unit_lower_inverse(alpha)
-    W, G = T @ A0, T @ beta
+    X = block_forward_substitution(alpha, np.hstack([A0, beta]))
+    W, G = X[:, :64], X[:, 64:]
     Q, E = R0 + rho @ W, sigma + rho @ G
     A = np.diag(np.exp(gL)) + Bh.T @ W
     F = Bh.T @ G + Kh.T
@@ -76,6 +89,15 @@ def test_blocked_inverse_matches_dense_inverse():
     alpha = np.tril(0.3 * rng.standard_normal((64, 64)), -1)
     T = blocked_unit_lower_inverse(alpha)
     assert rel_max(T @ (np.eye(64) - alpha), np.eye(64)) < 1e-12
+
+
+def test_block_forward_substitution_matches_dense_solve():
+    rng = np.random.default_rng(1)
+    alpha = np.tril(0.3 * rng.standard_normal((64, 64)), -1)
+    B = rng.standard_normal((64, 128))
+    X = block_forward_substitution(alpha, B)
+    assert rel_max(X, np.linalg.solve(np.eye(64) - alpha, B)) < 1e-12
+    assert rel_max(X, blocked_unit_lower_inverse(alpha) @ B) < 1e-12
 
 
 def test_chunked_form_reproduces_the_recurrence():
