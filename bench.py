@@ -9,10 +9,10 @@ value = algorithmic bytes / time: 33 664 B per (slot, head) per layer (16 KB sta
 768 B operands + 128 B output).
 
 Secondary (same line): chunked prefill B = 1, T = 4096, H = 64 (tok/s and fraction of its roofline), the
-speculative verify with snapshots (config 4), the mixed continuous-batching step in a HIP graph (config 3) and the
-CPU baseline (the oracle's fp32 loop on the host cores).
+speculative verify with snapshots (config 4), the mixed continuous-batching step in a HIP graph (config 3), the
+fused time-mix prologue/epilogue at the prefill shape, and the CPU baseline (the oracle's fp32 loop on the host cores).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu] [--only decode|prefill|verify|mixed]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu] [--only decode|prefill|verify|mixed|timemix]
 """
 import argparse
 import json
@@ -171,6 +171,58 @@ def verify_bench(torch, kernels, synth, dev, steps, warmup):
     return {"ms": ms, "GBps": bytes_ / (ms * 1e-3) / 1e9, "bytes": bytes_}
 
 
+TIMEMIX_PROLOGUE_BYTES = 11 * 2     # per (token, channel): k, v, o_v, o_w, o_a, v_first read; w, k', v', a, b written
+TIMEMIX_EPILOGUE_BYTES = 6 * 2      # y, r, k', v', g read; out written
+
+
+def timemix_bench(torch, kernels, dev, steps, warmup):
+    """Fused time-mix prologue and epilogue (rwkv_next/model.py:142-158) at the prefill shape T = 4096, C = 4096,
+    beside the same math as the reference's chain of bf16 torch ops (timed on the same GPU, for scale)."""
+    F = torch.nn.functional
+    T, H = 4096, 64
+    Cc = H * 64
+    g = torch.Generator(device="cpu").manual_seed(1005)
+    rnd = lambda *s: torch.randn(*s, generator=g).to(torch.bfloat16).to(dev)
+    r, k, v, vf, gate, y = (rnd(T, Cc) for _ in range(6))
+    o = rnd(3, T, Cc)
+    b_w, b_a, b_v, kk_mul, ka_mul = (rnd(1, Cc) for _ in range(5))
+    lnx_w, lnx_b, r_k = rnd(Cc), rnd(Cc), rnd(H, 64)
+    eps = 1e-5 * 64
+
+    def fused():
+        ins, _ = kernels.timemix_prologue(r, k, v, o, vf, b_w, b_a, b_v, kk_mul, ka_mul, H, 64, False)
+        return ins, kernels.timemix_epilogue(y, r, ins[2], ins[3], gate, lnx_w, lnx_b, r_k, H, 64, eps)
+
+    def eager():
+        w = -F.softplus(-(b_w + o[1])) - 0.5
+        a = torch.sigmoid(b_a + o[2])
+        vv = v + (vf - v) * torch.sigmoid(b_v + o[0])
+        kk = F.normalize((k * kk_mul).view(T, H, 64), dim=-1, p=2.0).view(T, Cc)
+        kp = k * (1 + (a - 1) * ka_mul)
+        ins = (r, w, kp, vv, -kk, kk * a)
+        x = F.group_norm(y, H, lnx_w, lnx_b, eps)
+        x = x + ((r.view(T, H, 64) * kp.view(T, H, 64) * r_k).sum(-1, keepdim=True) * vv.view(T, H, 64)).view(T, Cc)
+        return ins, x * gate
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms = timed(fused)
+    ms_eager = timed(eager)
+    bytes_ = (TIMEMIX_PROLOGUE_BYTES + TIMEMIX_EPILOGUE_BYTES) * T * Cc
+    return {"ms": ms, "GBps": bytes_ / (ms * 1e-3) / 1e9, "frac_hbm": bytes_ / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "algorithmic_bytes": bytes_, "torch_eager_ms": ms_eager, "speedup_vs_eager": ms_eager / ms}
+
+
 def cpu_baseline(synth):
     """The oracle's fp32 loop (a restatement of rwkv_next/kernels/wkv7.py:65-77) on the host cores, on a bounded
     sample of the decode workload: B = 64 sequences of a 128-slot pool, H = 64, T = 1, one pool, repeated for
@@ -219,7 +271,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed", "timemix"], default=None)
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain device copy of 1 GiB (reference dispatch for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -254,6 +306,9 @@ def main():
     if args.only in (None, "mixed"):
         log("mixed")
         res["mixed"] = mixed_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
+    if args.only in (None, "timemix"):
+        log("timemix")
+        res["timemix"] = timemix_bench(torch, kernels, dev, max(5, args.steps // 5), args.warmup)
     cpu = None
     if not args.skip_cpu and args.only is None:
         log("cpu baseline")
@@ -288,6 +343,8 @@ def main():
         out["verify"] = res["verify"]
     if "mixed" in res:
         out["mixed"] = res["mixed"]
+    if "timemix" in res:
+        out["timemix"] = res["timemix"]
     if cpu:
         out["cpu_baseline"] = cpu
     print(json.dumps(out))

@@ -119,6 +119,43 @@ int wkv7_pool_move(float *pool, int32_t layers, int64_t rows, int32_t H, const i
 int wkv7_snapshot_restore(float *pool, int64_t rows, int32_t H, const int64_t *slots, const float *snapshots,
                           int32_t T, const int64_t *n_accepted, int32_t num_seqs, void *stream);
 
+/*
+ * Time-mix work around the recurrence, fused (one pass each instead of the reference's chain of elementwise torch
+ * ops).  All tensors bf16, rows of H*64 channels; head size 64, 1 <= H <= 65536.  Every pointer 16-byte aligned and
+ * row strides multiples of 8 elements (WKV7_ERR_ALIGN otherwise).  fp32 arithmetic, one bf16 rounding per output.
+ * Outputs must not overlap the inputs.
+ */
+
+/* Operand prologue, rwkv_next/model.py:142-152:
+ *   w = -softplus(-(b_w + o_w)) - 0.5;  a = sigmoid(b_a + o_a);
+ *   v' = v (v_first == NULL: first layer) or v + (v_first - v) * sigmoid(b_v + o_v);
+ *   kk = L2-normalise(k * kk_mul) per head (eps 1e-12);  k' = k * (1 + (a - 1) * ka_mul);
+ *   outputs w, k', v', a_out = -kk, b_out = kk * a  -- with r, the six WKV operands. */
+typedef struct wkv7_prologue_args {
+    const uint16_t *k, *v;                   /* projections [tokens][in_stride] */
+    const uint16_t *o_v, *o_w, *o_a;         /* LoRA outputs o[0], o[1], o[2] (model.py:135-140), same layout */
+    const uint16_t *v_first;                 /* the first layer's v, or NULL on the first layer */
+    const uint16_t *b_w, *b_a, *b_v, *kk_mul, *ka_mul;  /* per-channel parameters [H*64] (b_v unused if no v_first) */
+    uint16_t *w_out, *k_out, *v_out, *a_out, *b_out;    /* [tokens][out_stride] */
+    int64_t tokens, in_stride, out_stride;  /* strides in elements, >= H*64 */
+    int32_t H, head_size;
+} wkv7_prologue_args;
+
+/* Epilogue up to the output projection, rwkv_next/model.py:156-158:
+ *   out = (group_norm(y; one group per head, lnx_w, lnx_b, eps) + sum_c(r * k' * r_k) * v') * g */
+typedef struct wkv7_epilogue_args {
+    const uint16_t *y, *r, *k, *v, *g;       /* recurrence output, r, k', v', gate [tokens][in_stride] */
+    const uint16_t *lnx_w, *lnx_b;           /* group-norm affine [H*64] */
+    const uint16_t *r_k;                     /* bonus weights [H][64] */
+    uint16_t *out;                           /* [tokens][out_stride] */
+    int64_t tokens, in_stride, out_stride;
+    float eps;                               /* the model's 1e-5 * head_size_divisor^2 (model.py:266) */
+    int32_t H, head_size;
+} wkv7_epilogue_args;
+
+int wkv7_timemix_prologue(const wkv7_prologue_args *args, void *stream);
+int wkv7_timemix_epilogue(const wkv7_epilogue_args *args, void *stream);
+
 /* Static description of a return code. */
 const char *wkv7_strerror(int code);
 

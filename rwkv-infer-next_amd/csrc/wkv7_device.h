@@ -17,13 +17,11 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
 
-// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN).
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even fp32 -> bf16 (NaN stays NaN); gfx950 converts in hardware (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, (__bf16)f); }
 
 // Unpack two bf16 held in one 32-bit word (low half first).
 __device__ __forceinline__ void bf16x2_to_f32(uint32_t x, float& lo, float& hi) {
@@ -31,8 +29,10 @@ __device__ __forceinline__ void bf16x2_to_f32(uint32_t x, float& lo, float& hi) 
     hi = __uint_as_float(x & 0xffff0000u);
 }
 
+// Two fp32 -> two bf16 in one word (lo in the low half), one v_cvt_pk_bf16_f32.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    const f2_t x = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2_t));
 }
 
 // Decay d = exp(-exp(w)) of the raw w (rwkv_next/kernels/wkv7.py:74), with the device library's full-precision

@@ -23,7 +23,8 @@ ALGO_RECURRENT = 1
 ALGO_CHUNKED = 2
 
 EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
-            "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore")
+            "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore", "wkv7_timemix_prologue",
+            "wkv7_timemix_epilogue")
 MAX_MOVES = 1024
 
 _vp = ctypes.c_void_p
@@ -56,6 +57,21 @@ class Wkv7Args(ctypes.Structure):
         ("algo", ctypes.c_int32),
         ("rec_max_len", ctypes.c_int32),
     ]
+
+
+class PrologueArgs(ctypes.Structure):
+    """Mirror of `wkv7_prologue_args` (include/wkv7.h)."""
+    _fields_ = [(n, _vp) for n in ("k", "v", "o_v", "o_w", "o_a", "v_first", "b_w", "b_a", "b_v", "kk_mul", "ka_mul",
+                                   "w_out", "k_out", "v_out", "a_out", "b_out")] + [
+        ("tokens", ctypes.c_int64), ("in_stride", ctypes.c_int64), ("out_stride", ctypes.c_int64),
+        ("H", ctypes.c_int32), ("head_size", ctypes.c_int32)]
+
+
+class EpilogueArgs(ctypes.Structure):
+    """Mirror of `wkv7_epilogue_args` (include/wkv7.h)."""
+    _fields_ = [(n, _vp) for n in ("y", "r", "k", "v", "g", "lnx_w", "lnx_b", "r_k", "out")] + [
+        ("tokens", ctypes.c_int64), ("in_stride", ctypes.c_int64), ("out_stride", ctypes.c_int64),
+        ("eps", ctypes.c_float), ("H", ctypes.c_int32), ("head_size", ctypes.c_int32)]
 
 
 class Wkv7Error(RuntimeError):
@@ -95,6 +111,10 @@ def load(path: str = LIB_PATH):
     lib.wkv7_pool_move.argtypes = [_vp, i32, i64, i32, _vp, _vp, i32, _vp]
     lib.wkv7_snapshot_restore.restype = ctypes.c_int
     lib.wkv7_snapshot_restore.argtypes = [_vp, i64, i32, _vp, _vp, i32, _vp, i32, _vp]
+    lib.wkv7_timemix_prologue.restype = ctypes.c_int
+    lib.wkv7_timemix_prologue.argtypes = [ctypes.POINTER(PrologueArgs), _vp]
+    lib.wkv7_timemix_epilogue.restype = ctypes.c_int
+    lib.wkv7_timemix_epilogue.argtypes = [ctypes.POINTER(EpilogueArgs), _vp]
     if lib.wkv7_abi_version() != WKV7_ABI_VERSION:
         raise ImportError(f"{path}: ABI version {lib.wkv7_abi_version()} != {WKV7_ABI_VERSION}")
     if lib.wkv7_args_size() != ctypes.sizeof(Wkv7Args):

@@ -123,3 +123,38 @@ def test_pool_entry_points_validate_before_launch():
     assert lib.wkv7_snapshot_restore(fake, 4, 2, fake, None, 5, fake, 1, None) == E.WKV7_ERR_NULL
     assert lib.wkv7_snapshot_restore(fake, 4, 2, fake, fake + 4, 5, fake, 1, None) == E.WKV7_ERR_ALIGN
     assert lib.wkv7_snapshot_restore(None, 4, 2, None, None, 5, None, 0, None) == E.WKV7_OK
+
+
+def test_timemix_entry_points_validate_before_launch():
+    """Prologue / epilogue reject bad sizes and NULL or misaligned pointers on the host; zero tokens is a no-op."""
+    lib = _lib.load()
+    fake = 0x10000
+    p = _lib.PrologueArgs()
+    for n in ("k", "v", "o_v", "o_w", "o_a", "b_w", "b_a", "b_v", "kk_mul", "ka_mul", "w_out", "k_out", "v_out",
+              "a_out", "b_out"):
+        setattr(p, n, fake)
+    p.tokens, p.in_stride, p.out_stride, p.H, p.head_size = 3, 128, 128, 2, 64
+    for field, value, code in [("head_size", 32, _lib.WKV7_ERR_SHAPE), ("in_stride", 64, _lib.WKV7_ERR_SHAPE),
+                               ("H", 1 << 17, _lib.WKV7_ERR_SHAPE), ("kk_mul", None, _lib.WKV7_ERR_NULL),
+                               ("w_out", fake + 8, _lib.WKV7_ERR_ALIGN), ("out_stride", 130, _lib.WKV7_ERR_ALIGN)]:
+        q = _lib.PrologueArgs.from_buffer_copy(p)
+        setattr(q, field, value)
+        assert lib.wkv7_timemix_prologue(ctypes.byref(q), None) == code, field
+    q = _lib.PrologueArgs.from_buffer_copy(p)
+    q.v_first, q.o_v = fake, None                       # mixing towards v_first needs o_v
+    assert lib.wkv7_timemix_prologue(ctypes.byref(q), None) == _lib.WKV7_ERR_NULL
+    q = _lib.PrologueArgs.from_buffer_copy(p)
+    q.tokens = 0
+    assert lib.wkv7_timemix_prologue(ctypes.byref(q), None) == _lib.WKV7_OK
+    e = _lib.EpilogueArgs()
+    for n in ("y", "r", "k", "v", "g", "lnx_w", "lnx_b", "r_k", "out"):
+        setattr(e, n, fake)
+    e.tokens, e.in_stride, e.out_stride, e.eps, e.H, e.head_size = 3, 128, 128, 6.4e-4, 2, 64
+    for field, value, code in [("eps", 0.0, _lib.WKV7_ERR_ARG), ("H", 0, _lib.WKV7_ERR_SHAPE),
+                               ("r_k", None, _lib.WKV7_ERR_NULL), ("g", fake + 2, _lib.WKV7_ERR_ALIGN),
+                               ("in_stride", 132, _lib.WKV7_ERR_ALIGN)]:
+        q = _lib.EpilogueArgs.from_buffer_copy(e)
+        setattr(q, field, value)
+        assert lib.wkv7_timemix_epilogue(ctypes.byref(q), None) == code, field
+    assert ctypes.sizeof(_lib.PrologueArgs) == 16 * 8 + 3 * 8 + 2 * 4
+    assert ctypes.sizeof(_lib.EpilogueArgs) == 9 * 8 + 3 * 8 + 3 * 4 + 4  # trailing padding to 8 bytes
