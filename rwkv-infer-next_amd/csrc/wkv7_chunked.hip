@@ -45,18 +45,23 @@ typedef __bf16 bf4 __attribute__((ext_vector_type(4)));
 constexpr int C = kChunk;        // 64
 constexpr int PB = 72;           // LDS row pitch in bf16 (144 B: 16 rows of a ds_read_b128 hit distinct banks)
 constexpr int PF = 72;           // LDS row pitch in fp32 for the fp32 matrices (same bytes as a hi/lo pair)
-constexpr int PG = 68;           // LDS row pitch of the cumulative log-decay g (fp32): the 128-bit row-segment reads
-                                 // and writes of steps 1 and 3 (two rows per 16 lanes) hit distinct banks
 constexpr int SLOT = 64 * PB;    // bf16 elements of one 64 x 64 LDS matrix (9216 B)
 constexpr int NSLOT = 17;
 
-// Workspace record of one (chunk, head), byte offsets.
-constexpr int REC_AH = 0;                  // A hi, bf16 [k1][k2]
-constexpr int REC_AL = REC_AH + 2 * HS2;   // A lo
-constexpr int REC_HT = REC_AL + 2 * HS2;   // H^T fp32 [v][k]
-constexpr int REC_Q = REC_HT + 4 * HS2;    // Q bf16 [t][k]
-constexpr int REC_OT = REC_Q + 2 * HS2;    // O_intra bf16 [t][v]
+// Workspace record of one (chunk, head), byte offsets.  Every part is stored in the fragment order of the scan's
+// 16x16x16 MFMAs, so that each scan lane reads its operands as contiguous 16-byte pieces: a 16 x 16 tile is 64 lanes
+// x 4 values (lane (i, q) holds row i, columns 4 q .. 4 q + 3), and two tiles adjacent along the contraction share
+// one 16-byte piece per lane.
+constexpr int REC_AH = 0;                  // A hi, bf16: [k1 tile r][k2 tile pair][lane][8]
+constexpr int REC_AL = REC_AH + 2 * HS2;   // A lo, same
+constexpr int REC_HT = REC_AL + 2 * HS2;   // H^T fp32: [v tile vg][k tile r][lane][4]  (H[16 r + 4 q + e][16 vg + i])
+constexpr int REC_Q = REC_HT + 4 * HS2;    // Q bf16: [token tile t][k tile pair][lane][8]
+constexpr int REC_OT = REC_Q + 2 * HS2;    // O_intra bf16: [v tile vg][token tile pair][lane][8]
 static_assert(REC_OT + 2 * HS2 == kChunkBytes, "workspace record size");
+
+// Byte offset of tile (row tile a, contraction tile b) of a 64 x 64 bf16 record part, for this lane: tiles b = 2 c and
+// 2 c + 1 share a 16-byte piece per lane.
+__device__ __forceinline__ int frag_off_bf16(int a, int b, int lane) { return ((a * 2 + (b >> 1)) * 64 + lane) * 16 + (b & 1) * 8; }
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
@@ -169,17 +174,53 @@ __device__ __forceinline__ f4 mask_tile(f4 acc, int x0, int y0, int mode) {
     return acc;
 }
 
-// Chunk -> (row, chunk index) of the rows this launch owns.  Returns false if the workgroup has no chunk.
-__device__ __forceinline__ bool chunk_of(const Params& p, const int32_t* plan, int64_t max_chunks, int ncps,
-                                         int64_t j, int& n, int& c) {
+// Position of a prep work item: item = j * H + h (chunk slot j, head h) and, for dense calls, j = n * ncps + c (row
+// n, chunk c).  Divided out once per workgroup, then advanced by the grid stride with adds and a rare carry: the
+// CU's waves share one scalar unit, and a 64-bit division per item per wave cost more than a thousand cycles.
+struct ItemPos {
+    int64_t item, j;
+    int h, n, c;
+};
+
+__device__ __forceinline__ ItemPos item_pos(const Params& p, int ncps, int64_t item) {
+    ItemPos q;
+    q.item = item;
+    q.j = item / p.H;
+    q.h = (int)(item % p.H);
+    q.n = (int)(q.j / ncps);
+    q.c = (int)(q.j % ncps);
+    return q;
+}
+
+// q += stride, where stride = sj * H + sh (0 <= sh < H)
+__device__ __forceinline__ void advance(ItemPos& q, const Params& p, int ncps, int64_t stride, int64_t sj, int sh) {
+    q.item += stride;
+    int64_t dj = sj;
+    q.h += sh;
+    if (q.h >= p.H) {
+        q.h -= p.H;
+        ++dj;
+    }
+    q.j += dj;
+    int64_t c = q.c + dj;
+    if (c >= ncps) {
+        q.n += (int)(c / ncps);
+        c %= ncps;
+    }
+    q.c = (int)c;
+}
+
+// Chunk slot -> (row, chunk index) of the rows this launch owns.  Returns false if the slot has no chunk.
+__device__ __forceinline__ bool chunk_of(const Params& p, const int32_t* plan, int64_t max_chunks, const ItemPos& q,
+                                         int& n, int& c) {
     if (p.cu) {
         const int32_t total = plan[2 * max_chunks + p.num_seqs + 1];
-        if (j >= total) return false;
-        n = plan[j];
-        c = plan[max_chunks + j];
+        if (q.j >= total) return false;
+        n = plan[q.j];
+        c = plan[max_chunks + q.j];
     } else {
-        n = (int)(j / ncps);
-        c = (int)(j % ncps);
+        n = q.n;
+        c = q.c;
     }
     return true;
 }
@@ -212,6 +253,38 @@ __device__ __forceinline__ bf8 diag_operand(int y, int kb, __bf16 s) {
     return d;
 }
 
+// Inclusive scan over the 8 tokens of a wave for one channel, tokens in lanes 8 t + channel group: each 16-lane row
+// holds two tokens (DPP row_ror:8 swaps its halves), v_permlane16_swap pairs rows and v_permlane32_swap pairs the
+// wave's halves.  Returns g(t) and sets prev to g(t - 1) (0 for the first token); both are built from the same
+// partial sums, so g(t - 1) here and g(t - 1) returned to that token's lanes are the same float.
+// Cross-lane reads need every source lane active, so each is evaluated in all lanes before any select, and the empty
+// asm keeps the compiler from sinking it into the branch of a later select.
+__device__ __forceinline__ float dpp_ror8(float x) {
+    float r = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+    asm volatile("" : "+v"(r));
+    return r;
+}
+__device__ __forceinline__ float wave_scan8(float v, int lane, float& prev) {
+    const bool upper = (lane & 8) != 0;
+    const int rowi = lane >> 4;
+    const float vo = dpp_ror8(v);
+    const float y = upper ? vo + v : v;                  // inclusive within the row
+    const float yr = dpp_ror8(y);
+    const float t = upper ? y : yr;                      // the row's total, in both halves
+    const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+    float te = __uint_as_float(pr[0]), to = __uint_as_float(pr[1]);  // totals of the pair's even / odd row
+    asm volatile("" : "+v"(te), "+v"(to));
+    const float u = te + to;                                                // the pair's total
+    const auto hv = __builtin_amdgcn_permlane32_swap(__float_as_uint(u), __float_as_uint(u), false, false);
+    float p0 = __uint_as_float(hv[0]);                                      // rows 0-1 total
+    asm volatile("" : "+v"(p0));
+    const float before = (rowi & 1 ? te : 0.f) + (rowi >= 2 ? p0 : 0.f);  // tokens of the earlier rows
+    const float g = y + before;
+    const float gr = dpp_ror8(g);
+    prev = upper ? gr : before;
+    return g;
+}
+
 struct PrepSmem {
     __bf16 slot[NSLOT][SLOT];
     float m[HS], em[HS], eglm[HS], gam[HS];  // m, em, eglm, gam: base-2 midpoint and decay factors per channel
@@ -231,14 +304,14 @@ struct Item {
     int64_t rec;      // workspace record: (j, h), or the trash record after the last one for items without a chunk
 };
 
-__device__ __forceinline__ Item describe_item(const Params& p, const int32_t* plan, int64_t max_chunks, int ncps,
-                                             int64_t item) {
+__device__ __forceinline__ Item describe_item(const Params& p, const int32_t* plan, int64_t max_chunks,
+                                             const ItemPos& q) {
     Item it{};
-    it.j = item / p.H;
-    it.h = (int)(item % p.H);
+    it.j = q.j;
+    it.h = q.h;
     it.rec = max_chunks * p.H;  // trash
     int n, c;
-    if (!chunk_of(p, plan, max_chunks, ncps, it.j, n, c)) return it;
+    if (!chunk_of(p, plan, max_chunks, q, n, c)) return it;
     int64_t bos;
     int L;
     seq_extent(p, n, bos, L);
@@ -269,7 +342,7 @@ __device__ __forceinline__ RawIn load_item(const Params& p, const Item& it, int 
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Slots (each 64 x 72 bf16 = 9 KB; an fp32 64 x 72 matrix takes two):
-//   0-1   log2 d -> g (fp32) -> alpha (fp32, diagonal blocks replaced by their inverses T_ii) -> W hi/lo
+//   0-1   alpha (fp32, diagonal blocks replaced by their inverses T_ii) -> W hi/lo
 //   2-3   Aq hi/lo -> A0^T hi/lo -> F hi/lo
 //   4-5   Bk hi/lo -> Bh^T hi/lo
 //   6-7   Kk hi/lo -> Kh^T hi/lo
@@ -282,7 +355,6 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lq = lane >> 4;
     float* const F32 = reinterpret_cast<float*>(sm.slot[0]);   // slots 0-1 as fp32 [64][PF]
-    float* const G32 = F32;                                     // steps 1-3: g as fp32 [64][PG] in slots 0-1
     float* const SCR = reinterpret_cast<float*>(sm.slot[15]);  // slots 15-16 as fp32 scratch (4608 floats)
     const BM Aq{sm.slot[2], sm.slot[3]};
     const BM Bk{sm.slot[4], sm.slot[5]};
@@ -302,10 +374,15 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const bool valid = row < it.Lc;
     f4 rl[12];  // step 5 -> step 6: relayout tiles of waves 4-7
 
-    // ---- 1. log2-decay -> G32; V (row-major, exact) -> Vr.  log2 d = -e^w log2(e) = -2^{w log2(e)} log2(e).
+    // ---- 1. log2-decay lam = log2 d = -e^w log2(e) = -2^{w log2(e)} log2(e) of this thread's row and 8 channels,
+    //         and its inclusive cumulative sum over the rows: first within the wave (rows 8 wv .. 8 wv + 7 live in
+    //         lanes 8 r + channel group, so a scan over lanes with stride 8), then across waves through the wave
+    //         totals.  Every g below is (in-wave scan) + (sum of the earlier waves' totals, in wave order), so the
+    //         previous row's g, the midpoint (row 31) and the chunk total (row 63) are the same floats wherever
+    //         they are formed.  V (row-major, exact) -> Vr.
+    float lam[8], gin[8], gprev[8];
     {
         const uint32_t ww[4] = {raw.w.x, raw.w.y, raw.w.z, raw.w.w};
-        float lam[8];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
             float lo, hi;
@@ -313,38 +390,48 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             lam[2 * e] = valid ? -__builtin_amdgcn_exp2f(lo * kLog2e) * kLog2e : 0.f;
             lam[2 * e + 1] = valid ? -__builtin_amdgcn_exp2f(hi * kLog2e) * kLog2e : 0.f;
         }
-        *reinterpret_cast<f4*>(G32 + row * PG + cb) = f4{lam[0], lam[1], lam[2], lam[3]};
-        *reinterpret_cast<f4*>(G32 + row * PG + cb + 4) = f4{lam[4], lam[5], lam[6], lam[7]};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) gin[e] = wave_scan8(lam[e], lane, gprev[e]);
+        if (lane >= 56) {  // the wave's last row: its totals per channel
+            *reinterpret_cast<f4*>(&sm.bsum[wv][cb]) = f4{gin[0], gin[1], gin[2], gin[3]};
+            *reinterpret_cast<f4*>(&sm.bsum[wv][cb + 4]) = f4{gin[4], gin[5], gin[6], gin[7]};
+        }
         *reinterpret_cast<uint4*>(Vr.h + row * PB + cb) = valid ? raw.v : make_uint4(0u, 0u, 0u, 0u);
     }
     __syncthreads();
 
-    // ---- 2. g = inclusive cumulative log2-decay per channel (wave wv: rows 8 wv .. 8 wv + 7; lane = channel)
+    // ---- 2. g (inclusive) and g of the previous row; midpoint m = g_31 and chunk total g_63 per channel
+    float gi[8], ge[8], mk[8];
     {
-        float run = 0.f;
+        float off[8], g63[8];
 #pragma unroll
-        for (int r = 0; r < 8; ++r) {
-            float* e = G32 + (8 * wv + r) * PG + lane;
-            run += *e;
-            *e = run;
-        }
-        sm.bsum[wv][lane] = run;
-        __syncthreads();
-        if (wv > 0) {
-            float offs = 0.f;
-            for (int w2 = 0; w2 < wv; ++w2) offs += sm.bsum[w2][lane];
+        for (int e = 0; e < 8; ++e) off[e] = g63[e] = 0.f;
 #pragma unroll
-            for (int r = 0; r < 8; ++r) G32[(8 * wv + r) * PG + lane] += offs;
+        for (int w2 = 0; w2 < 8; ++w2) {
+            const f4 t0 = *reinterpret_cast<const f4*>(&sm.bsum[w2][cb]);
+            const f4 t1 = *reinterpret_cast<const f4*>(&sm.bsum[w2][cb + 4]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float t = e < 4 ? t0[e] : t1[e - 4];
+                if (w2 < wv) off[e] += t;
+                if (w2 == 4) mk[e] = g63[e];
+                g63[e] += t;
+            }
         }
-        __syncthreads();
-        if (tid < HS) {
-            const float m = G32[31 * PG + tid], gl = G32[63 * PG + tid];
-            sm.m[tid] = m;
-            sm.em[tid] = __builtin_amdgcn_exp2f(m);
-            sm.eglm[tid] = __builtin_amdgcn_exp2f(gl - m);
-            sm.gam[tid] = __builtin_amdgcn_exp2f(gl);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            gi[e] = gin[e] + off[e];
+            ge[e] = gprev[e] + off[e];
         }
-        __syncthreads();
+        if (tid < 8) {  // row 0's threads cover the 64 channels once
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                sm.m[cb + e] = mk[e];
+                sm.em[cb + e] = __builtin_amdgcn_exp2f(mk[e]);
+                sm.eglm[cb + e] = __builtin_amdgcn_exp2f(g63[e] - mk[e]);
+                sm.gam[cb + e] = __builtin_amdgcn_exp2f(g63[e]);
+            }
+        }
     }
 
     // ---- 3. Gram operands referenced to the chunk midpoint: Aq = a 2^{g_{t-1}-m}, Rq = r 2^{g_t-m},
@@ -352,13 +439,6 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     {
         const uint32_t aw[4] = {raw.a.x, raw.a.y, raw.a.z, raw.a.w}, bw[4] = {raw.b.x, raw.b.y, raw.b.z, raw.b.w};
         const uint32_t kw[4] = {raw.k.x, raw.k.y, raw.k.z, raw.k.w}, rw[4] = {raw.r.x, raw.r.y, raw.r.z, raw.r.w};
-        // g of this row and the previous one, and the midpoints, as 128-bit reads (row 0 reads itself and zeroes)
-        const int prow = row > 0 ? row - 1 : 0;
-        const f4 gi4[2] = {*reinterpret_cast<const f4*>(G32 + row * PG + cb),
-                           *reinterpret_cast<const f4*>(G32 + row * PG + cb + 4)};
-        const f4 ge4[2] = {*reinterpret_cast<const f4*>(G32 + prow * PG + cb),
-                           *reinterpret_cast<const f4*>(G32 + prow * PG + cb + 4)};
-        const f4 m4[2] = {*reinterpret_cast<const f4*>(sm.m + cb), *reinterpret_cast<const f4*>(sm.m + cb + 4)};
         bf8 aqh, aql, bkh, bkl, kkh, kkl, rqh;
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
@@ -370,11 +450,8 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int e = 2 * e2 + u;
-                const float gi = gi4[e >> 2][e & 3];
-                const float ge = row > 0 ? ge4[e >> 2][e & 3] : 0.f;
-                const float mk = m4[e >> 2][e & 3];
-                const float fa = __builtin_amdgcn_exp2f(ge - mk), fr = __builtin_amdgcn_exp2f(gi - mk);
-                const float fb = __builtin_amdgcn_exp2f(mk - gi);
+                const float fa = __builtin_amdgcn_exp2f(ge[e] - mk[e]), fr = __builtin_amdgcn_exp2f(gi[e] - mk[e]);
+                const float fb = __builtin_amdgcn_exp2f(mk[e] - gi[e]);
                 const float aq = valid ? a2[u] * fa : 0.f, rq = valid ? r2[u] * fr : 0.f;
                 const float bk = valid ? b2[u] * fb : 0.f, kq = valid ? k2[u] * fb : 0.f;
                 __bf16 h, l;
@@ -550,9 +627,6 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     //          A = Gamma + Bh^T W (x = k2, y = k1; 3 terms -> workspace hi/lo [k1][k2])
     //          F = Kh^T + Bh^T G (x = s', y = k; 3 terms -> slots 2-3 as F[k][s'])
     {
-        __bf16* const gQ = reinterpret_cast<__bf16*>(rec + REC_Q);
-        __bf16* const gAh = reinterpret_cast<__bf16*>(rec + REC_AH);
-        __bf16* const gAl = reinterpret_cast<__bf16*>(rec + REC_AL);
         // full contractions again: rho and G are exactly zero where the causal ranges end
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -564,7 +638,10 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
 #pragma unroll
                 for (int v = 0; v < 4; ++v) acc[v] = (float)r4[v] * sm.em[x0 + 4 * lq + v];
                 acc = mma<1>(acc, Wm, x0, Rho, y0, 0, 2);
-                st_hi(gQ, HS, x0, y0, acc);
+                bf4 hv;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) hv[v] = (__bf16)acc[v];
+                *reinterpret_cast<bf4*>(rec + REC_Q + frag_off_bf16(by, bx, lane)) = hv;  // Q[t][k]: t tile by
             } else if (prod == 1) {
                 const bf4 s4 = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
 #pragma unroll
@@ -583,8 +660,8 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
                     hv[v] = hh;
                     lv[v] = ll;
                 }
-                *reinterpret_cast<bf4*>(gAh + (y0 + li) * HS + x0 + 4 * lq) = hv;
-                *reinterpret_cast<bf4*>(gAl + (y0 + li) * HS + x0 + 4 * lq) = lv;
+                *reinterpret_cast<bf4*>(rec + REC_AH + frag_off_bf16(by, bx, lane)) = hv;  // A[k1][k2]: k1 tile by
+                *reinterpret_cast<bf4*>(rec + REC_AL + frag_off_bf16(by, bx, lane)) = lv;
             } else {
                 const bf4 kh4 = *reinterpret_cast<const bf4*>(Kht.h + (y0 + li) * PB + x0 + 4 * lq);
                 const bf4 kl4 = *reinterpret_cast<const bf4*>(Kht.l + (y0 + li) * PB + x0 + 4 * lq);
@@ -597,19 +674,22 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     }
     __syncthreads();
 
-    // ---- 9. H = F V (x = k, y = v; X split, V exact -> workspace fp32 [v][k]);
-    //          O_intra = E V (x = v, y = t -> workspace bf16 [t][v])
+    // ---- 9. H = F V (x = k, y = v; X split, V exact -> workspace fp32, H^T tiles);
+    //          O_intra = E V (x = v, y = t -> workspace bf16, tiles of O_intra[t][v])
     {
-        float* const gH = reinterpret_cast<float*>(rec + REC_HT);
-        __bf16* const gO = reinterpret_cast<__bf16*>(rec + REC_OT);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
             const int x0 = 16 * bx, y0 = 16 * by;
             if (prod == 0) {
-                st_f32(gH, HS, x0, y0, mma<2>(zero4(), Fm, x0, Vt, y0, 0, 2));
+                *reinterpret_cast<f4*>(rec + REC_HT + ((by * 4 + bx) * 64 + lane) * 16) =
+                    mma<2>(zero4(), Fm, x0, Vt, y0, 0, 2);  // H^T[v][k]: v tile by, k tile bx
             } else {
-                st_hi(gO, HS, x0, y0, mma<1>(zero4(), Vt, x0, Em, y0, 0, 2));  // E is zero for s' > t
+                const f4 acc = mma<1>(zero4(), Vt, x0, Em, y0, 0, 2);  // E is zero for s' > t
+                bf4 hv;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) hv[v] = (__bf16)acc[v];
+                *reinterpret_cast<bf4*>(rec + REC_OT + frag_off_bf16(bx, by, lane)) = hv;  // O[t][v]: v tile bx
             }
         }
     }
@@ -632,87 +712,80 @@ __global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, ch
         const int64_t used = plan[2 * max_chunks + p.num_seqs + 1];
         nitems = std::max<int64_t>(0, std::min<int64_t>(used, max_chunks)) * p.H;
     }
-    int64_t item = blockIdx.x;
-    if (item >= nitems) return;
-    Item cur = describe_item(p, plan, max_chunks, ncps, item);
+    if ((int64_t)blockIdx.x >= nitems) return;
+    const int64_t stride = gridDim.x, sj = stride / p.H;
+    const int sh = (int)(stride % p.H);
+    ItemPos pos = item_pos(p, ncps, blockIdx.x);
+    Item cur = describe_item(p, plan, max_chunks, pos);
     RawIn rc = load_item(p, cur, row, cb);
     settle(rc);
-    for (; item < nitems; item += gridDim.x) {
-        const int64_t nx = item + gridDim.x;
+    while (pos.item < nitems) {
+        ItemPos np = pos;
+        advance(np, p, ncps, stride, sj, sh);
         Item nxt{};
         nxt.rec = max_chunks * p.H;
-        if (nx < nitems) nxt = describe_item(p, plan, max_chunks, ncps, nx);
+        if (np.item < nitems) nxt = describe_item(p, plan, max_chunks, np);
         const RawIn rn = load_item(p, nxt, row, cb);  // in flight while `cur` is processed
         // every item runs the same instruction stream (an item without a chunk computes on zeros and writes the
         // trash record), so the number of vector memory operations between a prefetch and its use is fixed
         prep_item(p, cur, rc, wsc, sm);
         cur = nxt;
         rc = rn;
+        pos = np;
     }
 }
 
-// One chunk record's share of one scan lane: A hi/lo and Q rows (MFMA operands, shared by the workgroup's column
-// tiles), and per column tile the H^T and O_intra entries.
-template <int NT>
+// One chunk record's share of one scan lane (wavefront of column group vg): all of A (hi/lo) and Q, and the group's
+// columns of H^T and O_intra, in MFMA fragment order (16-byte pieces: two k tiles of A and Q per piece, two token
+// tiles of O per piece).
+typedef short s8 __attribute__((ext_vector_type(8)));
 struct ScanRec {
-    bf8 ah[2], al[2], q[2];
-    f4 hS[NT];
-    uint2 hO[NT];  // 4 bf16 each
+    s8 ah[4][2], al[4][2];  // [row tile r][k tile pair]
+    s8 q[4][2];             // [token tile t][k tile pair]
+    f4 h[4];                // [k tile r]: H[16 r + 4 q + e][16 vg + i]
+    s8 o[2];                // [token tile pair]: O_intra[16 t + i][16 vg + 4 q + e]
 };
 
-// Per-lane byte offsets inside a record (the same for every chunk).
-template <int NT>
-struct ScanOffs {
-    uint32_t a;      // A / Q row segment
-    uint32_t s[NT];  // H^T entry per column tile
-    uint32_t o[NT];  // O_intra entry per column tile
-};
-
-// `rec` is wave-uniform, so the loads address it as a scalar base plus the lane's 32-bit offset (no per-lane
-// 64-bit address registers to carry from one chunk to the next).
-template <int NT>
-__device__ __forceinline__ void scan_load(ScanRec<NT>& r, const char* rec, const ScanOffs<NT>& off) {
-    const char* const b = uniform_ptr(rec);
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        r.ah[kb] = *reinterpret_cast<const bf8*>(b + REC_AH + off.a + 64 * kb);
-        r.al[kb] = *reinterpret_cast<const bf8*>(b + REC_AL + off.a + 64 * kb);
-        r.q[kb] = *reinterpret_cast<const bf8*>(b + REC_Q + off.a + 64 * kb);
-    }
-#pragma unroll
-    for (int c = 0; c < NT; ++c) {
-        r.hS[c] = *reinterpret_cast<const f4*>(b + REC_HT + off.s[c]);
-        r.hO[c] = *reinterpret_cast<const uint2*>(b + REC_OT + off.o[c]);
-    }
+__device__ __forceinline__ s4 half4(s8 x, int hi) {
+    return hi ? __builtin_shufflevector(x, x, 4, 5, 6, 7) : __builtin_shufflevector(x, x, 0, 1, 2, 3);
 }
 
-constexpr int kScanDepth = 4;  // chunk records in flight per lane (register ring)
-// 16-column tiles per scan workgroup (the kernel supports 1, 2 or 4).  One is fastest on MI355X at T = 4096,
-// H = 64 (scan 76 us vs 100 us with 2 and 155 us with 4): the scan is bound by each workgroup's serial per-chunk
-// chain, so more, smaller workgroups win even though the 4 column groups of a head each read the chunk's A and Q.
-constexpr int kScanTiles = 1;
+// `rec` is wave-uniform: the loads address it as a scalar base plus the lane's 32-bit offset.
+__device__ __forceinline__ void scan_load(ScanRec& r, const char* rec, int vg, int lane) {
+    const char* const b = uniform_ptr(rec);
+    const int lo = lane * 16;
+#pragma unroll
+    for (int x = 0; x < 4; ++x) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            r.ah[x][c] = *reinterpret_cast<const s8*>(b + REC_AH + (x * 2 + c) * 1024 + lo);
+            r.al[x][c] = *reinterpret_cast<const s8*>(b + REC_AL + (x * 2 + c) * 1024 + lo);
+            r.q[x][c] = *reinterpret_cast<const s8*>(b + REC_Q + (x * 2 + c) * 1024 + lo);
+        }
+        r.h[x] = *reinterpret_cast<const f4*>(b + REC_HT + (vg * 4 + x) * 1024 + lo);
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) r.o[c] = *reinterpret_cast<const s8*>(b + REC_OT + (vg * 2 + c) * 1024 + lo);
+}
 
-// One workgroup per (row, head, group of NT 16-column blocks); 4 / NT groups per (row, head).  Block b -> XCD
-// b % 8, and the groups of a (row, head) pair share an XCD.  Wave w owns state rows (and output tokens)
-// 16 w .. 16 w + 15 of all the group's columns.  S is carried exactly in fp32 accumulators and mirrored in LDS as a
-// hi/lo bf16 split S^T[v][k] that feeds the next chunk's MFMAs; the output tiles are computed transposed
-// (O^T = S^T Q^T), so each lane holds 4 consecutive columns of one token per tile and writes them with one 8-byte
-// store.  A workgroup owning more columns reads the chunk's A and Q rows once for all of them.
-//
-// Chunk records stream through a ring of kScanDepth register sets: after a chunk is consumed its set is refilled
-// with the record kScanDepth chunks ahead.  Every step issues the same memory operations -- the refill index is
-// clamped to the last chunk, steps past the end compute without effect, and stores that must not land (tokens
-// past the row's end, no output requested) go to the workspace's trash record -- so the compiler can count the
-// outstanding loads exactly and waits only for the record about to be used.
-template <int NT>
-__global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
-                                                              const int32_t* __restrict__ plan, int64_t max_chunks,
-                                                              int ncps) {
-    constexpr int NG = 4 / NT;  // column groups per (row, head)
-    __shared__ __attribute__((aligned(16))) __bf16 sth[NT * 16 * PB], stl[NT * 16 * PB];
+constexpr int kScanDepth = 2;  // chunk records in flight per lane (register ring)
+
+// One wavefront per (row, head, 16-column group vg); block b -> XCD b % 8, and the 4 groups of a (row, head) share an
+// XCD, so 3 of the 4 reads of a chunk's A and Q hit that XCD's L2.  The lane (i, q) holds S[16 r + 4 q + e][16 vg + i]
+// for the four k tiles r: exactly the B operand of the 16x16x16 MFMA for contraction tile r and the layout of its
+// result, so the state stays in registers from chunk to chunk (fp32, plus a hi/lo bf16 split as the next operand),
+// with no LDS and no barrier:
+//     S <- A S + H   (48 MFMAs: 4 x 4 tiles, 3 terms on the hi/lo split)
+//     y^T = S^T Q^T + O_intra^T   (16 MFMAs on S hi; S^T tile r is S tile r's registers read as the A operand)
+// Chunk records stream through a ring of kScanDepth register sets.  Every step issues the same memory operations
+// (the refill index is clamped to the last chunk; stores that must not land go to the workspace's trash record), so
+// the compiler counts the outstanding loads exactly and waits only for the record about to be used.
+__global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
+                                                             const int32_t* __restrict__ plan, int64_t max_chunks,
+                                                             int ncps) {
     const int b = blockIdx.x;
-    const int xcd = b & 7, rsl = b >> 3, vg = rsl % NG;
-    const int64_t pair = (int64_t)(rsl / NG) * 8 + xcd;
+    const int xcd = b & 7, rsl = b >> 3, vg = rsl & 3;
+    const int64_t pair = (int64_t)(rsl >> 2) * 8 + xcd;
     if (pair >= (int64_t)p.num_seqs * p.H) return;
     const int n = (int)(pair / p.H), h = (int)(pair % p.H);
     int64_t bos;
@@ -720,137 +793,102 @@ __global__ __launch_bounds__(256) void wkv7_chunk_scan_kernel(const Params p, ch
     seq_extent(p, n, bos, L);
     if (!owns_row(p, L)) return;
 
-    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int i = lane & 15, q = lane >> 4;
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
     const int64_t j0 = p.cu ? (int64_t)plan[2 * max_chunks + n] : (int64_t)n * ncps;
     // the chunk table never exceeds max_chunks for valid cu_seqlens; the clamp keeps invalid ones in bounds
     const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((L + C - 1) / C, max_chunks - j0));
     const float* src = state_src(p, n, h);
     float* dst = state_dst(p, n, h);
-    const int vcol0 = 16 * NT * vg;  // first state column of this workgroup
+    const int col = 16 * vg + i;  // the state column this lane holds
 
-    // initial state: thread (krow, c4) holds S0[krow][vcol0 + 16 c + c4 .. + 3] for each tile c
-    {
-        const int krow = tid >> 2, c4 = (tid & 3) * 4;
-        f4 x[NT];
+    f4 S[4];
 #pragma unroll
-        for (int c = 0; c < NT; ++c)
-            x[c] = src ? *reinterpret_cast<const f4*>(src + krow * HS + vcol0 + 16 * c + c4) : zero4();
-        if (nch == 0) {  // no chunks (length 0): the state passes through
-            if (dst) {
+    for (int r = 0; r < 4; ++r) {
 #pragma unroll
-                for (int c = 0; c < NT; ++c) *reinterpret_cast<f4*>(dst + krow * HS + vcol0 + 16 * c + c4) = x[c];
-            }
-            return;
-        }
-#pragma unroll
-        for (int c = 0; c < NT; ++c) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                __bf16 hh, ll;
-                split(x[c][e], hh, ll);
-                sth[(16 * c + c4 + e) * PB + krow] = hh;
-                stl[(16 * c + c4 + e) * PB + krow] = ll;
-            }
-        }
+        for (int e = 0; e < 4; ++e) S[r][e] = src ? src[(16 * r + 4 * q + e) * HS + col] : 0.f;
     }
-    __syncthreads();
+    if (nch == 0) {  // no chunks (length 0): the state passes through
+        if (dst) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dst[(16 * r + 4 * q + e) * HS + col] = S[r][e];
+            }
+        }
+        return;
+    }
+    s4 Sh[4], Sl[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) split4(S[r], Sh[r], Sl[r]);
 
-    const int xr = 16 * wv + i;          // operand row of A / Q this lane feeds; also its output token in a chunk
-    const int orow = 16 * wv + 4 * q;    // first state row this lane holds
     const char* const rec0 = wsc + (j0 * p.H + h) * (int64_t)kChunkBytes;
     const int64_t rec_stride = (int64_t)p.H * kChunkBytes;
-    // stores that must not land go to the trash record, 2 KB per workgroup slot (24 slots) so that workgroups do not
-    // all hit the same lines
-    uint2* const trash =
-        reinterpret_cast<uint2*>(wsc + max_chunks * p.H * (int64_t)kChunkBytes) + (b % 24) * 256 + tid;
-    ScanOffs<NT> offs;
-    offs.a = (uint32_t)(xr * HS + 8 * q) * 2u;
+    // stores that must not land go to the trash record, 2 KB per block slot (24 slots) so that blocks do not all hit
+    // the same lines
+    char* const trash = wsc + max_chunks * p.H * (int64_t)kChunkBytes + (b % 24) * 2048 + lane * 8;
+    uint16_t* const obase = p.o ? p.o + bos * p.o_tok_stride + (int64_t)h * HS + 16 * vg + 4 * q : nullptr;
+
+    ScanRec ring[kScanDepth];
 #pragma unroll
-    for (int c = 0; c < NT; ++c) {
-        offs.s[c] = (uint32_t)((vcol0 + 16 * c + i) * HS + orow) * 4u;
-        offs.o[c] = (uint32_t)(xr * HS + vcol0 + 16 * c + 4 * q) * 2u;
-    }
-    ScanRec<NT> ring[kScanDepth];
-#pragma unroll
-    for (int d = 0; d < kScanDepth; ++d) scan_load(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, offs);
+    for (int d = 0; d < kScanDepth; ++d) scan_load(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, vg, lane);
 #pragma unroll
     for (int d = 0; d < kScanDepth; ++d) settle(ring[d]);
-    f4 accS[NT];
-#pragma unroll
-    for (int c = 0; c < NT; ++c) accS[c] = zero4();
     for (int c0 = 0; c0 < nch; c0 += kScanDepth) {
 #pragma unroll
         for (int d = 0; d < kScanDepth; ++d) {
             const int cc = c0 + d;
             const bool live = cc < nch;  // wave-uniform
-            ScanRec<NT>& r = ring[d];
-            f4 newS[NT], accO[NT];
+            ScanRec& R = ring[d];
+            f4 nS[4];
 #pragma unroll
-            for (int c = 0; c < NT; ++c) {
-                newS[c] = r.hS[c];
-                float o0, o1, o2, o3;
-                bf16x2_to_f32(r.hO[c].x, o0, o1);
-                bf16x2_to_f32(r.hO[c].y, o2, o3);
-                accO[c] = f4{o0, o1, o2, o3};
-            }
+            for (int r = 0; r < 4; ++r) nS[r] = R.h[r];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
+            for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
-                for (int c = 0; c < NT; ++c) {
-                    const int so = (16 * c + i) * PB + 32 * kb + 8 * q;
-                    const bf8 ysh = ld8(sth + so), ysl = ld8(stl + so);
-                    newS[c] = mfma_bf16(r.ah[kb], ysl, newS[c]);
-                    newS[c] = mfma_bf16(r.al[kb], ysh, newS[c]);
-                    newS[c] = mfma_bf16(r.ah[kb], ysh, newS[c]);
-                    accO[c] = mfma_bf16(ysh, r.q[kb], accO[c]);  // O^T: lane (i, q): token xr, 4 columns
+                for (int r = 0; r < 4; ++r) {
+                    const s4 ah = half4(R.ah[r][kb >> 1], kb & 1), al = half4(R.al[r][kb >> 1], kb & 1);
+                    nS[r] = mfma16(ah, Sl[kb], nS[r]);
+                    nS[r] = mfma16(al, Sh[kb], nS[r]);
+                    nS[r] = mfma16(ah, Sh[kb], nS[r]);
                 }
             }
-            // the refill reuses the slot's registers only if it is not scheduled above the slot's last use;
-            // otherwise the ring rotates through copies that wait for the newest loads
+            f4 y[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const s4 o4 = half4(R.o[t >> 1], t & 1);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) y[t][e] = bf16_to_f32((uint16_t)o4[e]);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) y[t] = mfma16(Sh[r], half4(R.q[t][r >> 1], r & 1), y[t]);
+            }
+            // the refill reuses the slot's registers only if it is not scheduled above the slot's last use
             __builtin_amdgcn_sched_barrier(0);
-            scan_load(r, rec0 + std::min(cc + kScanDepth, nch - 1) * rec_stride, offs);
-            {
-                const int t = cc * C + xr;
-                const bool st = live && t < L && p.o;
+            scan_load(R, rec0 + std::min(cc + kScanDepth, nch - 1) * rec_stride, vg, lane);
 #pragma unroll
-                for (int c = 0; c < NT; ++c) {
-                    uint2 pk;
-                    pk.x = pack_bf16x2(accO[c][0], accO[c][1]);
-                    pk.y = pack_bf16x2(accO[c][2], accO[c][3]);
-                    uint2* const out =
-                        st ? reinterpret_cast<uint2*>(p.o + (bos + t) * p.o_tok_stride + (int64_t)h * HS + vcol0 +
-                                                      16 * c + 4 * q)
-                           : trash;
-                    *out = pk;
-                }
+            for (int t = 0; t < 4; ++t) {
+                // lane (i, q) holds y[token 16 t + i][columns 16 vg + 4 q .. + 3]
+                const int tok = cc * C + 16 * t + i;
+                uint2 pk;
+                pk.x = pack_bf16x2(y[t][0], y[t][1]);
+                pk.y = pack_bf16x2(y[t][2], y[t][3]);
+                char* const out = (live && tok < L && obase)
+                                      ? reinterpret_cast<char*>(obase + (int64_t)tok * p.o_tok_stride)
+                                      : trash + t * 512;
+                *reinterpret_cast<uint2*>(out) = pk;
             }
             if (live) {
 #pragma unroll
-                for (int c = 0; c < NT; ++c) accS[c] = newS[c];
+                for (int r = 0; r < 4; ++r) S[r] = nS[r];
             }
-            __syncthreads();
 #pragma unroll
-            for (int c = 0; c < NT; ++c) {
-                bf4 sh, sl;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    __bf16 hh, ll;
-                    split(accS[c][v], hh, ll);
-                    sh[v] = hh;
-                    sl[v] = ll;
-                }
-                *reinterpret_cast<bf4*>(sth + (16 * c + i) * PB + orow) = sh;
-                *reinterpret_cast<bf4*>(stl + (16 * c + i) * PB + orow) = sl;
-            }
-            __syncthreads();
+            for (int r = 0; r < 4; ++r) split4(S[r], Sh[r], Sl[r]);
         }
     }
     if (dst) {
 #pragma unroll
-        for (int c = 0; c < NT; ++c) {
+        for (int r = 0; r < 4; ++r) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) dst[(orow + v) * HS + vcol0 + 16 * c + i] = accS[c][v];
+            for (int e = 0; e < 4; ++e) dst[(16 * r + 4 * q + e) * HS + col] = S[r][e];
         }
     }
 }
@@ -942,8 +980,8 @@ hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* works
                            ws.max_chunks, ncps);
     }
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
-    const int64_t blocks = ((pairs + 7) / 8) * 8 * (4 / kScanTiles);
-    hipLaunchKernelGGL(wkv7_chunk_scan_kernel<kScanTiles>, dim3((unsigned)blocks), dim3(256), 0, stream, p, wsc, plan,
+    const int64_t blocks = ((pairs + 7) / 8) * 8 * 4;
+    hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, p, wsc, plan,
                        ws.max_chunks, ncps);
     return hipGetLastError();
 }
