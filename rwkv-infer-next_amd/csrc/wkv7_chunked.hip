@@ -134,6 +134,47 @@ __device__ __forceinline__ void split4(f4 x, s4& h, s4& l) {
     }
 }
 
+// LDS transposing read (ds_read_b64_tr_b16).  Within each 16-lane group, lane s reads 4 consecutive 16-bit values at
+// its own address; lane L then receives value (L & 3) of the reads of lanes (L & 15) / 4 + 4 e, e = 0..3.  With lane
+// L of group q addressing M[k0 + 4 q + ((L & 15) >> 2)][n0 + 4 (L & 3)] of a row-major matrix, lane L receives
+// M[k0 + 4 q + e][n0 + (L & 15)]: an MFMA operand whose contraction runs down the rows of M.
+typedef __attribute__((address_space(3))) s4 lds_s4;
+__device__ __forceinline__ s4 ld_tr4(const __bf16* p) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p));
+}
+
+// Operand of the 16x16x32 MFMA for contraction block kb (rows 32 kb .. of M) and column block n0 of a row-major
+// bf16 LDS matrix M[kappa][n]: lane (i, q) gets M[32 kb + 8 q + j][n0 + i], j = 0..7.
+__device__ __forceinline__ bf8 ld8_tr(const __bf16* M, int kb, int n0) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const __bf16* const p = M + (32 * kb + 8 * q + (i >> 2)) * PB + n0 + 4 * (i & 3);
+    const s4 a = ld_tr4(p), b = ld_tr4(p + 4 * PB);
+    return __builtin_bit_cast(bf8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// mma with the Y operand stored contraction-major (Y[y][kappa] = Yt[kappa][y]).
+template <int TERMS>
+__device__ __forceinline__ f4 mma_ty(f4 acc, BM X, int x0, BM Yt, int y0) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const int xo = (x0 + i) * PB + 32 * kb + 8 * q;
+        const bf8 xh = ld8(X.h + xo), yh = ld8_tr(Yt.h, kb, y0);
+        if constexpr (TERMS == 3) acc = mfma_bf16(xh, ld8_tr(Yt.l, kb, y0), acc);
+        if constexpr (TERMS >= 2) acc = mfma_bf16(ld8(X.l + xo), yh, acc);
+        acc = mfma_bf16(xh, yh, acc);
+    }
+    return acc;
+}
+
+// mma with the X operand stored contraction-major (X[x][kappa] = Xt[kappa][x]), one term.
+__device__ __forceinline__ f4 mma_tx1(f4 acc, BM Xt, int x0, BM Y, int y0) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) acc = mfma_bf16(ld8_tr(Xt.h, kb, x0), ld8(Y.h + (y0 + i) * PB + 32 * kb + 8 * q), acc);
+    return acc;
+}
+
 // Natural stores of a tile (element (x0 + 4q + v, y0 + i) at M[(y0 + i) * pitch + x0 + 4q + v]): 4 consecutive
 // elements per lane.
 __device__ __forceinline__ void st_hi(__bf16* M, int pitch, int x0, int y0, f4 acc) {
@@ -343,36 +384,34 @@ constexpr float kLog2e = 1.4426950408889634f;
 
 // Slots (each 64 x 72 bf16 = 9 KB; an fp32 64 x 72 matrix takes two):
 //   0-1   alpha (fp32, diagonal blocks replaced by their inverses T_ii) -> W hi/lo
-//   2-3   Aq hi/lo -> A0^T hi/lo -> F hi/lo
-//   4-5   Bk hi/lo -> Bh^T hi/lo
-//   6-7   Kk hi/lo -> Kh^T hi/lo
-//   8     Rq hi                     9  V^T (exact bf16)
+//   2-3   Aq hi/lo -> F hi/lo
+//   4-5   Bk hi/lo                  6-7   Kk hi/lo
+//   8     Rq hi
 //   10-11 beta hi/lo -> G hi/lo     12 rho    13 sigma    14 E
-//   15-16 V (row-major) -> fp32 scratch of the diagonal-block inversion
+//   15    V (row-major, exact)
+// The products that contract over tokens (W = T A0, A = Bh^T W, F = Kh^T + Bh^T G, H = F V, O_intra = E V) read Aq,
+// Bk, Kk and V where they lie, through transposing LDS reads, and apply the per-channel decay factors that separate
+// A0, Bh, Kh from Aq, Bk, Kk (2^m, 2^{g_C - m}) to their fp32 results.
 // Decays are handled in base 2 (g = cumulative log2 d), so every decay factor is one v_exp_f32.
 __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const RawIn& raw, char* wsc,
                                           PrepSmem& sm) {
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lq = lane >> 4;
     float* const F32 = reinterpret_cast<float*>(sm.slot[0]);   // slots 0-1 as fp32 [64][PF]
-    float* const SCR = reinterpret_cast<float*>(sm.slot[15]);  // slots 15-16 as fp32 scratch (4608 floats)
     const BM Aq{sm.slot[2], sm.slot[3]};
     const BM Bk{sm.slot[4], sm.slot[5]};
     const BM Kk{sm.slot[6], sm.slot[7]};
     const BM Rq{sm.slot[8], nullptr};
-    const BM Vt{sm.slot[9], nullptr};
     const BM Be{sm.slot[10], sm.slot[11]};
     const BM Rho{sm.slot[12], nullptr};
     const BM Sig{sm.slot[13], nullptr};
     const BM Em{sm.slot[14], nullptr};
     const BM Vr{sm.slot[15], nullptr};
-    const BM A0t = Aq, Bht = Bk, Kht = Kk;          // after step 6
-    const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 7
-    const BM Fm{sm.slot[2], sm.slot[3]};            // step 8 (A0^T is dead after step 7)
+    const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 7: W^T [k][t], G^T [s'][t]
+    const BM Fm{sm.slot[2], sm.slot[3]};            // step 8 (Aq is dead after step 7)
     char* const rec = wsc + it.rec * (int64_t)kChunkBytes;
     const int row = tid >> 3, cb = (tid & 7) * 8;
     const bool valid = row < it.Lc;
-    f4 rl[12];  // step 5 -> step 6: relayout tiles of waves 4-7
 
     // ---- 1. log2-decay lam = log2 d = -e^w log2(e) = -2^{w log2(e)} log2(e) of this thread's row and 8 channels,
     //         and its inclusive cumulative sum over the rows: first within the wave (rows 8 wv .. 8 wv + 7 live in
@@ -478,105 +517,76 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     }
     __syncthreads();
 
-    // ---- 4. Grams (natural store of P(x, y) is [y][x]) and V^T:
+    // ---- 4. Grams (natural store of P(x, y) is [y][x]):
     //   alpha: x = s, y = t  (X = Bk, Y = Aq, 3 terms), keep s < t, fp32 -> F32 as alpha[t][s]
     //   beta : x = s, y = s' (X = Aq, Y = Kk, 3 terms), keep s' < s, hi/lo -> Be as beta[s][s'] at [s'][s]
     //   rho  : x = s, y = t  (X = Bk, Y = Rq),            keep s <= t, -> Rho as rho[t][s]
     //   sigma: x = s', y = t (X = Kk, Y = Rq),            keep s' <= t, -> Sig as sigma[t][s']
-    //   V^T  : x = s, y = v  (X = V, Y = I, exact)        -> Vt as V^T[v][s]
-    // Wave wv computes tiles wv and wv + 8 of every product (prod = u >> 1 is a compile-time constant), each over
-    // the full contraction and masked afterwards: straight-line code whose independent MFMA chains the scheduler
-    // interleaves (fully masked tiles cost MFMAs but no branches).
+    // Wave wv owns tiles (bx, by) = (wv / 4 + 2 u, wv % 4), u = 0, 1 (the two waves on a SIMD cover one column of
+    // tiles).  All four products of a tile are formed together, each operand fragment loaded once; tiles a causal
+    // mask zeroes entirely skip their MFMAs and store zeros (later products contract over the full ranges).
 #pragma unroll
-    for (int u = 0; u < 10; ++u) {
-        const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
+    for (int u = 0; u < 2; ++u) {
+        const int bx = (wv >> 2) + 2 * u, by = wv & 3;
         const int x0 = 16 * bx, y0 = 16 * by;
-        f4 acc = zero4();
-        if (prod == 0) {
-            acc = mask_tile(mma<3>(acc, Bk, x0, Aq, y0, 0, 2), x0, y0, 1);
-            st_f32(F32, PF, x0, y0, acc);
-        } else if (prod == 1) {
-            acc = mask_tile(mma<3>(acc, Aq, x0, Kk, y0, 0, 2), x0, y0, 3);
-            st_split(Be, PB, x0, y0, acc);
-        } else if (prod == 2) {
-            acc = mask_tile(mma<1>(acc, Bk, x0, Rq, y0, 0, 2), x0, y0, 2);
-            st_hi(Rho.h, PB, x0, y0, acc);
-        } else if (prod == 3) {
-            acc = mask_tile(mma<1>(acc, Kk, x0, Rq, y0, 0, 2), x0, y0, 2);
-            st_hi(Sig.h, PB, x0, y0, acc);
-        } else {
-            const int kb = by >> 1;
-            acc = mfma_bf16(ld8(Vr.h + (x0 + li) * PB + 32 * kb + 8 * lq), diag_operand(y0 + li, kb, (__bf16)1.f), acc);
-            st_hi(Vt.h, PB, x0, y0, acc);
+        f4 aa = zero4(), bb = zero4(), rr = zero4(), ss = zero4();
+        if (bx <= by) {  // alpha, rho, sigma (lower part)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int xo = (x0 + li) * PB + 32 * kb + 8 * lq, yo = (y0 + li) * PB + 32 * kb + 8 * lq;
+                const bf8 bkh = ld8(Bk.h + xo), bkl = ld8(Bk.l + xo), kkh = ld8(Kk.h + xo);
+                const bf8 aqh = ld8(Aq.h + yo), aql = ld8(Aq.l + yo), rq = ld8(Rq.h + yo);
+                aa = mfma_bf16(bkh, aql, aa);
+                aa = mfma_bf16(bkl, aqh, aa);
+                aa = mfma_bf16(bkh, aqh, aa);
+                rr = mfma_bf16(bkh, rq, rr);
+                ss = mfma_bf16(kkh, rq, ss);
+            }
         }
+        if (bx >= by) {  // beta (upper part)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int xo = (x0 + li) * PB + 32 * kb + 8 * lq, yo = (y0 + li) * PB + 32 * kb + 8 * lq;
+                const bf8 aqh = ld8(Aq.h + xo), aql = ld8(Aq.l + xo);
+                const bf8 kkh = ld8(Kk.h + yo), kkl = ld8(Kk.l + yo);
+                bb = mfma_bf16(aqh, kkl, bb);
+                bb = mfma_bf16(aql, kkh, bb);
+                bb = mfma_bf16(aqh, kkh, bb);
+            }
+        }
+        st_f32(F32, PF, x0, y0, mask_tile(aa, x0, y0, 1));
+        st_split(Be, PB, x0, y0, mask_tile(bb, x0, y0, 3));
+        st_hi(Rho.h, PB, x0, y0, mask_tile(rr, x0, y0, 2));
+        st_hi(Sig.h, PB, x0, y0, mask_tile(ss, x0, y0, 2));
     }
     __syncthreads();
 
-    // ---- 5. waves 0-3: inverses of the diagonal 16 x 16 blocks of I - alpha by doubling,
-    //         (I - L)^{-1} = (I + L)(I + L^2)(I + L^4)(I + L^8) for strictly lower L, in fp32, written over alpha;
-    //         waves 4-7: A0^T = (Aq diag(2^m))^T, Bh^T = (Bk diag(2^{g_C-m}))^T, Kh^T = (Kk diag(2^{g_C-m}))^T as
-    //         MFMA products with a scaled identity, kept in registers until step 6.
-    if (wv < 4) {
-        float* const Lb = F32 + (16 * wv) * PF + 16 * wv;
-        float* const S1 = SCR + wv * 768;
-        float* const S2 = S1 + 256;
-        float* const S3 = S2 + 256;
-        const f4 l2 = mm_f32(zero4(), Lb, PF, 1, Lb, 1, PF, 16);                     // L^2
-        st_rows_f32(S1, 16, l2);
-        wave_lds_sync();
-        const f4 l4 = mm_f32(zero4(), S1, 16, 1, S1, 1, 16, 16);                     // L^4
-        const f4 pl = mm_f32(zero4(), Lb, PF, 1, S1, 1, 16, 16);                     // L^3
-        f4 aa;
+    // ---- 5. wave 0: inverses T_ii = (I - L)^{-1} of the four 16 x 16 diagonal blocks L = alpha_ii (strictly lower),
+    //         by forward substitution in fp32, one column per lane (lane = 16 block + column):
+    //         T[m][j] = delta_mj + sum_{p<m} L[m][p] T[p][j]; written over alpha_ii.
+    if (wv == 0) {
+        const int bb = lane >> 4, j = lane & 15;
+        float* const Lb = F32 + (16 * bb) * PF + 16 * bb;
+        // the strictly lower part of the block, all reads issued before the arithmetic (row m needs p < m)
+        f4 Lr[16][4];
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int x = 4 * lq + v;
-            aa[v] = (x == li ? 1.f : 0.f) + Lb[x * PF + li] + l2[v] + pl[v];  // A = I + L + L^2 + L^3
-        }
-        st_rows_f32(S2, 16, l4);
-        st_rows_f32(S3, 16, aa);
-        wave_lds_sync();
-        const f4 l8 = mm_f32(zero4(), S2, 16, 1, S2, 1, 16, 16);                     // L^8
-        st_rows_f32(S1, 16, l8);
-        wave_lds_sync();
-        const f4 l12 = mm_f32(zero4(), S2, 16, 1, S1, 1, 16, 16);                    // L^12
-        f4 bb;
+        for (int m = 1; m < 16; ++m) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int x = 4 * lq + v;
-            bb[v] = (x == li ? 1.f : 0.f) + l4[v] + l8[v] + l12[v];  // B = I + L^4 + L^8 + L^12
+            for (int c = 0; c < 4; ++c)
+                if (4 * c < m) Lr[m][c] = *reinterpret_cast<const f4*>(Lb + m * PF + 4 * c);
         }
-        wave_lds_sync();
-        st_rows_f32(S2, 16, bb);
-        wave_lds_sync();
-        st_rows_f32(Lb, PF, mm_f32(zero4(), S3, 16, 1, S2, 1, 16, 16));             // T_dd = A B
-    } else {
+        float t[16];
 #pragma unroll
-        for (int u = 0; u < 12; ++u) {
-            const int idx = (wv - 4) + 4 * u;
-            const int mat = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
-            const BM X = mat == 0 ? Aq : (mat == 1 ? Bk : Kk);
-            const int y = 16 * by + li, kb = by >> 1;
-            const float sc = mat == 0 ? sm.em[y] : sm.eglm[y];
-            __bf16 sh, sl;
-            split(sc, sh, sl);
-            const int xo = (16 * bx + li) * PB + 32 * kb + 8 * lq;
-            const bf8 xh = ld8(X.h + xo), xl = ld8(X.l + xo);
-            const bf8 dh = diag_operand(y, kb, sh), dl = diag_operand(y, kb, sl);
-            f4 a = mfma_bf16(xh, dl, zero4());
-            a = mfma_bf16(xl, dh, a);
-            rl[u] = mfma_bf16(xh, dh, a);
-        }
-    }
-    __syncthreads();
-
-    // ---- 6. waves 4-7: store A0^T, Bh^T, Kh^T over their sources
-    if (wv >= 4) {
+        for (int m = 0; m < 16; ++m) t[m] = m == j ? 1.f : 0.f;
 #pragma unroll
-        for (int u = 0; u < 12; ++u) {
-            const int idx = (wv - 4) + 4 * u;
-            const int mat = idx >> 4, tile = idx & 15, bx = tile >> 2, by = tile & 3;
-            st_split(mat == 0 ? Aq : (mat == 1 ? Bk : Kk), PB, 16 * bx, 16 * by, rl[u]);
+        for (int m = 1; m < 16; ++m) {
+            float a[4] = {t[m], 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int pp = 0; pp < m; ++pp) a[pp & 3] += Lr[m][pp >> 2][pp & 3] * t[pp];
+            t[m] = (a[0] + a[1]) + (a[2] + a[3]);
         }
+#pragma unroll
+        for (int m = 0; m < 16; ++m) Lb[m * PF + j] = t[m];
     }
     __syncthreads();
 
@@ -588,16 +598,27 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     {
         const bool is_w = wv < 4;
         const int col0 = 16 * (wv & 3);
-        const BM rhs = is_w ? A0t : Be;  // A0^T [k][t] / beta stored [s'][s]: column-major right-hand side
+        // right-hand side in the B layout, rows t = 16 bi + 4 lq + v, column col0 + li: A0 = Aq diag(2^m) read down
+        // Aq's rows (transposing read), beta from its [s'][s] store
+        const float sc = is_w ? sm.em[col0 + li] : 1.f;
         f4 X[4];
         s4 Xh[4], Xl[4];
 #pragma unroll
         for (int bi = 0; bi < 4; ++bi) {
-            const int o = (col0 + li) * PB + 16 * bi + 4 * lq;
-            const bf4 bh = *reinterpret_cast<const bf4*>(rhs.h + o), bl = *reinterpret_cast<const bf4*>(rhs.l + o);
+            s4 bh, bl;
+            if (is_w) {
+                const int o = (16 * bi + 4 * lq + (li >> 2)) * PB + col0 + 4 * (li & 3);
+                bh = ld_tr4(Aq.h + o);
+                bl = ld_tr4(Aq.l + o);
+            } else {
+                const int o = (col0 + li) * PB + 16 * bi + 4 * lq;
+                bh = *reinterpret_cast<const s4*>(Be.h + o);
+                bl = *reinterpret_cast<const s4*>(Be.l + o);
+            }
             f4 acc;
 #pragma unroll
-            for (int v = 0; v < 4; ++v) acc[v] = (float)bh[v] + (float)bl[v];
+            for (int v = 0; v < 4; ++v)
+                acc[v] = (bf16_to_f32((uint16_t)bh[v]) + bf16_to_f32((uint16_t)bl[v])) * sc;
 #pragma unroll
             for (int bj = 0; bj < bi; ++bj) {
                 const f4 al = *reinterpret_cast<const f4*>(F32 + (16 * bi + li) * PF + 16 * bj + 4 * lq);
@@ -624,58 +645,77 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
 
     // ---- 8. Q = R0 + rho W  (x = k, y = t; bf16 -> workspace [t][k])
     //          E = sigma + rho G (x = s', y = t; bf16 -> Em [t][s'], keep s' <= t)
-    //          A = Gamma + Bh^T W (x = k2, y = k1; 3 terms -> workspace hi/lo [k1][k2])
+    //          A = Gamma + Bh^T W (x = k2, y = k1; 3 terms -> workspace hi/lo)
     //          F = Kh^T + Bh^T G (x = s', y = k; 3 terms -> slots 2-3 as F[k][s'])
+    //          (Bh = Bk diag(2^{g_C - m}), Kh likewise: Bk and Kk read down their rows, the factor applied to the
+    //          fp32 result rows)
+    // Wave wv owns tiles (bx, by) = (wv / 4 + 2 u, wv % 4).  The four products of a tile share their operands (W and
+    // G as X, rho and the transposed Bk as Y), each fragment loaded once per contraction block.  rho is zero for
+    // s > t, so for token tiles by < 2 the second contraction block of Q and E is skipped.
     {
-        // full contractions again: rho and G are exactly zero where the causal ranges end
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int prod = u >> 1, tile = wv + 8 * (u & 1), bx = tile >> 2, by = tile & 3;
+        for (int u = 0; u < 2; ++u) {
+            const int bx = (wv >> 2) + 2 * u, by = wv & 3;
             const int x0 = 16 * bx, y0 = 16 * by;
-            f4 acc;
-            if (prod == 0) {
+            f4 aq, ae, aa = zero4(), af;
+            {
                 const bf4 r4 = *reinterpret_cast<const bf4*>(Rq.h + (y0 + li) * PB + x0 + 4 * lq);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[v] = (float)r4[v] * sm.em[x0 + 4 * lq + v];
-                acc = mma<1>(acc, Wm, x0, Rho, y0, 0, 2);
-                bf4 hv;
-#pragma unroll
-                for (int v = 0; v < 4; ++v) hv[v] = (__bf16)acc[v];
-                *reinterpret_cast<bf4*>(rec + REC_Q + frag_off_bf16(by, bx, lane)) = hv;  // Q[t][k]: t tile by
-            } else if (prod == 1) {
-                const bf4 s4 = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[v] = (float)s4[v];
-                acc = mask_tile(mma<1>(acc, Gm, x0, Rho, y0, 0, 2), x0, y0, 2);
-                st_hi(Em.h, PB, x0, y0, acc);
-            } else if (prod == 2) {
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[v] = (x0 + 4 * lq + v == y0 + li) ? sm.gam[y0 + li] : 0.f;
-                acc = mma<3>(acc, Wm, x0, Bht, y0, 0, 2);
-                bf4 hv, lv;
+                const bf4 s4v = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
+                const int o = (x0 + 4 * lq + (li >> 2)) * PB + y0 + 4 * (li & 3);
+                const s4 kh4 = ld_tr4(Kk.h + o), kl4 = ld_tr4(Kk.l + o);  // Kk[x0 + 4 lq + v][y0 + li]
 #pragma unroll
                 for (int v = 0; v < 4; ++v) {
-                    __bf16 hh, ll;
-                    split(acc[v], hh, ll);
-                    hv[v] = hh;
-                    lv[v] = ll;
+                    aq[v] = (float)r4[v] * sm.em[x0 + 4 * lq + v];
+                    ae[v] = (float)s4v[v];
+                    af[v] = bf16_to_f32((uint16_t)kh4[v]) + bf16_to_f32((uint16_t)kl4[v]);
                 }
-                *reinterpret_cast<bf4*>(rec + REC_AH + frag_off_bf16(by, bx, lane)) = hv;  // A[k1][k2]: k1 tile by
-                *reinterpret_cast<bf4*>(rec + REC_AL + frag_off_bf16(by, bx, lane)) = lv;
-            } else {
-                const bf4 kh4 = *reinterpret_cast<const bf4*>(Kht.h + (y0 + li) * PB + x0 + 4 * lq);
-                const bf4 kl4 = *reinterpret_cast<const bf4*>(Kht.l + (y0 + li) * PB + x0 + 4 * lq);
-#pragma unroll
-                for (int v = 0; v < 4; ++v) acc[v] = (float)kh4[v] + (float)kl4[v];
-                acc = mma<3>(acc, Gm, x0, Bht, y0, 0, 2);
-                st_split(Fm, PB, x0, y0, acc);
             }
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int xo = (x0 + li) * PB + 32 * kb + 8 * lq;
+                const bf8 wh = ld8(Wm.h + xo), wl = ld8(Wm.l + xo), gh = ld8(Gm.h + xo), gl = ld8(Gm.l + xo);
+                const bf8 bh = ld8_tr(Bk.h, kb, y0), bl = ld8_tr(Bk.l, kb, y0);
+                if (kb == 0 || by >= 2) {
+                    const bf8 rh = ld8(Rho.h + (y0 + li) * PB + 32 * kb + 8 * lq);
+                    aq = mfma_bf16(wh, rh, aq);
+                    ae = mfma_bf16(gh, rh, ae);
+                }
+                aa = mfma_bf16(wh, bl, aa);
+                aa = mfma_bf16(wl, bh, aa);
+                aa = mfma_bf16(wh, bh, aa);
+                af = mfma_bf16(gh, bl, af);
+                af = mfma_bf16(gl, bh, af);
+                af = mfma_bf16(gh, bh, af);
+            }
+            // Q -> record (Q[t][k]: t tile by)
+            bf4 qv;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) qv[v] = (__bf16)aq[v];
+            *reinterpret_cast<bf4*>(rec + REC_Q + frag_off_bf16(by, bx, lane)) = qv;
+            // E -> Em, keep s' <= t
+            st_hi(Em.h, PB, x0, y0, mask_tile(ae, x0, y0, 2));
+            // A[k1][k2] = gamma delta + 2^{g_C - m}[k1] sum_t W[t][k2] Bk[t][k1] -> record (k1 tile by)
+            // F[k][s'] = 2^{g_C - m}[k] (Kk[s'][k] + sum_t G[t][s'] Bk[t][k]) -> Fm
+            const float e1 = sm.eglm[y0 + li];
+            bf4 hv, lv;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float av = aa[v] * e1 + ((x0 + 4 * lq + v == y0 + li) ? sm.gam[y0 + li] : 0.f);
+                __bf16 hh, ll;
+                split(av, hh, ll);
+                hv[v] = hh;
+                lv[v] = ll;
+                af[v] *= e1;
+            }
+            *reinterpret_cast<bf4*>(rec + REC_AH + frag_off_bf16(by, bx, lane)) = hv;
+            *reinterpret_cast<bf4*>(rec + REC_AL + frag_off_bf16(by, bx, lane)) = lv;
+            st_split(Fm, PB, x0, y0, af);
         }
     }
     __syncthreads();
 
     // ---- 9. H = F V (x = k, y = v; X split, V exact -> workspace fp32, H^T tiles);
-    //          O_intra = E V (x = v, y = t -> workspace bf16, tiles of O_intra[t][v])
+    //          O_intra = E V (x = v, y = t -> workspace bf16, tiles of O_intra[t][v]); V read down its rows
     {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -683,9 +723,9 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             const int x0 = 16 * bx, y0 = 16 * by;
             if (prod == 0) {
                 *reinterpret_cast<f4*>(rec + REC_HT + ((by * 4 + bx) * 64 + lane) * 16) =
-                    mma<2>(zero4(), Fm, x0, Vt, y0, 0, 2);  // H^T[v][k]: v tile by, k tile bx
+                    mma_ty<2>(zero4(), Fm, x0, Vr, y0);  // H^T[v][k]: v tile by, k tile bx
             } else {
-                const f4 acc = mma<1>(zero4(), Vt, x0, Em, y0, 0, 2);  // E is zero for s' > t
+                const f4 acc = mma_tx1(zero4(), Vr, x0, Em, y0);  // E is zero for s' > t
                 bf4 hv;
 #pragma unroll
                 for (int v = 0; v < 4; ++v) hv[v] = (__bf16)acc[v];
