@@ -380,6 +380,11 @@ __device__ __forceinline__ RawIn load_item(const Params& p, const Item& it, int 
     return x;
 }
 
+// Element offset of this thread's operand row of an item (token 0 for rows outside the chunk, see load_item).
+__device__ __forceinline__ int64_t item_offset(const Params& p, const Item& it, int row, int cb) {
+    return row < it.Lc ? (it.tok0 + row) * p.in_tok_stride + (int64_t)it.h * HS + cb : (int64_t)cb;
+}
+
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Slots (each 64 x 72 bf16 = 9 KB; an fp32 64 x 72 matrix takes two):
@@ -393,8 +398,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Bk, Kk and V where they lie, through transposing LDS reads, and apply the per-channel decay factors that separate
 // A0, Bh, Kh from Aq, Bk, Kk (2^m, 2^{g_C - m}) to their fp32 results.
 // Decays are handled in base 2 (g = cumulative log2 d), so every decay factor is one v_exp_f32.
+// The next item's operands (element offset noff) are loaded into `next` one operand per phase, spread over the item
+// so that their issue does not queue behind one another.
 __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const RawIn& raw, char* wsc,
-                                          PrepSmem& sm) {
+                                          PrepSmem& sm, int64_t noff, RawIn& next) {
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int li = lane & 15, lq = lane >> 4;
     float* const F32 = reinterpret_cast<float*>(sm.slot[0]);   // slots 0-1 as fp32 [64][PF]
@@ -438,6 +445,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         *reinterpret_cast<uint4*>(Vr.h + row * PB + cb) = valid ? raw.v : make_uint4(0u, 0u, 0u, 0u);
     }
     __syncthreads();
+    next.w = *reinterpret_cast<const uint4*>(p.w + noff);
 
     // ---- 2. g (inclusive) and g of the previous row; midpoint m = g_31 and chunk total g_63 per channel
     float gi[8], ge[8], mk[8];
@@ -516,6 +524,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         *reinterpret_cast<bf8*>(Rq.h + o) = rqh;
     }
     __syncthreads();
+    next.a = *reinterpret_cast<const uint4*>(p.a + noff);
 
     // ---- 4. Grams (natural store of P(x, y) is [y][x]):
     //   alpha: x = s, y = t  (X = Bk, Y = Aq, 3 terms), keep s < t, fp32 -> F32 as alpha[t][s]
@@ -560,10 +569,14 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         st_hi(Sig.h, PB, x0, y0, mask_tile(ss, x0, y0, 2));
     }
     __syncthreads();
+    next.b = *reinterpret_cast<const uint4*>(p.b + noff);
 
     // ---- 5. wave 0: inverses T_ii = (I - L)^{-1} of the four 16 x 16 diagonal blocks L = alpha_ii (strictly lower),
     //         by forward substitution in fp32, one column per lane (lane = 16 block + column):
-    //         T[m][j] = delta_mj + sum_{p<m} L[m][p] T[p][j]; written over alpha_ii.
+    //         T[m][j] = delta_mj + sum_{p<m} L[m][p] T[p][j].
+    //         waves 1-6: the six blocks alpha_ij, i > j.
+    //         Both leave their block split hi/lo in place, as the A operand of step 7: each 64-byte row segment of
+    //         a 16 x 16 fp32 block becomes 16 bf16 hi followed by 16 bf16 lo.
     if (wv == 0) {
         const int bb = lane >> 4, j = lane & 15;
         float* const Lb = F32 + (16 * bb) * PF + 16 * bb;
@@ -586,13 +599,30 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             t[m] = (a[0] + a[1]) + (a[2] + a[3]);
         }
 #pragma unroll
-        for (int m = 0; m < 16; ++m) Lb[m * PF + j] = t[m];
+        for (int m = 0; m < 16; ++m) {
+            __bf16 hh, ll;
+            split(t[m], hh, ll);
+            __bf16* const seg = reinterpret_cast<__bf16*>(Lb + m * PF);
+            seg[j] = hh;
+            seg[16 + j] = ll;
+        }
+    } else if (wv <= 6) {
+        const int blk = wv - 1, r = lane >> 2, qq = lane & 3;  // one row segment per 4 lanes of one wave
+        const int bi = blk < 1 ? 1 : (blk < 3 ? 2 : 3), bj = blk < 1 ? 0 : (blk < 3 ? blk - 1 : blk - 3);
+        float* const segf = F32 + (16 * bi + r) * PF + 16 * bj;
+        const f4 x = *reinterpret_cast<const f4*>(segf + 4 * qq);
+        s4 h4, l4;
+        split4(x, h4, l4);
+        char* const seg = reinterpret_cast<char*>(segf);
+        *reinterpret_cast<s4*>(seg + 8 * qq) = h4;  // the segment's reads all precede these writes (one wave)
+        *reinterpret_cast<s4*>(seg + 32 + 8 * qq) = l4;
     }
     __syncthreads();
+    next.k = *reinterpret_cast<const uint4*>(p.k + noff);
 
     // ---- 7. W = T A0 and G = T beta without forming T: block forward substitution of (I - alpha) X = [A0 | beta]
     //         over the four 16-row blocks, X_i = T_ii (B_i + sum_{j<i} alpha_ij X_j), with the diagonal-block
-    //         inverses T_ii from step 5.  Wave w owns one 16-column tile of X (w < 4: W columns 16 w ..; w >= 4: G
+    //         inverses T_ii and the blocks alpha_ij already split hi/lo by step 5.  Wave w owns one 16-column tile of X (w < 4: W columns 16 w ..; w >= 4: G
     //         columns 16 (w - 4) ..) and keeps its X_j in registers: the 16x16x16 MFMA returns a tile in exactly the
     //         layout it takes as its B operand.  3-term hi/lo products throughout (state path).
     {
@@ -621,16 +651,15 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
                 acc[v] = (bf16_to_f32((uint16_t)bh[v]) + bf16_to_f32((uint16_t)bl[v])) * sc;
 #pragma unroll
             for (int bj = 0; bj < bi; ++bj) {
-                const f4 al = *reinterpret_cast<const f4*>(F32 + (16 * bi + li) * PF + 16 * bj + 4 * lq);
-                s4 ah4, al4;
-                split4(al, ah4, al4);
+                const char* const seg = reinterpret_cast<const char*>(F32 + (16 * bi + li) * PF + 16 * bj);
+                const s4 ah4 = *reinterpret_cast<const s4*>(seg + 8 * lq), al4 = *reinterpret_cast<const s4*>(seg + 32 + 8 * lq);
                 acc = mfma16(ah4, Xl[bj], acc);
                 acc = mfma16(al4, Xh[bj], acc);
                 acc = mfma16(ah4, Xh[bj], acc);
             }
-            const f4 tt = *reinterpret_cast<const f4*>(F32 + (16 * bi + li) * PF + 16 * bi + 4 * lq);
-            s4 th4, tl4, ch4, cl4;
-            split4(tt, th4, tl4);
+            const char* const tseg = reinterpret_cast<const char*>(F32 + (16 * bi + li) * PF + 16 * bi);
+            const s4 th4 = *reinterpret_cast<const s4*>(tseg + 8 * lq), tl4 = *reinterpret_cast<const s4*>(tseg + 32 + 8 * lq);
+            s4 ch4, cl4;
             split4(acc, ch4, cl4);
             f4 x = mfma16(th4, cl4, zero4());
             x = mfma16(tl4, ch4, x);
@@ -638,10 +667,13 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             split4(X[bi], Xh[bi], Xl[bi]);
         }
         __syncthreads();  // alpha / T_ii (slots 0-1) and beta are read above; W and G are written over them
+        next.r = *reinterpret_cast<const uint4*>(p.r + noff);
 #pragma unroll
         for (int bi = 0; bi < 4; ++bi) st_split(is_w ? Wm : Gm, PB, 16 * bi, col0, X[bi]);
     }
     __syncthreads();
+
+    next.v = *reinterpret_cast<const uint4*>(p.v + noff);
 
     // ---- 8. Q = R0 + rho W  (x = k, y = t; bf16 -> workspace [t][k])
     //          E = sigma + rho G (x = s', y = t; bf16 -> Em [t][s'], keep s' <= t)
@@ -765,10 +797,11 @@ __global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, ch
         Item nxt{};
         nxt.rec = max_chunks * p.H;
         if (np.item < nitems) nxt = describe_item(p, plan, max_chunks, np);
-        const RawIn rn = load_item(p, nxt, row, cb);  // in flight while `cur` is processed
-        // every item runs the same instruction stream (an item without a chunk computes on zeros and writes the
-        // trash record), so the number of vector memory operations between a prefetch and its use is fixed
-        prep_item(p, cur, rc, wsc, sm);
+        // the next item's operands are loaded during `cur`; every item runs the same instruction stream (an item
+        // without a chunk computes on zeros and writes the trash record), so the number of vector memory operations
+        // between a prefetch and its use is fixed
+        RawIn rn;
+        prep_item(p, cur, rc, wsc, sm, item_offset(p, nxt, row, cb), rn);
         cur = nxt;
         rc = rn;
         pos = np;
