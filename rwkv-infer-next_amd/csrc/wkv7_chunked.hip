@@ -49,19 +49,28 @@ constexpr int SLOT = 64 * PB;    // bf16 elements of one 64 x 64 LDS matrix (921
 constexpr int NSLOT = 17;
 
 // Workspace record of one (chunk, head), byte offsets.  Every part is stored in the fragment order of the scan's
-// 16x16x16 MFMAs, so that each scan lane reads its operands as contiguous 16-byte pieces: a 16 x 16 tile is 64 lanes
-// x 4 values (lane (i, q) holds row i, columns 4 q .. 4 q + 3), and two tiles adjacent along the contraction share
-// one 16-byte piece per lane.
-constexpr int REC_AH = 0;                  // A hi, bf16: [k1 tile r][k2 tile pair][lane][8]
+// MFMAs, so that each scan lane reads its operands as contiguous 16-byte pieces.  A and Q are 16x16x32 operands:
+// for row tile a and contraction block c (32 wide), lane (i, q) holds row 16 a + i, columns 32 c + 8 q .. + 7.  H^T
+// and O_intra are 16x16 results: lane (i, q) holds rows 4 q .. 4 q + 3 of column i (H), or row i, columns
+// 4 q .. 4 q + 3 (O_intra, two token tiles per 16-byte piece).
+constexpr int REC_AH = 0;                  // A hi, bf16: [k1 tile r][k2 block c][lane][8]
 constexpr int REC_AL = REC_AH + 2 * HS2;   // A lo, same
 constexpr int REC_HT = REC_AL + 2 * HS2;   // H^T fp32: [v tile vg][k tile r][lane][4]  (H[16 r + 4 q + e][16 vg + i])
-constexpr int REC_Q = REC_HT + 4 * HS2;    // Q bf16: [token tile t][k tile pair][lane][8]
+constexpr int REC_Q = REC_HT + 4 * HS2;    // Q bf16: [token tile t][k block c][lane][8]
 constexpr int REC_OT = REC_Q + 2 * HS2;    // O_intra bf16: [v tile vg][token tile pair][lane][8]
 static_assert(REC_OT + 2 * HS2 == kChunkBytes, "workspace record size");
 
 // Byte offset of tile (row tile a, contraction tile b) of a 64 x 64 bf16 record part, for this lane: tiles b = 2 c and
 // 2 c + 1 share a 16-byte piece per lane.
 __device__ __forceinline__ int frag_off_bf16(int a, int b, int lane) { return ((a * 2 + (b >> 1)) * 64 + lane) * 16 + (b & 1) * 8; }
+
+// Where a 16x16 result tile (row tile a, column tile b; lane (li, lq) holding row 16 a + li, columns 16 b + 4 lq ..
+// + 3) lands in the 16x16x32 operand order of a record part: scan lane li + 16 (2 (b & 1) + (lq >> 1)) of block
+// (a, b >> 1), values 4 (lq & 1) .. + 3 of its 8.
+__device__ __forceinline__ int frag32_off(int a, int b, int lane) {
+    const int li = lane & 15, lq = lane >> 4;
+    return ((a * 2 + (b >> 1)) * 64 + li + 16 * (2 * (b & 1) + (lq >> 1))) * 16 + 8 * (lq & 1);
+}
 
 __device__ __forceinline__ f4 zero4() { return f4{0.f, 0.f, 0.f, 0.f}; }
 
@@ -723,7 +732,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             bf4 qv;
 #pragma unroll
             for (int v = 0; v < 4; ++v) qv[v] = (__bf16)aq[v];
-            *reinterpret_cast<bf4*>(rec + REC_Q + frag_off_bf16(by, bx, lane)) = qv;
+            *reinterpret_cast<bf4*>(rec + REC_Q + frag32_off(by, bx, lane)) = qv;
             // E -> Em, keep s' <= t
             st_hi(Em.h, PB, x0, y0, mask_tile(ae, x0, y0, 2));
             // A[k1][k2] = gamma delta + 2^{g_C - m}[k1] sum_t W[t][k2] Bk[t][k1] -> record (k1 tile by)
@@ -739,8 +748,8 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
                 lv[v] = ll;
                 af[v] *= e1;
             }
-            *reinterpret_cast<bf4*>(rec + REC_AH + frag_off_bf16(by, bx, lane)) = hv;
-            *reinterpret_cast<bf4*>(rec + REC_AL + frag_off_bf16(by, bx, lane)) = lv;
+            *reinterpret_cast<bf4*>(rec + REC_AH + frag32_off(by, bx, lane)) = hv;
+            *reinterpret_cast<bf4*>(rec + REC_AL + frag32_off(by, bx, lane)) = lv;
             st_split(Fm, PB, x0, y0, af);
         }
     }
@@ -808,13 +817,12 @@ __global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, ch
     }
 }
 
-// One chunk record's share of one scan lane (wavefront of column group vg): all of A (hi/lo) and Q, and the group's
-// columns of H^T and O_intra, in MFMA fragment order (16-byte pieces: two k tiles of A and Q per piece, two token
-// tiles of O per piece).
+// One chunk record's share of one scan lane (wavefront of column group vg): all of A (hi/lo) and Q as 16x16x32 operand
+// fragments, and the group's columns of H^T and O_intra.
 typedef short s8 __attribute__((ext_vector_type(8)));
 struct ScanRec {
-    s8 ah[4][2], al[4][2];  // [row tile r][k tile pair]
-    s8 q[4][2];             // [token tile t][k tile pair]
+    s8 ah[4][2], al[4][2];  // [row tile r][k block c]: A[16 r + i][32 c + 8 q + j]
+    s8 q[4][2];             // [token tile t][k block c]: Q[16 t + i][32 c + 8 q + j]
     f4 h[4];                // [k tile r]: H[16 r + 4 q + e][16 vg + i]
     s8 o[2];                // [token tile pair]: O_intra[16 t + i][16 vg + 4 q + e]
 };
@@ -841,15 +849,55 @@ __device__ __forceinline__ void scan_load(ScanRec& r, const char* rec, int vg, i
     for (int c = 0; c < 2; ++c) r.o[c] = *reinterpret_cast<const s8*>(b + REC_OT + (vg * 2 + c) * 1024 + lo);
 }
 
+// The state as 16x16x32 operands.  Lane (i, q) holds S[16 r + 4 q + e][col] (e = 0..3) of the four k tiles r; the
+// operand of contraction block c needs S[32 c + 8 q + j][col], j = 0..7, which lanes 2 (q & 1) and 2 (q & 1) + 1 of
+// tile 2 c + (q >> 1) hold.  With X = tile 2 c, Y = tile 2 c + 1 and rows of 16 lanes: v_permlane32_swap(X, Y) gives
+// P = (X0, X1, Y0, Y1), Q = (X2, X3, Y2, Y3), and v_permlane16_swap(P, Q) gives (X0, X2, Y0, Y2) -- values j = 0..3
+// for every row q -- and (X1, X3, Y1, Y3) -- values j = 4..7.  The same vector is the A operand of S^T.
+__device__ __forceinline__ void state_operands(const f4 (&S)[4], bf8 (&Bh)[2], bf8 (&Bl)[2]) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        uint32_t h[2][2], l[2][2];  // [tile 2c, 2c + 1][dword]
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const f4 x = S[2 * c + u];
+            __bf16 hh[4], ll[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) split(x[e], hh[e], ll[e]);
+#pragma unroll
+            for (int w = 0; w < 2; ++w) {
+                h[u][w] = (uint32_t)__builtin_bit_cast(uint16_t, hh[2 * w]) |
+                          ((uint32_t)__builtin_bit_cast(uint16_t, hh[2 * w + 1]) << 16);
+                l[u][w] = (uint32_t)__builtin_bit_cast(uint16_t, ll[2 * w]) |
+                          ((uint32_t)__builtin_bit_cast(uint16_t, ll[2 * w + 1]) << 16);
+            }
+        }
+        uint32_t oh[4], ol[4];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+            const auto ph = __builtin_amdgcn_permlane32_swap(h[0][w], h[1][w], false, false);
+            const auto rh = __builtin_amdgcn_permlane16_swap(ph[0], ph[1], false, false);
+            oh[w] = rh[0];
+            oh[2 + w] = rh[1];
+            const auto pl = __builtin_amdgcn_permlane32_swap(l[0][w], l[1][w], false, false);
+            const auto rl = __builtin_amdgcn_permlane16_swap(pl[0], pl[1], false, false);
+            ol[w] = rl[0];
+            ol[2 + w] = rl[1];
+        }
+        Bh[c] = __builtin_bit_cast(bf8, oh);
+        Bl[c] = __builtin_bit_cast(bf8, ol);
+    }
+}
+
 constexpr int kScanDepth = 2;  // chunk records in flight per lane (register ring)
 
 // One wavefront per (row, head, 16-column group vg); block b -> XCD b % 8, and the 4 groups of a (row, head) share an
 // XCD, so 3 of the 4 reads of a chunk's A and Q hit that XCD's L2.  The lane (i, q) holds S[16 r + 4 q + e][16 vg + i]
-// for the four k tiles r: exactly the B operand of the 16x16x16 MFMA for contraction tile r and the layout of its
-// result, so the state stays in registers from chunk to chunk (fp32, plus a hi/lo bf16 split as the next operand),
-// with no LDS and no barrier:
-//     S <- A S + H   (48 MFMAs: 4 x 4 tiles, 3 terms on the hi/lo split)
-//     y^T = S^T Q^T + O_intra^T   (16 MFMAs on S hi; S^T tile r is S tile r's registers read as the A operand)
+// for the four k tiles r -- the layout of a 16x16 MFMA result -- so the state stays in registers from chunk to chunk
+// with no LDS and no barrier; each chunk re-forms it as 16x16x32 operands with two lane swaps per register
+// (state_operands) and runs
+//     S <- A S + H   (24 MFMAs: 4 row tiles x 2 contraction blocks, 3 terms on the hi/lo split)
+//     y^T = S^T Q^T + O_intra^T   (8 MFMAs on S hi)
 // Chunk records stream through a ring of kScanDepth register sets.  Every step issues the same memory operations
 // (the refill index is clamped to the last chunk; stores that must not land go to the workspace's trash record), so
 // the compiler counts the outstanding loads exactly and waits only for the record about to be used.
@@ -890,9 +938,8 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
         }
         return;
     }
-    s4 Sh[4], Sl[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) split4(S[r], Sh[r], Sl[r]);
+    bf8 Bh[2], Bl[2];
+    state_operands(S, Bh, Bl);
 
     const char* const rec0 = wsc + (j0 * p.H + h) * (int64_t)kChunkBytes;
     const int64_t rec_stride = (int64_t)p.H * kChunkBytes;
@@ -916,13 +963,13 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
 #pragma unroll
             for (int r = 0; r < 4; ++r) nS[r] = R.h[r];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb) {
+            for (int c = 0; c < 2; ++c) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const s4 ah = half4(R.ah[r][kb >> 1], kb & 1), al = half4(R.al[r][kb >> 1], kb & 1);
-                    nS[r] = mfma16(ah, Sl[kb], nS[r]);
-                    nS[r] = mfma16(al, Sh[kb], nS[r]);
-                    nS[r] = mfma16(ah, Sh[kb], nS[r]);
+                    const bf8 ah = __builtin_bit_cast(bf8, R.ah[r][c]), al = __builtin_bit_cast(bf8, R.al[r][c]);
+                    nS[r] = mfma_bf16(ah, Bl[c], nS[r]);
+                    nS[r] = mfma_bf16(al, Bh[c], nS[r]);
+                    nS[r] = mfma_bf16(ah, Bh[c], nS[r]);
                 }
             }
             f4 y[4];
@@ -932,7 +979,7 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
 #pragma unroll
                 for (int e = 0; e < 4; ++e) y[t][e] = bf16_to_f32((uint16_t)o4[e]);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) y[t] = mfma16(Sh[r], half4(R.q[t][r >> 1], r & 1), y[t]);
+                for (int c = 0; c < 2; ++c) y[t] = mfma_bf16(Bh[c], __builtin_bit_cast(bf8, R.q[t][c]), y[t]);
             }
             // the refill reuses the slot's registers only if it is not scheduled above the slot's last use
             __builtin_amdgcn_sched_barrier(0);
@@ -953,8 +1000,7 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
 #pragma unroll
                 for (int r = 0; r < 4; ++r) S[r] = nS[r];
             }
-#pragma unroll
-            for (int r = 0; r < 4; ++r) split4(S[r], Sh[r], Sl[r]);
+            state_operands(S, Bh, Bl);
         }
     }
     if (dst) {
