@@ -857,19 +857,15 @@ __device__ __forceinline__ void scan_load(ScanRec& r, const char* rec, int vg, i
 __device__ __forceinline__ void state_operands(const f4 (&S)[4], bf8 (&Bh)[2], bf8 (&Bl)[2]) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-        uint32_t h[2][2], l[2][2];  // [tile 2c, 2c + 1][dword]
+        uint32_t h[2][2], l[2][2];  // [tile 2c, 2c + 1][dword]: packed hi / lo pairs (values 2 w, 2 w + 1)
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
             const f4 x = S[2 * c + u];
-            __bf16 hh[4], ll[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) split(x[e], hh[e], ll[e]);
 #pragma unroll
             for (int w = 0; w < 2; ++w) {
-                h[u][w] = (uint32_t)__builtin_bit_cast(uint16_t, hh[2 * w]) |
-                          ((uint32_t)__builtin_bit_cast(uint16_t, hh[2 * w + 1]) << 16);
-                l[u][w] = (uint32_t)__builtin_bit_cast(uint16_t, ll[2 * w]) |
-                          ((uint32_t)__builtin_bit_cast(uint16_t, ll[2 * w + 1]) << 16);
+                const uint32_t hp = pack_bf16x2(x[2 * w], x[2 * w + 1]);
+                h[u][w] = hp;
+                l[u][w] = pack_bf16x2(x[2 * w] - __uint_as_float(hp << 16), x[2 * w + 1] - __uint_as_float(hp & 0xffff0000u));
             }
         }
         uint32_t oh[4], ol[4];
