@@ -10,9 +10,10 @@ value = algorithmic bytes / time: 33 664 B per (slot, head) per layer (16 KB sta
 
 Secondary (same line): chunked prefill B = 1, T = 4096, H = 64 (tok/s and fraction of its roofline), the
 speculative verify with snapshots (config 4), the mixed continuous-batching step in a HIP graph (config 3), the
-fused time-mix prologue/epilogue at the prefill shape, and the CPU baseline (the oracle's fp32 loop on the host cores).
+fused time-mix prologue/epilogue at the prefill shape, the W6A16 weight GEMM at K = 4096, N = 16384, and the CPU
+baseline (the oracle's fp32 loop on the host cores).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu] [--only decode|prefill|verify|mixed|timemix]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu] [--only decode|prefill|verify|mixed|timemix|int6]
 """
 import argparse
 import json
@@ -223,6 +224,66 @@ def timemix_bench(torch, kernels, dev, steps, warmup):
             "algorithmic_bytes": bytes_, "torch_eager_ms": ms_eager, "speedup_vs_eager": ms_eager / ms}
 
 
+def int6_bench(torch, kernels, dev, steps, warmup):
+    """W6A16 GEMM/GEMV (rwkv_next/kernels/int6_gemm.py) at the reference's quoted shape K = 4096, N = 16384
+    (int6_gemm.py:224-226), group_k = 128, for decode-sized M (the W6A16 kernel) and M = 4096 (dequantise, then the
+    library GEMM).  Eight weight sets (8 x 51 MB) are cycled so the 256 MB Infinity Cache cannot hold them: every
+    call streams its weight from HBM, as a model's consecutive layers do.  Each M is one HIP graph of 8 calls.
+    Beside it: torch.matmul on the same shape with a bf16 weight (hipBLASLt), cycled the same way."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    K, N, G, SETS = 4096, 16384, 128, 8
+    gen = torch.Generator(device=dev).manual_seed(1006)
+    lo = [torch.randint(0, 256, (K // 2, N), device=dev, dtype=torch.uint8, generator=gen) for _ in range(SETS)]
+    hi = [torch.randint(0, 256, (K // 4, N), device=dev, dtype=torch.uint8, generator=gen) for _ in range(SETS)]
+    sc = [(torch.rand(K // G, N, device=dev, generator=gen) * 0.05 + 0.002).half() for _ in range(SETS)]
+    wbf = [I6.dequantize_int6(lo[i], hi[i], sc[i], G, dtype=torch.bfloat16) for i in range(SETS)]
+    weight_bytes = K * N * 3 // 4 + (K // G) * N * 2
+
+    def graph_time(fn, reps):
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(max(1, warmup)):
+                fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            fn()
+        for _ in range(max(1, warmup)):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (reps * SETS)   # us per call
+
+    rows = []
+    for M in (1, 2, 4, 16, 64, 128, 256):
+        a = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+        sk, ud = I6.plan_int6(M, N, K, 1, dev)
+        us = graph_time(lambda: [I6.int6_matmul_op(a, lo[i], hi[i], sc[i], G, sk, ud) for i in range(SETS)], steps)
+        us_bf = graph_time(lambda: [torch.matmul(a, wbf[i]) for i in range(SETS)], steps)
+        byts = weight_bytes + M * K * 2 + M * N * 2
+        rows.append({"M": M, "split_k": sk, "us": us, "GBps": byts / (us * 1e-6) / 1e9,
+                     "frac_hbm": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "bf16_matmul_us": us_bf,
+                     "speedup_vs_bf16": us_bf / us})
+        log(f"int6 M={M} split={sk}: {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), bf16 matmul {us_bf:.2f} us")
+    # prefill-sized M: dequantise once, then the library GEMM
+    M = 4096
+    a = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
+    us = graph_time(lambda: [I6.int6_matmul(a, lo[i], hi[i], sc[i], G) for i in range(SETS)], max(2, steps // 10))
+    us_bf = graph_time(lambda: [torch.matmul(a, wbf[i]) for i in range(SETS)], max(2, steps // 10))
+    rows.append({"M": M, "path": "dequantize + library GEMM", "us": us, "TFLOPs": 2 * M * K * N / (us * 1e-6) / 1e12,
+                 "bf16_matmul_us": us_bf, "speedup_vs_bf16": us_bf / us})
+    log(f"int6 M={M}: {us:.1f} us, bf16 matmul {us_bf:.1f} us")
+    return {"K": K, "N": N, "group_k": G, "weight_bytes": weight_bytes, "rows": rows,
+            "reference_quoted_ms": {"M=128": 0.24, "M=4096": 5.9}}
+
+
 def cpu_baseline(synth):
     """The oracle's fp32 loop (a restatement of rwkv_next/kernels/wkv7.py:65-77) on the host cores, on a bounded
     sample of the decode workload: B = 64 sequences of a 128-slot pool, H = 64, T = 1, one pool, repeated for
@@ -271,7 +332,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed", "timemix"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed", "timemix", "int6"], default=None)
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain device copy of 1 GiB (reference dispatch for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -309,6 +370,9 @@ def main():
     if args.only in (None, "timemix"):
         log("timemix")
         res["timemix"] = timemix_bench(torch, kernels, dev, max(5, args.steps // 5), args.warmup)
+    if args.only in (None, "int6"):
+        log("int6")
+        res["int6"] = int6_bench(torch, kernels, dev, args.steps, args.warmup)
     cpu = None
     if not args.skip_cpu and args.only is None:
         log("cpu baseline")
@@ -345,6 +409,8 @@ def main():
         out["mixed"] = res["mixed"]
     if "timemix" in res:
         out["timemix"] = res["timemix"]
+    if "int6" in res:
+        out["int6"] = res["int6"]
     if cpu:
         out["cpu_baseline"] = cpu
     print(json.dumps(out))

@@ -1,0 +1,73 @@
+/*
+ * w6a16.h -- C ABI of the weight-only 6-bit GEMM in librwkv7_hip.so (gfx950).
+ *
+ * Replaces the reference's W6A16 Triton GEMM/GEMV `_w6a16` and its launcher `_impl`
+ * (rwkv_next/kernels/int6_gemm.py:156-215, 253-287), behind the op `rwkv_next::int6_matmul` (int6_gemm.py:316-323)
+ * that the model's quantised linear layers call (rwkv_next/model.py:63-66).  The weight format is the reference's
+ * own (int6_gemm.py:14-38, 73-112), so weights quantised by the reference load unchanged:
+ *   lo     uint8 [B'][K/2][N]   lo[c*32 + j][n] = lo4(row c*64 + j) | lo4(row c*64 + j + 32) << 4, j < 32
+ *   hi     uint8 [B'][K/4][N]   hi[c*16 + j][n] = hi2(j) | hi2(j + 16) << 2 | hi2(j + 32) << 4 | hi2(j + 48) << 6
+ *   scales fp16  [B'][K/group_k][N]
+ * with u = q + 32 in [0, 63] the stored code of q in [-32, 31] and w = scale * q.
+ *
+ * C[b][m][n] = sum_k A[b][m][k] * w[b][k][n], A bf16 row-major (k contiguous), fp32 accumulation.
+ * Return codes are the WKV7_* codes of wkv7.h.
+ */
+#ifndef RWKV_NEXT_AMD_W6A16_H
+#define RWKV_NEXT_AMD_W6A16_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "wkv7.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W6A16_OUT_BF16 0
+#define W6A16_OUT_F32 2
+
+typedef struct w6a16_args {
+    const uint16_t *a;                 /* bf16 activations [B][M][K] */
+    int64_t a_batch_stride, a_row_stride;          /* elements; row stride >= K, multiples of 8 */
+    const uint8_t *lo, *hi;            /* weight planes; batch strides 0 to share one weight across the batch */
+    int64_t lo_batch_stride, hi_batch_stride;      /* bytes */
+    const uint16_t *scales;            /* fp16, 4-byte aligned */
+    int64_t scales_batch_stride;       /* elements */
+    void *out;                         /* [B][M][N] bf16 or fp32 (out_dtype) */
+    int64_t out_batch_stride, out_row_stride;      /* elements */
+    void *workspace;                   /* split_k > 1: fp32 partials, w6a16_workspace_size bytes */
+    size_t workspace_bytes;
+    int32_t B, M, N, K;                /* K % 64 == 0, N % 16 == 0, B * ceil(M / 16) <= 65535 */
+    int32_t group_k;                   /* % 64 == 0, divides K */
+    int32_t split_k;                   /* 1 .. 256: K is cut into split_k ranges of 64-row chunks */
+    int32_t out_dtype;                 /* W6A16_OUT_BF16 or W6A16_OUT_F32 */
+} w6a16_args;
+
+/* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
+size_t w6a16_args_size(void);
+
+/* Bytes of fp32 split-K partials `w6a16_matmul` needs (0 for split_k == 1). */
+int w6a16_workspace_size(const w6a16_args *args, size_t *bytes);
+
+/* Split-K for a shape: the smallest power of two (<= 64) giving about two wavefronts per SIMD, keeping at least two
+ * chunks per range and split_k * M <= K / 20 (bounded partial traffic).  Replaces the split-K rule of plan_int6
+ * (rwkv_next/kernels/int6_gemm.py:239-250). */
+int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K);
+
+/* C = A @ dequant(W) on `stream` (hipStream_t).  Replaces `_impl` + `_w6a16` (int6_gemm.py:253-287, 156-215). */
+int w6a16_matmul(const w6a16_args *args, void *stream);
+
+/* w[b][k][n] = scale * q ([B][K][N], batch stride in elements) as bf16 (W6A16_OUT_BF16) or fp32 (W6A16_OUT_F32):
+ * the large-M path, where a library GEMM on the dequantised weight wins.  Replaces dequantize_int6
+ * (int6_gemm.py:115-131) on the device.  N % 16 == 0; all pointers 16-byte aligned. */
+int w6a16_dequantize(const uint8_t *lo, const uint8_t *hi, const uint16_t *scales, void *w, int32_t B, int32_t K,
+                     int32_t N, int32_t group_k, int64_t lo_batch_stride, int64_t hi_batch_stride,
+                     int64_t scales_batch_stride, int64_t w_batch_stride, int32_t out_dtype, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RWKV_NEXT_AMD_W6A16_H */

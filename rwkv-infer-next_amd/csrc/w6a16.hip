@@ -1,0 +1,390 @@
+// w6a16.hip -- weight-only 6-bit GEMM / GEMV (W6A16) on gfx950, reading the reference's bit-plane format directly.
+//
+// Format (rwkv_next/kernels/int6_gemm.py:14-38, 73-112): a (K, N) weight, N contiguous, quantised symmetrically to
+// q in [-32, 31] per (group of group_k rows, column) with an fp16 scale s, w ~ s q.  Stored as u = q + 32 in [0, 63]
+// split over two byte planes per 64-row chunk c:
+//     lo[c*32 + j][n] = (u[c*64 + j] & 15) | (u[c*64 + j + 32] & 15) << 4                         j < 32
+//     hi[c*16 + j][n] = u[c*64 + j] >> 4 | (u[.. + j + 16] >> 4) << 2 | (u[.. + j + 32] >> 4) << 4
+//                       | (u[.. + j + 48] >> 4) << 6                                                 j < 16
+// C[b][m][n] = sum_k A[b][m][k] s[k / group_k][n] q[k][n] with fp32 accumulation (int6_gemm.py:156-215).
+//
+// One wavefront computes a 16 (M) x 128 (N) output tile over a range of 64-row chunks (split-K over chunk ranges):
+//   * the chunk's 48 plane rows x 128 columns (6 KB) are loaded coalesced (16 bytes per lane, 8 lanes per row),
+//     one chunk ahead in registers, and written to the wave's own LDS buffer (no workgroup barrier: a wave's LDS
+//     operations execute in order);
+//   * ds_read_b64_tr_b8 hands each lane 8 consecutive plane rows of one column -- within each 16-lane group, lane
+//     L receives byte L & 7 of the 8-byte reads of lanes (L & 15) / 8 + 2 e, so lane s of group q reading
+//     row base + s / 2, columns 8 (s & 1) .. gives lane (i, q) rows base + e of column i -- which is exactly the
+//     B operand of v_mfma_f32_16x16x32_bf16 (8 consecutive k of one column).  One read of the lo plane covers both
+//     32-row halves of the chunk (low and high nibbles), one read of the hi plane supplies the top 2 bits;
+//   * the 6-bit code u becomes a bf16 operand without conversion instructions: 0x4300 | u is the bf16 of 128 + u,
+//     exact, assembled for two values with one v_perm_b32 against a register of 0x43 bytes.  One extra MFMA per
+//     chunk against a constant B of -160 removes the bias (128 + u - 160 = q) exactly, shared by the 8 tiles;
+//   * each chunk's fp32 tile is scaled by s (fp16) and accumulated; the result (or an fp32 split-K partial) is
+//     stored at the end.
+// Rows m >= M and columns n >= N are zero-filled on load and not stored.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "w6a16.h"
+
+namespace w6 {
+namespace {
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
+typedef int v2i __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) v2i lds_v2i;
+
+constexpr int kTileN = 128;          // columns per wavefront
+constexpr int kTiles = kTileN / 16;  // 16x16 MFMA tiles per wavefront
+constexpr int kPitch = 136;          // LDS row pitch in bytes (128 + 8: the 8 rows of one transposing read differ in bank)
+constexpr int kRows = 48;            // plane rows per chunk: 32 lo + 16 hi
+constexpr int kScaleOff = kRows * kPitch;    // the chunk's 128 fp16 scales follow the plane rows
+constexpr int kBuf = kScaleOff + 2 * kTileN;
+
+struct Args {
+    const uint16_t* a;
+    int64_t sa_b, sa_m;
+    const uint8_t *lo, *hi;
+    int64_t sl_b, sh_b;
+    const uint16_t* sc;
+    int64_t ss_b;
+    void* out;
+    int64_t so_b, so_m;
+    float* part;  // split-K partials [split][B][M][N] fp32, or null
+    int32_t B, M, N, K, group_k, split_k, out_dtype, m_tiles, chunks_per_split;
+};
+
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+__device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+
+// Orders LDS traffic between the lanes of one wavefront (its LDS instructions execute in issue order).
+__device__ __forceinline__ void wave_lds_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// 4 codes u (one per byte) -> 4 bf16 values 128 + u as two dwords.
+__device__ __forceinline__ void codes_to_bf16(uint32_t u, uint32_t& lo2, uint32_t& hi2) {
+    lo2 = __builtin_amdgcn_perm(0x43434343u, u, 0x04010400u);  // bytes: u0, 0x43, u1, 0x43
+    hi2 = __builtin_amdgcn_perm(0x43434343u, u, 0x04030402u);  // bytes: u2, 0x43, u3, 0x43
+}
+
+__device__ __forceinline__ void store8(__bf16* dst, const float (&v)[8]) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        o[e] = (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[2 * e]) |
+               (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)v[2 * e + 1]) << 16;
+    *reinterpret_cast<u4*>(dst) = u4{o[0], o[1], o[2], o[3]};
+}
+
+__device__ __forceinline__ void store8(float* dst, const float (&v)[8]) {
+    *reinterpret_cast<f4*>(dst) = f4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f4*>(dst + 4) = f4{v[4], v[5], v[6], v[7]};
+}
+
+// One chunk's operands, held in registers between its load and its use.
+struct Stage {
+    u4 plane[6];   // plane rows 8 k + lane / 8 of the chunk (0..31 lo, 32..47 hi), 16 columns each
+    u4 a[2];       // A[m0 + i][chunk * 64 + 32 h + 8 q .. + 7]
+    uint32_t sc;   // scales of columns n0 + 2 lane, n0 + 2 lane + 1 for the chunk's group
+};
+
+// Loads never branch: a column or row outside the matrix is clamped to one inside it.  Output columns depend only
+// on their own weight columns and scales, output rows only on their own A rows, so the clamped values land in
+// outputs that are never stored.
+__device__ __forceinline__ void load_stage(const Args& p, int b, int m0, int n0, int c, Stage& s) {
+    const int lane = threadIdx.x & 63;
+    const int seg = lane & 7, rr = lane >> 3;
+    const int n = min(n0 + 16 * seg, p.N - 16);
+    const uint8_t* const lo = p.lo + (int64_t)b * p.sl_b + ((int64_t)c * 32 + rr) * p.N + n;
+    const uint8_t* const hi = p.hi + (int64_t)b * p.sh_b + ((int64_t)c * 16 + rr) * p.N + n;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s.plane[k] = *reinterpret_cast<const u4*>(lo + (int64_t)(8 * k) * p.N);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) s.plane[4 + k] = *reinterpret_cast<const u4*>(hi + (int64_t)(8 * k) * p.N);
+    const int i = lane & 15, q = lane >> 4;
+    const int m = min(m0 + i, p.M - 1);
+    const uint16_t* const arow = p.a + (int64_t)b * p.sa_b + (int64_t)m * p.sa_m + (int64_t)c * 64 + 8 * q;
+    s.a[0] = *reinterpret_cast<const u4*>(arow);
+    s.a[1] = *reinterpret_cast<const u4*>(arow + 32);
+    const int g = (c * 64) / p.group_k;
+    const int col = min(n0 + 2 * lane, p.N - 2);
+    s.sc = *reinterpret_cast<const uint32_t*>(p.sc + (int64_t)b * p.ss_b + (int64_t)g * p.N + col);
+}
+
+// Contract one chunk into acc: stage it in the wave's LDS buffer, read it back transposed, dequantise, MFMA.
+__device__ __forceinline__ void process_stage(const Stage& s, uint8_t* buf, f4 (&acc)[kTiles]) {
+    const int lane = threadIdx.x & 63, q = lane >> 4, i = lane & 15;
+    const int seg = lane & 7, rr = lane >> 3;
+    wave_lds_sync();  // the previous chunk's reads of buf are issued before these writes
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        uint8_t* dst = buf + (8 * k + rr) * kPitch + 16 * seg;
+        *reinterpret_cast<uint2*>(dst) = uint2{s.plane[k][0], s.plane[k][1]};
+        *reinterpret_cast<uint2*>(dst + 8) = uint2{s.plane[k][2], s.plane[k][3]};
+    }
+    *reinterpret_cast<uint32_t*>(buf + kScaleOff + 4 * lane) = s.sc;
+    wave_lds_sync();
+    const bf8 bias = __builtin_bit_cast(bf8, u4{0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u});  // -160
+    const bf8 a0 = __builtin_bit_cast(bf8, s.a[0]), a1 = __builtin_bit_cast(bf8, s.a[1]);
+    f4 corr = mfma(a0, bias, f4{0.f, 0.f, 0.f, 0.f});
+    corr = mfma(a1, bias, corr);
+    const int sel = 2 * (q >> 1);  // hi-plane field of rows 8 q .. (first half); the second half's is 4 bits up
+    const int r = lane & 15;
+    const int off = (r >> 1) * kPitch + 8 * (r & 1);
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const v2i lov = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(buf + (8 * q) * kPitch + off + 16 * t));
+        const v2i hiv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(buf + (32 + 8 * (q & 1)) * kPitch + off + 16 * t));
+        const float sv = h2f(*reinterpret_cast<const uint16_t*>(buf + kScaleOff + 2 * (16 * t + i)));
+        // lov: lo-plane rows 8 q + e of column i (e = 0..7, one byte each); hiv: hi-plane rows 8 (q & 1) + e
+        uint32_t o0[4], o1[4];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const uint32_t L = (uint32_t)lov[d], H = (uint32_t)hiv[d];
+            const uint32_t u0 = (L & 0x0F0F0F0Fu) | ((H >> sel) << 4 & 0x30303030u);       // rows 8 q + e
+            const uint32_t u1 = ((L >> 4) & 0x0F0F0F0Fu) | ((H >> sel) & 0x30303030u);   // rows 32 + 8 q + e
+            codes_to_bf16(u0, o0[2 * d], o0[2 * d + 1]);
+            codes_to_bf16(u1, o1[2 * d], o1[2 * d + 1]);
+        }
+        const bf8 w0 = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
+        const bf8 w1 = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+        f4 tc = mfma(a0, w0, corr);
+        tc = mfma(a1, w1, tc);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[t][v] += tc[v] * sv;
+    }
+}
+
+__global__ __launch_bounds__(64) void w6a16_kernel(const Args p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kBuf];
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int n0 = blockIdx.x * kTileN;
+    const int split = blockIdx.y;
+    const int b = blockIdx.z / p.m_tiles, m0 = (blockIdx.z % p.m_tiles) * 16;
+    const int nchunks = p.K / 64;
+    const int c0 = split * p.chunks_per_split;
+    const int c1 = min(nchunks, c0 + p.chunks_per_split);
+
+    f4 acc[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+
+    if (c0 < c1) {
+        // Two chunks in flight: while one is contracted the next one's loads are outstanding.  The last chunk is
+        // re-loaded in place of chunks past the range (a cache hit), so every load is unconditional.
+        Stage s0, s1;
+        load_stage(p, b, m0, n0, c0, s0);
+        load_stage(p, b, m0, n0, min(c0 + 1, c1 - 1), s1);
+        for (int c = c0; c < c1; c += 2) {
+            process_stage(s0, lds, acc);
+            load_stage(p, b, m0, n0, min(c + 2, c1 - 1), s0);
+            if (c + 1 < c1) process_stage(s1, lds, acc);
+            load_stage(p, b, m0, n0, min(c + 3, c1 - 1), s1);
+        }
+    }
+
+    // lane (i, q) holds C[m0 + 4 q + v][n0 + 16 t + i]
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int n = n0 + 16 * t + i;
+        if (n >= p.N) continue;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+            const int m = m0 + 4 * q + v;
+            if (m >= p.M) continue;
+            if (p.part) {
+                p.part[(((int64_t)split * p.B + b) * p.M + m) * p.N + n] = acc[t][v];
+            } else if (p.out_dtype == W6A16_OUT_F32) {
+                reinterpret_cast<float*>(p.out)[(int64_t)b * p.so_b + (int64_t)m * p.so_m + n] = acc[t][v];
+            } else {
+                reinterpret_cast<__bf16*>(p.out)[(int64_t)b * p.so_b + (int64_t)m * p.so_m + n] = (__bf16)acc[t][v];
+            }
+        }
+    }
+}
+
+// out[b][m][n] = sum over splits of the fp32 partials.
+__global__ __launch_bounds__(256) void w6a16_reduce_kernel(const Args p) {
+    const int64_t total = (int64_t)p.B * p.M * p.N;
+    for (int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x; x < total; x += (int64_t)gridDim.x * 256) {
+        float s = 0.f;
+        for (int sp = 0; sp < p.split_k; ++sp) s += p.part[sp * total + x];
+        const int n = (int)(x % p.N);
+        const int64_t bm = x / p.N;
+        const int m = (int)(bm % p.M), b = (int)(bm / p.M);
+        const int64_t o = (int64_t)b * p.so_b + (int64_t)m * p.so_m + n;
+        if (p.out_dtype == W6A16_OUT_F32)
+            reinterpret_cast<float*>(p.out)[o] = s;
+        else
+            reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)s;
+    }
+}
+
+// Dequantise: w[b][k][n] = s q as bf16 or fp32 (the large-M path hands the result to a library GEMM).  One thread
+// per (lo row c * 32 + j, 16 columns): it writes rows c * 64 + j and c * 64 + j + 32 of those columns.
+template <typename OutT>
+__global__ __launch_bounds__(256) void w6a16_dequant_kernel(const uint8_t* lo, const uint8_t* hi, const uint16_t* sc,
+                                                            OutT* w, int32_t K, int32_t N, int32_t group_k,
+                                                            int64_t sl_b, int64_t sh_b, int64_t ss_b, int64_t sw_b,
+                                                            int32_t B) {
+    const int n16 = N / 16;
+    const int64_t per = (int64_t)(K / 2) * n16;
+    for (int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x; x < per * B; x += (int64_t)gridDim.x * 256) {
+        const int b = (int)(x / per);
+        const int64_t y = x % per;
+        const int n = (int)(y % n16) * 16;
+        const int lrow = (int)(y / n16);  // c * 32 + j
+        const int c = lrow >> 5, j = lrow & 31;
+        const u4 L = *reinterpret_cast<const u4*>(lo + b * sl_b + (int64_t)lrow * N + n);
+        const u4 H = *reinterpret_cast<const u4*>(hi + b * sh_b + ((int64_t)c * 16 + (j & 15)) * N + n);
+        const int sh0 = 2 * (j >> 4), sh1 = sh0 + 4;  // 2-bit fields of rows j and j + 32
+        const int r0 = c * 64 + j, r1 = r0 + 32;
+        const uint16_t* const s0 = sc + b * ss_b + (int64_t)(r0 / group_k) * N + n;
+        const uint16_t* const s1 = sc + b * ss_b + (int64_t)(r1 / group_k) * N + n;
+        OutT* const w0 = w + b * sw_b + (int64_t)r0 * N + n;
+        OutT* const w1 = w + b * sw_b + (int64_t)r1 * N + n;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {  // columns n + 8 h .. + 7
+            const u4 sa = *reinterpret_cast<const u4*>(s0 + 8 * h), sb = *reinterpret_cast<const u4*>(s1 + 8 * h);
+            float va[8], vb[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int col = 8 * h + e, wd = col >> 2, by = 8 * (col & 3);
+                const uint32_t l = (L[wd] >> by) & 0xFF, hh = (H[wd] >> by) & 0xFF;
+                const int q0 = (int)((l & 15) | (((hh >> sh0) & 3) << 4)) - 32;
+                const int q1 = (int)((l >> 4) | (((hh >> sh1) & 3) << 4)) - 32;
+                va[e] = h2f((uint16_t)(sa[e >> 1] >> (16 * (e & 1)))) * (float)q0;  // exact: 11 x 6 bit product
+                vb[e] = h2f((uint16_t)(sb[e >> 1] >> (16 * (e & 1)))) * (float)q1;
+            }
+            store8(w0 + 8 * h, va);
+            store8(w1 + 8 * h, vb);
+        }
+    }
+}
+
+int cu_count() {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
+        return v;
+    return 256;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+int validate(const w6a16_args* a) {
+    if (!a) return WKV7_ERR_NULL;
+    if (a->B < 1 || a->M < 0 || a->N < 1 || a->K < 64 || a->K % 64 || a->N % 16) return WKV7_ERR_SHAPE;
+    if (a->group_k < 64 || a->group_k % 64 || a->K % a->group_k) return WKV7_ERR_SHAPE;
+    if (a->split_k < 1 || a->split_k > 256) return WKV7_ERR_ARG;
+    if (a->out_dtype != W6A16_OUT_BF16 && a->out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
+    if (a->M == 0) return WKV7_OK;
+    if (!a->a || !a->lo || !a->hi || !a->scales || !a->out) return WKV7_ERR_NULL;
+    if (!aligned16(a->a) || !aligned16(a->lo) || !aligned16(a->hi) || (reinterpret_cast<uintptr_t>(a->scales) & 3) ||
+        a->a_row_stride % 8 || a->a_batch_stride % 8 || a->lo_batch_stride % 16 || a->hi_batch_stride % 16 ||
+        a->scales_batch_stride % 2)
+        return WKV7_ERR_ALIGN;
+    if (a->a_row_stride < a->K || a->out_row_stride < a->N) return WKV7_ERR_SHAPE;
+    if ((int64_t)a->B * ((a->M + 15) / 16) > 65535) return WKV7_ERR_SHAPE;  // grid z: batch x 16-row tiles
+    if (a->split_k > 1 && (!a->workspace || a->workspace_bytes < (size_t)a->split_k * a->B * a->M * a->N * 4))
+        return WKV7_ERR_WORKSPACE;
+    return WKV7_OK;
+}
+
+}  // namespace
+}  // namespace w6
+
+extern "C" {
+
+size_t w6a16_args_size(void) { return sizeof(w6a16_args); }
+
+int w6a16_workspace_size(const w6a16_args* a, size_t* bytes) {
+    if (!a || !bytes) return WKV7_ERR_NULL;
+    *bytes = a->split_k > 1 ? (size_t)a->split_k * a->B * (size_t)a->M * a->N * 4 : 0;
+    return WKV7_OK;
+}
+
+int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
+    if (B < 1 || M < 1 || N < 1 || K < 64) return 1;
+    const int64_t waves = (int64_t)B * ((M + 15) / 16) * ((N + w6::kTileN - 1) / w6::kTileN);
+    const int chunks = K / 64;
+    const int64_t target = 8LL * w6::cu_count();  // two wavefronts per SIMD
+    // The fp32 partials (written, then read by the reduction: 8 bytes per split, row and column) stay under about
+    // half the weight's own 0.77 bytes per element: split * M <= K / 20.
+    int sk = 1;
+    while (waves * sk < target && sk * 2 <= 64 && chunks / (sk * 2) >= 2 && (int64_t)sk * 2 * M * 20 <= K) sk *= 2;
+    return sk;
+}
+
+int w6a16_matmul(const w6a16_args* a, void* stream) {
+    const int rc = w6::validate(a);
+    if (rc != WKV7_OK || a->M == 0) return rc;
+    w6::Args p{};
+    p.a = a->a;
+    p.sa_b = a->a_batch_stride;
+    p.sa_m = a->a_row_stride;
+    p.lo = a->lo;
+    p.hi = a->hi;
+    p.sl_b = a->lo_batch_stride;
+    p.sh_b = a->hi_batch_stride;
+    p.sc = a->scales;
+    p.ss_b = a->scales_batch_stride;
+    p.out = a->out;
+    p.so_b = a->out_batch_stride;
+    p.so_m = a->out_row_stride;
+    p.part = a->split_k > 1 ? static_cast<float*>(a->workspace) : nullptr;
+    p.B = a->B;
+    p.M = a->M;
+    p.N = a->N;
+    p.K = a->K;
+    p.group_k = a->group_k;
+    p.split_k = a->split_k;
+    p.out_dtype = a->out_dtype;
+    p.m_tiles = (a->M + 15) / 16;
+    const int chunks = a->K / 64;
+    p.chunks_per_split = (chunks + a->split_k - 1) / a->split_k;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const dim3 grid((a->N + w6::kTileN - 1) / w6::kTileN, a->split_k, a->B * p.m_tiles);
+    hipLaunchKernelGGL(w6::w6a16_kernel, grid, dim3(64), 0, s, p);
+    if (a->split_k > 1) {
+        const int64_t total = (int64_t)a->B * a->M * a->N;
+        const int64_t blocks = std::min<int64_t>((total + 255) / 256, 8LL * w6::cu_count());
+        hipLaunchKernelGGL(w6::w6a16_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+    }
+    return static_cast<int>(hipGetLastError());
+}
+
+int w6a16_dequantize(const uint8_t* lo, const uint8_t* hi, const uint16_t* scales, void* w, int32_t B, int32_t K,
+                     int32_t N, int32_t group_k, int64_t lo_batch_stride, int64_t hi_batch_stride,
+                     int64_t scales_batch_stride, int64_t w_batch_stride, int32_t out_dtype, void* stream) {
+    if (!lo || !hi || !scales || !w) return WKV7_ERR_NULL;
+    if (B < 1 || N < 16 || N % 16 || K < 64 || K % 64 || group_k < 64 || group_k % 64 || K % group_k)
+        return WKV7_ERR_SHAPE;
+    if (out_dtype != W6A16_OUT_BF16 && out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
+    if (!w6::aligned16(lo) || !w6::aligned16(hi) || !w6::aligned16(scales) || !w6::aligned16(w) ||
+        lo_batch_stride % 16 || hi_batch_stride % 16 || scales_batch_stride % 8 || w_batch_stride % 8)
+        return WKV7_ERR_ALIGN;
+    const int64_t total = (int64_t)B * (K / 2) * (N / 16);
+    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 16LL * w6::cu_count());
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (out_dtype == W6A16_OUT_F32)
+        hipLaunchKernelGGL(w6::w6a16_dequant_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s, lo, hi, scales,
+                           static_cast<float*>(w), K, N, group_k, lo_batch_stride, hi_batch_stride,
+                           scales_batch_stride, w_batch_stride, B);
+    else
+        hipLaunchKernelGGL(w6::w6a16_dequant_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, s, lo, hi, scales,
+                           static_cast<__bf16*>(w), K, N, group_k, lo_batch_stride, hi_batch_stride,
+                           scales_batch_stride, w_batch_stride, B);
+    return static_cast<int>(hipGetLastError());
+}
+
+}  // extern "C"

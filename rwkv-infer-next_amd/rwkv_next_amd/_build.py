@@ -1,4 +1,4 @@
-"""Build librwkv7_hip.so: the HIP kernels and the C ABI of include/wkv7.h, compiled for gfx950 with hipcc.
+"""Build librwkv7_hip.so: the HIP kernels and the C ABI of include/wkv7.h and include/w6a16.h, compiled for gfx950 with hipcc.
 
 The library is a plain shared object (no torch symbols); the Python layer loads it with ctypes after torch, so it
 binds to the HIP runtime torch already loaded (same SONAME, libamdhip64.so.7).
@@ -21,7 +21,7 @@ LIB_NAME = "librwkv7_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 BUILD_DIR = os.path.join(PROJECT_DIR, "_build")
 
-SOURCES = ("wkv7_recurrent.hip", "wkv7_chunked.hip", "wkv7_pool.hip", "wkv7_timemix.hip", "wkv7_capi.hip")
+SOURCES = ("wkv7_recurrent.hip", "wkv7_chunked.hip", "wkv7_pool.hip", "wkv7_timemix.hip", "w6a16.hip", "wkv7_capi.hip")
 HEADERS = ("wkv7_device.h", "wkv7_launch.h")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -69,7 +69,7 @@ def sources_newer_than_library() -> bool:
     if not os.path.exists(LIB_PATH):
         return True
     t = os.path.getmtime(LIB_PATH)
-    files = [os.path.join(CSRC, f) for f in SOURCES + HEADERS] + [os.path.join(INCLUDE, "wkv7.h")]
+    files = [os.path.join(CSRC, f) for f in SOURCES + HEADERS] + [os.path.join(INCLUDE, h) for h in ("wkv7.h", "w6a16.h")]
     return any(os.path.getmtime(f) > t for f in files)
 
 

@@ -1,4 +1,4 @@
-"""ctypes binding of librwkv7_hip.so (the C ABI declared in include/wkv7.h).
+"""ctypes binding of librwkv7_hip.so (the C ABI declared in include/wkv7.h and include/w6a16.h).
 
 The library must have been built (rwkv_next_amd._build / __graft_entry__.build()).  There is no fallback: if the
 shared object is missing or does not match this binding, importing the kernels raises.
@@ -25,6 +25,10 @@ ALGO_CHUNKED = 2
 EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
             "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore", "wkv7_timemix_prologue",
             "wkv7_timemix_epilogue")
+W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split", "w6a16_matmul",
+                  "w6a16_dequantize")
+W6A16_OUT_BF16 = 0
+W6A16_OUT_F32 = 2
 MAX_MOVES = 1024
 
 _vp = ctypes.c_void_p
@@ -74,6 +78,19 @@ class EpilogueArgs(ctypes.Structure):
         ("eps", ctypes.c_float), ("H", ctypes.c_int32), ("head_size", ctypes.c_int32)]
 
 
+class W6a16Args(ctypes.Structure):
+    """Mirror of `w6a16_args` (include/w6a16.h)."""
+    _fields_ = [
+        ("a", _vp), ("a_batch_stride", ctypes.c_int64), ("a_row_stride", ctypes.c_int64),
+        ("lo", _vp), ("hi", _vp), ("lo_batch_stride", ctypes.c_int64), ("hi_batch_stride", ctypes.c_int64),
+        ("scales", _vp), ("scales_batch_stride", ctypes.c_int64),
+        ("out", _vp), ("out_batch_stride", ctypes.c_int64), ("out_row_stride", ctypes.c_int64),
+        ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
+        ("B", ctypes.c_int32), ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
+        ("group_k", ctypes.c_int32), ("split_k", ctypes.c_int32), ("out_dtype", ctypes.c_int32),
+    ]
+
+
 class Wkv7Error(RuntimeError):
     def __init__(self, code: int, msg: str):
         super().__init__(f"wkv7 error {code}: {msg}")
@@ -115,10 +132,21 @@ def load(path: str = LIB_PATH):
     lib.wkv7_timemix_prologue.argtypes = [ctypes.POINTER(PrologueArgs), _vp]
     lib.wkv7_timemix_epilogue.restype = ctypes.c_int
     lib.wkv7_timemix_epilogue.argtypes = [ctypes.POINTER(EpilogueArgs), _vp]
+    lib.w6a16_args_size.restype = ctypes.c_size_t
+    lib.w6a16_workspace_size.restype = ctypes.c_int
+    lib.w6a16_workspace_size.argtypes = [ctypes.POINTER(W6a16Args), ctypes.POINTER(ctypes.c_size_t)]
+    lib.w6a16_plan_split.restype = ctypes.c_int
+    lib.w6a16_plan_split.argtypes = [i32, i32, i32, i32]
+    lib.w6a16_matmul.restype = ctypes.c_int
+    lib.w6a16_matmul.argtypes = [ctypes.POINTER(W6a16Args), _vp]
+    lib.w6a16_dequantize.restype = ctypes.c_int
+    lib.w6a16_dequantize.argtypes = [_vp, _vp, _vp, _vp, i32, i32, i32, i32, i64, i64, i64, i64, i32, _vp]
     if lib.wkv7_abi_version() != WKV7_ABI_VERSION:
         raise ImportError(f"{path}: ABI version {lib.wkv7_abi_version()} != {WKV7_ABI_VERSION}")
     if lib.wkv7_args_size() != ctypes.sizeof(Wkv7Args):
         raise ImportError(f"{path}: sizeof(wkv7_args) {lib.wkv7_args_size()} != binding {ctypes.sizeof(Wkv7Args)}")
+    if lib.w6a16_args_size() != ctypes.sizeof(W6a16Args):
+        raise ImportError(f"{path}: sizeof(w6a16_args) {lib.w6a16_args_size()} != binding {ctypes.sizeof(W6a16Args)}")
     _lib = lib
     return lib
 

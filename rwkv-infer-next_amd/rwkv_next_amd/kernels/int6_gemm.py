@@ -1,0 +1,225 @@
+"""Weight-only 6-bit GEMM / GEMV (W6A16) on the HIP kernels of include/w6a16.h.
+
+Same calls, arguments and weight format as the reference module rwkv_next/kernels/int6_gemm.py, so weights
+quantised there load unchanged:
+
+    quantize_int6(w, group_k=128, clip_search=True) -> (lo, hi, scales, group_k)       (int6_gemm.py:73-112)
+    dequantize_int6(lo, hi, sc, group_k, dtype)     -> w                               (int6_gemm.py:115-131)
+    plan_int6(M, N, K, n_batch, device)             -> (split_k, use_dot)              (int6_gemm.py:239-250)
+    int6_matmul(a, lo, hi, s, group_k, split_k=None, use_dot=None)                    (int6_gemm.py:296-308)
+    int6_matmul_op(a, lo, hi, s, group_k, split_k, use_dot)  op rwkv_next_amd::int6_matmul   (int6_gemm.py:316-323)
+
+Format: a (K, N) weight (N contiguous) is quantised to q in [-32, 31] per (group of group_k rows, column) with an
+fp16 scale, w ~ s q; the code u = q + 32 is split into bit planes per 64-row chunk c:
+    lo[c*32 + j] = lo4(row j) | lo4(row j + 32) << 4                                        j < 32
+    hi[c*16 + j] = hi2(row j) | hi2(row j + 16) << 2 | hi2(row j + 32) << 4 | hi2(row j + 48) << 6   j < 16
+
+Compute: one MFMA kernel for every M up to MAX_M (the reference's reduction form for M = 1 has no counterpart:
+an MFMA with M padded to 16 rows costs the CDNA4 matrix core less than a VALU reduction costs the vector units, and
+the weight bytes, not the arithmetic, bound both).  `use_dot` is accepted for the reference's signature and does
+not change the computation.  Above MAX_M the weight is dequantised once to bf16 and the product goes to the
+library GEMM (hipBLASLt through torch.matmul), which is compute-bound there.
+
+Activations are bf16; the result is bf16 (fp32 accumulation).  Every call runs on the current stream, no host sync.
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+
+from .. import _lib
+
+CHUNK = 64
+QMIN, QMAX = -32, 31
+# Largest M that the W6A16 kernel serves; larger M dequantises once and runs the library GEMM.
+MAX_M = int(os.environ.get("RWKV_INT6_MAX_M", "256"))
+_RATIOS = (1.0, 0.97, 0.94, 0.91, 0.88, 0.85)
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# quantisation / packing (host-side preparation of the weights, run once at load time on the weight's device)
+# ----------------------------------------------------------------------------------------------------------------
+@torch.no_grad()
+def quantize_int6(w, group_k=128, clip_search=True):
+    """(K, N) or (B, K, N) float -> (lo uint8 (.., K/2, N), hi uint8 (.., K/4, N), scales fp16 (.., K/group_k, N),
+    group_k).  group_k outside (0, K) means one group of K rows; it must be a multiple of 64 dividing K.
+
+    The scale of each (group, column) is fp16(absmax * r / 31.5) for the clip ratio r in
+    (1, .97, .94, .91, .88, .85) (only 1 without clip_search) whose rounded weights have the least squared error,
+    the first such r on ties; q = clamp(round(w / s), -32, 31) with the stored fp16 scale (int6_gemm.py:92-104).
+    """
+    squeeze = w.dim() == 2
+    if squeeze:
+        w = w.unsqueeze(0)
+    B, K, N = w.shape
+    g = group_k if group_k and 0 < group_k < K else K
+    if K % CHUNK or g % CHUNK or K % g:
+        raise ValueError(f"int6 needs K % 64 == 0 and group_k % 64 == 0 dividing K (K={K}, group_k={g})")
+    G, C = K // g, K // CHUNK
+    lo = torch.empty((B, K // 2, N), dtype=torch.uint8, device=w.device)
+    hi = torch.empty((B, K // 4, N), dtype=torch.uint8, device=w.device)
+    sc = torch.empty((B, G, N), dtype=torch.float16, device=w.device)
+    cols = max(256, (1 << 23) // K)  # column blocks keep the fp32 temporaries to ~32 MB
+    ratios = _RATIOS if clip_search else _RATIOS[:1]
+    for b in range(B):
+        for n0 in range(0, N, cols):
+            n1 = min(N, n0 + cols)
+            x = w[b, :, n0:n1].float().view(G, g, n1 - n0)
+            amax = x.abs().amax(dim=1, keepdim=True).clamp_min(1e-10)
+            best_s = best_err = None
+            for r in ratios:
+                s = (amax * r / 31.5).half().float()
+                err = (torch.round(x / s).clamp(QMIN, QMAX) * s - x).square().sum(dim=1, keepdim=True)
+                if best_s is None:
+                    best_s, best_err = s, err
+                else:
+                    better = err < best_err
+                    best_s = torch.where(better, s, best_s)
+                    best_err = torch.where(better, err, best_err)
+            u = (torch.round(x / best_s).clamp(QMIN, QMAX) + 32).to(torch.uint8).view(C, CHUNK, n1 - n0)
+            sc[b, :, n0:n1] = best_s.view(G, n1 - n0).half()
+            lo[b, :, n0:n1] = ((u[:, :32] & 15) | ((u[:, 32:] & 15) << 4)).view(K // 2, n1 - n0)
+            h2 = u >> 4
+            hi[b, :, n0:n1] = (h2[:, :16] | (h2[:, 16:32] << 2) | (h2[:, 32:48] << 4) | (h2[:, 48:] << 6)).view(
+                K // 4, n1 - n0)
+    if squeeze:
+        lo, hi, sc = lo[0], hi[0], sc[0]
+    return lo.contiguous(), hi.contiguous(), sc.contiguous(), g
+
+
+def _weights3(lo, hi, s):
+    L = lo if lo.dim() == 3 else lo.unsqueeze(0)
+    H = hi if hi.dim() == 3 else hi.unsqueeze(0)
+    S = s if s.dim() == 3 else s.unsqueeze(0)
+    if L.dtype != torch.uint8 or H.dtype != torch.uint8 or S.dtype != torch.float16:
+        raise TypeError("int6 weights are (lo uint8, hi uint8, scales float16)")
+    for t, name in ((L, "lo"), (H, "hi"), (S, "scales")):
+        if t.device.type != "cuda":
+            raise ValueError(f"{name} must be on a GPU (got {t.device})")
+    Bq, K2, N = L.shape
+    K = 2 * K2
+    if H.shape != (Bq, K // 4, N) or S.shape[0] != Bq or S.shape[2] != N:
+        raise ValueError(f"int6 planes do not match: lo {tuple(L.shape)}, hi {tuple(H.shape)}, s {tuple(S.shape)}")
+    return _aligned(L), _aligned(H), _aligned(S), Bq, K, N
+
+
+def _aligned(t: torch.Tensor) -> torch.Tensor:
+    """t contiguous at a 16-byte aligned address (the kernels load 16 bytes per lane)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _group_k(group_k, K, n_groups):
+    g = group_k if group_k and 0 < group_k < K else K
+    if g % CHUNK or K % g or K // g != n_groups:
+        raise ValueError(f"group_k {group_k} does not match K = {K} with {n_groups} scale rows")
+    return g
+
+
+@torch.no_grad()
+def dequantize_int6(lo, hi, sc, group_k, dtype=torch.float32):
+    """w = s q, (K, N) or (B, K, N) in `dtype` (bfloat16 or float32; float32 is exact), on the device."""
+    squeeze = lo.dim() == 2
+    L, H, S, Bq, K, N = _weights3(lo, hi, sc)
+    g = _group_k(group_k, K, S.shape[1])
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"dequantize_int6 writes bfloat16 or float32 (got {dtype})")
+    w = torch.empty((Bq, K, N), dtype=dtype, device=L.device)
+    with torch.cuda.device(L.device):
+        _lib.check(_lib.load().w6a16_dequantize(
+            L.data_ptr(), H.data_ptr(), S.data_ptr(), w.data_ptr(), Bq, K, N, g, L.stride(0), H.stride(0),
+            S.stride(0), w.stride(0), _lib.W6A16_OUT_F32 if dtype == torch.float32 else _lib.W6A16_OUT_BF16,
+            torch.cuda.current_stream(L.device).cuda_stream))
+    return w[0] if squeeze else w
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# dispatch
+# ----------------------------------------------------------------------------------------------------------------
+def plan_int6(M, N, K, n_batch, device=None):
+    """(split_k, use_dot) for one shape.  split_k is the kernel's rule (w6a16_plan_split: about two wavefronts per
+    SIMD, at least two 64-row chunks per split, split_k * M <= K / 20); use_dot is M > 1 as in the reference and
+    does not change the computation."""
+    if device is not None and torch.device(device).type == "cuda":
+        with torch.cuda.device(device):
+            sk = _lib.load().w6a16_plan_split(n_batch, M, N, K)
+    else:
+        sk = _lib.load().w6a16_plan_split(n_batch, M, N, K)
+    return int(sk), M > 1
+
+
+def _impl(a, lo, hi, s, group_k, split_k, out_dtype=None):
+    batched = a.dim() == 3
+    A = a if batched else a.unsqueeze(0)
+    if A.dtype != torch.bfloat16:
+        raise TypeError(f"int6_matmul takes bfloat16 activations (got {A.dtype})")
+    if A.device.type != "cuda":
+        raise ValueError(f"a must be on a GPU (got {A.device})")
+    L, H, S, Bq, K, N = _weights3(lo, hi, s)
+    B, M, Ka = A.shape
+    if Ka != K:
+        raise ValueError(f"K mismatch: a has {Ka}, int6 weight has {K}")
+    if Bq not in (1, B):
+        raise ValueError(f"weight batch {Bq} does not match activation batch {B}")
+    g = _group_k(group_k, K, S.shape[1])
+    odt = A.dtype if out_dtype is None else out_dtype
+    if odt not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"int6_matmul writes bfloat16 or float32 (got {odt})")
+    if M > MAX_M:  # prefill: compute-bound, dequantise once and use the library GEMM
+        w = dequantize_int6(L, H, S, g, dtype=torch.bfloat16)
+        C = torch.matmul(A, w[0] if Bq == 1 else w)
+        C = C.to(odt)
+        return C if batched else C[0]
+    out = torch.empty((B, M, N), dtype=odt, device=A.device)
+    if M == 0:
+        return out if batched else out[0]
+    if A.stride(2) != 1 or A.stride(1) % 8 or A.stride(0) % 8 or A.data_ptr() % 16:
+        A = _aligned(A)
+    args = _lib.W6a16Args()
+    args.a, args.a_batch_stride, args.a_row_stride = A.data_ptr(), A.stride(0), A.stride(1)
+    args.lo, args.hi, args.scales = L.data_ptr(), H.data_ptr(), S.data_ptr()
+    shared = Bq == 1 and B > 1
+    args.lo_batch_stride = 0 if shared else L.stride(0)
+    args.hi_batch_stride = 0 if shared else H.stride(0)
+    args.scales_batch_stride = 0 if shared else S.stride(0)
+    args.out, args.out_batch_stride, args.out_row_stride = out.data_ptr(), out.stride(0), out.stride(1)
+    args.B, args.M, args.N, args.K, args.group_k = B, M, N, K, g
+    args.split_k = max(1, int(split_k))
+    args.out_dtype = _lib.W6A16_OUT_F32 if odt == torch.float32 else _lib.W6A16_OUT_BF16
+    lib = _lib.load()
+    ws = None
+    if args.split_k > 1:
+        import ctypes
+        n = ctypes.c_size_t(0)
+        _lib.check(lib.w6a16_workspace_size(args, ctypes.byref(n)))
+        ws = torch.empty(int(n.value), dtype=torch.uint8, device=A.device)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), int(n.value)
+    _lib.check(lib.w6a16_matmul(args, torch.cuda.current_stream(A.device).cuda_stream))
+    return out if batched else out[0]
+
+
+def int6_matmul(a, lo, hi, s, group_k, split_k=None, use_dot=None, *, out_dtype=None):
+    """a (M, K) | (B, M, K) bf16 @ dequant(int6 weight (K, N) | (B, K, N)) -> (M, N) | (B, M, N) in a.dtype (or
+    out_dtype: bfloat16 / float32).  A single weight (K, N) is shared by every batch row.  Eager entry point; the
+    model-facing functional op is int6_matmul_op."""
+    B = a.shape[0] if a.dim() == 3 else 1
+    M, K, N = a.shape[-2], a.shape[-1], lo.shape[-1]
+    if split_k is None:
+        split_k, _ = plan_int6(M, N, K, B, a.device)
+    with torch.cuda.device(a.device):
+        return _impl(a, lo, hi, s, group_k, split_k, out_dtype)
+
+
+@torch.library.custom_op("rwkv_next_amd::int6_matmul", mutates_args=())
+def int6_matmul_op(a: torch.Tensor, lo: torch.Tensor, hi: torch.Tensor, s: torch.Tensor, group_k: int, split_k: int,
+                   use_dot: bool) -> torch.Tensor:
+    """Functional op with the schema of the reference's rwkv_next::int6_matmul (int6_gemm.py:316-323); the plan
+    (split_k, use_dot) comes from plan_int6, resolved by the caller."""
+    with torch.cuda.device(a.device):
+        return _impl(a, lo, hi, s, group_k, split_k)
+
+
+@int6_matmul_op.register_fake
+def _(a, lo, hi, s, group_k, split_k, use_dot):
+    return a.new_empty((*a.shape[:-1], lo.shape[-1]))

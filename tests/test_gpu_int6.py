@@ -1,0 +1,195 @@
+"""W6A16 on the GPU through the C ABI (include/w6a16.h), against the numpy oracle on the same weights.
+
+Tolerances (stated per test):
+  * dequantisation: exact (s q is exact in fp32; bf16 is its round-to-nearest-even);
+  * the W6A16 kernel, fp32 result: |C - C_ref| <= 2e-5 (|a| @ |w|) element-wise (fp32 accumulation of exact
+    bf16 x int6 products, scaled per 64-row chunk);
+  * bf16 result: that plus one bf16 rounding, 2^-8 |C_ref|;
+  * the dequantise-then-library-GEMM path (M > MAX_M): 8e-3 (|a| @ |w|) (the weight is rounded to bf16 first).
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_util import say
+
+from oracle import int6_ref as R
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+KERNEL_TOL = 2e-5
+GEMM_TOL = 8e-3
+
+
+def _weights(rng, Bq, K, N, g):
+    u = rng.integers(0, 64, size=(Bq, K, N), dtype=np.uint8)
+    lo, hi = R.pack_codes(u)
+    sc = rng.uniform(0.002, 0.05, size=(Bq, K // g, N)).astype(np.float16)
+    return lo, hi, sc
+
+
+def _act(rng, B, M, K):
+    a = torch.from_numpy(rng.standard_normal((B, M, K)).astype(np.float32)).to(torch.bfloat16)
+    return a
+
+
+def _dev(*xs):
+    return [torch.from_numpy(np.ascontiguousarray(x)).to(DEV) for x in xs]
+
+
+def _check(C, a_bf, lo, hi, sc, g, tol, bf16_out=False, shared=False):
+    a64 = a_bf.float().numpy().astype(np.float64)
+    L, H, S = (lo[0], hi[0], sc[0]) if shared else (lo, hi, sc)
+    ref = R.int6_matmul_ref(a64, L, H, S, g)
+    bound = R.abs_bound(a64, L, H, S, g)
+    got = C.float().cpu().numpy().astype(np.float64)
+    lim = tol * bound + (2.0 ** -8 * np.abs(ref) if bf16_out else 0.0) + 1e-30
+    err = np.abs(got - ref)
+    worst = np.unravel_index(np.argmax(err / lim), err.shape)
+    assert (err <= lim).all(), f"worst at {worst}: got {got[worst]}, ref {ref[worst]}, limit {lim[worst]}"
+
+
+@pytest.mark.parametrize("B,M,N,K,g,split", [
+    (1, 1, 256, 512, 128, None),
+    (1, 1, 4096, 4096, 128, None),
+    (1, 2, 1024, 2048, 128, None),
+    (1, 16, 2048, 1024, 64, None),
+    (1, 37, 640, 1024, 128, None),
+    (1, 64, 1024, 4096, 128, None),
+    (1, 1, 16, 128, 128, None),       # narrowest N: one 16-column tile
+    (1, 5, 144, 256, 256, None),      # N not a multiple of the 128-column wave tile; one group of K rows
+    (1, 3, 512, 1024, 128, 1),
+    (1, 3, 512, 1024, 128, 3),        # uneven split ranges
+    (1, 1, 512, 640, 64, 7),          # 10 chunks over 7 splits: one empty range
+    (1, 1, 256, 4096, 128, 64),
+])
+def test_matmul_matches_oracle(B, M, N, K, g, split):
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    say("int6_matmul", dict(B=B, M=M, N=N, K=K, g=g, split=split))
+    rng = np.random.default_rng(100 + M + N + K)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    C = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert C.shape == (M, N) and C.dtype == torch.float32
+    _check(C[None], a, lo, hi, sc, g, KERNEL_TOL)
+    Cb = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g, split_k=split)
+    torch.cuda.synchronize()
+    assert Cb.dtype == torch.bfloat16
+    _check(Cb[None], a, lo, hi, sc, g, KERNEL_TOL, bf16_out=True)
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_batched(shared):
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    B, M, N, K, g = 3, 7, 384, 1024, 128
+    say("int6_matmul batched", dict(B=B, M=M, shared=shared))
+    rng = np.random.default_rng(11)
+    lo, hi, sc = _weights(rng, 1 if shared else B, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    if shared:
+        Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    C = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert C.shape == (B, M, N)
+    _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=shared)
+
+
+def test_strided_and_misaligned_activations():
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K, g = 9, 256, 512, 128
+    say("int6_matmul strided", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(12)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    a = _act(rng, 1, M, K)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    wide = torch.zeros(M, K + 64, dtype=torch.bfloat16, device=DEV)
+    wide[:, 8:8 + K] = a[0].to(DEV)
+    view = wide[:, 8:8 + K]                       # row stride K + 64, 16-byte aligned start
+    C = I6.int6_matmul(view, Ld, Hd, Sd, g, out_dtype=torch.float32)
+    flat = torch.zeros(M * K + 1, dtype=torch.bfloat16, device=DEV)
+    flat[1:] = a[0].to(DEV).reshape(-1)
+    mis = flat[1:].view(M, K)                     # 2-byte offset: the wrapper re-aligns it
+    C2 = I6.int6_matmul(mis, Ld, Hd, Sd, g, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    _check(C[None], a, lo, hi, sc, g, KERNEL_TOL)
+    assert torch.equal(C, C2)
+
+
+def test_split_k_is_deterministic_and_consistent():
+    """Every split gives the oracle's result within tolerance, and the same call twice gives identical bits."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K, g = 4, 1024, 4096, 128
+    say("int6_matmul split sweep", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(13)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    a = _act(rng, 1, M, K)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    ad = a[0].to(DEV)
+    for sk in (1, 2, 4, 8, 16, 32, 64):
+        C = I6.int6_matmul(ad, Ld, Hd, Sd, g, split_k=sk, out_dtype=torch.float32)
+        C2 = I6.int6_matmul(ad, Ld, Hd, Sd, g, split_k=sk, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        assert torch.equal(C, C2), sk
+        _check(C[None], a, lo, hi, sc, g, KERNEL_TOL)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_dequantize_is_exact(dtype):
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    K, N, g = 512, 272, 128
+    say("dequantize_int6", dict(K=K, N=N, dtype=str(dtype)))
+    rng = np.random.default_rng(14)
+    lo, hi, sc = _weights(rng, 2, K, N, g)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    w = I6.dequantize_int6(Ld, Hd, Sd, g, dtype=dtype)
+    w0 = I6.dequantize_int6(Ld[1], Hd[1], Sd[1], g, dtype=dtype)
+    torch.cuda.synchronize()
+    ref = torch.from_numpy(R.dequantize_ref(lo, hi, sc, g).astype(np.float32)).to(dtype)
+    assert w.shape == (2, K, N) and w0.shape == (K, N)
+    assert torch.equal(w.cpu(), ref)
+    assert torch.equal(w0.cpu(), ref[1])
+
+
+def test_large_m_dequantises_then_library_gemm():
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K, g = I6.MAX_M + 44, 512, 1024, 128
+    say("int6_matmul large M", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(15)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    a = _act(rng, 1, M, K)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    C = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g)
+    torch.cuda.synchronize()
+    assert C.shape == (M, N) and C.dtype == torch.bfloat16
+    _check(C[None], a, lo, hi, sc, g, GEMM_TOL, bf16_out=True)
+
+
+def test_quantise_on_device_then_matmul():
+    """The reference's load-time flow: quantize_int6 on the GPU, then the op with plan_int6's plan."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K = 4, 768, 2048
+    say("quantize_int6 + op", dict(M=M, N=N, K=K))
+    torch.manual_seed(16)
+    w = (torch.randn(K, N) * 0.02).to(DEV)
+    lo, hi, sc, g = I6.quantize_int6(w, 128)
+    assert g == 128 and lo.shape == (K // 2, N) and hi.shape == (K // 4, N) and sc.shape == (K // g, N)
+    # the codes are the rounding of w by the stored scales, clamped to [-32, 31]
+    q = R.unpack_codes(lo.cpu().numpy(), hi.cpu().numpy()).astype(np.float32) - 32
+    s = sc.cpu().float().numpy()[np.arange(K) // g]
+    mism = q != np.clip(np.round(w.cpu().numpy() / s), -32, 31)
+    assert mism.mean() < 1e-4, mism.sum()          # exact but for last-ulp divisions landing on a .5 boundary
+    a = torch.randn(M, K).to(torch.bfloat16)
+    sk, ud = I6.plan_int6(M, N, K, 1, torch.device(DEV))
+    C = I6.int6_matmul_op(a.to(DEV), lo, hi, sc, g, sk, ud)
+    Ce = I6.int6_matmul(a.to(DEV), lo, hi, sc, g)
+    torch.cuda.synchronize()
+    assert torch.equal(C, Ce)
+    _check(C[None], a[None], lo.cpu().numpy(), hi.cpu().numpy(), sc.cpu().numpy(), g, KERNEL_TOL, bf16_out=True)
+    # quantisation error against the float weight stays at the int6 level
+    wq = I6.dequantize_int6(lo, hi, sc, g).cpu()
+    rel = ((wq - w.cpu()).norm() / w.cpu().norm()).item()
+    assert rel < 0.03, rel
