@@ -268,10 +268,11 @@ def int6_bench(torch, kernels, dev, steps, warmup):
         us = graph_time(lambda: [I6.int6_matmul_op(a, lo[i], hi[i], sc[i], G, sk, ud) for i in range(SETS)], steps)
         us_bf = graph_time(lambda: [torch.matmul(a, wbf[i]) for i in range(SETS)], steps)
         byts = weight_bytes + M * K * 2 + M * N * 2
-        rows.append({"M": M, "split_k": sk, "us": us, "GBps": byts / (us * 1e-6) / 1e9,
-                     "frac_hbm": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, "bf16_matmul_us": us_bf,
-                     "speedup_vs_bf16": us_bf / us})
-        log(f"int6 M={M} split={sk}: {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), bf16 matmul {us_bf:.2f} us")
+        path = "w6a16 kernel" if M <= I6.MAX_M else "dequantize + library GEMM"
+        rows.append({"M": M, "path": path, "split_k": sk if M <= I6.MAX_M else None, "us": us,
+                     "GBps": byts / (us * 1e-6) / 1e9, "frac_hbm": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                     "bf16_matmul_us": us_bf, "speedup_vs_bf16": us_bf / us})
+        log(f"int6 M={M} ({path}, split {sk}): {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), bf16 matmul {us_bf:.2f} us")
     # prefill-sized M: dequantise once, then the library GEMM
     M = 4096
     a = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)

@@ -37,7 +37,7 @@ typedef struct w6a16_args {
     int64_t scales_batch_stride;       /* elements */
     void *out;                         /* [B][M][N] bf16 or fp32 (out_dtype) */
     int64_t out_batch_stride, out_row_stride;      /* elements */
-    void *workspace;                   /* split_k > 1: fp32 partials, w6a16_workspace_size bytes */
+    void *workspace;                   /* split_k > 1: w6a16_workspace_size bytes, 256-byte aligned, see below */
     size_t workspace_bytes;
     int32_t B, M, N, K;                /* K % 64 == 0, N % 16 == 0, B * ceil(M / 16) <= 65535 */
     int32_t group_k;                   /* % 64 == 0, divides K */
@@ -48,12 +48,16 @@ typedef struct w6a16_args {
 /* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
 size_t w6a16_args_size(void);
 
-/* Bytes of fp32 split-K partials `w6a16_matmul` needs (0 for split_k == 1). */
+/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1): arrival counters, then fp32 partial tiles.  The split
+ * that completes a tile last reduces it inside the kernel, so no second launch is made.  Contract: the workspace
+ * must be zero-filled before its first use; every completed call leaves its counters at zero again, so one
+ * workspace serves any number of calls issued one after another (stream order).  Calls that can run at the same
+ * time (different streams) need different workspaces. */
 int w6a16_workspace_size(const w6a16_args *args, size_t *bytes);
 
-/* Split-K for a shape: the smallest power of two (<= 64) giving about two wavefronts per SIMD, keeping at least two
- * chunks per range and split_k * M <= K / 20 (bounded partial traffic).  Replaces the split-K rule of plan_int6
- * (rwkv_next/kernels/int6_gemm.py:239-250). */
+/* Split-K for a shape: the smallest power of two (<= 64) giving at least one workgroup per CU, then doubled while
+ * ranges keep at least eight 64-row chunks and the launch stays within two workgroups per CU.  Replaces the split-K
+ * rule of plan_int6 (rwkv_next/kernels/int6_gemm.py:239-250). */
 int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K);
 
 /* C = A @ dequant(W) on `stream` (hipStream_t).  Replaces `_impl` + `_w6a16` (int6_gemm.py:253-287, 156-215). */

@@ -8,9 +8,11 @@
 //                       | (u[.. + j + 48] >> 4) << 6                                                 j < 16
 // C[b][m][n] = sum_k A[b][m][k] s[k / group_k][n] q[k][n] with fp32 accumulation (int6_gemm.py:156-215).
 //
-// One wavefront computes a 16 (M) x 128 (N) output tile over a range of 64-row chunks (split-K over chunk ranges):
-//   * the chunk's 48 plane rows x 128 columns (6 KB) are loaded coalesced (16 bytes per lane, 8 lanes per row),
-//     one chunk ahead in registers, and written to the wave's own LDS buffer (no workgroup barrier: a wave's LDS
+// A workgroup of four wavefronts covers four adjacent 128-column strips (512 columns: neighbouring strips share DRAM
+// pages, which the four wavefronts read at about the same time) for one range of 64-row chunks (split-K over chunk
+// ranges) and up to 64 rows of A.  Each wavefront computes MT 16 (M) x 128 (N) tiles:
+//   * the chunk's 48 plane rows x 128 columns (6 KB) are loaded coalesced (16 bytes per lane, 8 lanes per row), with
+//     the next chunk's loads in flight, and written to the wave's own LDS buffer (no workgroup barrier: a wave's LDS
 //     operations execute in order);
 //   * ds_read_b64_tr_b8 hands each lane 8 consecutive plane rows of one column -- within each 16-lane group, lane
 //     L receives byte L & 7 of the 8-byte reads of lanes (L & 15) / 8 + 2 e, so lane s of group q reading
@@ -18,11 +20,13 @@
 //     B operand of v_mfma_f32_16x16x32_bf16 (8 consecutive k of one column).  One read of the lo plane covers both
 //     32-row halves of the chunk (low and high nibbles), one read of the hi plane supplies the top 2 bits;
 //   * the 6-bit code u becomes a bf16 operand without conversion instructions: 0x4300 | u is the bf16 of 128 + u,
-//     exact, assembled for two values with one v_perm_b32 against a register of 0x43 bytes.  One extra MFMA per
-//     chunk against a constant B of -160 removes the bias (128 + u - 160 = q) exactly, shared by the 8 tiles;
-//   * each chunk's fp32 tile is scaled by s (fp16) and accumulated; the result (or an fp32 split-K partial) is
-//     stored at the end.
-// Rows m >= M and columns n >= N are zero-filled on load and not stored.
+//     exact, assembled for two values with one v_perm_b32 against a register of 0x43 bytes.  One extra MFMA pair
+//     per chunk and M tile against a constant B of -160 removes the bias (128 + u - 160 = q) exactly;
+//   * the dequantised operand serves all MT M tiles; each chunk's fp32 tile is scaled by s (fp16) and accumulated.
+// Split-K partials are reduced inside the kernel: every split stores its tile (fp32, in register order) and
+// increments the tile's arrival counter; the split that arrives last sums the partials in split order (a fixed
+// order: the result does not depend on which split arrives last), stores the result and resets the counter to zero.
+// Rows m >= M and columns n >= N are clamped on load (they only feed outputs that are not stored).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -40,11 +44,13 @@ typedef int v2i __attribute__((ext_vector_type(2)));
 typedef __attribute__((address_space(3))) v2i lds_v2i;
 
 constexpr int kTileN = 128;          // columns per wavefront
-constexpr int kTiles = kTileN / 16;  // 16x16 MFMA tiles per wavefront
+constexpr int kTiles = kTileN / 16;  // 16x16 MFMA tiles per wavefront and M tile
+constexpr int kWaves = 4;            // wavefronts per workgroup (adjacent column strips)
 constexpr int kPitch = 136;          // LDS row pitch in bytes (128 + 8: the 8 rows of one transposing read differ in bank)
 constexpr int kRows = 48;            // plane rows per chunk: 32 lo + 16 hi
 constexpr int kScaleOff = kRows * kPitch;    // the chunk's 128 fp16 scales follow the plane rows
 constexpr int kBuf = kScaleOff + 2 * kTileN;
+constexpr int kCounterAlign = 256;   // bytes: the partials follow the counters at this alignment
 
 struct Args {
     const uint16_t* a;
@@ -55,8 +61,9 @@ struct Args {
     int64_t ss_b;
     void* out;
     int64_t so_b, so_m;
-    float* part;  // split-K partials [split][B][M][N] fp32, or null
-    int32_t B, M, N, K, group_k, split_k, out_dtype, m_tiles, chunks_per_split;
+    uint32_t* cnt;  // split_k > 1: arrival counters, one per (batch, M group, column strip); zero between calls
+    float* part;    // split_k > 1: partial tiles [tile][split][16 MT rows][128 columns]
+    int32_t B, M, N, K, group_k, split_k, out_dtype, m_groups, n_strips, chunks_per_split;
 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -90,17 +97,30 @@ __device__ __forceinline__ void store8(float* dst, const float (&v)[8]) {
     *reinterpret_cast<f4*>(dst + 4) = f4{v[4], v[5], v[6], v[7]};
 }
 
+// Device-coherent accesses to the split-K partials: relaxed atomics at agent scope, which the compiler emits as
+// plain stores / loads that bypass the caches that are not coherent across the chip (sc1).
+__device__ __forceinline__ void coherent_store(float* p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float2 coherent_load2(const float* p) {
+    const uint64_t u = __hip_atomic_load(reinterpret_cast<const uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return __builtin_bit_cast(float2, u);
+}
+
 // One chunk's operands, held in registers between its load and its use.
+template <int MT>
 struct Stage {
     u4 plane[6];   // plane rows 8 k + lane / 8 of the chunk (0..31 lo, 32..47 hi), 16 columns each
-    u4 a[2];       // A[m0 + i][chunk * 64 + 32 h + 8 q .. + 7]
+    u4 a[MT][2];   // A[m0 + 16 mt + i][chunk * 64 + 32 h + 8 q .. + 7]
     uint32_t sc;   // scales of columns n0 + 2 lane, n0 + 2 lane + 1 for the chunk's group
 };
 
 // Loads never branch: a column or row outside the matrix is clamped to one inside it.  Output columns depend only
 // on their own weight columns and scales, output rows only on their own A rows, so the clamped values land in
 // outputs that are never stored.
-__device__ __forceinline__ void load_stage(const Args& p, int b, int m0, int n0, int c, Stage& s) {
+template <int MT>
+__device__ __forceinline__ void load_stage(const Args& p, int b, int m0, int n0, int c, Stage<MT>& s) {
     const int lane = threadIdx.x & 63;
     const int seg = lane & 7, rr = lane >> 3;
     const int n = min(n0 + 16 * seg, p.N - 16);
@@ -111,17 +131,21 @@ __device__ __forceinline__ void load_stage(const Args& p, int b, int m0, int n0,
 #pragma unroll
     for (int k = 0; k < 2; ++k) s.plane[4 + k] = *reinterpret_cast<const u4*>(hi + (int64_t)(8 * k) * p.N);
     const int i = lane & 15, q = lane >> 4;
-    const int m = min(m0 + i, p.M - 1);
-    const uint16_t* const arow = p.a + (int64_t)b * p.sa_b + (int64_t)m * p.sa_m + (int64_t)c * 64 + 8 * q;
-    s.a[0] = *reinterpret_cast<const u4*>(arow);
-    s.a[1] = *reinterpret_cast<const u4*>(arow + 32);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = min(m0 + 16 * mt + i, p.M - 1);
+        const uint16_t* const arow = p.a + (int64_t)b * p.sa_b + (int64_t)m * p.sa_m + (int64_t)c * 64 + 8 * q;
+        s.a[mt][0] = *reinterpret_cast<const u4*>(arow);
+        s.a[mt][1] = *reinterpret_cast<const u4*>(arow + 32);
+    }
     const int g = (c * 64) / p.group_k;
     const int col = min(n0 + 2 * lane, p.N - 2);
     s.sc = *reinterpret_cast<const uint32_t*>(p.sc + (int64_t)b * p.ss_b + (int64_t)g * p.N + col);
 }
 
 // Contract one chunk into acc: stage it in the wave's LDS buffer, read it back transposed, dequantise, MFMA.
-__device__ __forceinline__ void process_stage(const Stage& s, uint8_t* buf, f4 (&acc)[kTiles]) {
+template <int MT>
+__device__ __forceinline__ void process_stage(const Stage<MT>& s, uint8_t* buf, f4 (&acc)[MT][kTiles]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, i = lane & 15;
     const int seg = lane & 7, rr = lane >> 3;
     wave_lds_sync();  // the previous chunk's reads of buf are issued before these writes
@@ -134,9 +158,12 @@ __device__ __forceinline__ void process_stage(const Stage& s, uint8_t* buf, f4 (
     *reinterpret_cast<uint32_t*>(buf + kScaleOff + 4 * lane) = s.sc;
     wave_lds_sync();
     const bf8 bias = __builtin_bit_cast(bf8, u4{0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u});  // -160
-    const bf8 a0 = __builtin_bit_cast(bf8, s.a[0]), a1 = __builtin_bit_cast(bf8, s.a[1]);
-    f4 corr = mfma(a0, bias, f4{0.f, 0.f, 0.f, 0.f});
-    corr = mfma(a1, bias, corr);
+    f4 corr[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), bias, f4{0.f, 0.f, 0.f, 0.f});
+        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), bias, corr[mt]);
+    }
     const int sel = 2 * (q >> 1);  // hi-plane field of rows 8 q .. (first half); the second half's is 4 bits up
     const int r = lane & 15;
     const int off = (r >> 1) * kPitch + 8 * (r & 1);
@@ -149,125 +176,186 @@ __device__ __forceinline__ void process_stage(const Stage& s, uint8_t* buf, f4 (
         uint32_t o0[4], o1[4];
 #pragma unroll
         for (int d = 0; d < 2; ++d) {
-            const uint32_t L = (uint32_t)lov[d], H = (uint32_t)hiv[d];
-            const uint32_t u0 = (L & 0x0F0F0F0Fu) | ((H >> sel) << 4 & 0x30303030u);       // rows 8 q + e
-            const uint32_t u1 = ((L >> 4) & 0x0F0F0F0Fu) | ((H >> sel) & 0x30303030u);   // rows 32 + 8 q + e
+            const uint32_t L = (uint32_t)lov[d], Hs = (uint32_t)hiv[d] >> sel;
+            const uint32_t u0 = (L & 0x0F0F0F0Fu) | ((Hs & 0x03030303u) << 4);          // rows 8 q + e
+            const uint32_t u1 = ((L >> 4) & 0x0F0F0F0Fu) | (Hs & 0x30303030u);          // rows 32 + 8 q + e
             codes_to_bf16(u0, o0[2 * d], o0[2 * d + 1]);
             codes_to_bf16(u1, o1[2 * d], o1[2 * d + 1]);
         }
         const bf8 w0 = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
         const bf8 w1 = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
-        f4 tc = mfma(a0, w0, corr);
-        tc = mfma(a1, w1, tc);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[t][v] += tc[v] * sv;
+        for (int mt = 0; mt < MT; ++mt) {
+            f4 tc = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), w0, corr[mt]);
+            tc = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), w1, tc);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[mt][t][v] += tc[v] * sv;
+        }
     }
 }
 
-__global__ __launch_bounds__(64) void w6a16_kernel(const Args p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kBuf];
+template <int MT>
+__device__ __forceinline__ void store_tile(const Args& p, int b, int m0, int n0, const f4 (&acc)[MT][kTiles]) {
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-    const int n0 = blockIdx.x * kTileN;
+    // lane (i, q) holds C[m0 + 16 mt + 4 q + v][n0 + 16 t + i]
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) {
+            const int n = n0 + 16 * t + i;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = m0 + 16 * mt + 4 * q + v;
+                if (n >= p.N || m >= p.M) continue;
+                const int64_t o = (int64_t)b * p.so_b + (int64_t)m * p.so_m + n;
+                if (p.out_dtype == W6A16_OUT_F32)
+                    reinterpret_cast<float*>(p.out)[o] = acc[mt][t][v];
+                else
+                    reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)acc[mt][t][v];
+            }
+        }
+}
+
+template <int MT, int D>
+__global__ __launch_bounds__(64 * kWaves) void w6a16_kernel(const Args p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kWaves][kBuf];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, q = lane >> 4;
+    const int strip = blockIdx.x * kWaves + wv;
+    if (strip >= p.n_strips) return;  // no workgroup barrier follows: the other wavefronts do not wait for this one
+    const int n0 = strip * kTileN;
     const int split = blockIdx.y;
-    const int b = blockIdx.z / p.m_tiles, m0 = (blockIdx.z % p.m_tiles) * 16;
+    const int b = blockIdx.z / p.m_groups, mg = blockIdx.z % p.m_groups;
+    const int m0 = mg * 16 * MT;
     const int nchunks = p.K / 64;
     const int c0 = split * p.chunks_per_split;
     const int c1 = min(nchunks, c0 + p.chunks_per_split);
+    uint8_t* const buf = lds[wv];
 
-    f4 acc[kTiles];
+    f4 acc[MT][kTiles];
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[mt][t] = f4{0.f, 0.f, 0.f, 0.f};
 
     if (c0 < c1) {
-        // Two chunks in flight: while one is contracted the next one's loads are outstanding.  The last chunk is
+        // D chunks in flight: while one is contracted the next ones' loads are outstanding.  The last chunk is
         // re-loaded in place of chunks past the range (a cache hit), so every load is unconditional.
-        Stage s0, s1;
-        load_stage(p, b, m0, n0, c0, s0);
-        load_stage(p, b, m0, n0, min(c0 + 1, c1 - 1), s1);
-        for (int c = c0; c < c1; c += 2) {
-            process_stage(s0, lds, acc);
-            load_stage(p, b, m0, n0, min(c + 2, c1 - 1), s0);
-            if (c + 1 < c1) process_stage(s1, lds, acc);
-            load_stage(p, b, m0, n0, min(c + 3, c1 - 1), s1);
-        }
-    }
-
-    // lane (i, q) holds C[m0 + 4 q + v][n0 + 16 t + i]
+        Stage<MT> st[D];
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) {
-        const int n = n0 + 16 * t + i;
-        if (n >= p.N) continue;
+        for (int j = 0; j < D; ++j) load_stage<MT>(p, b, m0, n0, min(c0 + j, c1 - 1), st[j]);
+        for (int c = c0; c < c1; c += D) {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-            const int m = m0 + 4 * q + v;
-            if (m >= p.M) continue;
-            if (p.part) {
-                p.part[(((int64_t)split * p.B + b) * p.M + m) * p.N + n] = acc[t][v];
-            } else if (p.out_dtype == W6A16_OUT_F32) {
-                reinterpret_cast<float*>(p.out)[(int64_t)b * p.so_b + (int64_t)m * p.so_m + n] = acc[t][v];
-            } else {
-                reinterpret_cast<__bf16*>(p.out)[(int64_t)b * p.so_b + (int64_t)m * p.so_m + n] = (__bf16)acc[t][v];
+            for (int j = 0; j < D; ++j) {
+                if (c + j < c1) process_stage<MT>(st[j], buf, acc);
+                load_stage<MT>(p, b, m0, n0, min(c + j + D, c1 - 1), st[j]);
             }
         }
     }
-}
 
-// out[b][m][n] = sum over splits of the fp32 partials.
-__global__ __launch_bounds__(256) void w6a16_reduce_kernel(const Args p) {
-    const int64_t total = (int64_t)p.B * p.M * p.N;
-    for (int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x; x < total; x += (int64_t)gridDim.x * 256) {
-        float s = 0.f;
-        for (int sp = 0; sp < p.split_k; ++sp) s += p.part[sp * total + x];
-        const int n = (int)(x % p.N);
-        const int64_t bm = x / p.N;
-        const int m = (int)(bm % p.M), b = (int)(bm / p.M);
-        const int64_t o = (int64_t)b * p.so_b + (int64_t)m * p.so_m + n;
-        if (p.out_dtype == W6A16_OUT_F32)
-            reinterpret_cast<float*>(p.out)[o] = s;
-        else
-            reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)s;
+    if (p.split_k == 1) {
+        store_tile<MT>(p, b, m0, n0, acc);
+        return;
     }
+    // Split-K: publish this split's tile, count arrivals; the last split to arrive reduces in split order.
+    // Partial tiles are row-major [16 MT rows][128 columns] fp32 per (tile, split); rows >= M are not written.
+    const int64_t tile = ((int64_t)b * p.m_groups + mg) * p.n_strips + strip;
+    constexpr int kTileFloats = 16 * MT * kTileN;
+    float* const part = p.part + tile * p.split_k * kTileFloats;
+    const int rows = min(16 * MT, p.M - m0);  // valid rows of this tile
+    {
+        float* const mine = part + (int64_t)split * kTileFloats + (lane & 15);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int r = 16 * mt + 4 * q + v;
+                    if (r < rows) coherent_store(mine + r * kTileN + 16 * t, acc[mt][t][v]);
+                }
+    }
+    // The partials are device-coherent stores (they bypass the non-coherent caches); waiting for them to complete
+    // before the counter increment publishes them without writing back the whole L2, which an agent-scope release
+    // fence would do once per wavefront.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    uint32_t arrived = 0;
+    if (lane == 0) arrived = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrived = __builtin_amdgcn_readfirstlane(arrived);
+    if (arrived != (uint32_t)p.split_k - 1) return;
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the loads below are issued only after the counter returned
+    // Reduce: lane l sums columns 2 l, 2 l + 1 of every valid row, split by split in order 0, 1, ...; the loads of
+    // eight splits are issued together.
+    const int64_t ob = (int64_t)b * p.so_b;
+    const int n = n0 + 2 * lane;
+    for (int r = 0; r < rows; ++r) {
+        const float* src = part + r * kTileN + 2 * lane;
+        float s0 = 0.f, s1 = 0.f;
+        int sp = 0;
+        for (; sp + 8 <= p.split_k; sp += 8) {
+            float2 x[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) x[j] = coherent_load2(src + (int64_t)(sp + j) * kTileFloats);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                s0 += x[j].x;
+                s1 += x[j].y;
+            }
+        }
+        for (; sp < p.split_k; ++sp) {
+            const float2 x = coherent_load2(src + (int64_t)sp * kTileFloats);
+            s0 += x.x;
+            s1 += x.y;
+        }
+        if (n < p.N) {
+            const int64_t o = ob + (int64_t)(m0 + r) * p.so_m + n;
+            if (p.out_dtype == W6A16_OUT_F32) {
+                reinterpret_cast<float*>(p.out)[o] = s0;
+                reinterpret_cast<float*>(p.out)[o + 1] = s1;
+            } else {
+                reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)s0;
+                reinterpret_cast<__bf16*>(p.out)[o + 1] = (__bf16)s1;
+            }
+        }
+    }
+    if (lane == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Dequantise: w[b][k][n] = s q as bf16 or fp32 (the large-M path hands the result to a library GEMM).  One thread
-// per (lo row c * 32 + j, 16 columns): it writes rows c * 64 + j and c * 64 + j + 32 of those columns.
+// Dequantise: w[b][k][n] = s q as bf16 or fp32 (the large-M path hands the result to a library GEMM).  Grid
+// (ceil(N / 4096), K / 2, B): one thread per (lo row c * 32 + j, 16 columns); it writes rows c * 64 + j and
+// c * 64 + j + 32 of those columns.
 template <typename OutT>
 __global__ __launch_bounds__(256) void w6a16_dequant_kernel(const uint8_t* lo, const uint8_t* hi, const uint16_t* sc,
                                                             OutT* w, int32_t K, int32_t N, int32_t group_k,
-                                                            int64_t sl_b, int64_t sh_b, int64_t ss_b, int64_t sw_b,
-                                                            int32_t B) {
-    const int n16 = N / 16;
-    const int64_t per = (int64_t)(K / 2) * n16;
-    for (int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x; x < per * B; x += (int64_t)gridDim.x * 256) {
-        const int b = (int)(x / per);
-        const int64_t y = x % per;
-        const int n = (int)(y % n16) * 16;
-        const int lrow = (int)(y / n16);  // c * 32 + j
-        const int c = lrow >> 5, j = lrow & 31;
-        const u4 L = *reinterpret_cast<const u4*>(lo + b * sl_b + (int64_t)lrow * N + n);
-        const u4 H = *reinterpret_cast<const u4*>(hi + b * sh_b + ((int64_t)c * 16 + (j & 15)) * N + n);
-        const int sh0 = 2 * (j >> 4), sh1 = sh0 + 4;  // 2-bit fields of rows j and j + 32
-        const int r0 = c * 64 + j, r1 = r0 + 32;
-        const uint16_t* const s0 = sc + b * ss_b + (int64_t)(r0 / group_k) * N + n;
-        const uint16_t* const s1 = sc + b * ss_b + (int64_t)(r1 / group_k) * N + n;
-        OutT* const w0 = w + b * sw_b + (int64_t)r0 * N + n;
-        OutT* const w1 = w + b * sw_b + (int64_t)r1 * N + n;
+                                                            int64_t sl_b, int64_t sh_b, int64_t ss_b, int64_t sw_b) {
+    const int n = (blockIdx.x * 256 + threadIdx.x) * 16;
+    if (n >= N) return;
+    const int lrow = blockIdx.y, b = blockIdx.z;
+    const int c = lrow >> 5, j = lrow & 31;
+    const u4 L = *reinterpret_cast<const u4*>(lo + b * sl_b + (int64_t)lrow * N + n);
+    const u4 H = *reinterpret_cast<const u4*>(hi + b * sh_b + ((int64_t)c * 16 + (j & 15)) * N + n);
+    const int sh0 = 2 * (j >> 4), sh1 = sh0 + 4;  // 2-bit fields of rows j and j + 32
+    const int r0 = c * 64 + j, r1 = r0 + 32;
+    const uint16_t* const s0 = sc + b * ss_b + (int64_t)(r0 / group_k) * N + n;
+    const uint16_t* const s1 = sc + b * ss_b + (int64_t)(r1 / group_k) * N + n;
+    OutT* const w0 = w + b * sw_b + (int64_t)r0 * N + n;
+    OutT* const w1 = w + b * sw_b + (int64_t)r1 * N + n;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {  // columns n + 8 h .. + 7
-            const u4 sa = *reinterpret_cast<const u4*>(s0 + 8 * h), sb = *reinterpret_cast<const u4*>(s1 + 8 * h);
-            float va[8], vb[8];
+    for (int h = 0; h < 2; ++h) {  // columns n + 8 h .. + 7
+        const u4 sa = *reinterpret_cast<const u4*>(s0 + 8 * h), sb = *reinterpret_cast<const u4*>(s1 + 8 * h);
+        float va[8], vb[8];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int col = 8 * h + e, wd = col >> 2, by = 8 * (col & 3);
-                const uint32_t l = (L[wd] >> by) & 0xFF, hh = (H[wd] >> by) & 0xFF;
-                const int q0 = (int)((l & 15) | (((hh >> sh0) & 3) << 4)) - 32;
-                const int q1 = (int)((l >> 4) | (((hh >> sh1) & 3) << 4)) - 32;
-                va[e] = h2f((uint16_t)(sa[e >> 1] >> (16 * (e & 1)))) * (float)q0;  // exact: 11 x 6 bit product
-                vb[e] = h2f((uint16_t)(sb[e >> 1] >> (16 * (e & 1)))) * (float)q1;
-            }
-            store8(w0 + 8 * h, va);
-            store8(w1 + 8 * h, vb);
+        for (int e = 0; e < 8; ++e) {
+            const int col = 8 * h + e, wd = col >> 2, by = 8 * (col & 3);
+            const uint32_t l = (L[wd] >> by) & 0xFF, hh = (H[wd] >> by) & 0xFF;
+            const int q0 = (int)((l & 15) | (((hh >> sh0) & 3) << 4)) - 32;
+            const int q1 = (int)((l >> 4) | (((hh >> sh1) & 3) << 4)) - 32;
+            va[e] = h2f((uint16_t)(sa[e >> 1] >> (16 * (e & 1)))) * (float)q0;  // exact: 11 x 6 bit product
+            vb[e] = h2f((uint16_t)(sb[e >> 1] >> (16 * (e & 1)))) * (float)q1;
         }
+        store8(w0 + 8 * h, va);
+        store8(w1 + 8 * h, vb);
     }
 }
 
@@ -280,6 +368,29 @@ int cu_count() {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// M tiles per wavefront: above 32 rows two 16-row tiles share each dequantised weight operand (measured at
+// K = 4096, N = 16384: M = 32 is faster with one tile per wavefront and two M groups, M = 64 with two; four tiles
+// per wavefront leave one wavefront per SIMD and lose at every split).
+int m_tiles_per_wave(int M) { return M <= 32 ? 1 : 2; }
+
+struct Layout {
+    int mt, m_groups, n_strips;
+    size_t counter_bytes, partial_bytes;
+};
+
+Layout layout(const w6a16_args* a) {
+    Layout l{};
+    l.mt = m_tiles_per_wave(a->M);
+    l.m_groups = (a->M + 16 * l.mt - 1) / (16 * l.mt);
+    l.n_strips = (a->N + kTileN - 1) / kTileN;
+    if (a->split_k > 1) {
+        const size_t tiles = (size_t)a->B * l.m_groups * l.n_strips;
+        l.counter_bytes = (tiles * 4 + kCounterAlign - 1) / kCounterAlign * kCounterAlign;
+        l.partial_bytes = tiles * a->split_k * (size_t)l.mt * kTiles * 4 * 64 * 4;
+    }
+    return l;
+}
 
 int validate(const w6a16_args* a) {
     if (!a) return WKV7_ERR_NULL;
@@ -294,10 +405,19 @@ int validate(const w6a16_args* a) {
         a->scales_batch_stride % 2)
         return WKV7_ERR_ALIGN;
     if (a->a_row_stride < a->K || a->out_row_stride < a->N) return WKV7_ERR_SHAPE;
-    if ((int64_t)a->B * ((a->M + 15) / 16) > 65535) return WKV7_ERR_SHAPE;  // grid z: batch x 16-row tiles
-    if (a->split_k > 1 && (!a->workspace || a->workspace_bytes < (size_t)a->split_k * a->B * a->M * a->N * 4))
-        return WKV7_ERR_WORKSPACE;
+    const Layout l = layout(a);
+    if ((int64_t)a->B * l.m_groups > 65535) return WKV7_ERR_SHAPE;  // grid z: batch x M groups
+    if (a->split_k > 1) {
+        if (!a->workspace || a->workspace_bytes < l.counter_bytes + l.partial_bytes) return WKV7_ERR_WORKSPACE;
+        if (reinterpret_cast<uintptr_t>(a->workspace) % kCounterAlign) return WKV7_ERR_ALIGN;
+    }
     return WKV7_OK;
+}
+
+template <int MT, int D>
+void launch(const Args& p, const Layout& l, hipStream_t s) {
+    const dim3 grid((l.n_strips + kWaves - 1) / kWaves, p.split_k, p.B * l.m_groups);
+    hipLaunchKernelGGL((w6a16_kernel<MT, D>), grid, dim3(64 * kWaves), 0, s, p);
 }
 
 }  // namespace
@@ -309,25 +429,34 @@ size_t w6a16_args_size(void) { return sizeof(w6a16_args); }
 
 int w6a16_workspace_size(const w6a16_args* a, size_t* bytes) {
     if (!a || !bytes) return WKV7_ERR_NULL;
-    *bytes = a->split_k > 1 ? (size_t)a->split_k * a->B * (size_t)a->M * a->N * 4 : 0;
+    if (a->split_k <= 1 || a->M <= 0 || a->B < 1 || a->N < 1) {
+        *bytes = 0;
+        return WKV7_OK;
+    }
+    const w6::Layout l = w6::layout(a);
+    *bytes = l.counter_bytes + l.partial_bytes;
     return WKV7_OK;
 }
 
 int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
     if (B < 1 || M < 1 || N < 1 || K < 64) return 1;
-    const int64_t waves = (int64_t)B * ((M + 15) / 16) * ((N + w6::kTileN - 1) / w6::kTileN);
+    const int mt = w6::m_tiles_per_wave(M);
+    const int64_t strips = (N + w6::kTileN - 1) / w6::kTileN;
+    const int64_t groups = (int64_t)B * ((M + 16 * mt - 1) / (16 * mt)) * ((strips + w6::kWaves - 1) / w6::kWaves);
     const int chunks = K / 64;
-    const int64_t target = 8LL * w6::cu_count();  // two wavefronts per SIMD
-    // The fp32 partials (written, then read by the reduction: 8 bytes per split, row and column) stay under about
-    // half the weight's own 0.77 bytes per element: split * M <= K / 20.
+    const int64_t cus = w6::cu_count();
+    // At least one workgroup per CU; beyond that, ranges of about eight chunks (measured best at K = 4096 for every
+    // M up to 64) while the launch stays within two workgroups per CU.  Every range keeps at least one chunk.
     int sk = 1;
-    while (waves * sk < target && sk * 2 <= 64 && chunks / (sk * 2) >= 2 && (int64_t)sk * 2 * M * 20 <= K) sk *= 2;
+    while (groups * sk < cus && sk * 2 <= 64 && chunks / (sk * 2) >= 1) sk *= 2;
+    while (chunks / (sk * 2) >= 8 && groups * sk * 2 <= 2 * cus && sk * 2 <= 64) sk *= 2;
     return sk;
 }
 
 int w6a16_matmul(const w6a16_args* a, void* stream) {
     const int rc = w6::validate(a);
     if (rc != WKV7_OK || a->M == 0) return rc;
+    const w6::Layout l = w6::layout(a);
     w6::Args p{};
     p.a = a->a;
     p.sa_b = a->a_batch_stride;
@@ -341,7 +470,10 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     p.out = a->out;
     p.so_b = a->out_batch_stride;
     p.so_m = a->out_row_stride;
-    p.part = a->split_k > 1 ? static_cast<float*>(a->workspace) : nullptr;
+    if (a->split_k > 1) {
+        p.cnt = static_cast<uint32_t*>(a->workspace);
+        p.part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + l.counter_bytes);
+    }
     p.B = a->B;
     p.M = a->M;
     p.N = a->N;
@@ -349,16 +481,14 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     p.group_k = a->group_k;
     p.split_k = a->split_k;
     p.out_dtype = a->out_dtype;
-    p.m_tiles = (a->M + 15) / 16;
+    p.m_groups = l.m_groups;
+    p.n_strips = l.n_strips;
     const int chunks = a->K / 64;
     p.chunks_per_split = (chunks + a->split_k - 1) / a->split_k;
     const hipStream_t s = static_cast<hipStream_t>(stream);
-    const dim3 grid((a->N + w6::kTileN - 1) / w6::kTileN, a->split_k, a->B * p.m_tiles);
-    hipLaunchKernelGGL(w6::w6a16_kernel, grid, dim3(64), 0, s, p);
-    if (a->split_k > 1) {
-        const int64_t total = (int64_t)a->B * a->M * a->N;
-        const int64_t blocks = std::min<int64_t>((total + 255) / 256, 8LL * w6::cu_count());
-        hipLaunchKernelGGL(w6::w6a16_reduce_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
+    switch (l.mt) {
+        case 1: w6::launch<1, 2>(p, l, s); break;
+        default: w6::launch<2, 2>(p, l, s); break;
     }
     return static_cast<int>(hipGetLastError());
 }
@@ -373,17 +503,17 @@ int w6a16_dequantize(const uint8_t* lo, const uint8_t* hi, const uint16_t* scale
     if (!w6::aligned16(lo) || !w6::aligned16(hi) || !w6::aligned16(scales) || !w6::aligned16(w) ||
         lo_batch_stride % 16 || hi_batch_stride % 16 || scales_batch_stride % 8 || w_batch_stride % 8)
         return WKV7_ERR_ALIGN;
-    const int64_t total = (int64_t)B * (K / 2) * (N / 16);
-    const int64_t blocks = std::min<int64_t>((total + 255) / 256, 16LL * w6::cu_count());
+    if (K / 2 > 65535 || B > 65535) return WKV7_ERR_SHAPE;  // grid y and z
+    const dim3 grid((N / 16 + 255) / 256, K / 2, B);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (out_dtype == W6A16_OUT_F32)
-        hipLaunchKernelGGL(w6::w6a16_dequant_kernel<float>, dim3((unsigned)blocks), dim3(256), 0, s, lo, hi, scales,
+        hipLaunchKernelGGL(w6::w6a16_dequant_kernel<float>, grid, dim3(256), 0, s, lo, hi, scales,
                            static_cast<float*>(w), K, N, group_k, lo_batch_stride, hi_batch_stride,
-                           scales_batch_stride, w_batch_stride, B);
+                           scales_batch_stride, w_batch_stride);
     else
-        hipLaunchKernelGGL(w6::w6a16_dequant_kernel<__bf16>, dim3((unsigned)blocks), dim3(256), 0, s, lo, hi, scales,
+        hipLaunchKernelGGL(w6::w6a16_dequant_kernel<__bf16>, grid, dim3(256), 0, s, lo, hi, scales,
                            static_cast<__bf16*>(w), K, N, group_k, lo_batch_stride, hi_batch_stride,
-                           scales_batch_stride, w_batch_stride, B);
+                           scales_batch_stride, w_batch_stride);
     return static_cast<int>(hipGetLastError());
 }
 

@@ -24,6 +24,7 @@ Activations are bf16; the result is bf16 (fp32 accumulation).  Every call runs o
 """
 from __future__ import annotations
 
+import ctypes
 import os
 
 import torch
@@ -33,7 +34,7 @@ from .. import _lib
 CHUNK = 64
 QMIN, QMAX = -32, 31
 # Largest M that the W6A16 kernel serves; larger M dequantises once and runs the library GEMM.
-MAX_M = int(os.environ.get("RWKV_INT6_MAX_M", "256"))
+MAX_M = int(os.environ.get("RWKV_INT6_MAX_M", "128"))
 _RATIOS = (1.0, 0.97, 0.94, 0.91, 0.88, 0.85)
 
 
@@ -188,15 +189,31 @@ def _impl(a, lo, hi, s, group_k, split_k, out_dtype=None):
     args.split_k = max(1, int(split_k))
     args.out_dtype = _lib.W6A16_OUT_F32 if odt == torch.float32 else _lib.W6A16_OUT_BF16
     lib = _lib.load()
-    ws = None
     if args.split_k > 1:
-        import ctypes
         n = ctypes.c_size_t(0)
         _lib.check(lib.w6a16_workspace_size(args, ctypes.byref(n)))
-        ws = torch.empty(int(n.value), dtype=torch.uint8, device=A.device)
-        args.workspace, args.workspace_bytes = ws.data_ptr(), int(n.value)
+        ws = _workspace(A.device, int(n.value))
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check(lib.w6a16_matmul(args, torch.cuda.current_stream(A.device).cuda_stream))
     return out if batched else out[0]
+
+
+_WORKSPACES: dict = {}
+_RETIRED: list = []
+
+
+def _workspace(device, nbytes):
+    """The device's split-K workspace (arrival counters + partials), zero-filled when created; every completed call
+    leaves its counters at zero, so calls issued in stream order share it.  A larger request replaces it; the old
+    buffer is kept alive, since a captured HIP graph may still address it."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _WORKSPACES.get(idx)
+    if ws is None or ws.numel() < nbytes:
+        if ws is not None:
+            _RETIRED.append(ws)
+        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
+        _WORKSPACES[idx] = ws
+    return ws
 
 
 def int6_matmul(a, lo, hi, s, group_k, split_k=None, use_dot=None, *, out_dtype=None):

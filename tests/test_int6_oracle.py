@@ -196,7 +196,7 @@ def base_args(**kw):
     ("group_k", 96, _lib.WKV7_ERR_SHAPE),
     ("group_k", 1024, _lib.WKV7_ERR_SHAPE),
     ("B", 0, _lib.WKV7_ERR_SHAPE),
-    ("M", 16 * 65536, _lib.WKV7_ERR_SHAPE),           # grid z = batch x 16-row tiles
+    ("M", 64 * 65536, _lib.WKV7_ERR_SHAPE),           # grid z = batch x 64-row groups
     ("a_row_stride", 256, _lib.WKV7_ERR_SHAPE),       # < K
     ("out_row_stride", 128, _lib.WKV7_ERR_SHAPE),     # < N
     ("split_k", 0, _lib.WKV7_ERR_ARG),
@@ -222,9 +222,17 @@ def test_matmul_empty_and_workspace_size():
     n = ctypes.c_size_t(1)
     assert lib.w6a16_workspace_size(ctypes.byref(base_args()), ctypes.byref(n)) == 0 and n.value == 0
     assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=8, B=2, M=3)), ctypes.byref(n)) == 0
-    assert n.value == 8 * 2 * 3 * 256 * 4
-    small = base_args(split_k=8, B=2, M=3, workspace=0x10000, workspace_bytes=n.value - 4)
+    # tiles = B x M groups x 128-column strips = 2 x 1 x 2; one u32 counter each (rounded up to 256 bytes), then per
+    # tile and split a 16 x 128 fp32 partial tile
+    tiles = 2 * 1 * 2
+    assert n.value == 256 + tiles * 8 * 16 * 128 * 4
+    # M = 40 takes two 16-row tiles per wavefront: two M groups of 32 rows, two strips (N = 256): four tiles
+    assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=2, M=40)), ctypes.byref(n)) == 0
+    assert n.value == 256 + (2 * 2) * 2 * 32 * 128 * 4
+    small = base_args(split_k=8, B=2, M=3, workspace=0x10000, workspace_bytes=256 + tiles * 8 * 16 * 128 * 4 - 4)
     assert lib.w6a16_matmul(ctypes.byref(small), None) == _lib.WKV7_ERR_WORKSPACE
+    odd = base_args(split_k=8, B=2, M=3, workspace=0x10080, workspace_bytes=1 << 24)
+    assert lib.w6a16_matmul(ctypes.byref(odd), None) == _lib.WKV7_ERR_ALIGN
 
 
 def test_dequantize_validates_before_launch():
@@ -251,7 +259,10 @@ def test_split_rule():
                        (1, 1, 256, 128), (1, 200, 65536, 8192)]:
         sk = lib.w6a16_plan_split(B, M, N, K)
         assert 1 <= sk <= 64 and sk & (sk - 1) == 0
-        if sk > 1:
-            assert (K // 64) // sk >= 2 and sk * M * 20 <= K
+        assert (K // 64) // sk >= 1
+    # without a GPU the CU count is taken as 256: K = 4096, N = 16384 has 32 groups of four 128-column strips
+    assert lib.w6a16_plan_split(1, 1, 16384, 4096) == 8
+    assert lib.w6a16_plan_split(1, 64, 16384, 4096) == 8        # two M groups of 32 rows
+    assert lib.w6a16_plan_split(1, 1, 4096, 16384) == 32
     assert I6.plan_int6(1, 4096, 4096, 1) == (lib.w6a16_plan_split(1, 1, 4096, 4096), False)
     assert I6.plan_int6(8, 4096, 4096, 1)[1] is True
