@@ -226,8 +226,8 @@ def timemix_bench(torch, kernels, dev, steps, warmup):
 
 def int6_bench(torch, kernels, dev, steps, warmup):
     """W6A16 GEMM/GEMV (rwkv_next/kernels/int6_gemm.py) at the reference's quoted shape K = 4096, N = 16384
-    (int6_gemm.py:224-226), group_k = 128, for decode-sized M (the W6A16 kernel) and M = 4096 (dequantise, then the
-    library GEMM).  Eight weight sets (8 x 51 MB) are cycled so the 256 MB Infinity Cache cannot hold them: every
+    (int6_gemm.py:224-226), group_k = 128, for decode-sized M (the W6A16 kernel, on the reference's planes and on the
+    packed layout of prepack_int6) and M = 4096 (dequantise, then the library GEMM).  Eight weight sets (8 x 51 MB) are cycled so the 256 MB Infinity Cache cannot hold them: every
     call streams its weight from HBM, as a model's consecutive layers do.  Each M is one HIP graph of 8 calls.
     Beside it: torch.matmul on the same shape with a bf16 weight (hipBLASLt), cycled the same way."""
     from rwkv_next_amd.kernels import int6_gemm as I6
@@ -237,6 +237,7 @@ def int6_bench(torch, kernels, dev, steps, warmup):
     hi = [torch.randint(0, 256, (K // 4, N), device=dev, dtype=torch.uint8, generator=gen) for _ in range(SETS)]
     sc = [(torch.rand(K // G, N, device=dev, generator=gen) * 0.05 + 0.002).half() for _ in range(SETS)]
     wbf = [I6.dequantize_int6(lo[i], hi[i], sc[i], G, dtype=torch.bfloat16) for i in range(SETS)]
+    pk = [I6.prepack_int6(lo[i], hi[i], sc[i], G) for i in range(SETS)]
     weight_bytes = K * N * 3 // 4 + (K // G) * N * 2
 
     def graph_time(fn, reps):
@@ -266,13 +267,18 @@ def int6_bench(torch, kernels, dev, steps, warmup):
         a = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
         sk, ud = I6.plan_int6(M, N, K, 1, dev)
         us = graph_time(lambda: [I6.int6_matmul_op(a, lo[i], hi[i], sc[i], G, sk, ud) for i in range(SETS)], steps)
+        us_pk = graph_time(lambda: [I6.int6_matmul_packed_op(a, pk[i].weight, pk[i].scales, 0, K, N, G, sk)
+                                    for i in range(SETS)], steps)
         us_bf = graph_time(lambda: [torch.matmul(a, wbf[i]) for i in range(SETS)], steps)
         byts = weight_bytes + M * K * 2 + M * N * 2
         path = "w6a16 kernel" if M <= I6.MAX_M else "dequantize + library GEMM"
         rows.append({"M": M, "path": path, "split_k": sk if M <= I6.MAX_M else None, "us": us,
                      "GBps": byts / (us * 1e-6) / 1e9, "frac_hbm": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
-                     "bf16_matmul_us": us_bf, "speedup_vs_bf16": us_bf / us})
-        log(f"int6 M={M} ({path}, split {sk}): {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), bf16 matmul {us_bf:.2f} us")
+                     "packed_us": us_pk, "packed_GBps": byts / (us_pk * 1e-6) / 1e9,
+                     "packed_frac_hbm": byts / (us_pk * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                     "bf16_matmul_us": us_bf, "speedup_vs_bf16": us_bf / us, "packed_speedup_vs_bf16": us_bf / us_pk})
+        log(f"int6 M={M} ({path}, split {sk}): {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), packed {us_pk:.2f} us "
+            f"({rows[-1]['packed_GBps']:.0f} GB/s), bf16 matmul {us_bf:.2f} us")
     # prefill-sized M: dequantise once, then the library GEMM
     M = 4096
     a = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)

@@ -28,6 +28,10 @@ extern "C" {
 #define W6A16_OUT_BF16 0
 #define W6A16_OUT_F32 2
 
+/* Weight formats of w6a16_args.format */
+#define W6A16_FORMAT_PLANES 0   /* the reference's planes: lo, hi, scales as above */
+#define W6A16_FORMAT_PACKED 1   /* w6a16_pack's layout: lo = packed weight, scales = packed scales, hi unused */
+
 typedef struct w6a16_args {
     const uint16_t *a;                 /* bf16 activations [B][M][K] */
     int64_t a_batch_stride, a_row_stride;          /* elements; row stride >= K, multiples of 8 */
@@ -43,6 +47,7 @@ typedef struct w6a16_args {
     int32_t group_k;                   /* % 64 == 0, divides K */
     int32_t split_k;                   /* 1 .. 256: K is cut into split_k ranges of 64-row chunks */
     int32_t out_dtype;                 /* W6A16_OUT_BF16 or W6A16_OUT_F32 */
+    int32_t format;                    /* W6A16_FORMAT_PLANES or W6A16_FORMAT_PACKED */
 } w6a16_args;
 
 /* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
@@ -69,6 +74,22 @@ int w6a16_matmul(const w6a16_args *args, void *stream);
 int w6a16_dequantize(const uint8_t *lo, const uint8_t *hi, const uint16_t *scales, void *w, int32_t B, int32_t K,
                      int32_t N, int32_t group_k, int64_t lo_batch_stride, int64_t hi_batch_stride,
                      int64_t scales_batch_stride, int64_t w_batch_stride, int32_t out_dtype, void *stream);
+
+/* The packed layout (no counterpart in the reference; a load-time re-layout of the same bits): per (batch, 128-column
+ * strip, 64-row chunk) one contiguous 6144-byte block in MFMA operand order, and per (batch, strip, group) 128 fp16
+ * scales.  Sizes for a (B, K, N) weight; columns are padded to whole strips. */
+int w6a16_packed_size(int32_t B, int32_t K, int32_t N, int32_t group_k, size_t *weight_bytes, size_t *scale_bytes);
+
+/* Re-lay out reference planes (as passed to w6a16_matmul in W6A16_FORMAT_PLANES) into the packed layout on `stream`.
+ * Packed batches are contiguous: batch strides w6a16_packed_size(1, ...).  Used with W6A16_FORMAT_PACKED, a call
+ * streams each wavefront's weight linearly and skips the LDS transposition the planes need. */
+int w6a16_pack(const uint8_t *lo, const uint8_t *hi, const uint16_t *scales, int32_t B, int32_t K, int32_t N,
+               int32_t group_k, int64_t lo_batch_stride, int64_t hi_batch_stride, int64_t scales_batch_stride,
+               void *packed, uint16_t *packed_scales, void *stream);
+
+/* w6a16_dequantize for the packed layout (batches contiguous, as w6a16_pack writes them). */
+int w6a16_dequantize_packed(const void *packed, const uint16_t *packed_scales, void *w, int32_t B, int32_t K,
+                            int32_t N, int32_t group_k, int64_t w_batch_stride, int32_t out_dtype, void *stream);
 
 #ifdef __cplusplus
 }

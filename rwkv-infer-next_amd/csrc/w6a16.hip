@@ -31,6 +31,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "w6a16.h"
 
@@ -45,7 +46,7 @@ typedef __attribute__((address_space(3))) v2i lds_v2i;
 
 constexpr int kTileN = 128;          // columns per wavefront
 constexpr int kTiles = kTileN / 16;  // 16x16 MFMA tiles per wavefront and M tile
-constexpr int kWaves = 4;            // wavefronts per workgroup (adjacent column strips)
+constexpr int kStrips = 4;           // adjacent 128-column strips per workgroup
 constexpr int kPitch = 136;          // LDS row pitch in bytes (128 + 8: the 8 rows of one transposing read differ in bank)
 constexpr int kRows = 48;            // plane rows per chunk: 32 lo + 16 hi
 constexpr int kScaleOff = kRows * kPitch;    // the chunk's 128 fp16 scales follow the plane rows
@@ -216,42 +217,12 @@ __device__ __forceinline__ void store_tile(const Args& p, int b, int m0, int n0,
         }
 }
 
-template <int MT, int D>
-__global__ __launch_bounds__(64 * kWaves) void w6a16_kernel(const Args p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kWaves][kBuf];
-    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, q = lane >> 4;
-    const int strip = blockIdx.x * kWaves + wv;
-    if (strip >= p.n_strips) return;  // no workgroup barrier follows: the other wavefronts do not wait for this one
-    const int n0 = strip * kTileN;
-    const int split = blockIdx.y;
-    const int b = blockIdx.z / p.m_groups, mg = blockIdx.z % p.m_groups;
-    const int m0 = mg * 16 * MT;
-    const int nchunks = p.K / 64;
-    const int c0 = split * p.chunks_per_split;
-    const int c1 = min(nchunks, c0 + p.chunks_per_split);
-    uint8_t* const buf = lds[wv];
-
-    f4 acc[MT][kTiles];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int t = 0; t < kTiles; ++t) acc[mt][t] = f4{0.f, 0.f, 0.f, 0.f};
-
-    if (c0 < c1) {
-        // D chunks in flight: while one is contracted the next ones' loads are outstanding.  The last chunk is
-        // re-loaded in place of chunks past the range (a cache hit), so every load is unconditional.
-        Stage<MT> st[D];
-#pragma unroll
-        for (int j = 0; j < D; ++j) load_stage<MT>(p, b, m0, n0, min(c0 + j, c1 - 1), st[j]);
-        for (int c = c0; c < c1; c += D) {
-#pragma unroll
-            for (int j = 0; j < D; ++j) {
-                if (c + j < c1) process_stage<MT>(st[j], buf, acc);
-                load_stage<MT>(p, b, m0, n0, min(c + j + D, c1 - 1), st[j]);
-            }
-        }
-    }
-
+// Stores the wavefront's tile, or (split-K) publishes it and, in the split that completes the tile last, reduces the
+// partials in split order and stores the result.
+template <int MT>
+__device__ __forceinline__ void finish_tile(const Args& p, int b, int mg, int strip, int split, int m0, int n0,
+                                            f4 (&acc)[MT][kTiles]) {
+    const int lane = threadIdx.x & 63, q = lane >> 4;
     if (p.split_k == 1) {
         store_tile<MT>(p, b, m0, n0, acc);
         return;
@@ -320,6 +291,292 @@ __global__ __launch_bounds__(64 * kWaves) void w6a16_kernel(const Args p) {
         }
     }
     if (lane == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------------------------------------------
+// Packed layout: the same 6 bits per weight and fp16 scales, re-laid out once (w6a16_pack) so that each wavefront's
+// 64-row chunk of a 128-column strip is one contiguous 6 KB block already in MFMA operand order.  Block (b, strip,
+// chunk) lies at ((b * strips + strip) * chunks + chunk) * 6144; load instruction k (0..5) of lane l reads bytes
+// k * 1024 + 16 l .. + 15, i.e. dwords 4 k .. 4 k + 3 of lane l's 24-dword record R.  For lane (i, q) = (l & 15,
+// l >> 4) and tile t (column n = 128 strip + 16 t + i):
+//   R[2 t], R[2 t + 1]  bytes e = 0..7: lo plane row chunk * 32 + 8 q + e (low nibble: row 8 q + e of the chunk,
+//                       high nibble: row 32 + 8 q + e)
+//   R[16 + t]           byte e' = 0..3: the top 2 bits of rows 8 q + e', 32 + 8 q + e', 8 q + 4 + e',
+//                       32 + 8 q + 4 + e' at bits 0-1, 2-3, 4-5, 6-7
+// Scales: block (b, strip, group) of 128 fp16 at ((b * strips + strip) * groups + group) * 128, ordered [i][t], so
+// lane (i, q) reads its eight columns' scales as one 16-byte load.  Columns past N hold zero codes and scales.
+constexpr int kPackBytes = 6144;
+
+template <int MT>
+struct PStage {
+    u4 w[6];       // the lane's 24-dword record
+    u4 a[MT][2];   // A[m0 + 16 mt + i][chunk * 64 + 32 h + 8 q .. + 7]
+    u4 sc;         // scales of columns n0 + 16 t + i, t = 0..7 (fp16)
+};
+
+template <int MT>
+__device__ __forceinline__ void load_pstage(const Args& p, int b, int m0, int strip, int c, PStage<MT>& s) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int nchunks = p.K / 64;
+    const uint8_t* const blk =
+        p.lo + (int64_t)b * p.sl_b + ((int64_t)strip * nchunks + c) * kPackBytes + 16 * lane;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) s.w[k] = *reinterpret_cast<const u4*>(blk + 1024 * k);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = min(m0 + 16 * mt + i, p.M - 1);
+        const uint16_t* const arow = p.a + (int64_t)b * p.sa_b + (int64_t)m * p.sa_m + (int64_t)c * 64 + 8 * q;
+        s.a[mt][0] = *reinterpret_cast<const u4*>(arow);
+        s.a[mt][1] = *reinterpret_cast<const u4*>(arow + 32);
+    }
+    const int g = (c * 64) / p.group_k, groups = p.K / p.group_k;
+    s.sc = *reinterpret_cast<const u4*>(p.sc + (int64_t)b * p.ss_b + ((int64_t)strip * groups + g) * kTileN + 8 * i);
+}
+
+template <int MT>
+__device__ __forceinline__ void process_pstage(const PStage<MT>& s, f4 (&acc)[MT][kTiles]) {
+    const bf8 bias = __builtin_bit_cast(bf8, u4{0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u});  // -160
+    f4 corr[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), bias, f4{0.f, 0.f, 0.f, 0.f});
+        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), bias, corr[mt]);
+    }
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const uint32_t L0 = s.w[t >> 1][2 * (t & 1)], L1 = s.w[t >> 1][2 * (t & 1) + 1];
+        const uint32_t Hd = s.w[4 + (t >> 2)][t & 3];
+        const uint32_t u0a = (L0 & 0x0F0F0F0Fu) | ((Hd & 0x03030303u) << 4);         // rows 8 q + 0..3
+        const uint32_t u0b = (L1 & 0x0F0F0F0Fu) | (Hd & 0x30303030u);                // rows 8 q + 4..7
+        const uint32_t u1a = ((L0 >> 4) & 0x0F0F0F0Fu) | ((Hd & 0x0C0C0C0Cu) << 2);  // rows 32 + 8 q + 0..3
+        const uint32_t u1b = ((L1 >> 4) & 0x0F0F0F0Fu) | ((Hd >> 2) & 0x30303030u);  // rows 32 + 8 q + 4..7
+        uint32_t o0[4], o1[4];
+        codes_to_bf16(u0a, o0[0], o0[1]);
+        codes_to_bf16(u0b, o0[2], o0[3]);
+        codes_to_bf16(u1a, o1[0], o1[1]);
+        codes_to_bf16(u1b, o1[2], o1[3]);
+        const bf8 w0 = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
+        const bf8 w1 = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+        const float sv = h2f((uint16_t)(s.sc[t >> 1] >> (16 * (t & 1))));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+            f4 tc = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), w0, corr[mt]);
+            tc = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), w1, tc);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) acc[mt][t][v] += tc[v] * sv;
+        }
+    }
+}
+
+// One kernel for both weight formats.  A workgroup holds KS x 4 wavefronts: four adjacent 128-column strips, and
+// for each strip KS wavefronts splitting the workgroup's chunk range in KS parts (more loads in flight per CU at the
+// same global split).  The KS partial tiles of a strip are summed through LDS in part order 0, 1, .. (fixed), then
+// the tile is finished as a whole (stored, or split-K published and reduced).
+template <int MT, int D, int KS, bool PACKED>
+__global__ __launch_bounds__(64 * kStrips * KS) void w6a16_kernel(const Args p) {
+    constexpr int kStage = PACKED ? 16 : kStrips * KS * kBuf;  // planes: each wavefront's staging buffer
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kStage];
+    __shared__ __attribute__((aligned(16))) f4 red[KS > 1 ? (KS - 1) * kStrips * MT * kTiles * 64 : 1];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int sw = wv % kStrips, part = wv / kStrips;
+    const int strip = blockIdx.x * kStrips + sw;
+    const bool live = strip < p.n_strips;
+    const int n0 = strip * kTileN;
+    const int split = blockIdx.y;
+    const int b = blockIdx.z / p.m_groups, mg = blockIdx.z % p.m_groups;
+    const int m0 = mg * 16 * MT;
+    const int nchunks = p.K / 64;
+    const int s0 = split * p.chunks_per_split, s1 = min(nchunks, s0 + p.chunks_per_split);
+    const int per = (max(0, s1 - s0) + KS - 1) / KS;
+    const int c0 = s0 + part * per, c1 = min(s1, c0 + per);
+    uint8_t* const buf = lds + (PACKED ? 0 : wv * kBuf);
+
+    f4 acc[MT][kTiles];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) acc[mt][t] = f4{0.f, 0.f, 0.f, 0.f};
+
+    if (live && c0 < c1) {
+        // D chunks in flight.  Chunks past the range re-load the last one (a cache hit), so every load is
+        // unconditional.  Packed: whole groups of D chunks run unconditionally (a use of a stage under a condition
+        // let the compiler sink that stage's loads to the use, leaving no load in flight) and a scheduling barrier
+        // keeps each stage's loads where they are issued; the remainder (fewer than D chunks, already loaded)
+        // follows.
+        typedef typename std::conditional<PACKED, PStage<MT>, Stage<MT>>::type S;
+        S st[D];
+        auto load = [&](int c, S& x) {
+            if constexpr (PACKED) load_pstage<MT>(p, b, m0, strip, c, x);
+            else load_stage<MT>(p, b, m0, n0, c, x);
+        };
+        auto work = [&](const S& x) {
+            if constexpr (PACKED) process_pstage<MT>(x, acc);
+            else process_stage<MT>(x, buf, acc);
+        };
+#pragma unroll
+        for (int j = 0; j < D; ++j) load(min(c0 + j, c1 - 1), st[j]);
+        if constexpr (PACKED) {
+            const int full = c0 + (c1 - c0) / D * D;
+            for (int c = c0; c < full; c += D) {
+#pragma unroll
+                for (int j = 0; j < D; ++j) {
+                    work(st[j]);
+                    load(min(c + j + D, c1 - 1), st[j]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j + 1 < D; ++j)
+                if (full + j < c1) work(st[j]);
+        } else {
+            // the planes' stages are consumed by LDS stores: here the compiler keeps the loads in place on its own
+            // (measured 1 us faster per call than the form above)
+            for (int c = c0; c < c1; c += D) {
+#pragma unroll
+                for (int j = 0; j < D; ++j) {
+                    if (c + j < c1) work(st[j]);
+                    load(min(c + j + D, c1 - 1), st[j]);
+                }
+            }
+        }
+    }
+
+    if constexpr (KS > 1) {
+        f4* const r = red + (int64_t)sw * MT * kTiles * 64 + lane;
+        constexpr int kPartStride = kStrips * MT * kTiles * 64;
+        if (part > 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < kTiles; ++t) r[(part - 1) * kPartStride + (mt * kTiles + t) * 64] = acc[mt][t];
+        }
+        __syncthreads();
+        if (part > 0) return;
+#pragma unroll
+        for (int k = 1; k < KS; ++k)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int t = 0; t < kTiles; ++t) acc[mt][t] += r[(k - 1) * kPartStride + (mt * kTiles + t) * 64];
+    }
+    if (!live) return;
+    finish_tile<MT>(p, b, mg, strip, split, m0, n0, acc);
+}
+
+// Dequantise the packed layout: one thread per (b, strip, chunk, lane) writes its 16 rows x 8 columns (rows
+// 8 q + e and 32 + 8 q + e, columns 128 strip + 16 t + i); for each (row, tile) the 16 lanes of a row group store
+// 16 consecutive columns.
+template <typename OutT>
+__global__ __launch_bounds__(256) void w6a16_dequant_packed_kernel(const uint8_t* pk, const uint16_t* psc, OutT* w,
+                                                                   int32_t K, int32_t N, int32_t group_k,
+                                                                   int32_t strips, int64_t sw_b) {
+    const int nchunks = K / 64, groups = K / group_k;
+    const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int b = blockIdx.y;
+    if (x >= (int64_t)strips * nchunks * 64) return;
+    const int lane = (int)(x & 63);
+    const int64_t sc = x >> 6;
+    const int c = (int)(sc % nchunks), strip = (int)(sc / nchunks);
+    const int i = lane & 15, q = lane >> 4;
+    const uint8_t* const blk = pk + ((int64_t)b * strips * nchunks + sc) * kPackBytes + 16 * lane;
+    uint32_t R[24];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+        const u4 v = *reinterpret_cast<const u4*>(blk + 1024 * k);
+        R[4 * k] = v[0];
+        R[4 * k + 1] = v[1];
+        R[4 * k + 2] = v[2];
+        R[4 * k + 3] = v[3];
+    }
+    const int g = (c * 64) / group_k;
+    const u4 sv = *reinterpret_cast<const u4*>(psc + ((int64_t)b * strips * groups + (int64_t)strip * groups + g) * kTileN + 8 * i);
+    OutT* const wb = w + b * sw_b;
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int n = strip * kTileN + 16 * t + i;
+        if (n >= N) continue;
+        const float s = h2f((uint16_t)(sv[t >> 1] >> (16 * (t & 1))));
+        const uint32_t Lw[2] = {R[2 * t], R[2 * t + 1]}, Hd = R[16 + t];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t lb = (Lw[e >> 2] >> (8 * (e & 3))) & 0xFF;
+            const uint32_t hb = (Hd >> (8 * (e & 3) + 4 * (e >> 2))) & 0xF;  // bits 0-1: row 8 q + e, 2-3: row 32 + ..
+            const int q0 = (int)((lb & 15) | ((hb & 3) << 4)) - 32;
+            const int q1 = (int)((lb >> 4) | ((hb >> 2) << 4)) - 32;
+            const int64_t r0 = (int64_t)c * 64 + 8 * q + e;
+            wb[r0 * N + n] = (OutT)(s * (float)q0);
+            wb[(r0 + 32) * N + n] = (OutT)(s * (float)q1);
+        }
+    }
+}
+
+// Repack: one thread per (b, strip, chunk, lane) writes the lane's 24-dword record.
+__global__ __launch_bounds__(256) void w6a16_pack_kernel(const uint8_t* lo, const uint8_t* hi, uint8_t* out, int32_t K,
+                                                         int32_t N, int32_t strips, int64_t sl_b, int64_t sh_b) {
+    const int nchunks = K / 64;
+    const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;  // ((strip * nchunks + c) * 64 + lane) within batch
+    const int b = blockIdx.y;
+    if (x >= (int64_t)strips * nchunks * 64) return;
+    const int lane = (int)(x & 63);
+    const int64_t sc = x >> 6;
+    const int c = (int)(sc % nchunks), strip = (int)(sc / nchunks);
+    const int i = lane & 15, q = lane >> 4;
+    const uint8_t* const L = lo + b * sl_b;
+    const uint8_t* const H = hi + b * sh_b;
+    uint32_t R[24];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const int n = strip * kTileN + 16 * t + i;
+        uint32_t l0 = 0, l1 = 0, hd = 0;
+        if (n < N) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                l0 |= (uint32_t)L[((int64_t)c * 32 + 8 * q + e) * N + n] << (8 * e);
+                l1 |= (uint32_t)L[((int64_t)c * 32 + 8 * q + 4 + e) * N + n] << (8 * e);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int rows[4] = {8 * q + e, 32 + 8 * q + e, 8 * q + 4 + e, 32 + 8 * q + 4 + e};
+                uint32_t byte = 0;
+#pragma unroll
+                for (int f = 0; f < 4; ++f) {
+                    const int r = rows[f];
+                    const uint32_t top = (H[((int64_t)c * 16 + (r & 15)) * N + n] >> (2 * (r >> 4))) & 3u;
+                    byte |= top << (2 * f);
+                }
+                hd |= byte << (8 * e);
+            }
+        }
+        R[2 * t] = l0;
+        R[2 * t + 1] = l1;
+        R[16 + t] = hd;
+    }
+    uint8_t* const blk = out + ((int64_t)b * strips * nchunks + sc) * kPackBytes + 16 * lane;
+#pragma unroll
+    for (int k = 0; k < 6; ++k) *reinterpret_cast<u4*>(blk + 1024 * k) = u4{R[4 * k], R[4 * k + 1], R[4 * k + 2], R[4 * k + 3]};
+}
+
+// Repack the scales: one thread per (b, strip, group, i) writes the eight scales of columns 128 strip + 16 t + i.
+__global__ __launch_bounds__(256) void w6a16_pack_scales_kernel(const uint16_t* sc, uint16_t* out, int32_t groups,
+                                                                int32_t N, int32_t strips, int64_t ss_b) {
+    const int64_t x = (int64_t)blockIdx.x * 256 + threadIdx.x;  // ((strip * groups + g) * 16 + i) within batch
+    const int b = blockIdx.y;
+    if (x >= (int64_t)strips * groups * 16) return;
+    const int i = (int)(x & 15);
+    const int64_t sg = x >> 4;
+    const int g = (int)(sg % groups), strip = (int)(sg / groups);
+    uint32_t o[4];
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+        uint32_t v[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int n = strip * kTileN + 16 * (2 * h + u) + i;
+            v[u] = n < N ? sc[b * ss_b + (int64_t)g * N + n] : 0u;
+        }
+        o[h] = v[0] | v[1] << 16;
+    }
+    *reinterpret_cast<u4*>(out + ((int64_t)b * strips * groups + sg) * kTileN + 8 * i) = u4{o[0], o[1], o[2], o[3]};
 }
 
 // Dequantise: w[b][k][n] = s q as bf16 or fp32 (the large-M path hands the result to a library GEMM).  Grid
@@ -399,10 +656,15 @@ int validate(const w6a16_args* a) {
     if (a->split_k < 1 || a->split_k > 256) return WKV7_ERR_ARG;
     if (a->out_dtype != W6A16_OUT_BF16 && a->out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
     if (a->M == 0) return WKV7_OK;
-    if (!a->a || !a->lo || !a->hi || !a->scales || !a->out) return WKV7_ERR_NULL;
-    if (!aligned16(a->a) || !aligned16(a->lo) || !aligned16(a->hi) || (reinterpret_cast<uintptr_t>(a->scales) & 3) ||
-        a->a_row_stride % 8 || a->a_batch_stride % 8 || a->lo_batch_stride % 16 || a->hi_batch_stride % 16 ||
-        a->scales_batch_stride % 2)
+    if (a->format != W6A16_FORMAT_PLANES && a->format != W6A16_FORMAT_PACKED) return WKV7_ERR_ARG;
+    const bool packed = a->format == W6A16_FORMAT_PACKED;
+    if (!a->a || !a->lo || (!packed && !a->hi) || !a->scales || !a->out) return WKV7_ERR_NULL;
+    if (!aligned16(a->a) || !aligned16(a->lo) || a->a_row_stride % 8 || a->a_batch_stride % 8 ||
+        a->lo_batch_stride % 16)
+        return WKV7_ERR_ALIGN;
+    if (packed ? (!aligned16(a->scales) || a->scales_batch_stride % 8)
+               : (!aligned16(a->hi) || (reinterpret_cast<uintptr_t>(a->scales) & 3) || a->hi_batch_stride % 16 ||
+                  a->scales_batch_stride % 2))
         return WKV7_ERR_ALIGN;
     if (a->a_row_stride < a->K || a->out_row_stride < a->N) return WKV7_ERR_SHAPE;
     const Layout l = layout(a);
@@ -414,10 +676,16 @@ int validate(const w6a16_args* a) {
     return WKV7_OK;
 }
 
+constexpr int kParts = 1;  // wavefronts per strip (KS); 2 was measured: no gain at M = 1, slower at M = 64
+
 template <int MT, int D>
-void launch(const Args& p, const Layout& l, hipStream_t s) {
-    const dim3 grid((l.n_strips + kWaves - 1) / kWaves, p.split_k, p.B * l.m_groups);
-    hipLaunchKernelGGL((w6a16_kernel<MT, D>), grid, dim3(64 * kWaves), 0, s, p);
+void launch(const Args& p, const Layout& l, bool packed, hipStream_t s) {
+    const dim3 grid((l.n_strips + kStrips - 1) / kStrips, p.split_k, p.B * l.m_groups);
+    const dim3 block(64 * kStrips * kParts);
+    if (packed)
+        hipLaunchKernelGGL((w6a16_kernel<MT, D, kParts, true>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((w6a16_kernel<MT, D, kParts, false>), grid, block, 0, s, p);
 }
 
 }  // namespace
@@ -442,7 +710,7 @@ int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
     if (B < 1 || M < 1 || N < 1 || K < 64) return 1;
     const int mt = w6::m_tiles_per_wave(M);
     const int64_t strips = (N + w6::kTileN - 1) / w6::kTileN;
-    const int64_t groups = (int64_t)B * ((M + 16 * mt - 1) / (16 * mt)) * ((strips + w6::kWaves - 1) / w6::kWaves);
+    const int64_t groups = (int64_t)B * ((M + 16 * mt - 1) / (16 * mt)) * ((strips + w6::kStrips - 1) / w6::kStrips);
     const int chunks = K / 64;
     const int64_t cus = w6::cu_count();
     // At least one workgroup per CU; beyond that, ranges of about eight chunks (measured best at K = 4096 for every
@@ -486,10 +754,62 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     const int chunks = a->K / 64;
     p.chunks_per_split = (chunks + a->split_k - 1) / a->split_k;
     const hipStream_t s = static_cast<hipStream_t>(stream);
+    const bool packed = a->format == W6A16_FORMAT_PACKED;
     switch (l.mt) {
-        case 1: w6::launch<1, 2>(p, l, s); break;
-        default: w6::launch<2, 2>(p, l, s); break;
+        case 1: w6::launch<1, 2>(p, l, packed, s); break;
+        default: w6::launch<2, 2>(p, l, packed, s); break;
     }
+    return static_cast<int>(hipGetLastError());
+}
+
+int w6a16_dequantize_packed(const void* packed, const uint16_t* packed_scales, void* w, int32_t B, int32_t K,
+                            int32_t N, int32_t group_k, int64_t w_batch_stride, int32_t out_dtype, void* stream) {
+    if (!packed || !packed_scales || !w) return WKV7_ERR_NULL;
+    if (B < 1 || N < 16 || N % 16 || K < 64 || K % 64 || group_k < 64 || group_k % 64 || K % group_k)
+        return WKV7_ERR_SHAPE;
+    if (out_dtype != W6A16_OUT_BF16 && out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
+    if (!w6::aligned16(packed) || !w6::aligned16(packed_scales)) return WKV7_ERR_ALIGN;
+    if (B > 65535) return WKV7_ERR_SHAPE;
+    const int strips = (N + w6::kTileN - 1) / w6::kTileN;
+    const int64_t nw = (int64_t)strips * (K / 64) * 64;
+    const dim3 grid((unsigned)((nw + 255) / 256), B);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const uint8_t* pk = static_cast<const uint8_t*>(packed);
+    if (out_dtype == W6A16_OUT_F32)
+        hipLaunchKernelGGL(w6::w6a16_dequant_packed_kernel<float>, grid, dim3(256), 0, s, pk, packed_scales,
+                           static_cast<float*>(w), K, N, group_k, strips, w_batch_stride);
+    else
+        hipLaunchKernelGGL(w6::w6a16_dequant_packed_kernel<__bf16>, grid, dim3(256), 0, s, pk, packed_scales,
+                           static_cast<__bf16*>(w), K, N, group_k, strips, w_batch_stride);
+    return static_cast<int>(hipGetLastError());
+}
+
+int w6a16_packed_size(int32_t B, int32_t K, int32_t N, int32_t group_k, size_t* weight_bytes, size_t* scale_bytes) {
+    if (!weight_bytes || !scale_bytes) return WKV7_ERR_NULL;
+    if (B < 1 || N < 16 || N % 16 || K < 64 || K % 64 || group_k < 64 || group_k % 64 || K % group_k)
+        return WKV7_ERR_SHAPE;
+    const size_t strips = (N + w6::kTileN - 1) / w6::kTileN;
+    *weight_bytes = (size_t)B * strips * (K / 64) * w6::kPackBytes;
+    *scale_bytes = (size_t)B * strips * (K / group_k) * w6::kTileN * 2;
+    return WKV7_OK;
+}
+
+int w6a16_pack(const uint8_t* lo, const uint8_t* hi, const uint16_t* scales, int32_t B, int32_t K, int32_t N,
+               int32_t group_k, int64_t lo_batch_stride, int64_t hi_batch_stride, int64_t scales_batch_stride,
+               void* packed, uint16_t* packed_scales, void* stream) {
+    size_t wb = 0, sb = 0;
+    const int rc = w6a16_packed_size(B, K, N, group_k, &wb, &sb);
+    if (rc != WKV7_OK) return rc;
+    if (!lo || !hi || !scales || !packed || !packed_scales) return WKV7_ERR_NULL;
+    if (!w6::aligned16(packed) || !w6::aligned16(packed_scales)) return WKV7_ERR_ALIGN;
+    if (B > 65535) return WKV7_ERR_SHAPE;
+    const int strips = (N + w6::kTileN - 1) / w6::kTileN, groups = K / group_k;
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    const int64_t nw = (int64_t)strips * (K / 64) * 64, ns = (int64_t)strips * groups * 16;
+    hipLaunchKernelGGL(w6::w6a16_pack_kernel, dim3((unsigned)((nw + 255) / 256), B), dim3(256), 0, s, lo, hi,
+                       static_cast<uint8_t*>(packed), K, N, strips, lo_batch_stride, hi_batch_stride);
+    hipLaunchKernelGGL(w6::w6a16_pack_scales_kernel, dim3((unsigned)((ns + 255) / 256), B), dim3(256), 0, s, scales,
+                       packed_scales, groups, N, strips, scales_batch_stride);
     return static_cast<int>(hipGetLastError());
 }
 

@@ -26,7 +26,9 @@ EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_versio
             "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore", "wkv7_timemix_prologue",
             "wkv7_timemix_epilogue")
 W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split", "w6a16_matmul",
-                  "w6a16_dequantize")
+                  "w6a16_dequantize", "w6a16_packed_size", "w6a16_pack", "w6a16_dequantize_packed")
+W6A16_FORMAT_PLANES = 0
+W6A16_FORMAT_PACKED = 1
 W6A16_OUT_BF16 = 0
 W6A16_OUT_F32 = 2
 MAX_MOVES = 1024
@@ -88,6 +90,7 @@ class W6a16Args(ctypes.Structure):
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("B", ctypes.c_int32), ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
         ("group_k", ctypes.c_int32), ("split_k", ctypes.c_int32), ("out_dtype", ctypes.c_int32),
+        ("format", ctypes.c_int32),
     ]
 
 
@@ -141,6 +144,13 @@ def load(path: str = LIB_PATH):
     lib.w6a16_matmul.argtypes = [ctypes.POINTER(W6a16Args), _vp]
     lib.w6a16_dequantize.restype = ctypes.c_int
     lib.w6a16_dequantize.argtypes = [_vp, _vp, _vp, _vp, i32, i32, i32, i32, i64, i64, i64, i64, i32, _vp]
+    lib.w6a16_packed_size.restype = ctypes.c_int
+    lib.w6a16_packed_size.argtypes = [i32, i32, i32, i32, ctypes.POINTER(ctypes.c_size_t),
+                                      ctypes.POINTER(ctypes.c_size_t)]
+    lib.w6a16_pack.restype = ctypes.c_int
+    lib.w6a16_pack.argtypes = [_vp, _vp, _vp, i32, i32, i32, i32, i64, i64, i64, _vp, _vp, _vp]
+    lib.w6a16_dequantize_packed.restype = ctypes.c_int
+    lib.w6a16_dequantize_packed.argtypes = [_vp, _vp, _vp, i32, i32, i32, i32, i64, i32, _vp]
     if lib.wkv7_abi_version() != WKV7_ABI_VERSION:
         raise ImportError(f"{path}: ABI version {lib.wkv7_abi_version()} != {WKV7_ABI_VERSION}")
     if lib.wkv7_args_size() != ctypes.sizeof(Wkv7Args):

@@ -8,6 +8,9 @@ quantised there load unchanged:
     plan_int6(M, N, K, n_batch, device)             -> (split_k, use_dot)              (int6_gemm.py:239-250)
     int6_matmul(a, lo, hi, s, group_k, split_k=None, use_dot=None)                    (int6_gemm.py:296-308)
     int6_matmul_op(a, lo, hi, s, group_k, split_k, use_dot)  op rwkv_next_amd::int6_matmul   (int6_gemm.py:316-323)
+plus a load-time re-layout with no counterpart in the reference:
+    prepack_int6(lo, hi, s, group_k) -> Int6Packed      accepted by int6_matmul in place of lo, and by
+    int6_matmul_packed_op(a, weight, scales, batches, K, N, group_k, split_k)   op rwkv_next_amd::int6_matmul_packed
 
 Format: a (K, N) weight (N contiguous) is quantised to q in [-32, 31] per (group of group_k rows, column) with an
 fp16 scale, w ~ s q; the code u = q + 32 is split into bit planes per 64-row chunk c:
@@ -26,6 +29,7 @@ from __future__ import annotations
 
 import ctypes
 import os
+from typing import NamedTuple
 
 import torch
 
@@ -150,26 +154,103 @@ def plan_int6(M, N, K, n_batch, device=None):
     return int(sk), M > 1
 
 
-def _impl(a, lo, hi, s, group_k, split_k, out_dtype=None):
+class Int6Packed(NamedTuple):
+    """A W6A16 weight in the packed layout (include/w6a16.h, w6a16_pack): the same 6-bit codes and fp16 scales,
+    re-laid out once so that each wavefront streams one contiguous 6 KB block per 64-row chunk and needs no LDS
+    transposition.  Made by prepack_int6; accepted by int6_matmul / int6_matmul_packed_op in place of (lo, hi, s)."""
+    weight: torch.Tensor   # uint8 [batches or 1][strips][K / 64][6144], flattened per batch
+    scales: torch.Tensor   # float16 [batches or 1][strips][K / group_k][128]
+    batches: int           # 0: one (K, N) weight; else the number of (K, N) weights
+    K: int
+    N: int
+    group_k: int
+
+
+@torch.no_grad()
+def prepack_int6(lo, hi, s, group_k) -> Int6Packed:
+    """Re-lay out a quantised weight (quantize_int6's planes, (K, N) or (B, K, N)) into the packed layout, on its
+    device.  The codes and scales are unchanged, so results equal int6_matmul on the planes bit for bit."""
+    L, H, S, Bq, K, N = _weights3(lo, hi, s)
+    g = _group_k(group_k, K, S.shape[1])
+    lib = _lib.load()
+    wb, sb = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _lib.check(lib.w6a16_packed_size(Bq, K, N, g, ctypes.byref(wb), ctypes.byref(sb)))
+    weight = torch.empty(int(wb.value), dtype=torch.uint8, device=L.device)
+    scales = torch.empty(int(sb.value) // 2, dtype=torch.float16, device=L.device)
+    with torch.cuda.device(L.device):
+        _lib.check(lib.w6a16_pack(L.data_ptr(), H.data_ptr(), S.data_ptr(), Bq, K, N, g, L.stride(0), H.stride(0),
+                                  S.stride(0), weight.data_ptr(), scales.data_ptr(),
+                                  torch.cuda.current_stream(L.device).cuda_stream))
+    return Int6Packed(weight.view(Bq, -1), scales.view(Bq, -1), 0 if lo.dim() == 2 else Bq, K, N, g)
+
+
+@torch.no_grad()
+def dequantize_int6_packed(pk: Int6Packed, dtype=torch.float32):
+    """dequantize_int6 for a packed weight: (K, N) or (B, K, N) in bfloat16 or float32."""
+    if dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"dequantize_int6_packed writes bfloat16 or float32 (got {dtype})")
+    Bq = pk.weight.shape[0]
+    w = torch.empty((Bq, pk.K, pk.N), dtype=dtype, device=pk.weight.device)
+    with torch.cuda.device(w.device):
+        _lib.check(_lib.load().w6a16_dequantize_packed(
+            pk.weight.data_ptr(), pk.scales.data_ptr(), w.data_ptr(), Bq, pk.K, pk.N, pk.group_k, w.stride(0),
+            _lib.W6A16_OUT_F32 if dtype == torch.float32 else _lib.W6A16_OUT_BF16,
+            torch.cuda.current_stream(w.device).cuda_stream))
+    return w if pk.batches else w[0]
+
+
+class _W(NamedTuple):
+    """A weight as the kernel sees it: format, the base pointers' tensors and batch strides."""
+    fmt: int
+    w0: torch.Tensor       # lo plane, or the packed weight
+    w1: torch.Tensor       # hi plane, or None
+    sc: torch.Tensor       # scales (planes [Bq][G][N] or packed [Bq][...])
+    Bq: int
+    K: int
+    N: int
+    g: int
+
+
+def _planes(lo, hi, s, group_k) -> _W:
+    L, H, S, Bq, K, N = _weights3(lo, hi, s)
+    return _W(_lib.W6A16_FORMAT_PLANES, L, H, S, Bq, K, N, _group_k(group_k, K, S.shape[1]))
+
+
+def _packed(pk: Int6Packed) -> _W:
+    for t, name, dt in ((pk.weight, "weight", torch.uint8), (pk.scales, "scales", torch.float16)):
+        if t.dtype != dt or t.device.type != "cuda" or t.dim() != 2:
+            raise ValueError(f"packed {name} must be a 2-D {dt} GPU tensor (from prepack_int6)")
+    return _W(_lib.W6A16_FORMAT_PACKED, _aligned(pk.weight), None, _aligned(pk.scales), pk.weight.shape[0], pk.K,
+              pk.N, pk.group_k)
+
+
+def _dequant(w: _W):
+    if w.fmt == _lib.W6A16_FORMAT_PACKED:
+        return dequantize_int6_packed(Int6Packed(w.w0, w.sc, w.Bq, w.K, w.N, w.g), dtype=torch.bfloat16)
+    return dequantize_int6(w.w0, w.w1, w.sc, w.g, dtype=torch.bfloat16)
+
+
+def _impl(a, w: _W, split_k, out_dtype=None):
     batched = a.dim() == 3
     A = a if batched else a.unsqueeze(0)
     if A.dtype != torch.bfloat16:
         raise TypeError(f"int6_matmul takes bfloat16 activations (got {A.dtype})")
     if A.device.type != "cuda":
         raise ValueError(f"a must be on a GPU (got {A.device})")
-    L, H, S, Bq, K, N = _weights3(lo, hi, s)
     B, M, Ka = A.shape
+    Bq, K, N = w.Bq, w.K, w.N
     if Ka != K:
         raise ValueError(f"K mismatch: a has {Ka}, int6 weight has {K}")
     if Bq not in (1, B):
         raise ValueError(f"weight batch {Bq} does not match activation batch {B}")
-    g = _group_k(group_k, K, S.shape[1])
     odt = A.dtype if out_dtype is None else out_dtype
     if odt not in (torch.float32, torch.bfloat16):
         raise TypeError(f"int6_matmul writes bfloat16 or float32 (got {odt})")
     if M > MAX_M:  # prefill: compute-bound, dequantise once and use the library GEMM
-        w = dequantize_int6(L, H, S, g, dtype=torch.bfloat16)
-        C = torch.matmul(A, w[0] if Bq == 1 else w)
+        wd = _dequant(w)
+        if wd.dim() == 2:
+            wd = wd.unsqueeze(0)
+        C = torch.matmul(A, wd[0] if Bq == 1 else wd)
         C = C.to(odt)
         return C if batched else C[0]
     out = torch.empty((B, M, N), dtype=odt, device=A.device)
@@ -179,13 +260,15 @@ def _impl(a, lo, hi, s, group_k, split_k, out_dtype=None):
         A = _aligned(A)
     args = _lib.W6a16Args()
     args.a, args.a_batch_stride, args.a_row_stride = A.data_ptr(), A.stride(0), A.stride(1)
-    args.lo, args.hi, args.scales = L.data_ptr(), H.data_ptr(), S.data_ptr()
     shared = Bq == 1 and B > 1
-    args.lo_batch_stride = 0 if shared else L.stride(0)
-    args.hi_batch_stride = 0 if shared else H.stride(0)
-    args.scales_batch_stride = 0 if shared else S.stride(0)
+    args.format = w.fmt
+    args.lo, args.scales = w.w0.data_ptr(), w.sc.data_ptr()
+    args.lo_batch_stride = 0 if shared else w.w0.stride(0)
+    args.scales_batch_stride = 0 if shared else w.sc.stride(0)
+    if w.w1 is not None:
+        args.hi, args.hi_batch_stride = w.w1.data_ptr(), 0 if shared else w.w1.stride(0)
     args.out, args.out_batch_stride, args.out_row_stride = out.data_ptr(), out.stride(0), out.stride(1)
-    args.B, args.M, args.N, args.K, args.group_k = B, M, N, K, g
+    args.B, args.M, args.N, args.K, args.group_k = B, M, N, K, w.g
     args.split_k = max(1, int(split_k))
     args.out_dtype = _lib.W6A16_OUT_F32 if odt == torch.float32 else _lib.W6A16_OUT_BF16
     lib = _lib.load()
@@ -216,16 +299,18 @@ def _workspace(device, nbytes):
     return ws
 
 
-def int6_matmul(a, lo, hi, s, group_k, split_k=None, use_dot=None, *, out_dtype=None):
+def int6_matmul(a, lo, hi=None, s=None, group_k=None, split_k=None, use_dot=None, *, out_dtype=None):
     """a (M, K) | (B, M, K) bf16 @ dequant(int6 weight (K, N) | (B, K, N)) -> (M, N) | (B, M, N) in a.dtype (or
-    out_dtype: bfloat16 / float32).  A single weight (K, N) is shared by every batch row.  Eager entry point; the
-    model-facing functional op is int6_matmul_op."""
+    out_dtype: bfloat16 / float32).  The weight is the planes (lo, hi, s, group_k) or an Int6Packed passed as `lo`
+    (hi, s, group_k then unused).  A single weight (K, N) is shared by every batch row.  Eager entry point; the
+    model-facing functional ops are int6_matmul_op and int6_matmul_packed_op."""
+    w = _packed(lo) if isinstance(lo, Int6Packed) else _planes(lo, hi, s, group_k)
     B = a.shape[0] if a.dim() == 3 else 1
-    M, K, N = a.shape[-2], a.shape[-1], lo.shape[-1]
+    M = a.shape[-2]
     if split_k is None:
-        split_k, _ = plan_int6(M, N, K, B, a.device)
+        split_k, _ = plan_int6(M, w.N, w.K, B, a.device)
     with torch.cuda.device(a.device):
-        return _impl(a, lo, hi, s, group_k, split_k, out_dtype)
+        return _impl(a, w, split_k, out_dtype)
 
 
 @torch.library.custom_op("rwkv_next_amd::int6_matmul", mutates_args=())
@@ -234,7 +319,20 @@ def int6_matmul_op(a: torch.Tensor, lo: torch.Tensor, hi: torch.Tensor, s: torch
     """Functional op with the schema of the reference's rwkv_next::int6_matmul (int6_gemm.py:316-323); the plan
     (split_k, use_dot) comes from plan_int6, resolved by the caller."""
     with torch.cuda.device(a.device):
-        return _impl(a, lo, hi, s, group_k, split_k)
+        return _impl(a, _planes(lo, hi, s, group_k), split_k)
+
+
+@torch.library.custom_op("rwkv_next_amd::int6_matmul_packed", mutates_args=())
+def int6_matmul_packed_op(a: torch.Tensor, weight: torch.Tensor, scales: torch.Tensor, batches: int, K: int, N: int,
+                          group_k: int, split_k: int) -> torch.Tensor:
+    """int6_matmul_op for a packed weight (the fields of an Int6Packed); no counterpart in the reference."""
+    with torch.cuda.device(a.device):
+        return _impl(a, _packed(Int6Packed(weight, scales, batches, K, N, group_k)), split_k)
+
+
+@int6_matmul_packed_op.register_fake
+def _(a, weight, scales, batches, K, N, group_k, split_k):
+    return a.new_empty((*a.shape[:-1], N))
 
 
 @int6_matmul_op.register_fake

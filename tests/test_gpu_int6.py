@@ -193,3 +193,79 @@ def test_quantise_on_device_then_matmul():
     wq = I6.dequantize_int6(lo, hi, sc, g).cpu()
     rel = ((wq - w.cpu()).norm() / w.cpu().norm()).item()
     assert rel < 0.03, rel
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# packed layout (prepack_int6): same codes, re-laid out; results must equal the planes' bit for bit
+# ----------------------------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("B,K,N,g", [(1, 512, 384, 128), (1, 256, 144, 256), (2, 192, 272, 64)])
+def test_prepack_matches_oracle_layout(B, K, N, g):
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    say("prepack_int6", dict(B=B, K=K, N=N, g=g))
+    rng = np.random.default_rng(20 + K + N)
+    lo, hi, sc = _weights(rng, B, K, N, g)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    if B == 1:
+        Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    pk = I6.prepack_int6(Ld, Hd, Sd, g)
+    torch.cuda.synchronize()
+    w_ref, s_ref = R.pack_packed(lo, hi, sc, g)
+    assert pk.batches == (0 if B == 1 else B) and (pk.K, pk.N, pk.group_k) == (K, N, g)
+    np.testing.assert_array_equal(pk.weight.cpu().numpy(), w_ref)
+    np.testing.assert_array_equal(pk.scales.cpu().view(torch.int16).numpy(), s_ref.view(np.int16))
+    # dequantising the packed weight gives the planes' weight exactly
+    for dt in (torch.float32, torch.bfloat16):
+        wp = I6.dequantize_int6_packed(pk, dtype=dt)
+        wq = I6.dequantize_int6(Ld, Hd, Sd, g, dtype=dt)
+        torch.cuda.synchronize()
+        assert torch.equal(wp, wq), dt
+
+
+@pytest.mark.parametrize("B,M,N,K,g,split,shared", [
+    (1, 1, 4096, 4096, 128, None, True),
+    (1, 3, 512, 1024, 128, 3, True),
+    (1, 16, 2048, 1024, 64, None, True),
+    (1, 40, 640, 1024, 128, None, True),      # two 16-row tiles per wavefront
+    (1, 5, 144, 256, 256, None, True),        # N not a multiple of 128
+    (1, 1, 512, 640, 64, 7, True),            # an empty split range
+    (3, 7, 384, 1024, 128, None, True),       # one weight shared by the batch
+    (3, 7, 384, 1024, 128, None, False),      # one weight per batch row
+])
+def test_packed_matmul_equals_planes(B, M, N, K, g, split, shared):
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    say("int6_matmul packed", dict(B=B, M=M, N=N, K=K, split=split, shared=shared))
+    rng = np.random.default_rng(30 + M + N + K)
+    Bq = 1 if shared else B
+    lo, hi, sc = _weights(rng, Bq, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    if shared:
+        Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    pk = I6.prepack_int6(Ld, Hd, Sd, g)
+    ad = a.to(DEV) if B > 1 else a[0].to(DEV)
+    for odt in (torch.float32, torch.bfloat16):
+        Cp = I6.int6_matmul(ad, pk, split_k=split, out_dtype=odt)
+        Cq = I6.int6_matmul(ad, Ld, Hd, Sd, g, split_k=split, out_dtype=odt)
+        torch.cuda.synchronize()
+        assert torch.equal(Cp, Cq), odt
+    _check(Cp.float() if B > 1 else Cp.float()[None], a, lo, hi, sc, g, KERNEL_TOL, bf16_out=True, shared=shared)
+    # the functional op
+    sk = split if split is not None else I6.plan_int6(M, N, K, B, torch.device(DEV))[0]
+    Co = I6.int6_matmul_packed_op(ad, pk.weight, pk.scales, pk.batches, K, N, g, sk)
+    torch.cuda.synchronize()
+    assert torch.equal(Co, Cp)
+
+
+def test_packed_large_m_path():
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K, g = I6.MAX_M + 9, 384, 512, 128
+    say("int6_matmul packed large M", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(41)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    a = _act(rng, 1, M, K)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    pk = I6.prepack_int6(Ld, Hd, Sd, g)
+    Cp = I6.int6_matmul(a[0].to(DEV), pk)
+    Cq = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g)
+    torch.cuda.synchronize()
+    assert torch.equal(Cp, Cq)

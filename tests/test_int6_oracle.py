@@ -101,6 +101,45 @@ def test_dequant_and_matmul_oracle():
     assert abs(C[1, i, j] - sum(a[1, i, k] * w[k, j] for k in range(K))) < 1e-10
 
 
+def test_known_answer_packed_records():
+    """Single codes land at the byte the packed layout's definition gives (include/w6a16.h, w6a16_pack):
+    record dword d of lane l sits at byte 1024 (d // 4) + 16 l + 4 (d % 4) of its 6144-byte block."""
+    K, N, g = 64, 256, 64
+    # row 5, column 35 = 16 * 2 + 3 (strip 0, tile 2, lane i = 3, q = 0, e = 5): lo byte row 5 -> dword 2 t + 1 = 5,
+    # byte 1; top bits -> dword 16 + t = 18, byte e' = 1, bits 4-5
+    # row 40 = 32 + 8, column 130 = 128 + 2 (strip 1, tile 0, i = 2, q = 1, e = 0): high nibble of lo row 8 ->
+    # dword 0, byte 0, bits 4-7; top bits -> dword 16, byte 0, bits 2-3
+    u = np.zeros((K, N), np.uint8)
+    u[5, 35] = 0x3F
+    u[40, 130] = 0x3F
+    lo, hi = R.pack_codes(u)
+    sc = np.ones((1, N), np.float16)
+    w, _ = R.pack_packed(lo, hi, sc, g)
+    w = w[0]
+    expect = np.zeros(2 * 6144, np.uint8)
+    lane = 3
+    expect[1024 * 1 + 16 * lane + 4 * 1 + 1] = 0x0F        # dword 5 = 0x00000F00
+    expect[1024 * 4 + 16 * lane + 4 * 2 + 1] = 0x30        # dword 18 = 0x00003000
+    lane = 16 + 2
+    expect[6144 + 16 * lane] = 0xF0                        # dword 0 = 0x000000F0
+    expect[6144 + 1024 * 4 + 16 * lane] = 0x0C             # dword 16 = 0x0000000C
+    np.testing.assert_array_equal(w, expect)
+
+
+def test_packed_layout_round_trip():
+    rng = np.random.default_rng(8)
+    for B, K, N, g in [(1, 128, 144, 64), (2, 192, 256, 192)]:
+        u = rng.integers(0, 64, size=(B, K, N), dtype=np.uint8)
+        lo, hi = R.pack_codes(u)
+        sc = rng.uniform(0.01, 0.1, size=(B, K // g, N)).astype(np.float16)
+        w, s = R.pack_packed(lo, hi, sc, g)
+        strips = (N + 127) // 128
+        assert w.shape == (B, strips * (K // 64) * 6144) and s.shape == (B, strips * (K // g) * 128)
+        u2, s2 = R.unpack_packed(w, s, K, N, g)
+        np.testing.assert_array_equal(u2, u)
+        np.testing.assert_array_equal(s2, sc)
+
+
 # ----------------------------------------------------------------------------------------------------------------
 # the product's quantiser (host code in torch; CPU here)
 # ----------------------------------------------------------------------------------------------------------------
@@ -233,6 +272,28 @@ def test_matmul_empty_and_workspace_size():
     assert lib.w6a16_matmul(ctypes.byref(small), None) == _lib.WKV7_ERR_WORKSPACE
     odd = base_args(split_k=8, B=2, M=3, workspace=0x10080, workspace_bytes=1 << 24)
     assert lib.w6a16_matmul(ctypes.byref(odd), None) == _lib.WKV7_ERR_ALIGN
+
+
+def test_packed_entry_points_validate_before_launch():
+    lib = _lib.load()
+    f = 0x10000
+    wb, sb = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    assert lib.w6a16_packed_size(2, 256, 144, 64, ctypes.byref(wb), ctypes.byref(sb)) == 0
+    assert wb.value == 2 * 2 * 4 * 6144 and sb.value == 2 * 2 * 4 * 128 * 2
+    assert lib.w6a16_packed_size(1, 256, 140, 64, ctypes.byref(wb), ctypes.byref(sb)) == _lib.WKV7_ERR_SHAPE
+    assert lib.w6a16_pack(f, f, f, 1, 256, 144, 96, 0, 0, 0, f, f, None) == _lib.WKV7_ERR_SHAPE
+    assert lib.w6a16_pack(f, None, f, 1, 256, 144, 64, 0, 0, 0, f, f, None) == _lib.WKV7_ERR_NULL
+    assert lib.w6a16_pack(f, f, f, 1, 256, 144, 64, 0, 0, 0, f + 8, f, None) == _lib.WKV7_ERR_ALIGN
+    assert lib.w6a16_dequantize_packed(f, None, f, 1, 256, 144, 64, 0, 0, None) == _lib.WKV7_ERR_NULL
+    assert lib.w6a16_dequantize_packed(f, f, f, 1, 256, 144, 64, 0, 3, None) == _lib.WKV7_ERR_ARG
+    # the matmul's format field: packed needs no hi plane but 16-byte aligned packed scales
+    a = base_args(format=_lib.W6A16_FORMAT_PACKED, hi=None)
+    assert lib.w6a16_matmul(ctypes.byref(base_args(format=2)), None) == _lib.WKV7_ERR_ARG
+    assert lib.w6a16_matmul(ctypes.byref(base_args(format=_lib.W6A16_FORMAT_PACKED, hi=None, scales=0x10004)),
+                            None) == _lib.WKV7_ERR_ALIGN
+    assert lib.w6a16_matmul(ctypes.byref(base_args(format=_lib.W6A16_FORMAT_PLANES, hi=None)), None) == \
+        _lib.WKV7_ERR_NULL
+    assert a.format == _lib.W6A16_FORMAT_PACKED
 
 
 def test_dequantize_validates_before_launch():
