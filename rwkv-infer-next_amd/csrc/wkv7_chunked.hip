@@ -459,6 +459,8 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     // ---- 2. g (inclusive) and g of the previous row; midpoint m = g_31 and chunk total g_63 per channel
     float gi[8], ge[8], mk[8];
     {
+        // running sum over the waves' totals in wave order; this wave's offset is the sum before its own total
+        // (wv is wave-uniform: the capture is a scalar branch, not a per-lane select)
         float off[8], g63[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) off[e] = g63[e] = 0.f;
@@ -466,12 +468,14 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         for (int w2 = 0; w2 < 8; ++w2) {
             const f4 t0 = *reinterpret_cast<const f4*>(&sm.bsum[w2][cb]);
             const f4 t1 = *reinterpret_cast<const f4*>(&sm.bsum[w2][cb + 4]);
+            if (w2 == wv) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) off[e] = g63[e];
+            }
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float t = e < 4 ? t0[e] : t1[e - 4];
-                if (w2 < wv) off[e] += t;
                 if (w2 == 4) mk[e] = g63[e];
-                g63[e] += t;
+                g63[e] += e < 4 ? t0[e] : t1[e - 4];
             }
         }
 #pragma unroll
@@ -493,12 +497,21 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     // ---- 3. Gram operands referenced to the chunk midpoint: Aq = a 2^{g_{t-1}-m}, Rq = r 2^{g_t-m},
     //         Bk = b 2^{m-g_t}, Kk = k 2^{m-g_t} (split hi/lo)
     {
-        const uint32_t aw[4] = {raw.a.x, raw.a.y, raw.a.z, raw.a.w}, bw[4] = {raw.b.x, raw.b.y, raw.b.z, raw.b.w};
-        const uint32_t kw[4] = {raw.k.x, raw.k.y, raw.k.z, raw.k.w}, rw[4] = {raw.r.x, raw.r.y, raw.r.z, raw.r.w};
-        bf8 aqh, aql, bkh, bkl, kkh, kkl, rqh;
+        // rows outside the chunk read token 0 (see load_item): their raw operands are zeroed once, word by word
+        const uint32_t vm = valid ? 0xffffffffu : 0u;
+        const uint32_t aw[4] = {raw.a.x & vm, raw.a.y & vm, raw.a.z & vm, raw.a.w & vm};
+        const uint32_t bw[4] = {raw.b.x & vm, raw.b.y & vm, raw.b.z & vm, raw.b.w & vm};
+        const uint32_t kw[4] = {raw.k.x & vm, raw.k.y & vm, raw.k.z & vm, raw.k.w & vm};
+        const uint32_t rw[4] = {raw.r.x & vm, raw.r.y & vm, raw.r.z & vm, raw.r.w & vm};
+        uint32_t aqh[4], aql[4], bkh[4], bkl[4], kkh[4], kkl[4], rqh[4];
+        // hi/lo split of a channel pair straight into packed words: hi = bf16(x), lo = bf16(x - hi)
+        auto split2 = [](float x0, float x1, uint32_t& hw, uint32_t& lw) {
+            hw = pack_bf16x2(x0, x1);
+            lw = pack_bf16x2(x0 - __uint_as_float(hw << 16), x1 - __uint_as_float(hw & 0xffff0000u));
+        };
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
-            float a2[2], b2[2], k2[2], r2[2];
+            float a2[2], b2[2], k2[2], r2[2], fa[2], fr[2], fb[2];
             bf16x2_to_f32(aw[e2], a2[0], a2[1]);
             bf16x2_to_f32(bw[e2], b2[0], b2[1]);
             bf16x2_to_f32(kw[e2], k2[0], k2[1]);
@@ -506,31 +519,26 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
 #pragma unroll
             for (int u = 0; u < 2; ++u) {
                 const int e = 2 * e2 + u;
-                const float fa = __builtin_amdgcn_exp2f(ge[e] - mk[e]), fr = __builtin_amdgcn_exp2f(gi[e] - mk[e]);
-                const float fb = __builtin_amdgcn_exp2f(mk[e] - gi[e]);
-                const float aq = valid ? a2[u] * fa : 0.f, rq = valid ? r2[u] * fr : 0.f;
-                const float bk = valid ? b2[u] * fb : 0.f, kq = valid ? k2[u] * fb : 0.f;
-                __bf16 h, l;
-                split(aq, h, l);
-                aqh[e] = h;
-                aql[e] = l;
-                split(bk, h, l);
-                bkh[e] = h;
-                bkl[e] = l;
-                split(kq, h, l);
-                kkh[e] = h;
-                kkl[e] = l;
-                rqh[e] = (__bf16)rq;
+                fa[u] = __builtin_amdgcn_exp2f(ge[e] - mk[e]);
+                fr[u] = __builtin_amdgcn_exp2f(gi[e] - mk[e]);
+                fb[u] = __builtin_amdgcn_exp2f(mk[e] - gi[e]);
             }
+            split2(a2[0] * fa[0], a2[1] * fa[1], aqh[e2], aql[e2]);
+            split2(b2[0] * fb[0], b2[1] * fb[1], bkh[e2], bkl[e2]);
+            split2(k2[0] * fb[0], k2[1] * fb[1], kkh[e2], kkl[e2]);
+            rqh[e2] = pack_bf16x2(r2[0] * fr[0], r2[1] * fr[1]);
         }
         const int o = row * PB + cb;
-        *reinterpret_cast<bf8*>(Aq.h + o) = aqh;
-        *reinterpret_cast<bf8*>(Aq.l + o) = aql;
-        *reinterpret_cast<bf8*>(Bk.h + o) = bkh;
-        *reinterpret_cast<bf8*>(Bk.l + o) = bkl;
-        *reinterpret_cast<bf8*>(Kk.h + o) = kkh;
-        *reinterpret_cast<bf8*>(Kk.l + o) = kkl;
-        *reinterpret_cast<bf8*>(Rq.h + o) = rqh;
+        auto st = [&](__bf16* dst, const uint32_t (&w)[4]) {
+            *reinterpret_cast<uint4*>(dst + o) = make_uint4(w[0], w[1], w[2], w[3]);
+        };
+        st(Aq.h, aqh);
+        st(Aq.l, aql);
+        st(Bk.h, bkh);
+        st(Bk.l, bkl);
+        st(Kk.h, kkh);
+        st(Kk.l, kkl);
+        st(Rq.h, rqh);
     }
     __syncthreads();
     next.a = *reinterpret_cast<const uint4*>(p.a + noff);
