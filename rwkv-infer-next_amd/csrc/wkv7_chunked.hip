@@ -588,51 +588,64 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     __syncthreads();
     next.b = *reinterpret_cast<const uint4*>(p.b + noff);
 
-    // ---- 5. wave 0: inverses T_ii = (I - L)^{-1} of the four 16 x 16 diagonal blocks L = alpha_ii (strictly lower),
-    //         by forward substitution in fp32, one column per lane (lane = 16 block + column):
-    //         T[m][j] = delta_mj + sum_{p<m} L[m][p] T[p][j].
-    //         waves 1-6: the six blocks alpha_ij, i > j.
+    // ---- 5. waves 0-3: inverse T_ii = (I - L)^{-1} of diagonal block i = wv (L = alpha_ii, strictly lower, so
+    //         L^16 = 0 and T = (I + L)(I + L^2)(I + L^4)(I + L^8), the factors commuting).  With Bl(M) the 16x16x16
+    //         MFMA's B / result layout (lane (c, q) holds M[4 q + v][c]) and Al(M) = Bl(M^T) its A layout, the
+    //         powers P_k = L^(2^k) and Q_k = (L^T)^(2^k) feed each other: Bl(P_k) = mfma(Bl(Q_{k-1}), Bl(P_{k-1})),
+    //         Bl(Q_k) = mfma(Bl(P_{k-1}), Bl(Q_{k-1})), and Bl(T^T) = prod (I + Q_k) accumulates as
+    //         Z_k = mfma(Bl(I + P_k), Z_{k-1}).  Lane (c, q) then holds T[c][4 q + v], the row segment the
+    //         substitution below reads as its A operand; 3-term hi/lo products throughout (state path).
+    //         waves 4-7: the six blocks alpha_ij, i > j.
     //         Both leave their block split hi/lo in place, as the A operand of step 7: each 64-byte row segment of
     //         a 16 x 16 fp32 block becomes 16 bf16 hi followed by 16 bf16 lo.
-    if (wv == 0) {
-        const int bb = lane >> 4, j = lane & 15;
-        float* const Lb = F32 + (16 * bb) * PF + 16 * bb;
-        // the strictly lower part of the block, all reads issued before the arithmetic (row m needs p < m)
-        f4 Lr[16][4];
+    if (wv < 4) {
+        float* const Lb = F32 + (16 * wv) * PF + 16 * wv;
+        f4 P, Q;
 #pragma unroll
-        for (int m = 1; m < 16; ++m) {
+        for (int v = 0; v < 4; ++v) P[v] = Lb[(4 * lq + v) * PF + li];  // Bl(L)
+        Q = *reinterpret_cast<const f4*>(Lb + li * PF + 4 * lq);        // Bl(L^T)
+        auto plus_i = [&](f4 x) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c)
-                if (4 * c < m) Lr[m][c] = *reinterpret_cast<const f4*>(Lb + m * PF + 4 * c);
+            for (int v = 0; v < 4; ++v) x[v] += (4 * lq + v == li) ? 1.f : 0.f;
+            return x;
+        };
+        auto mul3 = [](f4 a, f4 b) {  // Bl(A B) from Bl(A^T) and Bl(B), hi/lo
+            s4 ah, al, bh, bl;
+            split4(a, ah, al);
+            split4(b, bh, bl);
+            f4 acc = mfma16(ah, bl, zero4());
+            acc = mfma16(al, bh, acc);
+            return mfma16(ah, bh, acc);
+        };
+        f4 Z = plus_i(Q);  // Bl(I + Q_0)
+#pragma unroll
+        for (int k = 1; k < 4; ++k) {
+            const f4 Pn = mul3(Q, P);
+            if (k < 3) Q = mul3(P, Q);
+            P = Pn;
+            Z = mul3(plus_i(P), Z);
         }
-        float t[16];
+        s4 zh, zl;
+        split4(Z, zh, zl);
+        char* const seg = reinterpret_cast<char*>(Lb + li * PF);  // row li: hi at bytes 0..31, lo at 32..63
+        *reinterpret_cast<s4*>(seg + 8 * lq) = zh;
+        *reinterpret_cast<s4*>(seg + 32 + 8 * lq) = zl;
+    } else {
+        const int r = lane >> 2, qq = lane & 3;  // one row segment per 4 lanes of one wave
 #pragma unroll
-        for (int m = 0; m < 16; ++m) t[m] = m == j ? 1.f : 0.f;
-#pragma unroll
-        for (int m = 1; m < 16; ++m) {
-            float a[4] = {t[m], 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int pp = 0; pp < m; ++pp) a[pp & 3] += Lr[m][pp >> 2][pp & 3] * t[pp];
-            t[m] = (a[0] + a[1]) + (a[2] + a[3]);
+        for (int u = 0; u < 2; ++u) {
+            const int blk = (wv - 4) + 4 * u;  // blocks 0..5: (1,0) (2,0) (2,1) (3,0) (3,1) (3,2)
+            if (blk < 6) {
+                const int bi = blk < 1 ? 1 : (blk < 3 ? 2 : 3), bj = blk < 1 ? 0 : (blk < 3 ? blk - 1 : blk - 3);
+                float* const segf = F32 + (16 * bi + r) * PF + 16 * bj;
+                const f4 x = *reinterpret_cast<const f4*>(segf + 4 * qq);
+                s4 h4, l4;
+                split4(x, h4, l4);
+                char* const seg = reinterpret_cast<char*>(segf);
+                *reinterpret_cast<s4*>(seg + 8 * qq) = h4;  // the segment's reads all precede these writes (one wave)
+                *reinterpret_cast<s4*>(seg + 32 + 8 * qq) = l4;
+            }
         }
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            __bf16 hh, ll;
-            split(t[m], hh, ll);
-            __bf16* const seg = reinterpret_cast<__bf16*>(Lb + m * PF);
-            seg[j] = hh;
-            seg[16 + j] = ll;
-        }
-    } else if (wv <= 6) {
-        const int blk = wv - 1, r = lane >> 2, qq = lane & 3;  // one row segment per 4 lanes of one wave
-        const int bi = blk < 1 ? 1 : (blk < 3 ? 2 : 3), bj = blk < 1 ? 0 : (blk < 3 ? blk - 1 : blk - 3);
-        float* const segf = F32 + (16 * bi + r) * PF + 16 * bj;
-        const f4 x = *reinterpret_cast<const f4*>(segf + 4 * qq);
-        s4 h4, l4;
-        split4(x, h4, l4);
-        char* const seg = reinterpret_cast<char*>(segf);
-        *reinterpret_cast<s4*>(seg + 8 * qq) = h4;  // the segment's reads all precede these writes (one wave)
-        *reinterpret_cast<s4*>(seg + 32 + 8 * qq) = l4;
     }
     __syncthreads();
     next.k = *reinterpret_cast<const uint4*>(p.k + noff);
