@@ -838,72 +838,70 @@ __global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, ch
     }
 }
 
-// One chunk record's share of one scan lane (wavefront of column group vg): all of A (hi/lo) and Q as 16x16x32 operand
-// fragments, and the group's columns of H^T and O_intra.
 typedef short s8 __attribute__((ext_vector_type(8)));
-struct ScanRec {
-    s8 ah[4][2], al[4][2];  // [row tile r][k block c]: A[16 r + i][32 c + 8 q + j]
-    s8 q[4][2];             // [token tile t][k block c]: Q[16 t + i][32 c + 8 q + j]
-    f4 h[4];                // [k tile r]: H[16 r + 4 q + e][16 vg + i]
-    s8 o[2];                // [token tile pair]: O_intra[16 t + i][16 vg + 4 q + e]
-};
 
 __device__ __forceinline__ s4 half4(s8 x, int hi) {
     return hi ? __builtin_shufflevector(x, x, 4, 5, 6, 7) : __builtin_shufflevector(x, x, 0, 1, 2, 3);
 }
 
-// `rec` is wave-uniform: the loads address it as a scalar base plus the lane's 32-bit offset.
-__device__ __forceinline__ void scan_load(ScanRec& r, const char* rec, int vg, int lane) {
+// One half of a record as one of the two wavefronts of a column group uses it: row tiles (of A, H) and token tiles
+// (of Q, O_intra) 2 hf and 2 hf + 1.
+struct ScanRecH {
+    s8 ah[2][2], al[2][2];  // [row tile 2 hf + x][k block c]
+    s8 q[2][2];             // [token tile 2 hf + x][k block c]
+    f4 h[2];                // [k tile 2 hf + x]
+    s8 o;                   // token tile pair hf
+};
+
+__device__ __forceinline__ void scan_load_half(ScanRecH& r, const char* rec, int vg, int hf, int lane) {
     const char* const b = uniform_ptr(rec);
     const int lo = lane * 16;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
+    for (int x = 0; x < 2; ++x) {
+        const int X = 2 * hf + x;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-            r.ah[x][c] = *reinterpret_cast<const s8*>(b + REC_AH + (x * 2 + c) * 1024 + lo);
-            r.al[x][c] = *reinterpret_cast<const s8*>(b + REC_AL + (x * 2 + c) * 1024 + lo);
-            r.q[x][c] = *reinterpret_cast<const s8*>(b + REC_Q + (x * 2 + c) * 1024 + lo);
+            r.ah[x][c] = *reinterpret_cast<const s8*>(b + REC_AH + (X * 2 + c) * 1024 + lo);
+            r.al[x][c] = *reinterpret_cast<const s8*>(b + REC_AL + (X * 2 + c) * 1024 + lo);
+            r.q[x][c] = *reinterpret_cast<const s8*>(b + REC_Q + (X * 2 + c) * 1024 + lo);
         }
-        r.h[x] = *reinterpret_cast<const f4*>(b + REC_HT + (vg * 4 + x) * 1024 + lo);
+        r.h[x] = *reinterpret_cast<const f4*>(b + REC_HT + (vg * 4 + X) * 1024 + lo);
     }
-#pragma unroll
-    for (int c = 0; c < 2; ++c) r.o[c] = *reinterpret_cast<const s8*>(b + REC_OT + (vg * 2 + c) * 1024 + lo);
+    r.o = *reinterpret_cast<const s8*>(b + REC_OT + (vg * 2 + hf) * 1024 + lo);
 }
 
-// The state as 16x16x32 operands.  Lane (i, q) holds S[16 r + 4 q + e][col] (e = 0..3) of the four k tiles r; the
-// operand of contraction block c needs S[32 c + 8 q + j][col], j = 0..7, which lanes 2 (q & 1) and 2 (q & 1) + 1 of
-// tile 2 c + (q >> 1) hold.  With X = tile 2 c, Y = tile 2 c + 1 and rows of 16 lanes: v_permlane32_swap(X, Y) gives
+// The state as 16x16x32 operands, one contraction block c at a time (X = S[2 c], Y = S[2 c + 1]).  Lane (i, q)
+// holds S[16 r + 4 q + e][col] (e = 0..3) of the k tiles r; the operand of contraction block c needs
+// S[32 c + 8 q + j][col], j = 0..7, which lanes 2 (q & 1) and 2 (q & 1) + 1 of tile 2 c + (q >> 1) hold.  With X = tile 2 c, Y = tile 2 c + 1 and rows of 16 lanes: v_permlane32_swap(X, Y) gives
 // P = (X0, X1, Y0, Y1), Q = (X2, X3, Y2, Y3), and v_permlane16_swap(P, Q) gives (X0, X2, Y0, Y2) -- values j = 0..3
 // for every row q -- and (X1, X3, Y1, Y3) -- values j = 4..7.  The same vector is the A operand of S^T.
-__device__ __forceinline__ void state_operands(const f4 (&S)[4], bf8 (&Bh)[2], bf8 (&Bl)[2]) {
+__device__ __forceinline__ void state_operand_block(const f4& X, const f4& Y, bf8& Bh, bf8& Bl) {
+    uint32_t h[2][2], l[2][2];
+    const f4 xs[2] = {X, Y};
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-        uint32_t h[2][2], l[2][2];  // [tile 2c, 2c + 1][dword]: packed hi / lo pairs (values 2 w, 2 w + 1)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-            const f4 x = S[2 * c + u];
-#pragma unroll
-            for (int w = 0; w < 2; ++w) {
-                const uint32_t hp = pack_bf16x2(x[2 * w], x[2 * w + 1]);
-                h[u][w] = hp;
-                l[u][w] = pack_bf16x2(x[2 * w] - __uint_as_float(hp << 16), x[2 * w + 1] - __uint_as_float(hp & 0xffff0000u));
-            }
-        }
-        uint32_t oh[4], ol[4];
+    for (int u = 0; u < 2; ++u) {
 #pragma unroll
         for (int w = 0; w < 2; ++w) {
-            const auto ph = __builtin_amdgcn_permlane32_swap(h[0][w], h[1][w], false, false);
-            const auto rh = __builtin_amdgcn_permlane16_swap(ph[0], ph[1], false, false);
-            oh[w] = rh[0];
-            oh[2 + w] = rh[1];
-            const auto pl = __builtin_amdgcn_permlane32_swap(l[0][w], l[1][w], false, false);
-            const auto rl = __builtin_amdgcn_permlane16_swap(pl[0], pl[1], false, false);
-            ol[w] = rl[0];
-            ol[2 + w] = rl[1];
+            const uint32_t hp = pack_bf16x2(xs[u][2 * w], xs[u][2 * w + 1]);
+            h[u][w] = hp;
+            l[u][w] = pack_bf16x2(xs[u][2 * w] - __uint_as_float(hp << 16),
+                                  xs[u][2 * w + 1] - __uint_as_float(hp & 0xffff0000u));
         }
-        Bh[c] = __builtin_bit_cast(bf8, oh);
-        Bl[c] = __builtin_bit_cast(bf8, ol);
     }
+    uint32_t oh[4], ol[4];
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+        const auto ph = __builtin_amdgcn_permlane32_swap(h[0][w], h[1][w], false, false);
+        const auto rh = __builtin_amdgcn_permlane16_swap(ph[0], ph[1], false, false);
+        oh[w] = rh[0];
+        oh[2 + w] = rh[1];
+        const auto pl = __builtin_amdgcn_permlane32_swap(l[0][w], l[1][w], false, false);
+        const auto rl = __builtin_amdgcn_permlane16_swap(pl[0], pl[1], false, false);
+        ol[w] = rl[0];
+        ol[2 + w] = rl[1];
+    }
+    Bh = __builtin_bit_cast(bf8, oh);
+    Bl = __builtin_bit_cast(bf8, ol);
 }
 
 constexpr int kScanDepth = 2;  // chunk records in flight per lane (register ring)
@@ -918,13 +916,17 @@ constexpr int kScanDepth = 2;  // chunk records in flight per lane (register rin
 // Chunk records stream through a ring of kScanDepth register sets.  Every step issues the same memory operations
 // (the refill index is clamped to the last chunk; stores that must not land go to the workspace's trash record), so
 // the compiler counts the outstanding loads exactly and waits only for the record about to be used.
-__global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
-                                                             const int32_t* __restrict__ plan, int64_t max_chunks,
-                                                             int ncps) {
+// A workgroup of two wavefronts owns one (sequence, head, 16-column group): wavefront hf computes row tiles
+// 2 hf, 2 hf + 1 of the new state and token tiles 2 hf, 2 hf + 1 of the output, and forms the state operand of
+// contraction block hf; the two operand halves are exchanged through LDS (double-buffered: one barrier per chunk).
+__global__ __launch_bounds__(128) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
+                                                              const int32_t* __restrict__ plan, int64_t max_chunks,
+                                                              int ncps) {
+    __shared__ bf8 ex[2][2][2][64];  // [buffer][half][hi, lo][lane]
     const int b = blockIdx.x;
     const int xcd = b & 7, rsl = b >> 3, vg = rsl & 3;
     const int64_t pair = (int64_t)(rsl >> 2) * 8 + xcd;
-    if (pair >= (int64_t)p.num_seqs * p.H) return;
+    if (pair >= (int64_t)p.num_seqs * p.H) return;  // uniform over the workgroup, as are the returns below
     const int n = (int)(pair / p.H), h = (int)(pair % p.H);
     int64_t bos;
     int L;
@@ -932,6 +934,7 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
     if (!owns_row(p, L)) return;
 
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int hf = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int64_t j0 = p.cu ? (int64_t)plan[2 * max_chunks + n] : (int64_t)n * ncps;
     // the chunk table never exceeds max_chunks for valid cu_seqlens; the clamp keeps invalid ones in bounds
     const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((L + C - 1) / C, max_chunks - j0));
@@ -939,24 +942,39 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
     float* dst = state_dst(p, n, h);
     const int col = 16 * vg + i;  // the state column this lane holds
 
-    f4 S[4];
+    f4 S[2];  // row tiles 2 hf, 2 hf + 1
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int x = 0; x < 2; ++x) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S[r][e] = src ? src[(16 * r + 4 * q + e) * HS + col] : 0.f;
+        for (int e = 0; e < 4; ++e) S[x][e] = src ? src[(16 * (2 * hf + x) + 4 * q + e) * HS + col] : 0.f;
     }
     if (nch == 0) {  // no chunks (length 0): the state passes through
         if (dst) {
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
+            for (int x = 0; x < 2; ++x) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dst[(16 * r + 4 * q + e) * HS + col] = S[r][e];
+                for (int e = 0; e < 4; ++e) dst[(16 * (2 * hf + x) + 4 * q + e) * HS + col] = S[x][e];
             }
         }
         return;
     }
     bf8 Bh[2], Bl[2];
-    state_operands(S, Bh, Bl);
+    int buf = 0;
+    auto exchange = [&]() {  // this half's operand block out, the other half's in
+        bf8 oh, ol;
+        state_operand_block(S[0], S[1], oh, ol);
+        ex[buf][hf][0][lane] = oh;
+        ex[buf][hf][1][lane] = ol;
+        __syncthreads();
+        const bf8 th = ex[buf][1 - hf][0][lane], tl = ex[buf][1 - hf][1][lane];
+        // whole-vector selects on the wave-uniform hf (an element index into Bh would become per-element selects)
+        Bh[0] = hf ? th : oh;
+        Bl[0] = hf ? tl : ol;
+        Bh[1] = hf ? oh : th;
+        Bl[1] = hf ? ol : tl;
+        buf ^= 1;  // the next writes go to the other buffer: the partner has read this one before the next barrier
+    };
+    exchange();
 
     const char* const rec0 = wsc + (j0 * p.H + h) * (int64_t)kChunkBytes;
     const int64_t rec_stride = (int64_t)p.H * kChunkBytes;
@@ -965,9 +983,9 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
     char* const trash = wsc + max_chunks * p.H * (int64_t)kChunkBytes + (b % 24) * 2048 + lane * 8;
     uint16_t* const obase = p.o ? p.o + bos * p.o_tok_stride + (int64_t)h * HS + 16 * vg + 4 * q : nullptr;
 
-    ScanRec ring[kScanDepth];
+    ScanRecH ring[kScanDepth];
 #pragma unroll
-    for (int d = 0; d < kScanDepth; ++d) scan_load(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, vg, lane);
+    for (int d = 0; d < kScanDepth; ++d) scan_load_half(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, vg, hf, lane);
 #pragma unroll
     for (int d = 0; d < kScanDepth; ++d) settle(ring[d]);
     for (int c0 = 0; c0 < nch; c0 += kScanDepth) {
@@ -975,39 +993,40 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
         for (int d = 0; d < kScanDepth; ++d) {
             const int cc = c0 + d;
             const bool live = cc < nch;  // wave-uniform
-            ScanRec& R = ring[d];
-            f4 nS[4];
+            ScanRecH& R = ring[d];
+            f4 nS[2];
 #pragma unroll
-            for (int r = 0; r < 4; ++r) nS[r] = R.h[r];
+            for (int x = 0; x < 2; ++x) nS[x] = R.h[x];
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const bf8 ah = __builtin_bit_cast(bf8, R.ah[r][c]), al = __builtin_bit_cast(bf8, R.al[r][c]);
-                    nS[r] = mfma_bf16(ah, Bl[c], nS[r]);
-                    nS[r] = mfma_bf16(al, Bh[c], nS[r]);
-                    nS[r] = mfma_bf16(ah, Bh[c], nS[r]);
+                for (int x = 0; x < 2; ++x) {
+                    const bf8 ah = __builtin_bit_cast(bf8, R.ah[x][c]), al = __builtin_bit_cast(bf8, R.al[x][c]);
+                    nS[x] = mfma_bf16(ah, Bl[c], nS[x]);
+                    nS[x] = mfma_bf16(al, Bh[c], nS[x]);
+                    nS[x] = mfma_bf16(ah, Bh[c], nS[x]);
                 }
             }
-            f4 y[4];
+            f4 y[2];
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                const s4 o4 = half4(R.o[t >> 1], t & 1);
+            for (int x = 0; x < 2; ++x) {
+                const s4 o4 = half4(R.o, x);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) y[t][e] = bf16_to_f32((uint16_t)o4[e]);
+                for (int e = 0; e < 4; ++e) y[x][e] = bf16_to_f32((uint16_t)o4[e]);
 #pragma unroll
-                for (int c = 0; c < 2; ++c) y[t] = mfma_bf16(Bh[c], __builtin_bit_cast(bf8, R.q[t][c]), y[t]);
+                for (int c = 0; c < 2; ++c) y[x] = mfma_bf16(Bh[c], __builtin_bit_cast(bf8, R.q[x][c]), y[x]);
             }
             // the refill reuses the slot's registers only if it is not scheduled above the slot's last use
             __builtin_amdgcn_sched_barrier(0);
-            scan_load(R, rec0 + std::min(cc + kScanDepth, nch - 1) * rec_stride, vg, lane);
+            scan_load_half(R, rec0 + std::min(cc + kScanDepth, nch - 1) * rec_stride, vg, hf, lane);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                // lane (i, q) holds y[token 16 t + i][columns 16 vg + 4 q .. + 3]
+            for (int x = 0; x < 2; ++x) {
+                // lane (i, q) holds y[token 16 t + i][columns 16 vg + 4 q .. + 3], t = 2 hf + x
+                const int t = 2 * hf + x;
                 const int tok = cc * C + 16 * t + i;
                 uint2 pk;
-                pk.x = pack_bf16x2(y[t][0], y[t][1]);
-                pk.y = pack_bf16x2(y[t][2], y[t][3]);
+                pk.x = pack_bf16x2(y[x][0], y[x][1]);
+                pk.y = pack_bf16x2(y[x][2], y[x][3]);
                 char* const out = (live && tok < L && obase)
                                       ? reinterpret_cast<char*>(obase + (int64_t)tok * p.o_tok_stride)
                                       : trash + t * 512;
@@ -1015,16 +1034,16 @@ __global__ __launch_bounds__(64) void wkv7_chunk_scan_kernel(const Params p, cha
             }
             if (live) {
 #pragma unroll
-                for (int r = 0; r < 4; ++r) S[r] = nS[r];
+                for (int x = 0; x < 2; ++x) S[x] = nS[x];
             }
-            state_operands(S, Bh, Bl);
+            exchange();
         }
     }
     if (dst) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int x = 0; x < 2; ++x) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dst[(16 * r + 4 * q + e) * HS + col] = S[r][e];
+            for (int e = 0; e < 4; ++e) dst[(16 * (2 * hf + x) + 4 * q + e) * HS + col] = S[x][e];
         }
     }
 }
@@ -1117,7 +1136,7 @@ hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* works
     }
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
     const int64_t blocks = ((pairs + 7) / 8) * 8 * 4;
-    hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(64), 0, stream, p, wsc, plan,
+    hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(128), 0, stream, p, wsc, plan,
                        ws.max_chunks, ncps);
     return hipGetLastError();
 }
