@@ -904,6 +904,8 @@ __device__ __forceinline__ void state_operand_block(const f4& X, const f4& Y, bf
     Bl = __builtin_bit_cast(bf8, ol);
 }
 
+constexpr int kPlanSortRows = 4096;    // ragged calls: longest-first ordering of up to this many chunked rows
+constexpr int kScanRaggedGrid = 2048;  // ragged calls: scan workgroups (about two rounds of residency)
 constexpr int kScanDepth = 2;  // chunk records in flight per lane (register ring)
 
 // One wavefront per (row, head, 16-column group vg); block b -> XCD b % 8, and the 4 groups of a (row, head) share an
@@ -919,15 +921,18 @@ constexpr int kScanDepth = 2;  // chunk records in flight per lane (register rin
 // A workgroup of two wavefronts owns one (sequence, head, 16-column group): wavefront hf computes row tiles
 // 2 hf, 2 hf + 1 of the new state and token tiles 2 hf, 2 hf + 1 of the output, and forms the state operand of
 // contraction block hf; the two operand halves are exchanged through LDS (double-buffered: one barrier per chunk).
-__global__ __launch_bounds__(128) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
-                                                              const int32_t* __restrict__ plan, int64_t max_chunks,
-                                                              int ncps) {
-    __shared__ bf8 ex[2][2][2][64];  // [buffer][half][hi, lo][lane]
-    const int b = blockIdx.x;
-    const int xcd = b & 7, rsl = b >> 3, vg = rsl & 3;
+// One work item b of the scan: (row, head) pair (b >> 5) * 8 + (b & 7) of the rows the call chunks, column group
+// (b >> 3) & 3 -- numbered so that, with a grid (or grid stride) that is a multiple of 8, the 4 column groups of a
+// pair run on one XCD and share its L2.  `rows` is the number of chunked rows; `row_of` lists them (ragged calls) or
+// is null (dense calls: every row).  `buf` is the exchange buffer index, carried across a workgroup's items.
+__device__ __forceinline__ void scan_item(const Params& p, char* __restrict__ wsc, const int32_t* __restrict__ plan,
+                                          int64_t max_chunks, int ncps, int64_t b, int64_t rows,
+                                          const int32_t* row_of, bf8 (&ex)[2][2][2][64], int& buf) {
+    const int xcd = (int)(b & 7), rsl = (int)(b >> 3), vg = rsl & 3;
     const int64_t pair = (int64_t)(rsl >> 2) * 8 + xcd;
-    if (pair >= (int64_t)p.num_seqs * p.H) return;  // uniform over the workgroup, as are the returns below
-    const int n = (int)(pair / p.H), h = (int)(pair % p.H);
+    if (pair >= rows * p.H) return;  // uniform over the workgroup, as are the returns below
+    const int k = (int)(pair / p.H), h = (int)(pair % p.H);
+    const int n = row_of ? row_of[k] : k;
     int64_t bos;
     int L;
     seq_extent(p, n, bos, L);
@@ -959,7 +964,6 @@ __global__ __launch_bounds__(128) void wkv7_chunk_scan_kernel(const Params p, ch
         return;
     }
     bf8 Bh[2], Bl[2];
-    int buf = 0;
     auto exchange = [&]() {  // this half's operand block out, the other half's in
         bf8 oh, ol;
         state_operand_block(S[0], S[1], oh, ol);
@@ -980,7 +984,7 @@ __global__ __launch_bounds__(128) void wkv7_chunk_scan_kernel(const Params p, ch
     const int64_t rec_stride = (int64_t)p.H * kChunkBytes;
     // stores that must not land go to the trash record, 2 KB per block slot (24 slots) so that blocks do not all hit
     // the same lines
-    char* const trash = wsc + max_chunks * p.H * (int64_t)kChunkBytes + (b % 24) * 2048 + lane * 8;
+    char* const trash = wsc + max_chunks * p.H * (int64_t)kChunkBytes + (int)(b % 24) * 2048 + lane * 8;
     uint16_t* const obase = p.o ? p.o + bos * p.o_tok_stride + (int64_t)h * HS + 16 * vg + 4 * q : nullptr;
 
     ScanRecH ring[kScanDepth];
@@ -1048,32 +1052,56 @@ __global__ __launch_bounds__(128) void wkv7_chunk_scan_kernel(const Params p, ch
     }
 }
 
+// Dense calls: one item per workgroup.  Ragged calls: a bounded grid walks the items of the rows the plan marked as
+// chunked (a grid over every row would be almost all empty workgroups when decode rows dominate, and their dispatch
+// costs more than the work).
+__global__ __launch_bounds__(128) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
+                                                              const int32_t* __restrict__ plan, int64_t max_chunks,
+                                                              int ncps) {
+    __shared__ bf8 ex[2][2][2][64];  // [buffer][half][hi, lo][lane]
+    int buf = 0;
+    if (!p.cu) {
+        scan_item(p, wsc, plan, max_chunks, ncps, blockIdx.x, p.num_seqs, nullptr, ex, buf);
+        return;
+    }
+    const int32_t* const rows_list = plan + 2 * max_chunks + p.num_seqs + 2;
+    const int64_t rows = std::min<int64_t>(std::max<int32_t>(rows_list[p.num_seqs], 0), p.num_seqs);
+    const int64_t items = ((rows * p.H + 7) / 8) * 8 * 4;
+    for (int64_t it = blockIdx.x; it < items; it += gridDim.x)
+        scan_item(p, wsc, plan, max_chunks, ncps, it, rows, rows_list, ex, buf);
+}
+
 // Chunk table of a ragged call: rows owned by the chunked path get ceil(len / C) consecutive chunk slots.
 __global__ __launch_bounds__(1024) void wkv7_chunk_plan_kernel(const Params p, int32_t* __restrict__ plan,
                                                                int64_t max_chunks) {
-    __shared__ int32_t scan[1024];
-    __shared__ int32_t base;
+    __shared__ int32_t scan[1024], fscan[1024];
+    __shared__ int32_t base, fbase;
     const int tid = threadIdx.x;
     int32_t* const chunk_seq = plan;
     int32_t* const chunk_idx = plan + max_chunks;
     int32_t* const seq_off = plan + 2 * max_chunks;
-    if (tid == 0) base = 0;
+    int32_t* const rows_list = seq_off + p.num_seqs + 2;  // the rows the chunked path owns, in order, then their count
+    if (tid == 0) base = fbase = 0;
     __syncthreads();
     for (int n0 = 0; n0 < p.num_seqs; n0 += 1024) {
         const int n = n0 + tid;
-        int32_t cnt = 0;
+        int32_t cnt = 0, flag = 0;  // flag: the chunked path owns the row (an empty owned row passes its state)
         if (n < p.num_seqs) {
             int64_t bos;
             int L;
             seq_extent(p, n, bos, L);
-            cnt = owns_row(p, L) ? (L + C - 1) / C : 0;
+            flag = owns_row(p, L) ? 1 : 0;
+            cnt = flag ? (L + C - 1) / C : 0;
         }
         scan[tid] = cnt;
+        fscan[tid] = flag;
         __syncthreads();
         for (int off = 1; off < 1024; off <<= 1) {
             const int32_t add = tid >= off ? scan[tid - off] : 0;
+            const int32_t fadd = tid >= off ? fscan[tid - off] : 0;
             __syncthreads();
             scan[tid] += add;
+            fscan[tid] += fadd;
             __syncthreads();
         }
         const int32_t excl = base + scan[tid] - cnt;
@@ -1085,14 +1113,50 @@ __global__ __launch_bounds__(1024) void wkv7_chunk_plan_kernel(const Params p, i
                     chunk_idx[excl + c] = c;
                 }
             }
+            if (flag) rows_list[fbase + fscan[tid] - 1] = n;
         }
         __syncthreads();
-        if (tid == 1023) base += scan[1023];
+        if (tid == 1023) {
+            base += scan[1023];
+            fbase += fscan[1023];
+        }
         __syncthreads();
     }
     if (tid == 0) {
         seq_off[p.num_seqs] = base;
         seq_off[p.num_seqs + 1] = (int32_t)min((int64_t)base, max_chunks);
+        rows_list[p.num_seqs] = fbase;
+    }
+    // Longest rows first: the scan walks rows_list in order with a bounded grid, so a long row that started last
+    // would set the call's length.  Rows are grouped by floor(log2(chunks)), descending (the order inside a group and
+    // the order itself do not change any result, only when each row's scan starts).  Lists longer than the LDS copy
+    // keep the natural order.
+    __syncthreads();
+    const int32_t count = fbase;
+    if (count > 1 && count <= kPlanSortRows) {
+        __shared__ int32_t rows_copy[kPlanSortRows];
+        __shared__ int32_t hist[33], cursor[33];
+        if (tid < 33) hist[tid] = 0;
+        for (int k = tid; k < count; k += 1024) rows_copy[k] = rows_list[k];
+        __syncthreads();
+        auto bucket = [&](int n) {
+            const int32_t cnt = seq_off[n + 1 < p.num_seqs ? n + 1 : p.num_seqs] - seq_off[n];  // chunks of row n
+            return cnt > 0 ? 32 - __builtin_clz((uint32_t)cnt) : 0;                            // 0 .. 32
+        };
+        for (int k = tid; k < count; k += 1024) atomicAdd(&hist[bucket(rows_copy[k])], 1);
+        __syncthreads();
+        if (tid == 0) {
+            int32_t acc = 0;
+            for (int b2 = 32; b2 >= 0; --b2) {
+                cursor[b2] = acc;
+                acc += hist[b2];
+            }
+        }
+        __syncthreads();
+        for (int k = tid; k < count; k += 1024) {
+            const int n = rows_copy[k];
+            rows_list[atomicAdd(&cursor[bucket(n)], 1)] = n;
+        }
     }
 }
 
@@ -1111,7 +1175,8 @@ ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_
         maxc = std::min<int64_t>(maxc, (total_tokens + C - 1) / C + long_rows);
     }
     ws.max_chunks = maxc;
-    ws.plan_bytes = varlen ? align256(sizeof(int32_t) * (size_t)(2 * maxc + num_seqs + 2)) : 0;
+    // chunk table (row, chunk index), row offsets + totals, the list of chunked rows + its length
+    ws.plan_bytes = varlen ? align256(sizeof(int32_t) * (size_t)(2 * maxc + 2 * (int64_t)num_seqs + 3)) : 0;
     ws.chunk_bytes = align256(((size_t)maxc * (size_t)H + 1) * kChunkBytes);  // + the trash record
     ws.total_bytes = ws.plan_bytes + ws.chunk_bytes;
     return ws;
@@ -1135,7 +1200,8 @@ hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* works
                            ws.max_chunks, ncps);
     }
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
-    const int64_t blocks = ((pairs + 7) / 8) * 8 * 4;
+    int64_t blocks = ((pairs + 7) / 8) * 8 * 4;
+    if (p.cu) blocks = std::min<int64_t>(blocks, kScanRaggedGrid);  // a multiple of 8: see scan_item
     hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(128), 0, stream, p, wsc, plan,
                        ws.max_chunks, ncps);
     return hipGetLastError();
