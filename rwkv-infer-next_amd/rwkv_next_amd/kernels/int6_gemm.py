@@ -286,16 +286,18 @@ _RETIRED: list = []
 
 
 def _workspace(device, nbytes):
-    """The device's split-K workspace (arrival counters + partials), zero-filled when created; every completed call
-    leaves its counters at zero, so calls issued in stream order share it.  A larger request replaces it; the old
-    buffer is kept alive, since a captured HIP graph may still address it."""
+    """The split-K workspace (arrival counters + partials) of the current stream on `device`, zero-filled when
+    created; every completed call leaves its counters at zero, so the calls of one stream (which run in order) share
+    it, and calls on different streams, which may overlap, never do.  A larger request replaces it; the old buffer is
+    kept alive, since a captured HIP graph may still address it."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    ws = _WORKSPACES.get(idx)
+    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
+    ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
         if ws is not None:
             _RETIRED.append(ws)
         ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
-        _WORKSPACES[idx] = ws
+        _WORKSPACES[key] = ws
     return ws
 
 

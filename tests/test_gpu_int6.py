@@ -269,3 +269,27 @@ def test_packed_large_m_path():
     Cq = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g)
     torch.cuda.synchronize()
     assert torch.equal(Cp, Cq)
+
+
+def test_two_streams_use_separate_workspaces():
+    """Split-K calls issued on two streams without synchronisation between them (they may run at the same time):
+    each stream has its own arrival counters, so every result equals the single-stream one bit for bit."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K, g = 2, 2048, 4096, 128
+    say("int6_matmul two streams", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(51)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    acts = [_act(rng, 1, M, K)[0].to(DEV) for _ in range(8)]
+    ref = [I6.int6_matmul(x, Ld, Hd, Sd, g, split_k=8, out_dtype=torch.float32) for x in acts]
+    torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    for s in streams:
+        s.wait_stream(torch.cuda.current_stream())
+    outs = []
+    for j, x in enumerate(acts):
+        with torch.cuda.stream(streams[j % 2]):
+            outs.append(I6.int6_matmul(x, Ld, Hd, Sd, g, split_k=8, out_dtype=torch.float32))
+    torch.cuda.synchronize()
+    for j in range(len(acts)):
+        assert torch.equal(outs[j], ref[j]), j
