@@ -53,16 +53,17 @@ typedef struct w6a16_args {
 /* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
 size_t w6a16_args_size(void);
 
-/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1): arrival counters, then fp32 partial tiles.  The split
- * that completes a tile last reduces it inside the kernel, so no second launch is made.  Contract: the workspace
- * must be zero-filled before its first use; every completed call leaves its counters at zero again, so one
- * workspace serves any number of calls issued one after another (stream order).  Calls that can run at the same
- * time (different streams) need different workspaces. */
+/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1): a fixed 1 MiB region of u32 arrival counters (one
+ * per output tile; a call with more than 262144 tiles is refused with WKV7_ERR_SHAPE), then fp32 partial tiles.  The
+ * split that completes a tile last reduces it inside the kernel, so no second launch is made.  Contract: the counter
+ * region (the first 1 MiB) must be zero before the workspace's first use; every completed call leaves it zero again
+ * and never writes partials into it, so one workspace serves any number of calls of any shapes issued one after
+ * another (stream order).  Calls that can run at the same time (different streams) need different workspaces. */
 int w6a16_workspace_size(const w6a16_args *args, size_t *bytes);
 
-/* Split-K for a shape: the smallest power of two (<= 64) giving at least one workgroup per CU, then doubled while
- * ranges keep at least eight 64-row chunks and the launch stays within two workgroups per CU.  Replaces the split-K
- * rule of plan_int6 (rwkv_next/kernels/int6_gemm.py:239-250). */
+/* Split-K for a shape: the smallest power of two (<= 64, every range keeping at least one 64-row chunk) that gives
+ * every CU at least one workgroup, then doubled while ranges keep at least sixteen 64-row chunks and the launch stays
+ * within two workgroups per CU.  Replaces the split-K rule of plan_int6 (rwkv_next/kernels/int6_gemm.py:239-250). */
 int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K);
 
 /* C = A @ dequant(W) on `stream` (hipStream_t).  Replaces `_impl` + `_w6a16` (int6_gemm.py:253-287, 156-215). */

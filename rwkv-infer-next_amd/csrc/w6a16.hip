@@ -51,7 +51,11 @@ constexpr int kPitch = 136;          // LDS row pitch in bytes (128 + 8: the 8 r
 constexpr int kRows = 48;            // plane rows per chunk: 32 lo + 16 hi
 constexpr int kScaleOff = kRows * kPitch;    // the chunk's 128 fp16 scales follow the plane rows
 constexpr int kBuf = kScaleOff + 2 * kTileN;
-constexpr int kCounterAlign = 256;   // bytes: the partials follow the counters at this alignment
+constexpr int kCounterAlign = 256;   // bytes: workspace alignment
+// The arrival counters occupy a fixed region at the start of the workspace, the partials follow it.  Calls with
+// different tile counts can share one workspace: the partials of one call never overlap the counters of another,
+// and every call leaves the counters it used at zero.
+constexpr size_t kCounterRegion = size_t(1) << 20;
 
 struct Args {
     const uint16_t* a;
@@ -217,6 +221,53 @@ __device__ __forceinline__ void store_tile(const Args& p, int b, int m0, int n0,
         }
 }
 
+// Split-K reduction of rows r0 .. r0 + R - 1 (those below `rows`) of a tile whose partials lie at `part`: lane l sums
+// columns 2 l, 2 l + 1 split by split in order 0, 1, ... and stores the result.  The loads of R rows x 8 splits are
+// issued together (each batch waits about one memory latency); rows past `rows` and splits past split_k re-read
+// valid entries whose values are not used.
+template <int R>
+__device__ __forceinline__ void reduce_rows(const Args& p, const float* part, int tile_floats, int r0, int rows,
+                                            int b, int m0, int n0) {
+    const int lane = threadIdx.x & 63;
+    const int n = n0 + 2 * lane;
+    const float* src[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) src[j] = part + min(r0 + j, rows - 1) * kTileN + 2 * lane;
+    float2 s[R];
+#pragma unroll
+    for (int j = 0; j < R; ++j) s[j] = float2{0.f, 0.f};
+    for (int sp = 0; sp < p.split_k; sp += 8) {
+        float2 x[R][8];
+#pragma unroll
+        for (int j = 0; j < R; ++j)
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                x[j][k] = coherent_load2(src[j] + (int64_t)min(sp + k, p.split_k - 1) * tile_floats);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            if (sp + k >= p.split_k) break;
+#pragma unroll
+            for (int j = 0; j < R; ++j) {
+                s[j].x += x[j][k].x;
+                s[j].y += x[j][k].y;
+            }
+        }
+    }
+    const int64_t ob = (int64_t)b * p.so_b;
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+        if (r0 + j >= rows || n >= p.N) continue;
+        const int64_t o = ob + (int64_t)(m0 + r0 + j) * p.so_m + n;
+        if (p.out_dtype == W6A16_OUT_F32) {
+            reinterpret_cast<float*>(p.out)[o] = s[j].x;
+            reinterpret_cast<float*>(p.out)[o + 1] = s[j].y;
+        } else {
+            reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)s[j].x;
+            reinterpret_cast<__bf16*>(p.out)[o + 1] = (__bf16)s[j].y;
+        }
+    }
+}
+
 // Stores the wavefront's tile, or (split-K) publishes it and, in the split that completes the tile last, reduces the
 // partials in split order and stores the result.
 template <int MT>
@@ -256,40 +307,10 @@ __device__ __forceinline__ void finish_tile(const Args& p, int b, int mg, int st
     arrived = __builtin_amdgcn_readfirstlane(arrived);
     if (arrived != (uint32_t)p.split_k - 1) return;
     __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the loads below are issued only after the counter returned
-    // Reduce: lane l sums columns 2 l, 2 l + 1 of every valid row, split by split in order 0, 1, ...; the loads of
-    // eight splits are issued together.
-    const int64_t ob = (int64_t)b * p.so_b;
-    const int n = n0 + 2 * lane;
-    for (int r = 0; r < rows; ++r) {
-        const float* src = part + r * kTileN + 2 * lane;
-        float s0 = 0.f, s1 = 0.f;
-        int sp = 0;
-        for (; sp + 8 <= p.split_k; sp += 8) {
-            float2 x[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) x[j] = coherent_load2(src + (int64_t)(sp + j) * kTileFloats);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                s0 += x[j].x;
-                s1 += x[j].y;
-            }
-        }
-        for (; sp < p.split_k; ++sp) {
-            const float2 x = coherent_load2(src + (int64_t)sp * kTileFloats);
-            s0 += x.x;
-            s1 += x.y;
-        }
-        if (n < p.N) {
-            const int64_t o = ob + (int64_t)(m0 + r) * p.so_m + n;
-            if (p.out_dtype == W6A16_OUT_F32) {
-                reinterpret_cast<float*>(p.out)[o] = s0;
-                reinterpret_cast<float*>(p.out)[o + 1] = s1;
-            } else {
-                reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)s0;
-                reinterpret_cast<__bf16*>(p.out)[o + 1] = (__bf16)s1;
-            }
-        }
-    }
+    if (rows == 1)
+        reduce_rows<1>(p, part, kTileFloats, 0, 1, b, m0, n0);
+    else
+        for (int r0 = 0; r0 < rows; r0 += 4) reduce_rows<4>(p, part, kTileFloats, r0, rows, b, m0, n0);
     if (lane == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -628,12 +649,14 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 // M tiles per wavefront: above 32 rows two 16-row tiles share each dequantised weight operand (measured at
 // K = 4096, N = 16384: M = 32 is faster with one tile per wavefront and two M groups, M = 64 with two; four tiles
-// per wavefront leave one wavefront per SIMD and lose at every split).
+// per wavefront leave one wavefront per SIMD and lose at every split).  Measured and not kept: a mode in which the
+// four wavefronts of a workgroup share one strip's dequantised chunk through LDS (each wavefront dequantising two
+// of the eight tiles, one barrier per chunk) -- 8 % faster at M = 64, no faster at M = 128, slower below 64 rows.
 int m_tiles_per_wave(int M) { return M <= 32 ? 1 : 2; }
 
 struct Layout {
     int mt, m_groups, n_strips;
-    size_t counter_bytes, partial_bytes;
+    size_t tiles, counter_bytes, partial_bytes;
 };
 
 Layout layout(const w6a16_args* a) {
@@ -643,7 +666,8 @@ Layout layout(const w6a16_args* a) {
     l.n_strips = (a->N + kTileN - 1) / kTileN;
     if (a->split_k > 1) {
         const size_t tiles = (size_t)a->B * l.m_groups * l.n_strips;
-        l.counter_bytes = (tiles * 4 + kCounterAlign - 1) / kCounterAlign * kCounterAlign;
+        l.tiles = tiles;
+        l.counter_bytes = kCounterRegion;
         l.partial_bytes = tiles * a->split_k * (size_t)l.mt * kTiles * 4 * 64 * 4;
     }
     return l;
@@ -670,6 +694,7 @@ int validate(const w6a16_args* a) {
     const Layout l = layout(a);
     if ((int64_t)a->B * l.m_groups > 65535) return WKV7_ERR_SHAPE;  // grid z: batch x M groups
     if (a->split_k > 1) {
+        if (l.tiles * 4 > kCounterRegion) return WKV7_ERR_SHAPE;  // more tiles than counters
         if (!a->workspace || a->workspace_bytes < l.counter_bytes + l.partial_bytes) return WKV7_ERR_WORKSPACE;
         if (reinterpret_cast<uintptr_t>(a->workspace) % kCounterAlign) return WKV7_ERR_ALIGN;
     }
@@ -713,11 +738,13 @@ int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
     const int64_t groups = (int64_t)B * ((M + 16 * mt - 1) / (16 * mt)) * ((strips + w6::kStrips - 1) / w6::kStrips);
     const int chunks = K / 64;
     const int64_t cus = w6::cu_count();
-    // At least one workgroup per CU; beyond that, ranges of about eight chunks (measured best at K = 4096 for every
-    // M up to 64) while the launch stays within two workgroups per CU.  Every range keeps at least one chunk.
+    // The smallest power of two that gives every CU a workgroup (every range keeps at least one chunk); then doubled
+    // while ranges keep at least 16 chunks and the launch stays within two workgroups per CU.  Measured at K = 4096,
+    // N = 16384: M = 128 is faster at split 4 than 2 (49.4 vs 51.1 us packed, 56.0 vs 61.4 planes), while M = 32 and
+    // M = 64 lose with ranges of eight chunks (split 8: 28.4 vs 24.3 us, 40.7 vs 33.9 us).
     int sk = 1;
     while (groups * sk < cus && sk * 2 <= 64 && chunks / (sk * 2) >= 1) sk *= 2;
-    while (chunks / (sk * 2) >= 8 && groups * sk * 2 <= 2 * cus && sk * 2 <= 64) sk *= 2;
+    while (chunks / (sk * 2) >= 16 && groups * sk * 2 <= 2 * cus && sk * 2 <= 64) sk *= 2;
     return sk;
 }
 

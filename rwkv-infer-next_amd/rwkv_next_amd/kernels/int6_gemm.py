@@ -143,9 +143,8 @@ def dequantize_int6(lo, hi, sc, group_k, dtype=torch.float32):
 # dispatch
 # ----------------------------------------------------------------------------------------------------------------
 def plan_int6(M, N, K, n_batch, device=None):
-    """(split_k, use_dot) for one shape.  split_k is the kernel's rule (w6a16_plan_split: about two wavefronts per
-    SIMD, at least two 64-row chunks per split, split_k * M <= K / 20); use_dot is M > 1 as in the reference and
-    does not change the computation."""
+    """(split_k, use_dot) for one shape.  split_k is the kernel's rule (w6a16_plan_split: the smallest power of two
+    that gives every CU a workgroup, doubled while ranges keep 16 chunks within two workgroups per CU); use_dot is M > 1 as in the reference and does not change the computation."""
     if device is not None and torch.device(device).type == "cuda":
         with torch.cuda.device(device):
             sk = _lib.load().w6a16_plan_split(n_batch, M, N, K)
@@ -281,24 +280,58 @@ def _impl(a, w: _W, split_k, out_dtype=None):
     return out if batched else out[0]
 
 
-_WORKSPACES: dict = {}
+_COUNTER_BYTES = 1 << 20   # the workspace's arrival-counter region (include/w6a16.h, w6a16_workspace_size)
+_WORKSPACES: dict = {}     # (device index, stream handle) -> [buffer, counters zeroed in stream order, capture id]
 _RETIRED: list = []
+_HIP = None
+
+
+def _capture_id(stream: int) -> int:
+    """The id of the HIP graph capture in progress on `stream` (hipStreamGetCaptureInfo)."""
+    global _HIP
+    if _HIP is None:
+        hip = ctypes.CDLL("libamdhip64.so")
+        hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
+        hip.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
+                                                ctypes.POINTER(ctypes.c_ulonglong)]
+        _HIP = hip
+    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    rc = _HIP.hipStreamGetCaptureInfo(ctypes.c_void_p(stream), ctypes.byref(status), ctypes.byref(cid))
+    if rc != 0:
+        raise RuntimeError(f"hipStreamGetCaptureInfo failed ({rc})")
+    return int(cid.value)
 
 
 def _workspace(device, nbytes):
-    """The split-K workspace (arrival counters + partials) of the current stream on `device`, zero-filled when
-    created; every completed call leaves its counters at zero, so the calls of one stream (which run in order) share
-    it, and calls on different streams, which may overlap, never do.  A larger request replaces it; the old buffer is
-    kept alive, since a captured HIP graph may still address it."""
+    """The split-K workspace (a fixed counter region, then partials) of the current stream on `device`.  The
+    counters must be zero when a call starts; every completed call leaves them zero, so the calls of one stream
+    (which run in order) share the workspace, and calls on different streams, which may overlap, never do.
+
+    A workspace created eagerly is zero-filled there.  One created during a HIP graph capture is zero-filled by a
+    node of that graph only, so until an eager call has zeroed it in stream order, every further capture that uses
+    it starts with a fill of its counter region (a graph may be replayed before the one that created the buffer).
+    A larger request replaces the buffer; the old one is kept alive, since a captured graph may still address it."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, torch.cuda.current_stream(idx).cuda_stream)
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        if ws is not None:
-            _RETIRED.append(ws)
-        ws = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
-        _WORKSPACES[key] = ws
-    return ws
+    stream = torch.cuda.current_stream(idx).cuda_stream
+    capturing = torch.cuda.is_current_stream_capturing()
+    key = (idx, stream)
+    entry = _WORKSPACES.get(key)
+    if entry is None or entry[0].numel() < nbytes:
+        if entry is not None:
+            _RETIRED.append(entry[0])
+        ws = torch.zeros(max(nbytes, 2 * _COUNTER_BYTES), dtype=torch.uint8, device=torch.device("cuda", idx))
+        entry = [ws, not capturing, _capture_id(stream) if capturing else None]
+        _WORKSPACES[key] = entry
+    if not entry[1]:
+        if capturing:
+            cid = _capture_id(stream)
+            if entry[2] != cid:
+                entry[0][:_COUNTER_BYTES].zero_()
+                entry[2] = cid
+        else:
+            entry[0][:_COUNTER_BYTES].zero_()
+            entry[1] = True
+    return entry[0]
 
 
 def int6_matmul(a, lo, hi=None, s=None, group_k=None, split_k=None, use_dot=None, *, out_dtype=None):

@@ -63,6 +63,10 @@ def _check(C, a_bf, lo, hi, sc, g, tol, bf16_out=False, shared=False):
     (1, 3, 512, 1024, 128, 3),        # uneven split ranges
     (1, 1, 512, 640, 64, 7),          # 10 chunks over 7 splits: one empty range
     (1, 1, 256, 4096, 128, 64),
+    (1, 17, 2048, 1024, 64, None),    # two M groups of one 16-row tile
+    (1, 48, 144, 512, 256, 2),        # two 16-row tiles per wavefront; N not a multiple of 128
+    (1, 100, 640, 1024, 128, 4),      # four M groups of 32 rows, the last one partly past M
+    (1, 128, 1024, 2048, 128, None),
 ])
 def test_matmul_matches_oracle(B, M, N, K, g, split):
     from rwkv_next_amd.kernels import int6_gemm as I6
@@ -269,6 +273,73 @@ def test_packed_large_m_path():
     Cq = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g)
     torch.cuda.synchronize()
     assert torch.equal(Cp, Cq)
+
+
+@pytest.mark.parametrize("packed", [False, True])
+def test_kernel_beyond_128_rows(monkeypatch, packed):
+    """The kernel itself takes any M (the module hands M > MAX_M to dequantise + library GEMM by default): 200 rows
+    are seven M groups of 32 rows, batched with a per-batch weight."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    monkeypatch.setattr(I6, "MAX_M", 1 << 20)
+    B, M, N, K, g = 2, 200, 384, 512, 128
+    say("int6_matmul kernel M > 128", dict(B=B, M=M, N=N, K=K, packed=packed))
+    rng = np.random.default_rng(63)
+    lo, hi, sc = _weights(rng, B, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    w = (I6.prepack_int6(Ld, Hd, Sd, g),) if packed else (Ld, Hd, Sd, g)
+    for split in (1, 2):
+        C = I6.int6_matmul(a.to(DEV), *w, split_k=split, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        _check(C, a, lo, hi, sc, g, KERNEL_TOL)
+
+
+def test_workspace_shared_across_shapes():
+    """One stream's workspace serves calls whose tile counts differ, in an order where a call with few tiles (and
+    large partials) precedes one with many: the counters live in a region the partials never reach."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    N, K, g = 2048, 1024, 128
+    rng = np.random.default_rng(61)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    for M, split in [(1, 16), (128, 4), (3, 16), (64, 2), (128, 8), (17, 4), (1, 8)]:
+        say("int6_matmul workspace sequence", dict(M=M, N=N, K=K, split=split))
+        a = _act(rng, 1, M, K)
+        C = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        _check(C[None], a, lo, hi, sc, g, KERNEL_TOL)
+
+
+def test_workspace_created_during_graph_capture():
+    """A workspace first created inside a HIP graph capture is zero-filled by that graph only; a second graph
+    captured on the same stream starts with its own fill of the counters, so either graph may be replayed first.
+    Each graph is replayed several times, with eager calls between the replays, and every replay is checked."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K, g = 64, 1024, 2048, 128
+    say("int6_matmul graph capture workspace", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(62)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    acts = [_act(rng, 1, M, K) for _ in range(2)]
+    xs = [x[0].to(DEV) for x in acts]
+    cs = torch.cuda.Stream()
+    I6._WORKSPACES.pop((torch.device(DEV).index or 0, cs.cuda_stream), None)   # force creation inside the capture
+    graphs, outs = [], []
+    torch.cuda.synchronize()
+    for x in xs:
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=cs):
+            outs.append(I6.int6_matmul_op(x, Ld, Hd, Sd, g, 4, True))
+        graphs.append(gr)
+    for rep in range(3):
+        for j in (1, 0):                      # the graph that did not create the workspace first
+            graphs[j].replay()
+            torch.cuda.synchronize()
+            _check(outs[j][None], acts[j], lo, hi, sc, g, KERNEL_TOL, bf16_out=True)
+        with torch.cuda.stream(cs):           # eager calls on the capture stream between replays
+            C = I6.int6_matmul(xs[rep % 2], Ld, Hd, Sd, g, split_k=4, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        _check(C[None], acts[rep % 2], lo, hi, sc, g, KERNEL_TOL)
 
 
 def test_two_streams_use_separate_workspaces():

@@ -261,15 +261,23 @@ def test_matmul_empty_and_workspace_size():
     n = ctypes.c_size_t(1)
     assert lib.w6a16_workspace_size(ctypes.byref(base_args()), ctypes.byref(n)) == 0 and n.value == 0
     assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=8, B=2, M=3)), ctypes.byref(n)) == 0
-    # tiles = B x M groups x 128-column strips = 2 x 1 x 2; one u32 counter each (rounded up to 256 bytes), then per
-    # tile and split a 16 x 128 fp32 partial tile
+    # the fixed 1 MiB counter region, then per tile (B x M groups x 128-column strips = 2 x 1 x 2) and split a
+    # 16 x 128 fp32 partial tile
     tiles = 2 * 1 * 2
-    assert n.value == 256 + tiles * 8 * 16 * 128 * 4
+    assert n.value == (1 << 20) + tiles * 8 * 16 * 128 * 4
     # M = 40 takes two 16-row tiles per wavefront: two M groups of 32 rows, two strips (N = 256): four tiles
     assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=2, M=40)), ctypes.byref(n)) == 0
-    assert n.value == 256 + (2 * 2) * 2 * 32 * 128 * 4
-    small = base_args(split_k=8, B=2, M=3, workspace=0x10000, workspace_bytes=256 + tiles * 8 * 16 * 128 * 4 - 4)
+    assert n.value == (1 << 20) + (2 * 2) * 2 * 32 * 128 * 4
+    # M = 100 takes two 16-row tiles per wavefront: four M groups of 32 rows, two strips: eight tiles
+    assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=2, M=100)), ctypes.byref(n)) == 0
+    assert n.value == (1 << 20) + (4 * 2) * 2 * 32 * 128 * 4
+    small = base_args(split_k=8, B=2, M=3, workspace=0x10000, workspace_bytes=(1 << 20) + tiles * 8 * 16 * 128 * 4 - 4)
     assert lib.w6a16_matmul(ctypes.byref(small), None) == _lib.WKV7_ERR_WORKSPACE
+    # at most 262144 tiles (the counter region's u32 counters): 40000 x 1 x 8 tiles are refused, 30000 x 1 x 8 reach
+    # the workspace check
+    many = dict(split_k=2, N=1024, out_row_stride=1024, out_batch_stride=4 * 1024, workspace=0x10000, workspace_bytes=1)
+    assert lib.w6a16_matmul(ctypes.byref(base_args(B=40000, **many)), None) == _lib.WKV7_ERR_SHAPE
+    assert lib.w6a16_matmul(ctypes.byref(base_args(B=30000, **many)), None) == _lib.WKV7_ERR_WORKSPACE
     odd = base_args(split_k=8, B=2, M=3, workspace=0x10080, workspace_bytes=1 << 24)
     assert lib.w6a16_matmul(ctypes.byref(odd), None) == _lib.WKV7_ERR_ALIGN
 
@@ -323,7 +331,9 @@ def test_split_rule():
         assert (K // 64) // sk >= 1
     # without a GPU the CU count is taken as 256: K = 4096, N = 16384 has 32 groups of four 128-column strips
     assert lib.w6a16_plan_split(1, 1, 16384, 4096) == 8
-    assert lib.w6a16_plan_split(1, 64, 16384, 4096) == 8        # two M groups of 32 rows
+    assert lib.w6a16_plan_split(1, 64, 16384, 4096) == 4        # two M groups of 32 rows: 64 groups
+    assert lib.w6a16_plan_split(1, 128, 16384, 4096) == 4       # 128 groups: 2 fills the chip, 4 keeps 16 chunks
+    assert lib.w6a16_plan_split(1, 1, 1024, 16384) == 64        # 2 groups, 256 chunks: capped at 64
     assert lib.w6a16_plan_split(1, 1, 4096, 16384) == 32
     assert I6.plan_int6(1, 4096, 4096, 1) == (lib.w6a16_plan_split(1, 1, 4096, 4096), False)
     assert I6.plan_int6(8, 4096, 4096, 1)[1] is True
