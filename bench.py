@@ -8,7 +8,8 @@ pools, so the 256 MB Infinity Cache cannot hold the state), the 32 launches capt
 value = algorithmic bytes / time: 33 664 B per (slot, head) per layer (16 KB state read + 16 KB written +
 768 B operands + 128 B output).
 
-Secondary (same line): chunked prefill B = 1, T = 4096, H = 64 (tok/s and fraction of its roofline), the
+Secondary (same line): the same decode step at configuration 1's H = 40 (pool [128, 40, 64, 64] x 32 layers,
+"decode_cfg1"), chunked prefill B = 1, T = 4096, H = 64 (tok/s and fraction of its roofline), the
 speculative verify with snapshots (config 4), the mixed continuous-batching step in a HIP graph (config 3), the
 fused time-mix prologue/epilogue at the prefill shape, the W6A16 weight GEMM at K = 4096, N = 16384, and the CPU
 baseline (the oracle's fp32 loop on the host cores).
@@ -48,8 +49,10 @@ def log(*a):
     print("[bench]", *a, file=sys.stderr, flush=True)
 
 
-def decode_bench(torch, kernels, synth, dev, steps, warmup):
-    L, S, B, H = 32, 128, 64, 64
+def decode_bench(torch, kernels, synth, dev, steps, warmup, H=64):
+    """B = 64 slots of a 128-slot pool, T = 1, 32 layer pools in one HIP graph.  H = 64 is the metric's shape;
+    H = 40 is configuration 1 (RWKV-7 2.9B, pool [128, 40, 64, 64])."""
+    L, S, B = 32, 128, 64
     g = torch.Generator(device=dev).manual_seed(1001)
     pools = [(0.1 * torch.randn(S, H, 64, 64, device=dev, generator=g)) for _ in range(L)]
     ins = []
@@ -372,6 +375,10 @@ def main():
     if args.only in (None, "decode"):
         log("decode")
         res["decode"] = decode_bench(torch, kernels, synth, dev, args.steps, args.warmup)
+        log("decode, configuration 1 (H = 40)")
+        c1 = decode_bench(torch, kernels, synth, dev, args.steps, args.warmup, H=40)
+        c1["frac_hbm"] = c1["GBps"] / HBM_PEAK_GBS
+        res["decode_cfg1"] = c1
     if args.only in (None, "prefill"):
         log("prefill")
         res["prefill"] = prefill_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
@@ -415,6 +422,8 @@ def main():
         out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": achieved / HBM_PEAK_GBS, "traffic": decode_traffic(),
                            "kernel": "wkv7_recurrent_kernel", "us_per_launch": d["us_per_launch"]}
+    if "decode_cfg1" in res:
+        out["decode_cfg1"] = res["decode_cfg1"]
     if "prefill" in res:
         out["prefill"] = res["prefill"]
     if "verify" in res:
