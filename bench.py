@@ -304,23 +304,44 @@ def int6_bench(torch, kernels, dev, steps, warmup):
 def cpu_baseline(synth):
     """The oracle's fp32 loop (a restatement of rwkv_next/kernels/wkv7.py:65-77) on the host cores, on a bounded
     sample of the decode workload: B = 64 sequences of a 128-slot pool, H = 64, T = 1, one pool, repeated for
-    about 10 s."""
+    about 10 s with every usable thread (at most 16) and about 4 s with one thread.  Beside it, configuration 0 in
+    full (B = 1, T = 512, H = 12, fp32, zero initial state) with all threads and with one."""
     import numpy as np
 
     import oracle
-    threads = min(16, len(os.sched_getaffinity(0)))
+    affinity = len(os.sched_getaffinity(0))
+    threads = min(16, affinity)
     B, S, H = 64, 128, 64
     ops = synth.operands_np((B, 1, H, 64), seed=3001)
     ins = [ops[n] for n in synth.OPERAND_NAMES]
     pool = synth.state_np((S, H, 64, 64), seed=3002)
     slots = np.random.default_rng(3003).permutation(S)[:B].astype(np.int64)
-    oracle.wkv7_ref(*ins, pool, state_idx=slots, precision="f32", threads=threads)  # warm-up
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < 10.0:
-        oracle.wkv7_ref(*ins, pool, state_idx=slots, precision="f32", threads=threads)
-        n += 1
-    dt = time.perf_counter() - t0
-    gbs = DECODE_BYTES_PER_PAIR * B * H * n / dt / 1e9
+
+    def decode_rate(nthreads, seconds):
+        oracle.wkv7_ref(*ins, pool, state_idx=slots, precision="f32", threads=nthreads)  # warm-up
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            oracle.wkv7_ref(*ins, pool, state_idx=slots, precision="f32", threads=nthreads)
+            n += 1
+        dt = time.perf_counter() - t0
+        return DECODE_BYTES_PER_PAIR * B * H * n / dt / 1e9, n, dt
+
+    gbs, n, dt = decode_rate(threads, 10.0)
+    gbs1, n1, dt1 = decode_rate(1, 4.0)
+
+    c0 = synth.operands_np((1, 512, 12, 64), seed=1000)          # configuration 0: seed 1000 + config index
+    c0_ins = [c0[nm] for nm in synth.OPERAND_NAMES]
+
+    def cfg0_ms(nthreads):
+        best = None
+        for _ in range(3):
+            t0 = time.perf_counter()
+            oracle.wkv7_ref(*c0_ins, None, precision="f32", threads=nthreads)
+            t = (time.perf_counter() - t0) * 1e3
+            best = t if best is None else min(best, t)
+        return best
+
+    ms_all, ms_one = cfg0_ms(threads), cfg0_ms(1)
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -329,7 +350,11 @@ def cpu_baseline(synth):
         pass
     return {"value": gbs, "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"decode B=64 of a 128-slot pool, H=64, T=1, one layer slice, {n} steps in {dt:.1f} s "
-                      f"(oracle fp32 loop, OpenMP); CPU: {model}"}
+                      f"(oracle fp32 loop, OpenMP); CPU: {model}",
+            "affinity": affinity, "value_1thread": gbs1, "sample_1thread": f"{n1} steps in {dt1:.1f} s",
+            "cfg0": {"shape": "B=1 T=512 H=12 fp32, zero initial state", "ms_all_threads": ms_all,
+                     "ms_1thread": ms_one, "tok_s_all_threads": 512 / (ms_all * 1e-3),
+                     "tok_s_1thread": 512 / (ms_one * 1e-3)}}
 
 
 def decode_traffic():
