@@ -1,7 +1,8 @@
 """Pins the CPU oracle (oracle/wkv7_oracle.cpp) against what the mathematics fixes, independently of how the
 oracle is written: closed forms evaluated with numpy matmuls, a textbook decay value, an asymmetric elementary
-row operation, explicit transition-matrix products, and the invariants the reference relies on (varlen ==
-per-sequence, chunked prefill continuation, n_keep == prefix, snapshots == prefix states).
+row operation, explicit transition-matrix products, exact rational arithmetic on tiny inputs, and the invariants the
+reference relies on (varlen == per-sequence, chunked prefill continuation, n_keep == prefix, snapshots == prefix
+states, slot relabelling, value-column independence).
 
 Reference semantics: rwkv_next/kernels/wkv7.py:4-7, 46-79; tools/test_wkv7.py:13-23.
 """
@@ -206,6 +207,68 @@ def test_pool_mode_updates_only_the_given_slots():
     for s in set(range(S_slots)) - set(slots.tolist()):
         assert np.array_equal(newpool[s], pool[s].astype(np.float64))
     assert np.array_equal(o, o2)
+
+
+def test_permuting_slots_permutes_the_results():
+    """Relabelling the pool's slots (pool'[pi(s)] = pool[s], indices pi(slots)) relabels the updated pool the same
+    way and leaves the outputs unchanged."""
+    rng = np.random.default_rng(12)
+    S_slots, B, T, H, K = 7, 3, 3, 2, 16
+    ins = model_like(rng, B, T, H, K)
+    pool = rnd(rng, S_slots, H, K, K, scale=0.1)
+    slots = np.array([5, 1, 3], np.int64)
+    pi = rng.permutation(S_slots)
+    pool_p = np.empty_like(pool)
+    pool_p[pi] = pool
+    o, new, _ = wkv7_ref(*ins, pool, state_idx=slots)
+    o_p, new_p, _ = wkv7_ref(*ins, pool_p, state_idx=pi[slots])
+    assert np.array_equal(o, o_p)
+    assert np.array_equal(new_p[pi], new)
+
+
+def test_value_columns_are_independent():
+    """Column j of the state and of y depends only on column j of S0 and on v[..., j]: changing one value column
+    (in v and in S0) changes exactly that column of every output."""
+    rng = np.random.default_rng(13)
+    B, T, H, K, j = 1, 6, 2, 16, 5
+    r, w, k, v, a, b = model_like(rng, B, T, H, K)
+    s0 = rnd(rng, B, H, K, K, scale=0.1)
+    o, S, _ = wkv7_ref(r, w, k, v, a, b, s0)
+    v2, s02 = v.copy(), s0.copy()
+    v2[..., j] = rnd(rng, B, T, H)
+    s02[..., j] = rnd(rng, B, H, K, scale=0.1)
+    o2, S2, _ = wkv7_ref(r, w, k, v2, a, b, s02)
+    others = [c for c in range(K) if c != j]
+    assert np.array_equal(o[..., others], o2[..., others])
+    assert np.array_equal(S[..., others], S2[..., others])
+    assert not np.allclose(o[..., j], o2[..., j]) and not np.allclose(S[..., j], S2[..., j])
+
+
+def test_exact_rational_brute_force_on_tiny_inputs():
+    """T = 3, K = 4: the recurrence in exact rational arithmetic (the decays d = exp(-exp(w)) taken as the exact
+    values of their float64 roundings) against the fp64 oracle; they agree to fp64 rounding."""
+    from fractions import Fraction
+    rng = np.random.default_rng(14)
+    B, T, H, K = 2, 3, 2, 4
+    r, w, k, v, a, b = model_like(rng, B, T, H, K)
+    s0 = rnd(rng, B, H, K, K, scale=0.5)
+    o, S, _ = wkv7_ref(r, w, k, v, a, b, s0)
+    Fr = np.vectorize(lambda x: Fraction(float(x)), otypes=[object])
+    d = Fr(np.exp(-np.exp(w.astype(np.float64))))
+    R, Kk, V, A, Bb, St = Fr(r), Fr(k), Fr(v), Fr(a), Fr(b), Fr(s0)
+    for n in range(B):
+        for h in range(H):
+            M = St[n, h].copy()                                        # M[k][j]
+            for t in range(T):
+                sa = [sum(A[n, t, h, i] * M[i, jj] for i in range(K)) for jj in range(K)]
+                M = np.array([[d[n, t, h, i] * M[i, jj] + Bb[n, t, h, i] * sa[jj] + Kk[n, t, h, i] * V[n, t, h, jj]
+                               for jj in range(K)] for i in range(K)], dtype=object)
+                y = [sum(R[n, t, h, i] * M[i, jj] for i in range(K)) for jj in range(K)]
+                for jj in range(K):
+                    assert abs(float(y[jj]) - o[n, t, h, jj]) <= 1e-13 * (1 + abs(float(y[jj])))
+            for i in range(K):
+                for jj in range(K):
+                    assert abs(float(M[i, jj]) - S[n, h, i, jj]) <= 1e-13 * (1 + abs(float(M[i, jj])))
 
 
 def test_fp32_vs_fp64_gap_on_config0():
