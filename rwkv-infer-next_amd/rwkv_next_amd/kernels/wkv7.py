@@ -299,6 +299,29 @@ class StatePool:
             _lib.check(_lib.load().wkv7_pool_reset(self.wkv.data_ptr(), self.L, self.S, self.H, i.data_ptr(),
                                                    i.numel(), _stream(self.device)))
 
+    # ---- speculative decoding (the WKV part of rwkv_next/model.py:475-508) -----------------------------------
+    def snapshot_buffer(self, B: int, T: int) -> torch.Tensor:
+        """Per-layer state snapshots for a verify of T tokens on B rows: (L, B, T, H, 64, 64) fp32 (the
+        reference keeps the operands instead and replays them)."""
+        return torch.empty(self.L, int(B), int(T), self.H, HEAD_SIZE, HEAD_SIZE, device=self.device,
+                           dtype=torch.float32)
+
+    def verify_(self, i: int, r, w, k, v, a, b, slots, snapshots: torch.Tensor):
+        """Layer i of a speculative verify (model.py:475-496, the wkv call with final=False): reads the states of
+        `slots`, writes nothing to the pool, and records the state after every token in snapshots[i].  Returns o."""
+        return wkv7_pool_(r, w, k, v, a, b, self.wkv[i], slots, self.H, HEAD_SIZE, final=False,
+                          snapshots=snapshots[i])
+
+    def rollback_(self, slots, n, snapshots: torch.Tensor) -> None:
+        """wkv[:, slots[b]] := the state after the first n[b] verified tokens (1 <= n[b] <= T; 0 keeps the slot),
+        layer by layer -- the WKV part of model.rollback (model.py:498-503), which replays the first n[b] recorded
+        steps with wkv7_replay; here one copy kernel per layer restores snapshots[i][b, n[b] - 1].  No host sync,
+        graph-capturable."""
+        if snapshots.dim() != 6 or snapshots.shape[0] != self.L:
+            raise ValueError(f"snapshots must be ({self.L}, B, T, {self.H}, 64, 64)")
+        for i in range(self.L):
+            restore_snapshots_(self.wkv[i], slots, snapshots[i], n)
+
     def move_slots(self, src, dst) -> None:
         """wkv[:, dst] = wkv[:, src] with gather-then-scatter semantics (swaps are exact); dst must be distinct
         (model.py:313-316)."""

@@ -136,3 +136,59 @@ def test_model_wrapper_casts_and_reshapes(dev, K):
     o_ref, S_ref, _ = wkv7_ref(*np_list(ops), s0.cpu().numpy())
     assert rel_max(as_np(o).reshape(o_ref.shape), o_ref) <= Y_TOL
     assert rel_max(as_np(S), S_ref) <= S_TOL
+
+
+def test_speculative_verify_and_rollback_across_layers(dev, K):
+    """BASELINE config 4 wired through the pool: every layer verifies T tokens (pool untouched, snapshots taken),
+    then rollback_ restores each row's accepted prefix in every layer.  The result equals, bit for bit, the
+    reference's method -- wkv7_replay of the first n[b] tokens per layer from the incoming states (model.py:498-503)
+    -- eagerly and inside one captured HIP graph replayed three times (the pool reset eagerly between replays)."""
+    say("spec verify + rollback")
+    L, S, H, B, T = 3, 16, 4, 6, 5
+    pool = random_pool(K, dev, L, S, H, seed=41)
+    pool0 = pool.wkv.clone()
+    slots = torch.tensor([7, 2, 11, 0, 14, 5], device=dev)
+    n = torch.tensor([1, 5, 3, 0, 2, 4], device=dev)
+    xs = [[t.clone() for t in to_dev(operands(B, T, H, seed=42 + i), dev)] for i in range(L)]
+    snaps = pool.snapshot_buffer(B, T)
+
+    def spec_step():
+        outs = [pool.verify_(i, *xs[i], slots, snaps) for i in range(L)]
+        pool.rollback_(slots, n, snaps)
+        return outs
+
+    outs_e = spec_step()
+    torch.cuda.synchronize()
+    # the reference's rollback: replay the first n tokens of each row from the incoming states, per layer
+    expect = pool0.clone()
+    for i in range(L):
+        st = expect[i][slots].contiguous()
+        K.wkv7_replay(*xs[i], st, torch.clamp(n, min=1), H, 64)
+        keep = (n > 0).view(-1, 1, 1, 1)
+        expect[i][slots] = torch.where(keep, st, expect[i][slots])
+        o_plain = K.wkv7_pool_(*xs[i], pool0[i].clone(), slots, H, 64, algo=1)
+        assert torch.equal(outs_e[i], o_plain), f"layer {i}: verify output"
+    torch.cuda.synchronize()
+    assert torch.equal(pool.wkv, expect)
+    untouched = [s for s in range(S) if s not in slots.tolist()]
+    assert torch.equal(pool.wkv[:, untouched], pool0[:, untouched])
+
+    pool.wkv.copy_(pool0)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        spec_step()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    pool.wkv.copy_(pool0)
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g):
+        outs_g = spec_step()
+    for it in range(3):
+        pool.wkv.copy_(pool0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(pool.wkv, expect), f"replay {it}"
+        for i in range(L):
+            assert torch.equal(outs_g[i], outs_e[i]), f"replay {it} layer {i}"
