@@ -179,7 +179,29 @@ def verify_bench(torch, kernels, synth, dev, steps, warmup):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     bytes_ = (16384 + T * 16384 + T * 896) * B * H
-    return {"ms": ms, "GBps": bytes_ / (ms * 1e-3) / 1e9, "bytes": bytes_}
+    # rollback to accepted prefixes n = j + 1, j ~ U{0..4}: the snapshot restore (16 KB read + 16 KB written per
+    # (row, head)) beside the reference's way, a replay of the first n tokens (rwkv_next/model.py:498-503)
+    n = torch.randint(1, T + 1, (B,), device=dev, generator=torch.Generator(device=dev).manual_seed(1005))
+
+    def timed(fn):
+        for _ in range(max(1, warmup)):
+            fn()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ms_plain = timed(lambda: kernels.wkv7_pool_(*x, pool, slots, H, 64, final=False))
+    ms_restore = timed(lambda: kernels.restore_snapshots_(pool, slots, snaps, n))
+    ms_replay = timed(lambda: kernels.wkv7_replay(*x, pool, n, H, 64))
+    rbytes = 2 * 16384 * B * H
+    return {"ms": ms, "GBps": bytes_ / (ms * 1e-3) / 1e9, "bytes": bytes_,
+            "rollback_restore_us": ms_restore * 1e3, "rollback_restore_GBps": rbytes / (ms_restore * 1e-3) / 1e9,
+            "rollback_replay_us": ms_replay * 1e3, "verify_without_snapshots_us": ms_plain * 1e3,
+            "step_snapshots_us": (ms + ms_restore) * 1e3, "step_replay_us": (ms_plain + ms_replay) * 1e3}
 
 
 TIMEMIX_PROLOGUE_BYTES = 11 * 2     # per (token, channel): k, v, o_v, o_w, o_a, v_first read; w, k', v', a, b written

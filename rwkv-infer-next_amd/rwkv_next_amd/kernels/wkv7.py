@@ -322,6 +322,14 @@ class StatePool:
         for i in range(self.L):
             restore_snapshots_(self.wkv[i], slots, snapshots[i], n)
 
+    def replay_(self, i: int, r, w, k, v, a, b, slots, n) -> None:
+        """The reference's rollback for layer i (model.py:498-503, wkv7_replay): wkv[i, slots[b]] := the recurrence
+        over the first n[b] of the verified tokens, in place (n[b] = 0 keeps the slot).  Bit-identical to rollback_ after a verify_ with
+        snapshots (one fixed per-token instruction sequence); cheaper per speculative step when the snapshots are not
+        needed otherwise (measured at B = 64, T = 5, H = 64: verify without snapshots + replay 58 us, verify with
+        snapshots + restore 98 us)."""
+        wkv7_pool_(r, w, k, v, a, b, self.wkv[i], slots, self.H, HEAD_SIZE, n_keep=n, store_o=False)
+
     def move_slots(self, src, dst) -> None:
         """wkv[:, dst] = wkv[:, src] with gather-then-scatter semantics (swaps are exact); dst must be distinct
         (model.py:313-316)."""

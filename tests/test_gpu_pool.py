@@ -172,6 +172,14 @@ def test_speculative_verify_and_rollback_across_layers(dev, K):
     assert torch.equal(pool.wkv, expect)
     untouched = [s for s in range(S) if s not in slots.tolist()]
     assert torch.equal(pool.wkv[:, untouched], pool0[:, untouched])
+    # the replay form of the rollback (no snapshots) lands on the same bits, n = 0 rows included
+    rp = K.StatePool(L, S, H, dev)
+    rp.wkv.copy_(pool0)
+    for i in range(L):
+        K.wkv7_pool_(*xs[i], rp.layer(i), slots, H, 64, final=False)
+        rp.replay_(i, *xs[i], slots, n)
+    torch.cuda.synchronize()
+    assert torch.equal(rp.wkv, expect)
 
     pool.wkv.copy_(pool0)
     s = torch.cuda.Stream()
