@@ -172,10 +172,17 @@ __device__ __forceinline__ void process_stage(const Stage<MT>& s, uint8_t* buf, 
     const int sel = 2 * (q >> 1);  // hi-plane field of rows 8 q .. (first half); the second half's is 4 bits up
     const int r = lane & 15;
     const int off = (r >> 1) * kPitch + 8 * (r & 1);
+    // every transposing read of the chunk is issued before the first use (one LDS latency per chunk)
+    v2i lo_t[kTiles], hi_t[kTiles];
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
-        const v2i lov = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(buf + (8 * q) * kPitch + off + 16 * t));
-        const v2i hiv = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(buf + (32 + 8 * (q & 1)) * kPitch + off + 16 * t));
+        lo_t[t] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(buf + (8 * q) * kPitch + off + 16 * t));
+        hi_t[t] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(buf + (32 + 8 * (q & 1)) * kPitch + off + 16 * t));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        const v2i lov = lo_t[t], hiv = hi_t[t];
         const float sv = h2f(*reinterpret_cast<const uint16_t*>(buf + kScaleOff + 2 * (16 * t + i)));
         // lov: lo-plane rows 8 q + e of column i (e = 0..7, one byte each); hiv: hi-plane rows 8 (q & 1) + e
         uint32_t o0[4], o1[4];
