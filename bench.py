@@ -382,7 +382,7 @@ def cpu_baseline(synth):
 def decode_traffic():
     """HBM bytes per decode launch from the committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE, each
     scaled by what the same counter reads for a 1 GiB device copy), or None if absent."""
-    path = os.path.join(REPO, "profiles", "wkv7_recurrent_decode_B64_H64.json")
+    path = os.path.join(REPO, "profiles", "wkv7_decode_B64_H64.json")
     try:
         with open(path) as f:
             return json.load(f)["traffic_bytes"]
@@ -468,7 +468,7 @@ def main():
         achieved = d["bytes_per_launch"] / (d["us_per_launch"] * 1e-6) / 1e9
         out["roofline"] = {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": achieved / HBM_PEAK_GBS, "traffic": decode_traffic(),
-                           "kernel": "wkv7_recurrent_kernel", "us_per_launch": d["us_per_launch"]}
+                           "kernel": "wkv7_decode_kernel", "us_per_launch": d["us_per_launch"]}
     if "decode_cfg1" in res:
         out["decode_cfg1"] = res["decode_cfg1"]
     if "prefill" in res:

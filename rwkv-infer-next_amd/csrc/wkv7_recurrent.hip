@@ -3,10 +3,11 @@
 //
 // Replaces the reference's fused recurrent Triton program _wkv7_raw (rwkv_next/kernels/wkv7.py:38-79) for
 // these cases.  Work decomposition (MI355X, wave64):
-//   * one wavefront per (sequence, head) pair at a time.  The grid holds at most two waves per SIMD; each wave
-//     walks pairs gw, gw + nwaves, ... and issues the next pair's state loads before working on the current
-//     pair, so state reads, the recurrence math and state writes of different pairs overlap (with one pair per
-//     wave all waves would read, then all compute, then all write);
+//   * one wavefront per (sequence, head) pair at a time.  wkv7_recurrent_kernel: at most two waves per SIMD;
+//     each wave walks pairs gw, gw + nwaves, ... and issues the next pair's state loads before working on the
+//     current pair, so state reads, the recurrence math and state writes of different pairs overlap.
+//     wkv7_decode_kernel (single-token rows, at least three pairs per SIMD): one wave per SIMD issues the loads of
+//     four pairs before updating and storing the first, so the grid's state reads run ahead of its writes;
 //   * lane L = 16 g + c owns state rows k = 4 i + g (i = 0..15) and columns v = 4 c .. 4 c + 3: 64 fp32 in VGPRs.
 //     Load instruction i of a wave reads rows 4i .. 4i+3, i.e. 1 KB contiguous, so a 16 KB state arrives in 16
 //     coalesced dwordx4 instructions.  State traffic is streamed with non-temporal loads and stores (each state
@@ -215,6 +216,38 @@ __global__ __launch_bounds__(64 * kWaves, kWavesPerSimd) void wkv7_recurrent_ker
     }
 }
 
+// Single-token rows (decode): one wavefront per SIMD; each wave issues the state loads of up to kGroup pairs
+// (w, w + nwaves, ...) before updating and storing the first of them, so that across the grid the state reads run
+// ahead of the state writes instead of mixing with them (a decode-shaped streaming probe: 64 MiB in place in
+// 22.9 us this way, 25.0 us with two pairs per wave and two waves per SIMD).
+constexpr int kGroup = 4;
+
+__global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Params p) {
+    __shared__ __attribute__((aligned(16))) float slab[kWaves][5 * HS];
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, c = lane & 15;
+    const uint32_t npairs = (uint32_t)p.num_seqs * (uint32_t)p.H;
+    const uint32_t nwaves = gridDim.x * kWaves;
+    for (uint32_t base = blockIdx.x * kWaves + wv; base < npairs; base += kGroup * nwaves) {
+        f4 S[kGroup][16];
+        TokenIn x[kGroup];
+        Pair q[kGroup];
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j) {
+            const uint32_t pj = base + j * nwaves;
+            q[j] = Pair{};
+            if (pj < npairs) {
+                q[j] = pair_of(p, pj);
+                prefetch_pair(p, q[j], lane, g, c, S[j], x[j]);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < kGroup; ++j)
+            if (base + j * nwaves < npairs) run_pair(p, q[j], lane, g, c, S[j], x[j], slab[wv]);
+    }
+}
+
 }  // namespace
 
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
@@ -224,6 +257,16 @@ hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
     if (hipGetDevice(&dev) == hipSuccess) {
         int v = 0;
         if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
+    }
+    // Dense single-token rows (decode) with at least three pairs per SIMD: the grouped kernel.  Measured per launch
+    // (B x H pairs; this kernel / the double-buffered one): 3072 pairs 20.0 / 20.6 us, 4096 25.2 / 27.1, 6144
+    // 40.1 / 41.0, 8192 50.8 / 53.6; fewer pairs do not fill its groups (2560: 19.5 / 17.6 us).
+    const int64_t simds = (int64_t)cus * 4;
+    if (p.T == 1 && !p.cu && pairs >= 3 * simds) {
+        const int64_t waves = simds;  // one wavefront per SIMD
+        const int64_t blocks = (waves + kWaves - 1) / kWaves;
+        hipLaunchKernelGGL(wkv7_decode_kernel, dim3((unsigned)blocks), dim3(64 * kWaves), 0, stream, p);
+        return hipGetLastError();
     }
     const int64_t max_waves = (int64_t)cus * 4 * kWavesPerSimd;  // 4 SIMDs per CU
     // As many waves as fit (measured: for H = 40, 2560 pairs, 2048 waves -- 512 of them taking a second pair -- run

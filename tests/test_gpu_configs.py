@@ -54,6 +54,28 @@ def test_config1_decode(dev, K):
     assert eo <= Y_TOL and es <= S_TOL
 
 
+@pytest.mark.parametrize("B,S_slots", [(64, 128), (56, 128), (128, 160)])
+def test_headline_decode_grouped_kernel(dev, K, B, S_slots):
+    """The metric's decode shape (H = 64, B = 64 of a 128-slot pool: 4096 pairs) and two others that take the
+    grouped single-token kernel (at least three pairs per SIMD): a partial last group (3584 pairs) and two groups
+    per wave (8192 pairs).  The whole pool is compared, so slots outside the batch must come back untouched."""
+    from oracle import wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H = 64
+    say("decode grouped", dict(B=B, S=S_slots, H=H))
+    ops = operands(B, 1, H, seed=1001 + B)
+    pool0 = synth.state_np((S_slots, H, 64, 64), seed=1101 + B)
+    slots = np.random.default_rng(1201 + B).permutation(S_slots)[:B].astype(np.int64)
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(ops), pool0, state_idx=slots)
+    pool = torch.from_numpy(pool0).to(dev)
+    o = K.wkv7_pool_(*to_dev(ops, dev), pool, torch.from_numpy(slots).to(dev), H, 64)
+    torch.cuda.synchronize()
+    eo, es = errs(o, o_ref, pool, pool_ref)
+    assert eo <= Y_TOL and es <= S_TOL
+    untouched = np.setdiff1d(np.arange(S_slots), slots)
+    assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
+
+
 @pytest.mark.parametrize("algo", [2, 1])
 def test_config2_prefill_T4096(dev, K, algo):
     from oracle import wkv7_ref
