@@ -76,6 +76,31 @@ def test_headline_decode_grouped_kernel(dev, K, B, S_slots):
     assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
 
 
+def test_grouped_decode_fresh_rows_snapshots_and_no_write_back(dev, K):
+    """The grouped single-token kernel (4096 pairs) with fresh rows (zero initial state), a T = 1 snapshot and
+    final=False: outputs match the oracle, the snapshot equals the updated state, and the pool is not written."""
+    from oracle import wkv7_ref
+    import rwkv_next_amd.synth as synth
+    B, S_slots, H = 64, 128, 64
+    say("decode grouped fresh/snapshot/final=False", dict(B=B, H=H))
+    ops = operands(B, 1, H, seed=1301)
+    pool0 = synth.state_np((S_slots, H, 64, 64), seed=1302)
+    slots = np.random.default_rng(1303).permutation(S_slots)[:B].astype(np.int64)
+    fresh = np.zeros(B, bool)
+    fresh[::5] = True
+    h0 = pool0[slots].copy()
+    h0[fresh] = 0.0
+    o_ref, S_ref, _ = wkv7_ref(*np_list(ops), h0)
+    pool = torch.from_numpy(pool0).to(dev)
+    snaps = torch.empty(B, 1, H, 64, 64, device=dev)
+    o = K.wkv7_pool_(*to_dev(ops, dev), pool, torch.from_numpy(slots).to(dev), H, 64,
+                     fresh=torch.from_numpy(fresh).to(dev), final=False, snapshots=snaps)
+    torch.cuda.synchronize()
+    eo, es = errs(o, o_ref, snaps[:, 0], S_ref)
+    assert eo <= Y_TOL and es <= S_TOL
+    assert np.array_equal(as_np(pool), pool0)
+
+
 @pytest.mark.parametrize("algo", [2, 1])
 def test_config2_prefill_T4096(dev, K, algo):
     from oracle import wkv7_ref
