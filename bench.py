@@ -89,6 +89,29 @@ def decode_bench(torch, kernels, synth, dev, steps, warmup, H=64):
             "launches_per_step": L, "pairs_per_launch": B * H}
 
 
+def cfg0_bench(torch, kernels, synth, dev, steps, warmup):
+    """Configuration 0's shape on the GPU (B = 1, T = 512, H = 12; bf16 operands, fp32 state from zeros), eager
+    calls, for every algorithm -- beside cpu_baseline.cfg0, the oracle's fp32 loop on the host at the same shape."""
+    T, H = 512, 12
+    ops = synth.operands_torch((1, T, H, 64), seed=1000, device=dev)
+    x = [ops[n].reshape(1, T, H * 64).contiguous() for n in synth.OPERAND_NAMES]
+    out = {"shape": "B=1 T=512 H=12, bf16 operands, fp32 state from zeros"}
+    for name, algo in (("auto", 0), ("recurrent", 1), ("chunked", 2)):
+        for _ in range(warmup):
+            kernels.wkv7(*x, None, H, 64, algo=algo)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            kernels.wkv7(*x, None, H, 64, algo=algo)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        out[f"ms_{name}"] = ms
+        out[f"tok_s_{name}"] = T / (ms * 1e-3)
+    return out
+
+
 def prefill_bench(torch, kernels, synth, dev, steps, warmup):
     T, H = 4096, 64
     ops = synth.operands_torch((1, T, H, 64), seed=1002, device=dev)
@@ -161,8 +184,8 @@ def mixed_bench(torch, kernels, synth, dev, steps, warmup):
     return {"ms": ms, "tokens": total, "tok_s": total / (ms * 1e-3), "prefill_lens": sorted(v for v in lens if v > 1)}
 
 
-def verify_bench(torch, kernels, synth, dev, steps, warmup):
-    B, T, H = 64, 5, 64
+def verify_bench(torch, kernels, synth, dev, steps, warmup, H=64):
+    B, T = 64, 5
     ops = synth.operands_torch((B, T, H, 64), seed=1004, device=dev)
     x = [ops[n].reshape(B, T, H * 64).contiguous() for n in synth.OPERAND_NAMES]
     pool = 0.1 * torch.randn(B, H, 64, 64, device=dev)
@@ -396,7 +419,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed", "timemix", "int6"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed", "timemix", "int6", "tp"], default=None)
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain device copy of 1 GiB (reference dispatch for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -426,9 +449,20 @@ def main():
         c1 = decode_bench(torch, kernels, synth, dev, args.steps, args.warmup, H=40)
         c1["frac_hbm"] = c1["GBps"] / HBM_PEAK_GBS
         res["decode_cfg1"] = c1
+    if args.only in (None, "tp"):
+        # one TP-8 rank's share of the 7.2B model (H = 8 per GPU): 512 pairs at B = 64, occupancy-limited
+        log("TP share (H = 8)")
+        tp = decode_bench(torch, kernels, synth, dev, args.steps, args.warmup, H=8)
+        tp["frac_hbm"] = tp["GBps"] / HBM_PEAK_GBS
+        v8 = verify_bench(torch, kernels, synth, dev, args.steps, args.warmup, H=8)
+        res["tp_share_H8"] = {"decode": tp, "verify_us": v8["ms"] * 1e3, "verify_GBps": v8["GBps"],
+                              "verify_frac_hbm": v8["GBps"] / HBM_PEAK_GBS,
+                              "rollback_restore_us": v8["rollback_restore_us"]}
     if args.only in (None, "prefill"):
         log("prefill")
         res["prefill"] = prefill_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
+        log("configuration 0 on the GPU")
+        res["cfg0_gpu"] = cfg0_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
     if args.only in (None, "verify"):
         log("verify")
         res["verify"] = verify_bench(torch, kernels, synth, dev, args.steps, args.warmup)
@@ -473,6 +507,10 @@ def main():
         out["decode_cfg1"] = res["decode_cfg1"]
     if "prefill" in res:
         out["prefill"] = res["prefill"]
+    if "cfg0_gpu" in res:
+        out["cfg0_gpu"] = res["cfg0_gpu"]
+    if "tp_share_H8" in res:
+        out["tp_share_H8"] = res["tp_share_H8"]
     if "verify" in res:
         out["verify"] = res["verify"]
     if "mixed" in res:

@@ -13,8 +13,9 @@
  * with the RAW w (the decay is computed in fp32 inside the kernels).  Head size K = V = 64.
  *
  * Plain C: no HIP, CUDA or torch types.  Pointers are device pointers; `stream` is a hipStream_t passed as
- * void*.  No function allocates device memory, synchronises the host, or keeps mutable global state, so every
- * call is reentrant and can be recorded into a hipGraph (scratch memory comes from the caller's workspace).
+ * void*.  No function allocates device memory or synchronises the host, and the only global state is a per-device
+ * cache of the compute-unit count, so every call is reentrant and can be recorded into a hipGraph (scratch memory
+ * comes from the caller's workspace).
  */
 #ifndef RWKV_NEXT_AMD_WKV7_H
 #define RWKV_NEXT_AMD_WKV7_H
@@ -26,7 +27,7 @@
 extern "C" {
 #endif
 
-#define WKV7_ABI_VERSION 1
+#define WKV7_ABI_VERSION 2
 
 /* Return codes.  Negative: argument validation failed before anything was launched.  Positive: the hipError_t
  * of a failed launch (the reference surfaces Triton/GPU errors as Python exceptions, engine.py:486-495). */
@@ -36,6 +37,15 @@ extern "C" {
 #define WKV7_ERR_ALIGN (-3)      /* operand/state pointers not 16-byte aligned, or strides not multiples of 8 */
 #define WKV7_ERR_WORKSPACE (-4)  /* workspace missing or smaller than wkv7_workspace_size() */
 #define WKV7_ERR_ARG (-5)        /* inconsistent arguments (snapshots on the chunked path, bad algo, ...) */
+
+/* Bits of the optional device status word (wkv7_args.status).  The kernels never read or clear it; they OR a bit in
+ * (one vector atomic) when they meet an index they must not follow, and go on as documented for that case, so every
+ * kernel still exits normally and no access leaves its buffer.  In the reference the same inputs raise from torch
+ * indexing (rwkv_next/model.py:366-396: index_select / index_copy_ / pool views). */
+#define WKV7_STATUS_H0_SLOT 1   /* an h0 index outside [0, h0_rows): that sequence started from a zero state */
+#define WKV7_STATUS_HT_SLOT 2   /* an ht index outside [0, ht_rows): that final state was not stored */
+#define WKV7_STATUS_SEQLENS 4   /* cu_seqlens entries not non-decreasing within [0, total_tokens]: extents clamped */
+#define WKV7_STATUS_NKEEP 8     /* a negative n_keep entry: treated as 0 */
 
 /* Algorithm selection (wkv7_args.algo). */
 #define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens, chunked otherwise */
@@ -79,6 +89,7 @@ typedef struct wkv7_args {
     int32_t head_size;            /* must be 64 */
     int32_t algo;                 /* WKV7_ALGO_* */
     int32_t rec_max_len;          /* AUTO: rows of at most this many tokens run token-serial; -1 = default */
+    int32_t *status;              /* NULL, or one device int32 that receives WKV7_STATUS_* bits (see above) */
 } wkv7_args;
 
 /* Bytes of device workspace `wkv7_run` needs for these arguments (0 when only the token-serial kernel runs).
@@ -164,6 +175,10 @@ int wkv7_abi_version(void);
 
 /* sizeof(wkv7_args) as compiled into the library, so a binding can check its struct layout. */
 size_t wkv7_args_size(void);
+
+/* Byte offsets of the fields of wkv7_args in declaration order, written to offsets[0 .. min(n, count) - 1]; returns
+ * the number of fields (count).  Lets a binding check every field's position, not only the total size. */
+int wkv7_args_layout(size_t *offsets, int n);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,7 @@
 #include <type_traits>
 
 #include "w6a16.h"
+#include "wkv7_launch.h"
 
 namespace w6 {
 namespace {
@@ -644,13 +645,7 @@ __global__ __launch_bounds__(256) void w6a16_dequant_kernel(const uint8_t* lo, c
     }
 }
 
-int cu_count() {
-    int dev = 0, v = 0;
-    if (hipGetDevice(&dev) == hipSuccess &&
-        hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0)
-        return v;
-    return 256;
-}
+int cu_count() { return wkv7::device_cu_count(); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 

@@ -3,10 +3,29 @@
 //
 // Everything here is decided from host-known sizes and flags (never from device data), so a call can be
 // recorded into a hipGraph and replayed with new device-side lengths, slots or n_keep values.
+#include <stddef.h>
 #include <stdint.h>
+
+#include <atomic>
 
 #include "wkv7.h"
 #include "wkv7_launch.h"
+
+namespace wkv7 {
+
+int device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    static std::atomic<int> cache[kMaxDevices];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+    int v = cache[dev].load(std::memory_order_relaxed);
+    if (v > 0) return v;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return 256;
+    cache[dev].store(v, std::memory_order_relaxed);
+    return v;
+}
+
+}  // namespace wkv7
 
 namespace {
 
@@ -104,6 +123,7 @@ Params to_params(const wkv7_args* a) {
     p.T = a->T;
     p.H = a->H;
     p.rec_max_len = -1;
+    p.status = a->status;
     return p;
 }
 
@@ -114,6 +134,22 @@ extern "C" {
 int wkv7_abi_version(void) { return WKV7_ABI_VERSION; }
 
 size_t wkv7_args_size(void) { return sizeof(wkv7_args); }
+
+int wkv7_args_layout(size_t* offsets, int n) {
+    const size_t off[] = {
+        offsetof(wkv7_args, r), offsetof(wkv7_args, w), offsetof(wkv7_args, k), offsetof(wkv7_args, v),
+        offsetof(wkv7_args, a), offsetof(wkv7_args, b), offsetof(wkv7_args, in_tok_stride), offsetof(wkv7_args, o),
+        offsetof(wkv7_args, o_tok_stride), offsetof(wkv7_args, h0), offsetof(wkv7_args, h0_idx),
+        offsetof(wkv7_args, h0_rows), offsetof(wkv7_args, ht), offsetof(wkv7_args, ht_idx),
+        offsetof(wkv7_args, ht_rows), offsetof(wkv7_args, fresh), offsetof(wkv7_args, cu_seqlens),
+        offsetof(wkv7_args, n_keep), offsetof(wkv7_args, snapshots), offsetof(wkv7_args, workspace),
+        offsetof(wkv7_args, workspace_bytes), offsetof(wkv7_args, num_seqs), offsetof(wkv7_args, T),
+        offsetof(wkv7_args, total_tokens), offsetof(wkv7_args, H), offsetof(wkv7_args, head_size),
+        offsetof(wkv7_args, algo), offsetof(wkv7_args, rec_max_len), offsetof(wkv7_args, status)};
+    const int count = (int)(sizeof(off) / sizeof(off[0]));
+    for (int i = 0; i < n && i < count && offsets; ++i) offsets[i] = off[i];
+    return count;
+}
 
 const char* wkv7_strerror(int code) {
     switch (code) {

@@ -1189,11 +1189,7 @@ hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* works
     const int ncps = (int)std::max<int64_t>(1, (p.T + C - 1) / C);
     if (p.cu) hipLaunchKernelGGL(wkv7_chunk_plan_kernel, dim3(1), dim3(1024), 0, stream, p, plan, ws.max_chunks);
     if (ws.max_chunks > 0) {
-        int dev = 0, cus = 256;
-        if (hipGetDevice(&dev) == hipSuccess) {
-            int v = 0;
-            if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-        }
+        const int cus = device_cu_count();
         const int64_t items = ws.max_chunks * p.H;
         const int64_t grid = std::min<int64_t>(items, cus);  // one 157 KB-LDS workgroup per CU
         hipLaunchKernelGGL(wkv7_chunk_prep_kernel, dim3((unsigned)grid), dim3(512), 0, stream, p, wsc, plan,

@@ -11,6 +11,10 @@
 namespace wkv7 {
 
 constexpr int kChunk = 64;                 // chunk length of the chunked prefill
+
+// Compute units of the current device.  Queried once per device and cached (the attribute query is a driver call
+// that costs microseconds; launchers run on every call).
+int device_cu_count();
 // Workspace record per (chunk, head): A hi/lo (bf16), H^T (fp32), Q (bf16), O_intra^T (bf16), 64 x 64 each.
 constexpr int kChunkBytes = 2 * 2 * HS2 + 4 * HS2 + 2 * HS2 + 2 * HS2;
 

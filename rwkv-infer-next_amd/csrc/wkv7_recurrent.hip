@@ -253,11 +253,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Param
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
     if (pairs == 0) return hipSuccess;
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-    }
+    const int cus = device_cu_count();
     // Dense single-token rows (decode) with at least three pairs per SIMD: the grouped kernel.  Measured per launch
     // (B x H pairs; this kernel / the double-buffered one): 3072 pairs 20.0 / 20.6 us, 4096 25.2 / 27.1, 6144
     // 40.1 / 41.0, 8192 50.8 / 53.6; fewer pairs do not fill its groups (2560: 19.5 / 17.6 us).

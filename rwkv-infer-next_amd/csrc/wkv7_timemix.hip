@@ -23,6 +23,7 @@
 
 #include "wkv7.h"
 #include "wkv7_device.h"
+#include "wkv7_launch.h"
 
 namespace wkv7 {
 namespace {
@@ -255,11 +256,7 @@ __global__ __launch_bounds__(64 * kWaves) void timemix_epilogue_kernel(const wkv
 // Workgroups for `tokens` tokens of H heads: enough wavefronts in flight to stream HBM (8 workgroups per CU),
 // and at least one wavefront per head group.
 int grid_for(int64_t tokens, int H) {
-    int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) {
-        int v = 0;
-        if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && v > 0) cus = v;
-    }
+    const int cus = device_cu_count();
     const int64_t groups = (H + kGroupHeads - 1) / kGroupHeads;
     const int64_t need = (tokens * groups + kWaves - 1) / kWaves;
     const int64_t cap = (int64_t)cus * 8;

@@ -10,7 +10,7 @@ import os
 
 from ._build import LIB_PATH
 
-WKV7_ABI_VERSION = 1
+WKV7_ABI_VERSION = 2
 WKV7_OK = 0
 WKV7_ERR_NULL = -1
 WKV7_ERR_SHAPE = -2
@@ -18,11 +18,17 @@ WKV7_ERR_ALIGN = -3
 WKV7_ERR_WORKSPACE = -4
 WKV7_ERR_ARG = -5
 
+WKV7_STATUS_H0_SLOT = 1
+WKV7_STATUS_HT_SLOT = 2
+WKV7_STATUS_SEQLENS = 4
+WKV7_STATUS_NKEEP = 8
+
 ALGO_AUTO = 0
 ALGO_RECURRENT = 1
 ALGO_CHUNKED = 2
 
 EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
+            "wkv7_args_layout",
             "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore", "wkv7_timemix_prologue",
             "wkv7_timemix_epilogue")
 W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split", "w6a16_matmul",
@@ -62,6 +68,7 @@ class Wkv7Args(ctypes.Structure):
         ("head_size", ctypes.c_int32),
         ("algo", ctypes.c_int32),
         ("rec_max_len", ctypes.c_int32),
+        ("status", _vp),
     ]
 
 
@@ -124,6 +131,8 @@ def load(path: str = LIB_PATH):
     lib.wkv7_strerror.argtypes = [ctypes.c_int]
     lib.wkv7_abi_version.restype = ctypes.c_int
     lib.wkv7_args_size.restype = ctypes.c_size_t
+    lib.wkv7_args_layout.restype = ctypes.c_int
+    lib.wkv7_args_layout.argtypes = [ctypes.POINTER(ctypes.c_size_t), ctypes.c_int]
     i32, i64 = ctypes.c_int32, ctypes.c_int64
     lib.wkv7_pool_reset.restype = ctypes.c_int
     lib.wkv7_pool_reset.argtypes = [_vp, i32, i64, i32, _vp, i32, _vp]
@@ -155,10 +164,26 @@ def load(path: str = LIB_PATH):
         raise ImportError(f"{path}: ABI version {lib.wkv7_abi_version()} != {WKV7_ABI_VERSION}")
     if lib.wkv7_args_size() != ctypes.sizeof(Wkv7Args):
         raise ImportError(f"{path}: sizeof(wkv7_args) {lib.wkv7_args_size()} != binding {ctypes.sizeof(Wkv7Args)}")
+    if args_layout(lib) != binding_layout():
+        raise ImportError(f"{path}: wkv7_args field offsets {args_layout(lib)} != binding {binding_layout()}")
     if lib.w6a16_args_size() != ctypes.sizeof(W6a16Args):
         raise ImportError(f"{path}: sizeof(w6a16_args) {lib.w6a16_args_size()} != binding {ctypes.sizeof(W6a16Args)}")
     _lib = lib
     return lib
+
+
+def args_layout(lib=None):
+    """Field offsets of wkv7_args as compiled into the library (declaration order)."""
+    lib = lib or load()
+    n = lib.wkv7_args_layout(None, 0)
+    buf = (ctypes.c_size_t * n)()
+    lib.wkv7_args_layout(buf, n)
+    return list(buf)
+
+
+def binding_layout():
+    """Field offsets of the ctypes mirror, in the same order."""
+    return [getattr(Wkv7Args, name).offset for name, _ in Wkv7Args._fields_]
 
 
 def strerror(code: int) -> str:

@@ -9,9 +9,12 @@ Per head the state S (K x V, fp32) evolves as
 rwkv_next/kernels/wkv7.py:
     wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True) -> (o, ht | None)      (wkv7.py:126-138)
     wkv7_replay(r, w, k, v, a, b, state, n_keep, H, K) -> state   (in place)                (wkv7.py:141-147)
-    torch op rwkv_next_amd::wkv7_fwd, functional, for torch.compile                          (wkv7.py:113-123)
+    torch op rwkv_next::wkv7_fwd (also rwkv_next_amd::wkv7_fwd), functional, for torch.compile (wkv7.py:113-123)
 plus the slot-pool entry the reference builds around the op in the model (model.py:366-371, 382-396, 485):
     wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, ...) -> o     (pool updated in place, optional snapshots)
+The in-place entries are registered torch ops too (rwkv_next_amd::wkv7_pool_, rwkv_next_amd::wkv7_replay_, with
+their mutated arguments declared and fake implementations), so a torch.compile'd caller such as the reference's
+part_att (model.py:334-342) traces through them without a graph break.
 
 Layouts: r, w, k, v, a, b (B, T, H*K) bf16 (w RAW); states (N, H, K, K) fp32; o like v.  K must be 64.
 All work runs in HIP kernels on the current stream; nothing here synchronises, so every entry point can be
@@ -22,6 +25,7 @@ from __future__ import annotations
 from typing import Optional
 
 import torch
+from torch import Tensor
 
 from .. import _lib
 
@@ -72,7 +76,8 @@ def _state_arg(state, rows_expected, H, K, name="state"):
 
 
 def _launch(ops, *, H, num_seqs, T, total, o=None, h0=None, h0_idx=None, h0_rows=0, ht=None, ht_idx=None,
-            ht_rows=0, fresh=None, cu=None, n_keep=None, snap=None, algo=_lib.ALGO_AUTO, rec_max_len=-1):
+            ht_rows=0, fresh=None, cu=None, n_keep=None, snap=None, algo=_lib.ALGO_AUTO, rec_max_len=-1,
+            status=None):
     dev = ops[0].device
     args = _lib.Wkv7Args()
     for name, t in zip(OPERANDS, ops):
@@ -88,6 +93,7 @@ def _launch(ops, *, H, num_seqs, T, total, o=None, h0=None, h0_idx=None, h0_rows
     args.snapshots = _ptr(snap)
     args.num_seqs, args.T, args.total_tokens = num_seqs, T, total
     args.H, args.head_size, args.algo, args.rec_max_len = H, HEAD_SIZE, algo, rec_max_len
+    args.status = _ptr(status)
     nbytes = _lib.workspace_size(args)
     ws = None
     if nbytes:
@@ -121,19 +127,36 @@ def _fwd_impl(r, w, k, v, a, b, h0, H: int, K: int, final: bool, algo: int = _li
     return o, ht
 
 
-@torch.library.custom_op("rwkv_next_amd::wkv7_fwd", mutates_args=())
-def wkv7_fwd(r: torch.Tensor, w: torch.Tensor, k: torch.Tensor, v: torch.Tensor, a: torch.Tensor, b: torch.Tensor,
-             h0: torch.Tensor, H: int, K: int, final: bool) -> tuple[torch.Tensor, torch.Tensor]:
+def _wkv7_fwd(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor, h0: Tensor, H: int, K: int,
+              final: bool) -> tuple[Tensor, Tensor]:
     """Functional form (fresh o and final state) with the schema of the reference's rwkv_next::wkv7_fwd
     (rwkv_next/kernels/wkv7.py:113-123).  h0 may be empty (0 rows) for a zero initial state."""
     return _fwd_impl(r, w, k, v, a, b, h0, H, K, final)
 
 
-@wkv7_fwd.register_fake
-def _(r, w, k, v, a, b, h0, H, K, final):
+def _wkv7_fwd_fake(r, w, k, v, a, b, h0, H, K, final):
     B = r.shape[0]
-    return torch.empty_like(v), (r.new_empty(B, H, K, K, dtype=torch.float32) if final
-                                 else r.new_empty(0, dtype=torch.float32))
+    o = v.new_empty(v.shape)  # contiguous, like the real output (empty_like would keep a strided v's strides)
+    return o, (r.new_empty(B, H, K, K, dtype=torch.float32) if final else r.new_empty(0, dtype=torch.float32))
+
+
+wkv7_fwd = torch.library.custom_op("rwkv_next_amd::wkv7_fwd", _wkv7_fwd, mutates_args=())
+wkv7_fwd.register_fake(_wkv7_fwd_fake)
+
+
+def _register_reference_name():
+    """The same op under the reference's name, rwkv_next::wkv7_fwd, so that callers binding torch.ops.rwkv_next
+    find it.  Skipped (returns None) when that name is already registered in this process, e.g. by the reference
+    package itself."""
+    try:
+        op = torch.library.custom_op("rwkv_next::wkv7_fwd", _wkv7_fwd, mutates_args=())
+    except RuntimeError:
+        return None
+    op.register_fake(_wkv7_fwd_fake)
+    return op
+
+
+wkv7_fwd_reference_name = _register_reference_name()
 
 
 def wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True, *, algo: int = _lib.ALGO_AUTO):
@@ -159,26 +182,66 @@ def wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True, *, algo: in
     return o, ht
 
 
+@torch.library.custom_op("rwkv_next_amd::wkv7_replay_", mutates_args=("state",))
+def wkv7_replay_(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor, state: Tensor, n_keep: Tensor,
+                 H: int, K: int) -> None:
+    """In-place rollback as a registered op: state (B, H, K, K) fp32 := the recurrence over the first n_keep[b]
+    steps of row b.  The body of the reference's wkv7_replay (rwkv_next/kernels/wkv7.py:141-147)."""
+    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    _launch(ops, H=H, num_seqs=B, T=T, total=B * T, h0=state, h0_rows=B, ht=state, ht_rows=B, n_keep=n_keep,
+            algo=_lib.ALGO_RECURRENT)
+
+
+@wkv7_replay_.register_fake
+def _(r, w, k, v, a, b, state, n_keep, H, K):
+    return None
+
+
 def wkv7_replay(r, w, k, v, a, b, state, n_keep, H, K):
     """Rollback: state (B, H, K, K) fp32 := the recurrence over the first n_keep[b] steps of row b, IN PLACE.
     No output is computed.  Mirrors rwkv_next/kernels/wkv7.py:141-147."""
-    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    B = r.shape[0]
     if state.dtype != torch.float32 or not state.is_contiguous() or tuple(state.shape) != (B, H, K, K):
         raise ValueError(f"state must be a contiguous float32 ({B}, {H}, {K}, {K}) tensor")
     nk = _index_tensor(n_keep, r.device, torch.int64, "n_keep")
     if nk.numel() != B:
         raise ValueError(f"n_keep has {nk.numel()} entries, expected {B}")
-    _launch(ops, H=H, num_seqs=B, T=T, total=B * T, h0=state, h0_rows=B, ht=state, ht_rows=B, n_keep=nk,
-            algo=_lib.ALGO_RECURRENT)
+    wkv7_replay_(r, w, k, v, a, b, state, nk, H, K)
     return state
 
 
 # --------------------------------------------------------------------------------------------------------------
 # slot-pool entry (the model's decode / prefill / verify call sites, model.py:366-371, 382-396, 485)
 # --------------------------------------------------------------------------------------------------------------
+@torch.library.custom_op("rwkv_next_amd::wkv7_pool_", mutates_args=("pool", "snapshots", "status"))
+def wkv7_pool_op(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor, pool: Tensor, slots: Tensor,
+                 H: int, K: int, cu_seqlens: Optional[Tensor], n_keep: Optional[Tensor], fresh: Optional[Tensor],
+                 final: bool, store_o: bool, snapshots: Optional[Tensor], status: Optional[Tensor], max_len: int,
+                 algo: int, rec_max_len: int) -> Tensor:
+    """The slot-pool recurrence as a registered op (arguments already checked and converted by wkv7_pool_).
+    Returns o, or an empty tensor when store_o is False."""
+    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    if cu_seqlens is not None:
+        N, Tn, total = cu_seqlens.numel() - 1, max_len, T
+    else:
+        N, Tn, total = B, T, B * T
+    o = torch.empty_like(ops[3]) if store_o else ops[3].new_empty(0)
+    _launch(ops, H=H, num_seqs=N, T=Tn, total=total, o=o if store_o else None, h0=pool, h0_idx=slots,
+            h0_rows=pool.shape[0], ht=pool if final else None, ht_idx=slots if final else None,
+            ht_rows=pool.shape[0], fresh=fresh, cu=cu_seqlens, n_keep=n_keep, snap=snapshots, algo=algo,
+            rec_max_len=rec_max_len, status=status)
+    return o
+
+
+@wkv7_pool_op.register_fake
+def _(r, w, k, v, a, b, pool, slots, H, K, cu_seqlens, n_keep, fresh, final, store_o, snapshots, status, max_len,
+      algo, rec_max_len):
+    return v.new_empty(v.shape) if store_o else v.new_empty(0)
+
+
 def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=None, fresh=None, final=True,
                store_o=True, snapshots=None, max_len: int = 0, algo: int = _lib.ALGO_AUTO,
-               rec_max_len: int = -1, check_slots: bool = False):
+               rec_max_len: int = -1, check_slots: bool = False, status=None):
     """Recurrence for N sequences whose states live in `pool` (S, H, K, K) fp32, updated IN PLACE.
 
     slots (N,) int64: pool row of each sequence (must be distinct).  Dense operands (N, T, H*K), or packed
@@ -188,8 +251,14 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
     snapshots: optional (N, T, H, K, K) fp32 receiving the state after every token (dense only); rolling back to
     an accepted prefix of n tokens is `restore_snapshots_(pool, slots, snapshots, n)`.
     max_len: ragged calls may pass an upper bound on any row's length (sizes the workspace; 0 = sumT).
-    Returns o like v (or None when store_o=False)."""
-    ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    status: optional int32 device tensor (one element, see new_status) into which the kernels OR WKV7_STATUS_*
+    bits when a slot index lies outside the pool, cu_seqlens is malformed or an n_keep entry is negative; the
+    kernels skip such reads and writes and go on.  Nothing synchronises: read it with check_status when
+    convenient.
+    Returns o like v (or None when store_o=False).  Runs as the registered op rwkv_next_amd::wkv7_pool_."""
+    if r.dim() not in (3, 4):
+        raise ValueError(f"operands must be (B, T, H*K) or (B, T, H, K), got {tuple(r.shape)}")
+    B, T = r.shape[0], r.shape[1]
     dev = r.device
     if pool.dtype != torch.float32 or not pool.is_contiguous() or tuple(pool.shape[1:]) != (H, K, K):
         raise ValueError(f"pool must be a contiguous float32 (S, {H}, {K}, {K}) tensor")
@@ -198,9 +267,9 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
         if B != 1:
             raise ValueError("cu_seqlens requires B == 1 (packed varlen)")
         cu = _index_tensor(cu_seqlens, dev, torch.int32, "cu_seqlens")
-        N, Tn, total = cu.numel() - 1, int(max_len), T
+        N = cu.numel() - 1
     else:
-        cu, N, Tn, total = None, B, T, B * T
+        cu, N = None, B
     if sl.numel() != N:
         raise ValueError(f"slots has {sl.numel()} entries, expected {N}")
     if check_slots:  # host sync: for tests and debugging, not for the graphed hot path
@@ -216,12 +285,30 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
         if snapshots.dtype != torch.float32 or not snapshots.is_contiguous() or \
                 tuple(snapshots.shape) != (N, T, H, K, K):
             raise ValueError(f"snapshots must be a contiguous float32 ({N}, {T}, {H}, {K}, {K}) tensor")
-    o = torch.empty_like(ops[3]) if store_o else None
-    S = pool.shape[0]
-    _launch(ops, H=H, num_seqs=N, T=Tn, total=total, o=o, h0=pool, h0_idx=sl, h0_rows=S,
-            ht=pool if final else None, ht_idx=sl if final else None, ht_rows=S, fresh=fr, cu=cu, n_keep=nk,
-            snap=snapshots, algo=algo, rec_max_len=rec_max_len)
-    return o
+    if status is not None and (status.dtype != torch.int32 or status.numel() < 1 or status.device != dev):
+        raise ValueError("status must be an int32 tensor of at least one element on the operands' device")
+    o = wkv7_pool_op(r, w, k, v, a, b, pool, sl, H, K, cu, nk, fr, final, store_o, snapshots, status,
+                     int(max_len), int(algo), int(rec_max_len))
+    return o if store_o else None
+
+
+def new_status(device) -> torch.Tensor:
+    """A zeroed status word for wkv7_pool_(..., status=...)."""
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+STATUS_REASONS = {_lib.WKV7_STATUS_H0_SLOT: "initial-state slot index outside the pool",
+                  _lib.WKV7_STATUS_HT_SLOT: "final-state slot index outside the pool",
+                  _lib.WKV7_STATUS_SEQLENS: "cu_seqlens not non-decreasing within [0, total tokens]",
+                  _lib.WKV7_STATUS_NKEEP: "negative n_keep"}
+
+
+def check_status(status: torch.Tensor) -> None:
+    """Raise ValueError naming every WKV7_STATUS_* bit set in `status` (synchronises the host: call it outside
+    graph capture and the hot loop)."""
+    bits = int(status.reshape(-1)[0].item())
+    if bits:
+        raise ValueError("wkv7: " + "; ".join(m for bit, m in STATUS_REASONS.items() if bits & bit))
 
 
 def check_distinct_slots(slots: torch.Tensor, num_slots: int) -> None:

@@ -1,11 +1,15 @@
 """Parity at BASELINE.json's full sizes (seeded synthetic inputs, seed = 1000 + config index):
 
+  config 0  the reference's CPU-runnable case, B = 1, T = 512, H = 12 (fp32 on the CPU there; here the same
+            operands rounded to bf16, the kernels' input type), on every algorithm
   config 1  batched decode: B = 64 of a 128-slot pool, H = 40, T = 1 (one layer slice)
   config 2  chunked prefill: B = 1, T = 4096, H = 64, chunk 64, fp32 state from zeros
   config 3  mixed step: 256-slot pool, H = 64, 8 prefill rows U[1, 2048] + 120 decode rows, packed varlen,
             captured in a HIP graph and replayed
   config 4  speculative verify: B = 64, T = 5, H = 64 with per-token snapshots [64, 5, 64, 64, 64]; rollback to a
             random accepted prefix must equal a re-run bit for bit
+  TP share  one tensor-parallel rank's slice of the 7.2B model at TP 8 (H = 8 per GPU, rwkv_next/model.py:8-16,
+            109-110): decode B = 64 (512 pairs, occupancy-limited) and the T = 5 verify with snapshots
 
 Tolerances: y <= 2e-2 and state <= 1e-4 max-relative against the fp64 oracle on the same bf16-rounded inputs."""
 import numpy as np
@@ -36,6 +40,19 @@ def errs(o_gpu, o_ref, S_gpu, S_ref):
     es = rel_max(as_np(S_gpu).reshape(S_ref.shape), S_ref) if S_gpu is not None else 0.0
     say(f"y max-rel {eo:.3e}  state max-rel {es:.3e}")
     return eo, es
+
+
+@pytest.mark.parametrize("algo", [0, 1, 2])
+def test_config0_B1_T512_H12(dev, K, algo):
+    from oracle import wkv7_ref
+    say("config 0", "algo", algo)
+    H, T = 12, 512
+    ops = operands(1, T, H, seed=1000)
+    o_ref, S_ref, _ = wkv7_ref(*np_list(ops))
+    o, S = K.wkv7(*to_dev(ops, dev), None, H, 64, algo=algo)
+    torch.cuda.synchronize()
+    eo, es = errs(o, o_ref, S, S_ref)
+    assert eo <= Y_TOL and es <= S_TOL
 
 
 def test_config1_decode(dev, K):
@@ -177,5 +194,51 @@ def test_config4_verify_snapshots_rollback(dev, K):
     torch.cuda.synchronize()
     assert torch.equal(pool, rerun)
     o_ref, _, snap_ref = wkv7_ref(*np_list(ops), pool0, snapshots=True)
+    eo, es = errs(o, o_ref, snaps, snap_ref)
+    assert eo <= Y_TOL and es <= S_TOL
+
+
+def test_tp_share_H8_decode(dev, K):
+    """One TP-8 rank of the 7.2B model: H = 8, B = 64 of a 128-slot pool, T = 1 (512 pairs); untouched slots stay
+    bit-identical."""
+    from oracle import wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H, S_slots, B = 8, 128, 64
+    say("TP share decode", dict(B=B, H=H))
+    ops = operands(B, 1, H, seed=1008)
+    pool0 = synth.state_np((S_slots, H, 64, 64), seed=1108)
+    slots = np.random.default_rng(1208).permutation(S_slots)[:B].astype(np.int64)
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(ops), pool0, state_idx=slots)
+    pool = torch.from_numpy(pool0).to(dev)
+    o = K.wkv7_pool_(*to_dev(ops, dev), pool, torch.from_numpy(slots).to(dev), H, 64)
+    torch.cuda.synchronize()
+    eo, es = errs(o, o_ref, pool, pool_ref)
+    assert eo <= Y_TOL and es <= S_TOL
+    untouched = np.setdiff1d(np.arange(S_slots), slots)
+    assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
+
+
+def test_tp_share_H8_verify_rollback(dev, K):
+    """The same rank's speculative verify (B = 64, T = 5, H = 8) with snapshots; rollback equals a re-run bit for
+    bit."""
+    from oracle import wkv7_ref
+    import rwkv_next_amd.synth as synth
+    B, T, H, S_slots = 64, 5, 8, 128
+    say("TP share verify", dict(B=B, T=T, H=H))
+    ops = operands(B, T, H, seed=1009)
+    pool0 = synth.state_np((S_slots, H, 64, 64), seed=1109)
+    slots_np = np.random.default_rng(1209).permutation(S_slots)[:B].astype(np.int64)
+    slots = torch.from_numpy(slots_np).to(dev)
+    x = to_dev(ops, dev)
+    pool = torch.from_numpy(pool0).to(dev)
+    snaps = torch.empty(B, T, H, 64, 64, device=dev)
+    o = K.wkv7_pool_(*x, pool, slots, H, 64, final=False, snapshots=snaps)
+    n = torch.from_numpy(np.random.default_rng(1210).integers(0, 5, size=B) + 1).to(dev)
+    K.restore_snapshots_(pool, slots, snaps, n)
+    rerun = torch.from_numpy(pool0).to(dev)
+    K.wkv7_pool_(*x, rerun, slots, H, 64, n_keep=n, store_o=False)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, rerun)
+    o_ref, _, snap_ref = wkv7_ref(*np_list(ops), pool0[slots_np], snapshots=True)
     eo, es = errs(o, o_ref, snaps, snap_ref)
     assert eo <= Y_TOL and es <= S_TOL
