@@ -37,6 +37,7 @@ extern "C" {
 #define WKV7_ERR_ALIGN (-3)      /* operand/state pointers not 16-byte aligned, or strides not multiples of 8 */
 #define WKV7_ERR_WORKSPACE (-4)  /* workspace missing or smaller than wkv7_workspace_size() */
 #define WKV7_ERR_ARG (-5)        /* inconsistent arguments (snapshots on the chunked path, bad algo, ...) */
+#define WKV7_ERR_SCRATCH_LIMIT (-6) /* wkv7_run_noalloc: the call needs more than WKV7_NOALLOC_SCRATCH_BYTES */
 
 /* Bits of the optional device status word (wkv7_args.status).  The kernels never read or clear it; they OR a bit in
  * (one vector atomic) when they meet an index they must not follow, and go on as documented for that case, so every
@@ -92,6 +93,9 @@ typedef struct wkv7_args {
     int32_t *status;              /* NULL, or one device int32 that receives WKV7_STATUS_* bits (see above) */
 } wkv7_args;
 
+/* Size of the device scratch array behind wkv7_run_noalloc (per GPU, held from module load to process exit). */
+#define WKV7_NOALLOC_SCRATCH_BYTES (128u << 20)
+
 /* Bytes of device workspace `wkv7_run` needs for these arguments (0 when only the token-serial kernel runs).
  * Depends only on host-side sizes and flags, never on device data.  No reference counterpart: the reference's
  * launcher allocates its outputs through the torch caching allocator (wkv7.py:93, 119, 135). */
@@ -105,6 +109,15 @@ int wkv7_workspace_size(const wkv7_args *args, size_t *bytes);
  * 485 verify with final=False) when h0/ht address the slot pool through h0_idx/ht_idx.
  * Asynchronous; returns after launching. */
 int wkv7_run(const wkv7_args *args, void *stream);
+
+/* wkv7_run without a caller-provided workspace, for callers that cannot allocate device memory (code under HIP
+ * graph capture that must not allocate, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
+ * the reference (its launcher allocates through the torch caching allocator, wkv7.py:93, 119, 135).  args->workspace
+ * and args->workspace_bytes are ignored: the scratch is a static device array of WKV7_NOALLOC_SCRATCH_BYTES per GPU.
+ * A call whose wkv7_workspace_size exceeds that returns WKV7_ERR_SCRATCH_LIMIT before launching anything.  Calls no
+ * hipMalloc/hipFree.  All calls on one GPU share its array: calls whose kernels overlap on one device (other streams,
+ * other threads) race; calls in stream order on one stream do not. */
+int wkv7_run_noalloc(const wkv7_args *args, void *stream);
 
 /*
  * Slot-pool maintenance on a pool of `layers` consecutive fp32 [rows][H][64][64] arrays (a model's per-layer state

@@ -17,6 +17,8 @@ WKV7_ERR_SHAPE = -2
 WKV7_ERR_ALIGN = -3
 WKV7_ERR_WORKSPACE = -4
 WKV7_ERR_ARG = -5
+WKV7_ERR_SCRATCH_LIMIT = -6
+WKV7_NOALLOC_SCRATCH_BYTES = 128 << 20
 
 WKV7_STATUS_H0_SLOT = 1
 WKV7_STATUS_HT_SLOT = 2
@@ -28,7 +30,7 @@ ALGO_RECURRENT = 1
 ALGO_CHUNKED = 2
 
 EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
-            "wkv7_args_layout",
+            "wkv7_args_layout", "wkv7_run_noalloc",
             "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore", "wkv7_timemix_prologue",
             "wkv7_timemix_epilogue")
 W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split", "w6a16_matmul",
@@ -125,6 +127,8 @@ def load(path: str = LIB_PATH):
     lib = ctypes.CDLL(path)
     lib.wkv7_run.restype = ctypes.c_int
     lib.wkv7_run.argtypes = [ctypes.POINTER(Wkv7Args), _vp]
+    lib.wkv7_run_noalloc.restype = ctypes.c_int
+    lib.wkv7_run_noalloc.argtypes = [ctypes.POINTER(Wkv7Args), _vp]
     lib.wkv7_workspace_size.restype = ctypes.c_int
     lib.wkv7_workspace_size.argtypes = [ctypes.POINTER(Wkv7Args), ctypes.POINTER(ctypes.c_size_t)]
     lib.wkv7_strerror.restype = ctypes.c_char_p

@@ -1,0 +1,105 @@
+"""wkv7_run_noalloc (the allocation-free variant of wkv7_run, include/wkv7.h) through the C ABI: two chunked calls
+in a row (the second smaller), a ragged call and a decode call, each bit-identical to wkv7_run with a
+caller-allocated workspace on the same inputs; a call that needs more than WKV7_NOALLOC_SCRATCH_BYTES is refused
+before anything is launched."""
+import ctypes
+
+import numpy as np
+import pytest
+
+from gpu_util import operands, say, to_dev
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU")
+    return torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from rwkv_next_amd import _lib
+    return _lib.load()
+
+
+def make_args(x, H, N, T, total, o, h0=None, ht=None, cu=None, algo=0):
+    from rwkv_next_amd import _lib
+    a = _lib.Wkv7Args()
+    for name, t in zip(("r", "w", "k", "v", "a", "b"), x):
+        setattr(a, name, t.data_ptr())
+    a.in_tok_stride = a.o_tok_stride = H * 64
+    a.o = o.data_ptr()
+    if h0 is not None:
+        a.h0, a.h0_rows = h0.data_ptr(), N
+    if ht is not None:
+        a.ht, a.ht_rows = ht.data_ptr(), N
+    if cu is not None:
+        a.cu_seqlens = cu.data_ptr()
+    a.num_seqs, a.T, a.total_tokens, a.H, a.head_size, a.algo, a.rec_max_len = N, T, total, H, 64, algo, -1
+    return a
+
+
+def run_both(lib, dev, x, H, N, T, total, h0=None, cu=None, algo=0):
+    """wkv7_run with a torch-allocated workspace, then wkv7_run_noalloc, on the same inputs."""
+    from rwkv_next_amd import _lib
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    outs = []
+    for noalloc in (False, True):
+        o = torch.full_like(x[3], float("nan"))
+        ht = torch.full((N, H, 64, 64), float("nan"), device=dev)
+        a = make_args(x, H, N, T, total, o, h0, ht, cu, algo)
+        if noalloc:
+            rc = lib.wkv7_run_noalloc(ctypes.byref(a), ctypes.c_void_p(stream))
+        else:
+            nbytes = _lib.workspace_size(a)
+            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+            a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+            rc = lib.wkv7_run(ctypes.byref(a), ctypes.c_void_p(stream))
+        assert rc == 0, _lib.strerror(rc)
+        torch.cuda.synchronize()
+        outs.append((o, ht))
+    (o0, s0), (o1, s1) = outs
+    assert torch.equal(o0, o1) and torch.equal(s0, s1)
+    assert not torch.isnan(o1.float()).any() and not torch.isnan(s1).any()
+
+
+def test_two_chunked_calls_in_a_row_second_smaller(dev, lib):
+    H = 8
+    for B, T, seed in ((2, 300, 1), (1, 100, 2)):
+        say("noalloc chunked", B, T)
+        x = to_dev(operands(B, T, H, seed=seed), dev)
+        h0 = torch.from_numpy((0.3 * np.random.default_rng(seed).standard_normal((B, H, 64, 64))).astype(np.float32)).to(dev)
+        run_both(lib, dev, x, H, B, T, B * T, h0=h0, algo=2)
+
+
+def test_ragged_and_decode_calls(dev, lib):
+    H = 8
+    lens = [5, 1, 130, 0, 64, 33]
+    say("noalloc ragged", lens)
+    total = sum(lens)
+    x = to_dev(operands(1, total, H, seed=3), dev)
+    cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=dev)
+    h0 = torch.from_numpy((0.3 * np.random.default_rng(4).standard_normal((len(lens), H, 64, 64))).astype(np.float32)).to(dev)
+    run_both(lib, dev, x, H, len(lens), 0, total, h0=h0, cu=cu)
+    say("noalloc decode")
+    x = to_dev(operands(16, 1, H, seed=5), dev)
+    h0 = torch.from_numpy((0.3 * np.random.default_rng(6).standard_normal((16, H, 64, 64))).astype(np.float32)).to(dev)
+    run_both(lib, dev, x, H, 16, 1, 16, h0=h0)
+
+
+def test_too_large_is_refused_before_launch(dev, lib):
+    from rwkv_next_amd import _lib
+    H, T = 64, 8192
+    say("noalloc over the limit")
+    x = [torch.zeros(1, T, H * 64, dtype=torch.bfloat16, device=dev) for _ in range(6)]
+    o = torch.full_like(x[3], 7.0)
+    a = make_args(x, H, 1, T, T, o, algo=2)
+    assert _lib.workspace_size(a) > _lib.WKV7_NOALLOC_SCRATCH_BYTES
+    rc = lib.wkv7_run_noalloc(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream))
+    assert rc == _lib.WKV7_ERR_SCRATCH_LIMIT
+    torch.cuda.synchronize()
+    assert bool((o == 7.0).all())
