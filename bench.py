@@ -95,19 +95,22 @@ def cfg0_bench(torch, kernels, synth, dev, steps, warmup):
     T, H = 512, 12
     ops = synth.operands_torch((1, T, H, 64), seed=1000, device=dev)
     x = [ops[n].reshape(1, T, H * 64).contiguous() for n in synth.OPERAND_NAMES]
-    out = {"shape": "B=1 T=512 H=12, bf16 operands, fp32 state from zeros"}
+    out = {"shape": "B=1 T=512 H=12, bf16 operands, fp32 state from zeros",
+           "timing": "ms: HIP graph replay per call; ms_eager: eager calls (host dispatch included)"}
     for name, algo in (("auto", 0), ("recurrent", 1), ("chunked", 2)):
+        fn = lambda algo=algo: kernels.wkv7(*x, None, H, 64, algo=algo)
+        ms = graph_us(torch, [fn], steps, warmup) * 1e-3
         for _ in range(warmup):
-            kernels.wkv7(*x, None, H, 64, algo=algo)
+            fn()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
-            kernels.wkv7(*x, None, H, 64, algo=algo)
+            fn()
         e1.record()
         torch.cuda.synchronize()
-        ms = e0.elapsed_time(e1) / steps
         out[f"ms_{name}"] = ms
+        out[f"ms_eager_{name}"] = e0.elapsed_time(e1) / steps
         out[f"tok_s_{name}"] = T / (ms * 1e-3)
     return out
 
@@ -125,7 +128,8 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
         kernels.wkv7(*x, None, H, 64)
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    ms_eager = e0.elapsed_time(e1) / steps
+    ms = graph_us(torch, [lambda: kernels.wkv7(*x, None, H, 64)], steps, warmup) * 1e-3
     chunks = T // C
     bytes_ = PREFILL_BYTES_PER_HEAD_TOKEN * T * H + 2 * 16384 * H
     t_hbm = bytes_ / (HBM_PEAK_GBS * 1e9)
@@ -138,7 +142,8 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
     # as the three bf16 passes these kernels run.
     t_fp32_state = f_state / (FP32_PEAK_TFLOPS * 1e12) + f_out / (BF16_PEAK_TFLOPS * 1e12)
     t_roof_fp32_state = max(t_hbm, t_fp32_state)
-    return {"ms": ms, "tok_s": T / (ms * 1e-3), "head_tok_s": T * H / (ms * 1e-3),
+    return {"ms": ms, "ms_eager": ms_eager, "timing": "ms: HIP graph replay per call; ms_eager: eager calls",
+            "tok_s": T / (ms * 1e-3), "head_tok_s": T * H / (ms * 1e-3),
             "roofline": {"bound": "hbm" if t_hbm >= t_mfma else "mfma", "t_roof_us": t_roof * 1e6,
                          "t_hbm_us": t_hbm * 1e6, "t_mfma_us": t_mfma * 1e6, "frac": t_roof / (ms * 1e-3),
                          "t_roof_fp32_state_path_us": t_roof_fp32_state * 1e6,
@@ -184,47 +189,60 @@ def mixed_bench(torch, kernels, synth, dev, steps, warmup):
     return {"ms": ms, "tokens": total, "tok_s": total / (ms * 1e-3), "prefill_lens": sorted(v for v in lens if v > 1)}
 
 
-def verify_bench(torch, kernels, synth, dev, steps, warmup, H=64):
-    B, T = 64, 5
-    ops = synth.operands_torch((B, T, H, 64), seed=1004, device=dev)
-    x = [ops[n].reshape(B, T, H * 64).contiguous() for n in synth.OPERAND_NAMES]
-    pool = 0.1 * torch.randn(B, H, 64, 64, device=dev)
-    slots = torch.arange(B, device=dev)
-    snaps = torch.empty(B, T, H, 64, 64, device=dev)
-    for _ in range(warmup):
-        kernels.wkv7_pool_(*x, pool, slots, H, 64, final=False, snapshots=snaps)
+def graph_us(torch, fns, steps, warmup):
+    """Capture the calls `fns` (one per layer copy) in one HIP graph and return the replay time per call in us."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for fn in fns:  # warm-up outside capture
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for fn in fns:
+            fn()
+    torch.cuda.synchronize()
+    for _ in range(max(1, warmup)):
+        graph.replay()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
-        kernels.wkv7_pool_(*x, pool, slots, H, 64, final=False, snapshots=snaps)
+        graph.replay()
     e1.record()
     torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
-    bytes_ = (16384 + T * 16384 + T * 896) * B * H
-    # rollback to accepted prefixes n = j + 1, j ~ U{0..4}: the snapshot restore (16 KB read + 16 KB written per
-    # (row, head)) beside the reference's way, a replay of the first n tokens (rwkv_next/model.py:498-503)
+    return e0.elapsed_time(e1) * 1e3 / (steps * len(fns))
+
+
+def verify_bench(torch, kernels, synth, dev, steps, warmup, H=64, copies=8):
+    """Configuration 4's speculative verify (B = 64 rows, T = 5 draft tokens) with per-token snapshots, and the two
+    rollbacks to accepted prefixes n = j + 1, j ~ U{0..4}: the snapshot restore (16 KB read + 16 KB written per
+    (row, head)) and the reference's way, a replay of the first n tokens (rwkv_next/model.py:498-503).  Each is
+    timed in a HIP graph over `copies` layer-sized copies of the pool and snapshot buffers (so no call finds its
+    state in the Infinity Cache), per call."""
+    B, T = 64, 5
+    ops = synth.operands_torch((B, T, H, 64), seed=1004, device=dev)
+    x = [ops[n].reshape(B, T, H * 64).contiguous() for n in synth.OPERAND_NAMES]
+    pools = [0.1 * torch.randn(B, H, 64, 64, device=dev) for _ in range(copies)]
+    snaps = [torch.empty(B, T, H, 64, 64, device=dev) for _ in range(copies)]
+    slots = torch.arange(B, device=dev)
     n = torch.randint(1, T + 1, (B,), device=dev, generator=torch.Generator(device=dev).manual_seed(1005))
-
-    def timed(fn):
-        for _ in range(max(1, warmup)):
-            fn()
-        torch.cuda.synchronize()
-        e0.record()
-        for _ in range(steps):
-            fn()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / steps
-
-    ms_plain = timed(lambda: kernels.wkv7_pool_(*x, pool, slots, H, 64, final=False))
-    ms_restore = timed(lambda: kernels.restore_snapshots_(pool, slots, snaps, n))
-    ms_replay = timed(lambda: kernels.wkv7_replay(*x, pool, n, H, 64))
+    us = graph_us(torch, [lambda i=i: kernels.wkv7_pool_(*x, pools[i], slots, H, 64, final=False, snapshots=snaps[i])
+                          for i in range(copies)], steps, warmup)
+    us_plain = graph_us(torch, [lambda i=i: kernels.wkv7_pool_(*x, pools[i], slots, H, 64, final=False)
+                                for i in range(copies)], steps, warmup)
+    us_restore = graph_us(torch, [lambda i=i: kernels.restore_snapshots_(pools[i], slots, snaps[i], n)
+                                  for i in range(copies)], steps, warmup)
+    us_replay = graph_us(torch, [lambda i=i: kernels.wkv7_replay(*x, pools[i], n, H, 64)
+                                 for i in range(copies)], steps, warmup)
+    bytes_ = (16384 + T * 16384 + T * 896) * B * H
     rbytes = 2 * 16384 * B * H
-    return {"ms": ms, "GBps": bytes_ / (ms * 1e-3) / 1e9, "bytes": bytes_,
-            "rollback_restore_us": ms_restore * 1e3, "rollback_restore_GBps": rbytes / (ms_restore * 1e-3) / 1e9,
-            "rollback_replay_us": ms_replay * 1e3, "verify_without_snapshots_us": ms_plain * 1e3,
-            "step_snapshots_us": (ms + ms_restore) * 1e3, "step_replay_us": (ms_plain + ms_replay) * 1e3}
+    return {"ms": us * 1e-3, "GBps": bytes_ / (us * 1e-6) / 1e9, "bytes": bytes_,
+            "rollback_restore_us": us_restore, "rollback_restore_GBps": rbytes / (us_restore * 1e-6) / 1e9,
+            "rollback_replay_us": us_replay, "verify_without_snapshots_us": us_plain,
+            "step_snapshots_us": us + us_restore, "step_replay_us": us_plain + us_replay,
+            "timing": f"HIP graph of {copies} calls on separate pool/snapshot copies, per call"}
 
 
 TIMEMIX_PROLOGUE_BYTES = 11 * 2     # per (token, channel): k, v, o_v, o_w, o_a, v_first read; w, k', v', a, b written

@@ -49,9 +49,12 @@ extern "C" {
 #define WKV7_STATUS_NKEEP 8     /* a negative n_keep entry: treated as 0 */
 
 /* Algorithm selection (wkv7_args.algo). */
-#define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens, chunked otherwise */
+#define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens, chunked otherwise; a
+                                * ragged call whose rows are short enough runs as one chain-kernel dispatch */
 #define WKV7_ALGO_RECURRENT 1  /* token-serial kernel for every row */
 #define WKV7_ALGO_CHUNKED 2    /* chunked MFMA prefill for every row */
+#define WKV7_ALGO_CHAIN 3      /* one dispatch: rows of at most rec_max_len tokens token-serial, longer rows chunked with
+                                * each (row, head) chain walked by one workgroup (no workspace; num_seqs <= 512) */
 
 /*
  * One call.  Operand element (token t, head h, channel i) is at ptr[t * in_tok_stride + h * 64 + i] (bf16 bit

@@ -38,6 +38,7 @@ constexpr int kDefaultRecMaxLen = 32;
 struct Plan {
     bool run_recurrent = false;
     bool run_chunked = false;
+    bool run_chain = false;
     int rec_len_rec = -1;    // Params.rec_max_len of the token-serial launch (-1: all rows)
     int rec_len_chunk = -1;  // Params.rec_max_len of the chunked launch (-1: all rows)
     wkv7::ChunkWorkspace ws{};
@@ -48,7 +49,8 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 int validate(const wkv7_args* a) {
     if (a->head_size != wkv7::HS) return WKV7_ERR_SHAPE;
     if (a->H < 1 || a->num_seqs < 0 || a->T < 0 || a->total_tokens < 0) return WKV7_ERR_SHAPE;
-    if (a->algo < WKV7_ALGO_AUTO || a->algo > WKV7_ALGO_CHUNKED) return WKV7_ERR_ARG;
+    if (a->algo < WKV7_ALGO_AUTO || a->algo > WKV7_ALGO_CHAIN) return WKV7_ERR_ARG;
+    if (a->algo == WKV7_ALGO_CHAIN && (a->num_seqs > wkv7::kChainMaxSeqs || a->snapshots)) return WKV7_ERR_ARG;
     if (a->rec_max_len < -1) return WKV7_ERR_ARG;
     if ((int64_t)a->num_seqs * a->H > ((int64_t)1 << 31)) return WKV7_ERR_SHAPE;
     if (!a->cu_seqlens && (int64_t)a->num_seqs * a->T > a->total_tokens) return WKV7_ERR_SHAPE;
@@ -79,6 +81,18 @@ int validate(const wkv7_args* a) {
     return WKV7_OK;
 }
 
+// AUTO on a ragged call: one chain-kernel dispatch when the longest possible row (the caller's bound, in chunks) is
+// no longer than twice the average chunk work per CU, so that walking each (row, head) chain on one CU does not set
+// the call's length -- e.g. a continuous-batching step of a few prefill rows up to 2048 tokens and many decode rows.
+// Long rows (one 4096-token prefill) keep the two-kernel path, which spreads a row's chunks over all CUs.
+bool chain_fits(const wkv7_args* a, int64_t bound, int thr) {
+    if (a->algo != WKV7_ALGO_AUTO || !a->cu_seqlens || a->snapshots || a->num_seqs > wkv7::kChainMaxSeqs) return false;
+    if (bound <= thr) return false;
+    const int64_t longest = (bound + wkv7::kChunk - 1) / wkv7::kChunk;
+    const int64_t chunk_items = (int64_t)a->H * ((a->total_tokens + wkv7::kChunk - 1) / wkv7::kChunk);
+    return longest * wkv7::device_cu_count() <= 2 * chunk_items;
+}
+
 Plan make_plan(const wkv7_args* a) {
     Plan pl;
     const bool varlen = a->cu_seqlens != nullptr;
@@ -86,6 +100,9 @@ Plan make_plan(const wkv7_args* a) {
     const int thr = a->rec_max_len >= 0 ? a->rec_max_len : kDefaultRecMaxLen;
     if (a->snapshots || a->algo == WKV7_ALGO_RECURRENT) {
         pl.run_recurrent = true;
+    } else if (a->algo == WKV7_ALGO_CHAIN || chain_fits(a, bound, thr)) {
+        pl.run_chain = true;
+        pl.rec_len_rec = thr;
     } else if (a->algo == WKV7_ALGO_CHUNKED) {
         pl.run_chunked = true;
     } else if (bound <= thr) {
@@ -185,6 +202,11 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     if (args->num_seqs == 0) return WKV7_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
     Params p = to_params(args);
+    if (pl.run_chain) {
+        p.rec_max_len = pl.rec_len_rec;
+        const hipError_t e = wkv7::launch_chain(p, s);
+        return e == hipSuccess ? WKV7_OK : static_cast<int>(e);
+    }
     if (pl.run_recurrent) {
         p.rec_max_len = pl.rec_len_rec;
         const hipError_t e = wkv7::launch_recurrent(p, s);

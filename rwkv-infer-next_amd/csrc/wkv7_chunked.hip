@@ -34,6 +34,7 @@
 
 #include "wkv7_device.h"
 #include "wkv7_launch.h"
+#include "wkv7_token.h"
 
 namespace wkv7 {
 
@@ -127,20 +128,13 @@ __device__ __forceinline__ f4 mma(f4 acc, BM X, int x0, BM Y, int y0, int kb0, i
     return acc;
 }
 
-__device__ __forceinline__ void split(float x, __bf16& h, __bf16& l) {
-    h = (__bf16)x;
-    l = (__bf16)(x - (float)h);
-}
-
-// Four fp32 values as hi/lo bf16 operands of mfma16.
+// Four fp32 values as hi/lo bf16 operands of mfma16 (split_pair on each half).
 __device__ __forceinline__ void split4(f4 x, s4& h, s4& l) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        __bf16 hh, ll;
-        split(x[v], hh, ll);
-        h[v] = __builtin_bit_cast(short, hh);
-        l[v] = __builtin_bit_cast(short, ll);
-    }
+    uint32_t hw[2], lw[2];
+    split_pair(x[0], x[1], hw[0], lw[0]);
+    split_pair(x[2], x[3], hw[1], lw[1]);
+    h = __builtin_bit_cast(s4, hw);
+    l = __builtin_bit_cast(s4, lw);
 }
 
 // LDS transposing read (ds_read_b64_tr_b16).  Within each 16-lane group, lane s reads 4 consecutive 16-bit values at
@@ -195,16 +189,10 @@ __device__ __forceinline__ void st_hi(__bf16* M, int pitch, int x0, int y0, f4 a
 }
 __device__ __forceinline__ void st_split(BM M, int pitch, int x0, int y0, f4 acc) {
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-    bf4 hv, lv;
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        __bf16 h, l;
-        split(acc[v], h, l);
-        hv[v] = h;
-        lv[v] = l;
-    }
-    *reinterpret_cast<bf4*>(M.h + (y0 + i) * pitch + x0 + 4 * q) = hv;
-    *reinterpret_cast<bf4*>(M.l + (y0 + i) * pitch + x0 + 4 * q) = lv;
+    s4 hv, lv;
+    split4(acc, hv, lv);
+    *reinterpret_cast<s4*>(M.h + (y0 + i) * pitch + x0 + 4 * q) = hv;
+    *reinterpret_cast<s4*>(M.l + (y0 + i) * pitch + x0 + 4 * q) = lv;
 }
 __device__ __forceinline__ void st_f32(float* M, int pitch, int x0, int y0, f4 acc) {
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
@@ -409,6 +397,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 // Decays are handled in base 2 (g = cumulative log2 d), so every decay factor is one v_exp_f32.
 // The next item's operands (element offset noff) are loaded into `next` one operand per phase, spread over the item
 // so that their issue does not queue behind one another.
+// Where the record of an item goes: the workspace (the two-kernel path: prep writes, the scan kernel reads), or the
+// LDS slots kRecSlot.. (the chain kernel, which applies the record to the state itself).  In LDS the record reuses
+// operand slots that step 8 still reads, so step 8's A and Q tiles are held in registers and stored in step 9.
+constexpr int kRecSlot = 4;  // LDS record: slots 4 .. 9 (48 KB of the 6 x 9 KB)
+
+template <bool LDS_REC>
 __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const RawIn& raw, char* wsc,
                                           PrepSmem& sm, int64_t noff, RawIn& next) {
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -425,7 +419,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const BM Vr{sm.slot[15], nullptr};
     const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 7: W^T [k][t], G^T [s'][t]
     const BM Fm{sm.slot[2], sm.slot[3]};            // step 8 (Aq is dead after step 7)
-    char* const rec = wsc + it.rec * (int64_t)kChunkBytes;
+    char* const rec = LDS_REC ? reinterpret_cast<char*>(sm.slot[kRecSlot]) : wsc + it.rec * (int64_t)kChunkBytes;
     const int row = tid >> 3, cb = (tid & 7) * 8;
     const bool valid = row < it.Lc;
 
@@ -456,41 +450,37 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     __syncthreads();
     next.w = *reinterpret_cast<const uint4*>(p.w + noff);
 
-    // ---- 2. g (inclusive) and g of the previous row; midpoint m = g_31 and chunk total g_63 per channel
-    float gi[8], ge[8], mk[8];
-    {
-        // running sum over the waves' totals in wave order; this wave's offset is the sum before its own total
-        // (wv is wave-uniform: the capture is a scalar branch, not a per-lane select)
-        float off[8], g63[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) off[e] = g63[e] = 0.f;
+    // ---- 2. per channel (one lane each): the waves' prefix offsets in wave order, the midpoint m = g_31 (waves
+    //         0-3) and the chunk total g_63, then the decay factors of the midpoint; every thread then forms g
+    //         (inclusive) and g of the previous row from its in-wave scan plus its wave's offset.  Every sum is
+    //         taken in wave order, so the midpoint and total here equal the g of rows 31 and 63 bit for bit.
+    if (tid < HS) {
+        float acc = 0.f, mid = 0.f;
 #pragma unroll
         for (int w2 = 0; w2 < 8; ++w2) {
-            const f4 t0 = *reinterpret_cast<const f4*>(&sm.bsum[w2][cb]);
-            const f4 t1 = *reinterpret_cast<const f4*>(&sm.bsum[w2][cb + 4]);
-            if (w2 == wv) {
-#pragma unroll
-                for (int e = 0; e < 8; ++e) off[e] = g63[e];
-            }
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                if (w2 == 4) mk[e] = g63[e];
-                g63[e] += e < 4 ? t0[e] : t1[e - 4];
-            }
+            const float t = sm.bsum[w2][tid];
+            sm.bsum[w2][tid] = acc;  // offset of wave w2: the sum of the earlier waves' totals
+            if (w2 == 4) mid = acc;
+            acc += t;
         }
+        sm.m[tid] = mid;
+        sm.em[tid] = __builtin_amdgcn_exp2f(mid);
+        sm.eglm[tid] = __builtin_amdgcn_exp2f(acc - mid);
+        sm.gam[tid] = __builtin_amdgcn_exp2f(acc);
+    }
+    __syncthreads();
+    float gi[8], ge[8], mk[8];
+    {
+        const f4 o0 = *reinterpret_cast<const f4*>(&sm.bsum[wv][cb]);
+        const f4 o1 = *reinterpret_cast<const f4*>(&sm.bsum[wv][cb + 4]);
+        const f4 m0 = *reinterpret_cast<const f4*>(&sm.m[cb]);
+        const f4 m1 = *reinterpret_cast<const f4*>(&sm.m[cb + 4]);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-            gi[e] = gin[e] + off[e];
-            ge[e] = gprev[e] + off[e];
-        }
-        if (tid < 8) {  // row 0's threads cover the 64 channels once
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                sm.m[cb + e] = mk[e];
-                sm.em[cb + e] = __builtin_amdgcn_exp2f(mk[e]);
-                sm.eglm[cb + e] = __builtin_amdgcn_exp2f(g63[e] - mk[e]);
-                sm.gam[cb + e] = __builtin_amdgcn_exp2f(g63[e]);
-            }
+            const float off = e < 4 ? o0[e] : o1[e - 4];
+            mk[e] = e < 4 ? m0[e] : m1[e - 4];
+            gi[e] = gin[e] + off;
+            ge[e] = gprev[e] + off;
         }
     }
 
@@ -504,11 +494,8 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
         const uint32_t kw[4] = {raw.k.x & vm, raw.k.y & vm, raw.k.z & vm, raw.k.w & vm};
         const uint32_t rw[4] = {raw.r.x & vm, raw.r.y & vm, raw.r.z & vm, raw.r.w & vm};
         uint32_t aqh[4], aql[4], bkh[4], bkl[4], kkh[4], kkl[4], rqh[4];
-        // hi/lo split of a channel pair straight into packed words: hi = bf16(x), lo = bf16(x - hi)
-        auto split2 = [](float x0, float x1, uint32_t& hw, uint32_t& lw) {
-            hw = pack_bf16x2(x0, x1);
-            lw = pack_bf16x2(x0 - __uint_as_float(hw << 16), x1 - __uint_as_float(hw & 0xffff0000u));
-        };
+        // hi/lo split of a channel pair straight into packed words
+        auto split2 = [](float x0, float x1, uint32_t& hw, uint32_t& lw) { split_pair(x0, x1, hw, lw); };
 #pragma unroll
         for (int e2 = 0; e2 < 4; ++e2) {
             float a2[2], b2[2], k2[2], r2[2], fa[2], fr[2], fb[2];
@@ -580,10 +567,16 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
                 bb = mfma_bf16(aqh, kkh, bb);
             }
         }
-        st_f32(F32, PF, x0, y0, mask_tile(aa, x0, y0, 1));
-        st_split(Be, PB, x0, y0, mask_tile(bb, x0, y0, 3));
-        st_hi(Rho.h, PB, x0, y0, mask_tile(rr, x0, y0, 2));
-        st_hi(Sig.h, PB, x0, y0, mask_tile(ss, x0, y0, 2));
+        if (bx == by) {  // only diagonal tiles straddle the causal boundary (bx, by are wave-uniform)
+            aa = mask_tile(aa, x0, y0, 1);
+            bb = mask_tile(bb, x0, y0, 3);
+            rr = mask_tile(rr, x0, y0, 2);
+            ss = mask_tile(ss, x0, y0, 2);
+        }
+        st_f32(F32, PF, x0, y0, aa);
+        st_split(Be, PB, x0, y0, bb);
+        st_hi(Rho.h, PB, x0, y0, rr);
+        st_hi(Sig.h, PB, x0, y0, ss);
     }
     __syncthreads();
     next.b = *reinterpret_cast<const uint4*>(p.b + noff);
@@ -714,6 +707,8 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     // Wave wv owns tiles (bx, by) = (wv / 4 + 2 u, wv % 4).  The four products of a tile share their operands (W and
     // G as X, rho and the transposed Bk as Y), each fragment loaded once per contraction block.  rho is zero for
     // s > t, so for token tiles by < 2 the second contraction block of Q and E is skipped.
+    bf4 q_keep[2];
+    s4 ah_keep[2], al_keep[2];
     {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -753,24 +748,35 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             bf4 qv;
 #pragma unroll
             for (int v = 0; v < 4; ++v) qv[v] = (__bf16)aq[v];
-            *reinterpret_cast<bf4*>(rec + REC_Q + frag32_off(by, bx, lane)) = qv;
+            if constexpr (LDS_REC) q_keep[u] = qv;
+            else *reinterpret_cast<bf4*>(rec + REC_Q + frag32_off(by, bx, lane)) = qv;
             // E -> Em, keep s' <= t
-            st_hi(Em.h, PB, x0, y0, mask_tile(ae, x0, y0, 2));
+            // E = sigma + rho G is exactly zero above the diagonal (sigma is stored masked, rho and G are exactly
+            // zero where the causal mask is), so only diagonal tiles are masked, as a guard
+            if (bx == by) ae = mask_tile(ae, x0, y0, 2);
+            st_hi(Em.h, PB, x0, y0, ae);
             // A[k1][k2] = gamma delta + 2^{g_C - m}[k1] sum_t W[t][k2] Bk[t][k1] -> record (k1 tile by)
             // F[k][s'] = 2^{g_C - m}[k] (Kk[s'][k] + sum_t G[t][s'] Bk[t][k]) -> Fm
             const float e1 = sm.eglm[y0 + li];
-            bf4 hv, lv;
+            f4 av;
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
-                const float av = aa[v] * e1 + ((x0 + 4 * lq + v == y0 + li) ? sm.gam[y0 + li] : 0.f);
-                __bf16 hh, ll;
-                split(av, hh, ll);
-                hv[v] = hh;
-                lv[v] = ll;
+                av[v] = aa[v] * e1;
                 af[v] *= e1;
             }
-            *reinterpret_cast<bf4*>(rec + REC_AH + frag32_off(by, bx, lane)) = hv;
-            *reinterpret_cast<bf4*>(rec + REC_AL + frag32_off(by, bx, lane)) = lv;
+            if (bx == by) {  // Gamma on the diagonal (bx, by are wave-uniform)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) av[v] += (4 * lq + v == li) ? sm.gam[y0 + li] : 0.f;
+            }
+            s4 hv, lv;
+            split4(av, hv, lv);
+            if constexpr (LDS_REC) {
+                ah_keep[u] = hv;
+                al_keep[u] = lv;
+            } else {
+                *reinterpret_cast<s4*>(rec + REC_AH + frag32_off(by, bx, lane)) = hv;
+                *reinterpret_cast<s4*>(rec + REC_AL + frag32_off(by, bx, lane)) = lv;
+            }
             st_split(Fm, PB, x0, y0, af);
         }
     }
@@ -778,6 +784,15 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
 
     // ---- 9. H = F V (x = k, y = v; X split, V exact -> workspace fp32, H^T tiles);
     //          O_intra = E V (x = v, y = t -> workspace bf16, tiles of O_intra[t][v]); V read down its rows
+    if constexpr (LDS_REC) {  // step 8's tiles of Q and A, now that their slots are free
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int bx = (wv >> 2) + 2 * u, by = wv & 3;
+            *reinterpret_cast<bf4*>(rec + REC_Q + frag32_off(by, bx, lane)) = q_keep[u];
+            *reinterpret_cast<s4*>(rec + REC_AH + frag32_off(by, bx, lane)) = ah_keep[u];
+            *reinterpret_cast<s4*>(rec + REC_AL + frag32_off(by, bx, lane)) = al_keep[u];
+        }
+    }
     {
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
@@ -831,7 +846,7 @@ __global__ __launch_bounds__(512) void wkv7_chunk_prep_kernel(const Params p, ch
         // without a chunk computes on zeros and writes the trash record), so the number of vector memory operations
         // between a prefetch and its use is fixed
         RawIn rn;
-        prep_item(p, cur, rc, wsc, sm, item_offset(p, nxt, row, cb), rn);
+        prep_item<false>(p, cur, rc, wsc, sm, item_offset(p, nxt, row, cb), rn);
         cur = nxt;
         rc = rn;
         pos = np;
@@ -853,8 +868,9 @@ struct ScanRecH {
     s8 o;                   // token tile pair hf
 };
 
+template <bool LDS_REC = false>
 __device__ __forceinline__ void scan_load_half(ScanRecH& r, const char* rec, int vg, int hf, int lane) {
-    const char* const b = uniform_ptr(rec);
+    const char* const b = LDS_REC ? rec : uniform_ptr(rec);
     const int lo = lane * 16;
 #pragma unroll
     for (int x = 0; x < 2; ++x) {
@@ -881,12 +897,7 @@ __device__ __forceinline__ void state_operand_block(const f4& X, const f4& Y, bf
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
-        for (int w = 0; w < 2; ++w) {
-            const uint32_t hp = pack_bf16x2(xs[u][2 * w], xs[u][2 * w + 1]);
-            h[u][w] = hp;
-            l[u][w] = pack_bf16x2(xs[u][2 * w] - __uint_as_float(hp << 16),
-                                  xs[u][2 * w + 1] - __uint_as_float(hp & 0xffff0000u));
-        }
+        for (int w = 0; w < 2; ++w) split_pair(xs[u][2 * w], xs[u][2 * w + 1], h[u][w], l[u][w]);
     }
     uint32_t oh[4], ol[4];
 #pragma unroll
@@ -1162,6 +1173,224 @@ __global__ __launch_bounds__(1024) void wkv7_chunk_plan_kernel(const Params p, i
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
+
+// ---------------------------------------------------------------------------------------------------------------
+// Chain kernel: a whole ragged step (token-serial rows and chunked rows) in one dispatch, with no workspace.
+// Each workgroup takes whole (row, head) chains of chunked rows and walks their chunks in order: prep_item builds
+// the chunk's record in LDS and chain_step applies it at once to the state, which stays in the registers of the
+// eight wavefronts (wavefront wv: column group wv >> 1, rows half wv & 1, the scan's layout).  So the 48 KB record
+// never leaves the CU, and no second kernel, plan kernel or cross-workgroup synchronisation is needed.  The price is
+// that a chain's chunks are serial on one CU: the launcher picks this kernel when the rows are short enough for that
+// not to set the call's length (many chains, few chunks each -- a continuous-batching step of prefill rows and
+// decode rows), and the two-kernel path for long rows.
+// ---------------------------------------------------------------------------------------------------------------
+
+// One chunk of a chain on the LDS record `rec`: y <- Q S + O_intra for this wavefront's token tiles 2 hf, 2 hf + 1
+// (column group vg), S <- A S + H for its row tiles, then the new state's operand halves are exchanged through
+// `ex` (one barrier).  (Bh, Bl) hold the state at the chunk start as 16x16x32 operands, as in scan_item.
+__device__ __forceinline__ void chain_step(const Params& p, const char* rec, f4 (&S)[2], bf8 (&Bh)[2], bf8 (&Bl)[2],
+                                           bf8 (*ex)[2][64], int vg, int hf, int lane, int64_t bos, int c, int L,
+                                           int h) {
+    const int i = lane & 15, q = lane >> 4;
+    ScanRecH R;
+    scan_load_half<true>(R, rec, vg, hf, lane);
+    f4 nS[2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) nS[x] = R.h[x];
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            const bf8 ah = __builtin_bit_cast(bf8, R.ah[x][cb]), al = __builtin_bit_cast(bf8, R.al[x][cb]);
+            nS[x] = mfma_bf16(ah, Bl[cb], nS[x]);
+            nS[x] = mfma_bf16(al, Bh[cb], nS[x]);
+            nS[x] = mfma_bf16(ah, Bh[cb], nS[x]);
+        }
+    }
+    f4 y[2];
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+        const s4 o4 = half4(R.o, x);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[x][e] = bf16_to_f32((uint16_t)o4[e]);
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) y[x] = mfma_bf16(Bh[cb], __builtin_bit_cast(bf8, R.q[x][cb]), y[x]);
+    }
+    if (p.o) {
+        uint16_t* const obase = p.o + bos * p.o_tok_stride + (int64_t)h * HS + 16 * vg + 4 * q;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            // lane (i, q) holds y[token 16 t + i][columns 16 vg + 4 q .. + 3], t = 2 hf + x
+            const int tok = c * C + 16 * (2 * hf + x) + i;
+            if (tok < L) {
+                uint2 pk;
+                pk.x = pack_bf16x2(y[x][0], y[x][1]);
+                pk.y = pack_bf16x2(y[x][2], y[x][3]);
+                *reinterpret_cast<uint2*>(obase + (int64_t)tok * p.o_tok_stride) = pk;
+            }
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x) S[x] = nS[x];
+}
+
+// The state's operand halves, exchanged between the two wavefronts of a column group (one barrier).
+__device__ __forceinline__ void chain_exchange(const f4 (&S)[2], bf8 (&Bh)[2], bf8 (&Bl)[2], bf8 (*ex)[2][64], int hf,
+                                               int lane) {
+    bf8 oh, ol;
+    state_operand_block(S[0], S[1], oh, ol);
+    ex[hf][0][lane] = oh;
+    ex[hf][1][lane] = ol;
+    __syncthreads();
+    const bf8 th = ex[1 - hf][0][lane], tl = ex[1 - hf][1][lane];
+    Bh[0] = hf ? th : oh;
+    Bl[0] = hf ? tl : ol;
+    Bh[1] = hf ? oh : th;
+    Bl[1] = hf ? ol : tl;
+}
+
+// Chain (row, head) -> Item of its chunk c (the chain's rows are longer than rec_max_len, so c < chunks exists).
+__device__ __forceinline__ Item chain_item(int h, int64_t bos, int L, int c) {
+    Item it{};
+    it.ok = true;
+    it.h = h;
+    it.Lc = min(C, L - c * C);
+    it.tok0 = bos + (int64_t)c * C;
+    return it;
+}
+
+__global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
+    __shared__ __attribute__((aligned(16))) PrepSmem sm;
+    __shared__ int32_t wave_count[8];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int G = (int)gridDim.x, b = (int)blockIdx.x;
+
+    // ---- 1. the rows the chains own (longer than rec_max_len), longest first -- the same list in every workgroup:
+    //         compaction in row order, then each row's rank = rows with more chunks, or as many and an earlier index.
+    //         num_seqs <= kChainMaxSeqs = the workgroup size (checked by the launcher): one row per thread.
+    int32_t* const crow = reinterpret_cast<int32_t*>(sm.slot[16]);  // chain rows in order, kept to the end
+    int nrows;
+    {
+        int32_t* const tmp_row = reinterpret_cast<int32_t*>(sm.slot[0]);
+        int32_t* const tmp_nch = tmp_row + kChainMaxSeqs;
+        int64_t bos = 0;
+        int L = 0;
+        bool chain = false;
+        if (tid < p.num_seqs) {
+            seq_extent(p, tid, bos, L);
+            chain = owns_row(p, L);
+        }
+        const uint64_t bal = __ballot(chain);
+        if (lane == 0) wave_count[wv] = __popcll(bal);
+        __syncthreads();
+        int off = 0;
+        nrows = 0;
+#pragma unroll
+        for (int w2 = 0; w2 < 8; ++w2) {
+            off += w2 < wv ? wave_count[w2] : 0;
+            nrows += wave_count[w2];
+        }
+        if (chain) {
+            const int k = off + __popcll(bal & ((1ull << lane) - 1));
+            tmp_row[k] = tid;
+            tmp_nch[k] = (L + C - 1) / C;
+        }
+        __syncthreads();
+        if (tid < nrows) {
+            const int mine = tmp_nch[tid];
+            int rank = 0;
+            for (int j = 0; j < nrows; ++j) {
+                const int o = tmp_nch[j];
+                rank += (o > mine || (o == mine && j < tid)) ? 1 : 0;
+            }
+            crow[rank] = tmp_row[tid];
+        }
+        __syncthreads();
+    }
+
+    // ---- 2. rows of at most rec_max_len tokens (decode rows, short prefills): one pair per wavefront at a time,
+    //         the token-serial kernel's code
+    {
+        float* const slab = reinterpret_cast<float*>(sm.slot[14]) + wv * 5 * HS;
+        const int g = lane >> 4, c = lane & 15;
+        const uint32_t npairs = (uint32_t)p.num_seqs * (uint32_t)p.H;
+        for (uint32_t pa = (uint32_t)b * 8 + wv; pa < npairs; pa += (uint32_t)G * 8) {
+            const Pair q = pair_of(p, pa);
+            if (!q.run) continue;
+            f4 S[16];
+            TokenIn x{};
+            prefetch_pair(p, q, lane, g, c, S, x);
+            run_pair(p, q, lane, g, c, S, x, slab);
+        }
+    }
+    __syncthreads();
+
+    // ---- 3. chains j = rank * H + h, snake-assigned: pass k covers chains [k G, (k + 1) G); workgroup b takes
+    //         k G + b on even passes and k G + G - 1 - b on odd ones (the longest chains are spread over all
+    //         workgroups, and the workgroups with a long chain in one pass get a short one in the next)
+    const int64_t nchains = (int64_t)nrows * p.H;
+    const int vg = wv >> 1, hf = wv & 1;
+    bf8 (*const ex)[2][64] = reinterpret_cast<bf8 (*)[2][64]>(sm.slot[12]) + 2 * vg;  // [hf][hi, lo][lane]
+    const int trow = tid >> 3, cb = (tid & 7) * 8;
+    const int i = lane & 15, q = lane >> 4, col = 16 * vg + i;
+    auto chain_at = [&](int64_t k, int& n, int& h) {
+        const int64_t j = k * G + ((k & 1) ? G - 1 - b : b);
+        if (j >= nchains) return false;
+        n = crow[j / p.H];
+        h = (int)(j % p.H);
+        return true;
+    };
+    int n, h;
+    if (!chain_at(0, n, h)) return;  // uniform: no barriers follow for this workgroup
+    int64_t bos;
+    int L;
+    seq_extent(p, n, bos, L);
+    RawIn raw = load_item(p, chain_item(h, bos, L, 0), trow, cb);
+    for (int64_t k = 0;; ++k) {
+        const int nch = (L + C - 1) / C;
+        const float* src = state_src(p, n, h);
+        float* dst = state_dst(p, n, h);
+        f4 S[2];
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) S[x][e] = src ? src[(16 * (2 * hf + x) + 4 * q + e) * HS + col] : 0.f;
+        }
+        // the next chain (for the look-ahead load of its first chunk)
+        int n2 = 0, h2 = 0, L2 = 0;
+        int64_t bos2 = 0;
+        const bool more = chain_at(k + 1, n2, h2);
+        if (more) seq_extent(p, n2, bos2, L2);
+        bf8 Bh[2], Bl[2];
+        __syncthreads();  // the previous chain's last exchange has been read
+        chain_exchange(S, Bh, Bl, ex, hf, lane);
+        for (int c = 0; c < nch; ++c) {
+            const Item it = chain_item(h, bos, L, c);
+            Item nx{};
+            if (c + 1 < nch) nx = chain_item(h, bos, L, c + 1);
+            else if (more) nx = chain_item(h2, bos2, L2, 0);
+            RawIn rn;
+            prep_item<true>(p, it, raw, nullptr, sm, item_offset(p, nx, trow, cb), rn);
+            chain_step(p, reinterpret_cast<const char*>(sm.slot[kRecSlot]), S, Bh, Bl, ex, vg, hf, lane, bos, c, L, h);
+            if (c + 1 < nch) chain_exchange(S, Bh, Bl, ex, hf, lane);
+            raw = rn;
+        }
+        if (dst) {
+#pragma unroll
+            for (int x = 0; x < 2; ++x) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) dst[(16 * (2 * hf + x) + 4 * q + e) * HS + col] = S[x][e];
+            }
+        }
+        if (!more) break;
+        n = n2;
+        h = h2;
+        bos = bos2;
+        L = L2;
+    }
+}
+
 }  // namespace
 
 ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_t max_len_bound, bool varlen,
@@ -1180,6 +1409,13 @@ ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_
     ws.chunk_bytes = align256(((size_t)maxc * (size_t)H + 1) * kChunkBytes);  // + the trash record
     ws.total_bytes = ws.plan_bytes + ws.chunk_bytes;
     return ws;
+}
+
+hipError_t launch_chain(const Params& p, hipStream_t stream) {
+    if (p.num_seqs == 0) return hipSuccess;
+    if (p.num_seqs > kChainMaxSeqs) return hipErrorInvalidValue;  // the C-ABI layer never routes such calls here
+    hipLaunchKernelGGL(wkv7_chain_kernel, dim3((unsigned)device_cu_count()), dim3(512), 0, stream, p);
+    return hipGetLastError();
 }
 
 hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* workspace, hipStream_t stream) {

@@ -35,6 +35,27 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, bf16x2_t));
 }
 
+// Hi/lo split of two fp32 values into bf16 pairs: hw = (bf16(x0), bf16(x1)) rounded to nearest even, lw = the bf16 of
+// the remainders x - hi.  Each remainder is exact in fp32 (hi holds x's top 8 significant bits) and is formed by one
+// v_dot2c_f32_bf16 (x + hi . (-1, 0)) instead of unpacking hi and subtracting.  x ~ hi + lo to about 2^-17 relative.
+// The selector pairs are kept in registers (an empty non-volatile asm, which the compiler may still hoist and share):
+// folded into an inline constant, the bf16 pair (-1, 0) is emitted as the operand "-1.0", which the hardware reads
+// as the pair (0, -1) -- measured on gfx950: every remainder wrong that way, all exact from a register.
+__device__ __forceinline__ bf16x2_t bf16_pair_in_register(uint32_t bits) {
+    asm("" : "+v"(bits));
+    return __builtin_bit_cast(bf16x2_t, bits);
+}
+
+__device__ __forceinline__ void split_pair(float x0, float x1, uint32_t& hw, uint32_t& lw) {
+    const f2_t x = {x0, x1};
+    const bf16x2_t h = __builtin_convertvector(x, bf16x2_t);
+    const bf16x2_t m0 = bf16_pair_in_register(0x0000BF80u), m1 = bf16_pair_in_register(0xBF800000u);
+    const float l0 = __builtin_amdgcn_fdot2_f32_bf16(h, m0, x0, false);
+    const float l1 = __builtin_amdgcn_fdot2_f32_bf16(h, m1, x1, false);
+    hw = __builtin_bit_cast(uint32_t, h);
+    lw = pack_bf16x2(l0, l1);
+}
+
 // Decay d = exp(-exp(w)) of the raw w (rwkv_next/kernels/wkv7.py:74), with the device library's full-precision
 // expf.
 __device__ __forceinline__ float decay(float w) { return expf(-expf(w)); }

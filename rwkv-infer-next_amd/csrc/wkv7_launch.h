@@ -35,6 +35,13 @@ struct ChunkWorkspace {
 ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_t max_len_bound, bool varlen,
                                int rec_max_len);
 
+// Rows a chain launch accepts (its row table has one entry per thread of a 512-thread workgroup).
+constexpr int kChainMaxSeqs = 512;
+
+// Single-dispatch chain kernel: rows of at most p.rec_max_len tokens token-serially, longer rows as (row, head) chains
+// whose chunk records stay in LDS.  No workspace.  p.num_seqs <= kChainMaxSeqs.
+hipError_t launch_chain(const Params& p, hipStream_t stream);
+
 // Chunked path over rows with len > p.rec_max_len (all rows when p.rec_max_len < 0): plan (varlen only), prep
 // (parallel over chunks), scan (sequential over chunks per (row, head, 16-column block)).
 hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* workspace, hipStream_t stream);

@@ -23,7 +23,7 @@ BUILD_DIR = os.path.join(PROJECT_DIR, "_build")
 
 SOURCES = ("wkv7_recurrent.hip", "wkv7_chunked.hip", "wkv7_pool.hip", "wkv7_timemix.hip", "w6a16.hip", "wkv7_capi.hip",
            "wkv7_noalloc.hip")
-HEADERS = ("wkv7_device.h", "wkv7_launch.h")
+HEADERS = ("wkv7_device.h", "wkv7_launch.h", "wkv7_token.h")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

@@ -28,6 +28,7 @@ WKV7_STATUS_NKEEP = 8
 ALGO_AUTO = 0
 ALGO_RECURRENT = 1
 ALGO_CHUNKED = 2
+ALGO_CHAIN = 3
 
 EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
             "wkv7_args_layout", "wkv7_run_noalloc",

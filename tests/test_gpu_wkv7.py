@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 H8 = 8
-ALGOS = {"auto": 0, "recurrent": 1, "chunked": 2}
+ALGOS = {"auto": 0, "recurrent": 1, "chunked": 2, "chain": 3}
 
 
 @pytest.fixture(scope="module")
@@ -147,6 +147,47 @@ def test_pool_ragged_mixed_rows(dev, K, algo):
                      cu_seqlens=torch.from_numpy(cu).to(dev), algo=ALGOS[algo])
     torch.cuda.synchronize()
     check(o, o_ref, pool, pool_ref)
+
+
+def test_chain_kernel_many_chains(dev, K):
+    """The single-dispatch chain kernel with more (row, head) chains than workgroups and very uneven rows: packed rows
+    of 0 .. 700 tokens (most above the 32-token token-serial bound, some below), distinct pool slots, fresh rows and
+    n_keep limits; every state and output against the oracle, and slots outside the batch untouched."""
+    from oracle import wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H, S_slots = 16, 64
+    rng = np.random.default_rng(77)
+    lens = [int(x) for x in rng.integers(0, 701, size=40)]
+    lens[3], lens[7], lens[11] = 1, 0, 32
+    say("chain kernel", len(lens), "rows", sum(lens), "tokens")
+    seqs = [operands(1, L, H, seed=300 + i) for i, L in enumerate(lens)]
+    cat = {n: np.concatenate([s[n] for s in seqs], axis=1) for n in seqs[0]}
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool0 = synth.state_np((S_slots, H, 64, 64), seed=301)
+    slots = rng.permutation(S_slots)[:len(lens)].astype(np.int64)
+    fresh = rng.random(len(lens)) < 0.2
+    n_keep = np.array([L if i % 5 else max(0, L - 17) for i, L in enumerate(lens)], np.int64)
+    pool_in = pool0.copy()
+    pool_in[slots[fresh]] = 0.0
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(cat), pool_in, cu_seqlens=cu, state_idx=slots, n_keep=n_keep)
+    pool = torch.from_numpy(pool0).to(dev)
+    status = K.new_status(dev)
+    o = K.wkv7_pool_(*to_dev(cat, dev), pool, torch.from_numpy(slots).to(dev), H, 64,
+                     cu_seqlens=torch.from_numpy(cu).to(dev), n_keep=torch.from_numpy(n_keep).to(dev),
+                     fresh=torch.from_numpy(fresh).to(dev), max_len=700, algo=3, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    # outputs past a row's n_keep are not produced (the reference's STORE_O loop stops at L = min(len, n_keep))
+    keep = np.zeros(sum(lens), bool)
+    for i in range(len(lens)):
+        keep[cu[i]:cu[i] + min(lens[i], n_keep[i])] = True
+    from oracle import rel_max
+    eo = rel_max(as_np(o).reshape(o_ref.shape)[:, keep], o_ref[:, keep])
+    es = rel_max(as_np(pool), pool_ref)
+    say(f"y max-rel {eo:.3e}  state max-rel {es:.3e}")
+    assert eo <= Y_TOL and es <= S_TOL
+    untouched = np.setdiff1d(np.arange(S_slots), slots)
+    assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
 
 
 def test_pool_final_false_leaves_pool_untouched(dev, K):
