@@ -304,17 +304,16 @@ __device__ __forceinline__ void finish_tile(const Args& p, int b, int mg, int st
                     if (r < rows) coherent_store(mine + r * kTileN + 16 * t, acc[mt][t][v]);
                 }
     }
-    // The partials are device-coherent stores (they bypass the non-coherent caches); waiting for them to complete
-    // before the counter increment publishes them without writing back the whole L2, which an agent-scope release
-    // fence would do once per wavefront.
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    // Hand-off (memory model, agent scope): every lane releases its partial stores with a release fence, then one
+    // lane counts the wavefront in; the last arriver's acquire fence makes all splits' partials visible before it
+    // reads them.  The partials themselves are agent-scope atomic stores, so the release finds little dirty data to
+    // write back.
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
     uint32_t arrived = 0;
     if (lane == 0) arrived = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     arrived = __builtin_amdgcn_readfirstlane(arrived);
     if (arrived != (uint32_t)p.split_k - 1) return;
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the loads below are issued only after the counter returned
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     if (rows == 1)
         reduce_rows<1>(p, part, kTileFloats, 0, 1, b, m0, n0);
     else

@@ -710,40 +710,52 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     bf4 q_keep[2];
     s4 ah_keep[2], al_keep[2];
     {
+        // both tiles of this wave (same by) are accumulated together, so the Y operands (rho's row tile and the
+        // transposed Bk tile, by) are read once per contraction block for the two
+        const int by = wv & 3, y0 = 16 * by;
+        f4 aqs[2], aes[2], aas[2], afs[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
-            const int bx = (wv >> 2) + 2 * u, by = wv & 3;
-            const int x0 = 16 * bx, y0 = 16 * by;
-            f4 aq, ae, aa = zero4(), af;
-            {
-                const bf4 r4 = *reinterpret_cast<const bf4*>(Rq.h + (y0 + li) * PB + x0 + 4 * lq);
-                const bf4 s4v = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
-                const int o = (x0 + 4 * lq + (li >> 2)) * PB + y0 + 4 * (li & 3);
-                const s4 kh4 = ld_tr4(Kk.h + o), kl4 = ld_tr4(Kk.l + o);  // Kk[x0 + 4 lq + v][y0 + li]
+            const int x0 = 16 * ((wv >> 2) + 2 * u);
+            const bf4 r4 = *reinterpret_cast<const bf4*>(Rq.h + (y0 + li) * PB + x0 + 4 * lq);
+            const bf4 s4v = *reinterpret_cast<const bf4*>(Sig.h + (y0 + li) * PB + x0 + 4 * lq);
+            const int o = (x0 + 4 * lq + (li >> 2)) * PB + y0 + 4 * (li & 3);
+            const s4 kh4 = ld_tr4(Kk.h + o), kl4 = ld_tr4(Kk.l + o);  // Kk[x0 + 4 lq + v][y0 + li]
+            aas[u] = zero4();
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    aq[v] = (float)r4[v] * sm.em[x0 + 4 * lq + v];
-                    ae[v] = (float)s4v[v];
-                    af[v] = bf16_to_f32((uint16_t)kh4[v]) + bf16_to_f32((uint16_t)kl4[v]);
-                }
+            for (int v = 0; v < 4; ++v) {
+                aqs[u][v] = (float)r4[v] * sm.em[x0 + 4 * lq + v];
+                aes[u][v] = (float)s4v[v];
+                afs[u][v] = bf16_to_f32((uint16_t)kh4[v]) + bf16_to_f32((uint16_t)kl4[v]);
             }
+        }
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const int xo = (x0 + li) * PB + 32 * kb + 8 * lq;
+        for (int kb = 0; kb < 2; ++kb) {
+            const bf8 bh = ld8_tr(Bk.h, kb, y0), bl = ld8_tr(Bk.l, kb, y0);
+            const bool use_rho = kb == 0 || by >= 2;
+            bf8 rh;
+            if (use_rho) rh = ld8(Rho.h + (y0 + li) * PB + 32 * kb + 8 * lq);
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int xo = (16 * ((wv >> 2) + 2 * u) + li) * PB + 32 * kb + 8 * lq;
                 const bf8 wh = ld8(Wm.h + xo), wl = ld8(Wm.l + xo), gh = ld8(Gm.h + xo), gl = ld8(Gm.l + xo);
-                const bf8 bh = ld8_tr(Bk.h, kb, y0), bl = ld8_tr(Bk.l, kb, y0);
-                if (kb == 0 || by >= 2) {
-                    const bf8 rh = ld8(Rho.h + (y0 + li) * PB + 32 * kb + 8 * lq);
-                    aq = mfma_bf16(wh, rh, aq);
-                    ae = mfma_bf16(gh, rh, ae);
+                if (use_rho) {
+                    aqs[u] = mfma_bf16(wh, rh, aqs[u]);
+                    aes[u] = mfma_bf16(gh, rh, aes[u]);
                 }
-                aa = mfma_bf16(wh, bl, aa);
-                aa = mfma_bf16(wl, bh, aa);
-                aa = mfma_bf16(wh, bh, aa);
-                af = mfma_bf16(gh, bl, af);
-                af = mfma_bf16(gl, bh, af);
-                af = mfma_bf16(gh, bh, af);
+                aas[u] = mfma_bf16(wh, bl, aas[u]);
+                aas[u] = mfma_bf16(wl, bh, aas[u]);
+                aas[u] = mfma_bf16(wh, bh, aas[u]);
+                afs[u] = mfma_bf16(gh, bl, afs[u]);
+                afs[u] = mfma_bf16(gl, bh, afs[u]);
+                afs[u] = mfma_bf16(gh, bh, afs[u]);
             }
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int bx = (wv >> 2) + 2 * u;
+            const int x0 = 16 * bx;
+            f4 aq = aqs[u], ae = aes[u], aa = aas[u], af = afs[u];
             // Q -> record (Q[t][k]: t tile by)
             bf4 qv;
 #pragma unroll
