@@ -1271,43 +1271,63 @@ __device__ __forceinline__ Item chain_item(int h, int64_t bos, int L, int c) {
     return it;
 }
 
+// Token-serial pairs per chunk-item of chain work, for balancing: a pair moves 33.7 KB (HBM-bound), a chunk-item
+// keeps a CU busy for about 10 us; with a few workgroups on the token-serial rows at a time, about 24 pairs take as
+// long as a chunk-item.
+constexpr int kPairsPerItem = 24;
+
 __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
     __shared__ __attribute__((aligned(16))) PrepSmem sm;
-    __shared__ int32_t wave_count[8];
+    __shared__ int32_t wave_count[8], wave_count2[8];
+    __shared__ int32_t max_load;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = (int)gridDim.x, b = (int)blockIdx.x;
 
-    // ---- 1. the rows the chains own (longer than rec_max_len), longest first -- the same list in every workgroup:
-    //         compaction in row order, then each row's rank = rows with more chunks, or as many and an earlier index.
-    //         num_seqs <= kChainMaxSeqs = the workgroup size (checked by the launcher): one row per thread.
-    int32_t* const crow = reinterpret_cast<int32_t*>(sm.slot[16]);  // chain rows in order, kept to the end
-    int nrows;
+    // ---- 1. plan, the same in every workgroup (num_seqs <= kChainMaxSeqs = the workgroup size, gridDim.x <=
+    //         kChainMaxSeqs: both checked by the launcher; one row / one workgroup per thread):
+    //   crow / cnch: the chain rows (longer than rec_max_len), longest first (rank = rows with more chunks, or as
+    //   many and an earlier index); srow: the token-serial rows in row order; start: each workgroup's range of
+    //   token-serial pairs, proportional to how far its chain work (snake assignment below) falls short of the
+    //   longest, plus an even share.
+    int32_t* const crow = reinterpret_cast<int32_t*>(sm.slot[16]);  // kept to the end of the kernel
+    int32_t* const cnch = crow + kChainMaxSeqs;
+    int32_t* const srow = cnch + kChainMaxSeqs;
+    int32_t* const start = srow + kChainMaxSeqs;                     // [G + 1]
+    int nrows, nshort;
     {
         int32_t* const tmp_row = reinterpret_cast<int32_t*>(sm.slot[0]);
         int32_t* const tmp_nch = tmp_row + kChainMaxSeqs;
         int64_t bos = 0;
         int L = 0;
-        bool chain = false;
+        bool chain = false, shrt = false;
         if (tid < p.num_seqs) {
             seq_extent(p, tid, bos, L);
             chain = owns_row(p, L);
+            shrt = !chain;
         }
-        const uint64_t bal = __ballot(chain);
-        if (lane == 0) wave_count[wv] = __popcll(bal);
+        const uint64_t bal = __ballot(chain), bal2 = __ballot(shrt);
+        if (lane == 0) {
+            wave_count[wv] = __popcll(bal);
+            wave_count2[wv] = __popcll(bal2);
+        }
         __syncthreads();
-        int off = 0;
-        nrows = 0;
+        int off = 0, off2 = 0;
+        nrows = nshort = 0;
 #pragma unroll
         for (int w2 = 0; w2 < 8; ++w2) {
             off += w2 < wv ? wave_count[w2] : 0;
+            off2 += w2 < wv ? wave_count2[w2] : 0;
             nrows += wave_count[w2];
+            nshort += wave_count2[w2];
         }
+        const uint64_t below = (1ull << lane) - 1;
         if (chain) {
-            const int k = off + __popcll(bal & ((1ull << lane) - 1));
+            const int k = off + __popcll(bal & below);
             tmp_row[k] = tid;
             tmp_nch[k] = (L + C - 1) / C;
         }
+        if (shrt) srow[off2 + __popcll(bal2 & below)] = tid;
         __syncthreads();
         if (tid < nrows) {
             const int mine = tmp_nch[tid];
@@ -1317,30 +1337,45 @@ __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
                 rank += (o > mine || (o == mine && j < tid)) ? 1 : 0;
             }
             crow[rank] = tmp_row[tid];
+            cnch[rank] = mine;
         }
+        if (tid == 0) max_load = 0;
+        __syncthreads();
+        // chain load (chunk-items) of workgroup tid under the snake assignment
+        const int64_t nchains = (int64_t)nrows * p.H;
+        int load = 0;
+        if (tid < G) {
+            for (int64_t k = 0;; ++k) {
+                const int64_t j = k * G + ((k & 1) ? G - 1 - tid : tid);
+                if (j >= nchains) break;
+                load += cnch[j / p.H];
+            }
+            atomicMax(&max_load, load);
+        }
+        __syncthreads();
+        // token-serial pairs: weight = deficit + even share (in pairs), then an exclusive prefix over workgroups
+        const int64_t npairs = (int64_t)nshort * p.H;
+        const int64_t even = (npairs + G - 1) / G;
+        int64_t* const wgt = reinterpret_cast<int64_t*>(tmp_row);  // [G + 1], reusing the scratch
+        if (tid < G) wgt[tid] = (int64_t)(max_load - load) * kPairsPerItem + even;
+        __syncthreads();
+        if (tid == 0) {
+            int64_t acc = 0;
+            for (int w2 = 0; w2 < G; ++w2) {
+                const int64_t x = wgt[w2];
+                wgt[w2] = acc;
+                acc += x;
+            }
+            wgt[G] = acc;
+        }
+        __syncthreads();
+        if (tid <= G) start[tid] = (int32_t)(wgt[G] > 0 ? npairs * wgt[tid] / wgt[G] : 0);
         __syncthreads();
     }
 
-    // ---- 2. rows of at most rec_max_len tokens (decode rows, short prefills): one pair per wavefront at a time,
-    //         the token-serial kernel's code
-    {
-        float* const slab = reinterpret_cast<float*>(sm.slot[14]) + wv * 5 * HS;
-        const int g = lane >> 4, c = lane & 15;
-        const uint32_t npairs = (uint32_t)p.num_seqs * (uint32_t)p.H;
-        for (uint32_t pa = (uint32_t)b * 8 + wv; pa < npairs; pa += (uint32_t)G * 8) {
-            const Pair q = pair_of(p, pa);
-            if (!q.run) continue;
-            f4 S[16];
-            TokenIn x{};
-            prefetch_pair(p, q, lane, g, c, S, x);
-            run_pair(p, q, lane, g, c, S, x, slab);
-        }
-    }
-    __syncthreads();
-
-    // ---- 3. chains j = rank * H + h, snake-assigned: pass k covers chains [k G, (k + 1) G); workgroup b takes
+    // ---- 2. chains j = rank * H + h, snake-assigned: pass k covers chains [k G, (k + 1) G); workgroup b takes
     //         k G + b on even passes and k G + G - 1 - b on odd ones (the longest chains are spread over all
-    //         workgroups, and the workgroups with a long chain in one pass get a short one in the next)
+    //         workgroups, and a workgroup with a long chain in one pass gets a short one in the next)
     const int64_t nchains = (int64_t)nrows * p.H;
     const int vg = wv >> 1, hf = wv & 1;
     bf8 (*const ex)[2][64] = reinterpret_cast<bf8 (*)[2][64]>(sm.slot[12]) + 2 * vg;  // [hf][hi, lo][lane]
@@ -1354,52 +1389,70 @@ __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
         return true;
     };
     int n, h;
-    if (!chain_at(0, n, h)) return;  // uniform: no barriers follow for this workgroup
-    int64_t bos;
-    int L;
-    seq_extent(p, n, bos, L);
-    RawIn raw = load_item(p, chain_item(h, bos, L, 0), trow, cb);
-    for (int64_t k = 0;; ++k) {
-        const int nch = (L + C - 1) / C;
-        const float* src = state_src(p, n, h);
-        float* dst = state_dst(p, n, h);
-        f4 S[2];
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-#pragma unroll
-            for (int e = 0; e < 4; ++e) S[x][e] = src ? src[(16 * (2 * hf + x) + 4 * q + e) * HS + col] : 0.f;
-        }
-        // the next chain (for the look-ahead load of its first chunk)
-        int n2 = 0, h2 = 0, L2 = 0;
-        int64_t bos2 = 0;
-        const bool more = chain_at(k + 1, n2, h2);
-        if (more) seq_extent(p, n2, bos2, L2);
-        bf8 Bh[2], Bl[2];
-        __syncthreads();  // the previous chain's last exchange has been read
-        chain_exchange(S, Bh, Bl, ex, hf, lane);
-        for (int c = 0; c < nch; ++c) {
-            const Item it = chain_item(h, bos, L, c);
-            Item nx{};
-            if (c + 1 < nch) nx = chain_item(h, bos, L, c + 1);
-            else if (more) nx = chain_item(h2, bos2, L2, 0);
-            RawIn rn;
-            prep_item<true>(p, it, raw, nullptr, sm, item_offset(p, nx, trow, cb), rn);
-            chain_step(p, reinterpret_cast<const char*>(sm.slot[kRecSlot]), S, Bh, Bl, ex, vg, hf, lane, bos, c, L, h);
-            if (c + 1 < nch) chain_exchange(S, Bh, Bl, ex, hf, lane);
-            raw = rn;
-        }
-        if (dst) {
+    if (chain_at(0, n, h)) {  // uniform over the workgroup
+        int64_t bos;
+        int L;
+        seq_extent(p, n, bos, L);
+        RawIn raw = load_item(p, chain_item(h, bos, L, 0), trow, cb);
+        for (int64_t k = 0;; ++k) {
+            const int nch = (L + C - 1) / C;
+            const float* src = state_src(p, n, h);
+            float* dst = state_dst(p, n, h);
+            f4 S[2];
 #pragma unroll
             for (int x = 0; x < 2; ++x) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e) dst[(16 * (2 * hf + x) + 4 * q + e) * HS + col] = S[x][e];
+                for (int e = 0; e < 4; ++e) S[x][e] = src ? src[(16 * (2 * hf + x) + 4 * q + e) * HS + col] : 0.f;
             }
+            // the next chain (for the look-ahead load of its first chunk)
+            int n2 = 0, h2 = 0, L2 = 0;
+            int64_t bos2 = 0;
+            const bool more = chain_at(k + 1, n2, h2);
+            if (more) seq_extent(p, n2, bos2, L2);
+            bf8 Bh[2], Bl[2];
+            __syncthreads();  // the previous chain's last exchange has been read
+            chain_exchange(S, Bh, Bl, ex, hf, lane);
+            for (int c = 0; c < nch; ++c) {
+                const Item it = chain_item(h, bos, L, c);
+                Item nx{};
+                if (c + 1 < nch) nx = chain_item(h, bos, L, c + 1);
+                else if (more) nx = chain_item(h2, bos2, L2, 0);
+                RawIn rn;
+                prep_item<true>(p, it, raw, nullptr, sm, item_offset(p, nx, trow, cb), rn);
+                chain_step(p, reinterpret_cast<const char*>(sm.slot[kRecSlot]), S, Bh, Bl, ex, vg, hf, lane, bos, c,
+                           L, h);
+                if (c + 1 < nch) chain_exchange(S, Bh, Bl, ex, hf, lane);
+                raw = rn;
+            }
+            if (dst) {
+#pragma unroll
+                for (int x = 0; x < 2; ++x) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) dst[(16 * (2 * hf + x) + 4 * q + e) * HS + col] = S[x][e];
+                }
+            }
+            if (!more) break;
+            n = n2;
+            h = h2;
+            bos = bos2;
+            L = L2;
         }
-        if (!more) break;
-        n = n2;
-        h = h2;
-        bos = bos2;
-        L = L2;
+    }
+    __syncthreads();  // the chain state of LDS is dead; the token-serial slabs reuse slots 14-15
+
+    // ---- 3. this workgroup's token-serial pairs (rows of at most rec_max_len tokens: decode rows, short prefills),
+    //         one pair per wavefront at a time, with the token-serial kernel's code
+    {
+        float* const slab = reinterpret_cast<float*>(sm.slot[14]) + wv * 5 * HS;
+        const int g = lane >> 4, c = lane & 15;
+        for (int64_t u = start[b] + wv; u < start[b + 1]; u += 8) {
+            const uint32_t pa = (uint32_t)srow[u / p.H] * (uint32_t)p.H + (uint32_t)(u % p.H);
+            const Pair qp = pair_of(p, pa);
+            f4 S[16];
+            TokenIn x{};
+            prefetch_pair(p, qp, lane, g, c, S, x);
+            run_pair(p, qp, lane, g, c, S, x, slab);
+        }
     }
 }
 
@@ -1426,7 +1479,8 @@ ChunkWorkspace chunk_workspace(int num_seqs, int H, int64_t total_tokens, int64_
 hipError_t launch_chain(const Params& p, hipStream_t stream) {
     if (p.num_seqs == 0) return hipSuccess;
     if (p.num_seqs > kChainMaxSeqs) return hipErrorInvalidValue;  // the C-ABI layer never routes such calls here
-    hipLaunchKernelGGL(wkv7_chain_kernel, dim3((unsigned)device_cu_count()), dim3(512), 0, stream, p);
+    const int grid = std::min(device_cu_count(), kChainMaxSeqs);   // one workgroup per CU (LDS-bound)
+    hipLaunchKernelGGL(wkv7_chain_kernel, dim3((unsigned)grid), dim3(512), 0, stream, p);
     return hipGetLastError();
 }
 
