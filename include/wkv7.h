@@ -39,10 +39,12 @@ extern "C" {
 #define WKV7_ERR_ARG (-5)        /* inconsistent arguments (snapshots on the chunked path, bad algo, ...) */
 #define WKV7_ERR_SCRATCH_LIMIT (-6) /* wkv7_run_noalloc: the call needs more than WKV7_NOALLOC_SCRATCH_BYTES */
 
-/* Bits of the optional device status word (wkv7_args.status).  The kernels never read or clear it; they OR a bit in
- * (one vector atomic) when they meet an index they must not follow, and go on as documented for that case, so every
- * kernel still exits normally and no access leaves its buffer.  In the reference the same inputs raise from torch
- * indexing (rwkv_next/model.py:366-396: index_select / index_copy_ / pool views). */
+/* Bits of the optional device status word (wkv7_args.status).  The recurrence kernels never follow an index outside
+ * its buffer: they go on as documented for each case below, so every kernel exits normally.  When status is set,
+ * wkv7_run first launches one small check over the call's per-sequence indices (in stream order, before the
+ * recurrence) that ORs the bits of every such case into the word; it never reads or clears it.  Calls with status ==
+ * NULL launch nothing extra.  In the reference the same inputs raise from torch indexing
+ * (rwkv_next/model.py:366-396: index_select / index_copy_ / pool views). */
 #define WKV7_STATUS_H0_SLOT 1   /* an h0 index outside [0, h0_rows): that sequence started from a zero state */
 #define WKV7_STATUS_HT_SLOT 2   /* an ht index outside [0, ht_rows): that final state was not stored */
 #define WKV7_STATUS_SEQLENS 4   /* cu_seqlens entries not non-decreasing within [0, total_tokens]: extents clamped */

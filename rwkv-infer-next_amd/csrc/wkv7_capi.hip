@@ -6,6 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include "wkv7.h"
@@ -140,8 +141,31 @@ Params to_params(const wkv7_args* a) {
     p.T = a->T;
     p.H = a->H;
     p.rec_max_len = -1;
-    p.status = a->status;
     return p;
+}
+
+// The optional status word: one pass over the call's sequences, launched before the recurrence only when the
+// caller passes a status pointer (so calls without one keep their single dispatch and pay nothing).  It checks
+// exactly what the kernels skip: an h0 slot outside [0, h0_rows) on a row that reads it (not fresh), an ht slot
+// outside [0, ht_rows), cu_seqlens entries that are not non-decreasing within [0, total_tokens], a negative n_keep.
+__global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, int32_t* __restrict__ status) {
+    int bits = 0;
+    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < p.num_seqs; n += gridDim.x * blockDim.x) {
+        if (p.h0 && !(p.fresh && p.fresh[n])) {
+            const int64_t s = p.h0_idx ? p.h0_idx[n] : n;
+            if (s < 0 || s >= p.h0_rows) bits |= WKV7_STATUS_H0_SLOT;
+        }
+        if (p.ht) {
+            const int64_t s = p.ht_idx ? p.ht_idx[n] : n;
+            if (s < 0 || s >= p.ht_rows) bits |= WKV7_STATUS_HT_SLOT;
+        }
+        if (p.cu) {
+            const int64_t b = p.cu[n], e = p.cu[n + 1];
+            if (b < 0 || e < b || e > p.total_tokens) bits |= WKV7_STATUS_SEQLENS;
+        }
+        if (p.n_keep && p.n_keep[n] < 0) bits |= WKV7_STATUS_NKEEP;
+    }
+    if (bits) __hip_atomic_fetch_or(status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -202,6 +226,12 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     if (args->num_seqs == 0) return WKV7_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
     Params p = to_params(args);
+    if (args->status) {
+        const int blocks = (int)std::min<int64_t>(((int64_t)args->num_seqs + 255) / 256, 1024);
+        hipLaunchKernelGGL(wkv7_status_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, args->status);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return static_cast<int>(e);
+    }
     if (pl.run_chain) {
         p.rec_max_len = pl.rec_len_rec;
         const hipError_t e = wkv7::launch_chain(p, s);

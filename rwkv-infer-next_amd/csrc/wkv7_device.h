@@ -103,26 +103,13 @@ struct Params {
     int32_t T;                      // dense tokens per sequence; snapshot time stride
     int32_t H;
     int32_t rec_max_len;            // chunked launches: rows this short run the recurrent path instead
-    int32_t* status;                // nullable: WKV7_STATUS_* bits of rejected indices are OR-ed in here
 };
-
-// Status bits (the WKV7_STATUS_* values of include/wkv7.h).
-constexpr int kStatusH0Slot = 1;
-constexpr int kStatusHtSlot = 2;
-constexpr int kStatusSeqlens = 4;
-constexpr int kStatusNKeep = 8;
-
-// Records a rejected index in the caller's status word (one vector atomic OR; error path only).
-__device__ __forceinline__ void report(const Params& p, int bit) {
-    if (p.status) __hip_atomic_fetch_or(p.status, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Extent of sequence n (rwkv_next/kernels/wkv7.py:46-54).
 __device__ __forceinline__ void seq_extent(const Params& p, int n, int64_t& bos, int& len) {
     if (p.cu) {
         // clamped to [0, total_tokens] so that a malformed cu_seqlens cannot index past the operands
         int64_t s = p.cu[n], e = p.cu[n + 1];
-        if (s < 0 || e < s || e > p.total_tokens) report(p, kStatusSeqlens);
         s = s < 0 ? 0 : (s > p.total_tokens ? p.total_tokens : s);
         e = e < s ? s : (e > p.total_tokens ? p.total_tokens : e);
         bos = s;
@@ -133,33 +120,26 @@ __device__ __forceinline__ void seq_extent(const Params& p, int n, int64_t& bos,
     }
     if (p.n_keep) {
         const int64_t nk = p.n_keep[n];
-        if (nk < 0) report(p, kStatusNKeep);
         if (nk < len) len = (int)(nk < 0 ? 0 : nk);
     }
     if (len < 0) len = 0;
 }
 
 // Initial state of (sequence n, head h), or nullptr for a zero state (no h0, a fresh row, or a slot index
-// outside [0, h0_rows): such rows start from zeros instead of reading out of bounds, and the index is reported).
+// outside [0, h0_rows): such rows start from zeros instead of reading out of bounds; wkv7_status_kernel reports
+// such indices when the caller asks for it).
 __device__ __forceinline__ const float* state_src(const Params& p, int n, int h) {
     if (!p.h0 || (p.fresh && p.fresh[n])) return nullptr;
     const int64_t s = p.h0_idx ? p.h0_idx[n] : n;
-    if (s < 0 || s >= p.h0_rows) {
-        report(p, kStatusH0Slot);
-        return nullptr;
-    }
+    if (s < 0 || s >= p.h0_rows) return nullptr;
     return p.h0 + (s * p.H + h) * (int64_t)HS2;
 }
 
-// Final-state destination, or nullptr when not stored (no ht, or a slot index outside [0, ht_rows), which is
-// reported).
+// Final-state destination, or nullptr when not stored (no ht, or a slot index outside [0, ht_rows)).
 __device__ __forceinline__ float* state_dst(const Params& p, int n, int h) {
     if (!p.ht) return nullptr;
     const int64_t s = p.ht_idx ? p.ht_idx[n] : n;
-    if (s < 0 || s >= p.ht_rows) {
-        report(p, kStatusHtSlot);
-        return nullptr;
-    }
+    if (s < 0 || s >= p.ht_rows) return nullptr;
     return p.ht + (s * p.H + h) * (int64_t)HS2;
 }
 
