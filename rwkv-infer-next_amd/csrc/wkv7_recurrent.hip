@@ -1,27 +1,27 @@
-// wkv7_recurrent.hip -- token-serial WKV7 kernel: decode (T = 1), speculative verify (short T) with per-token
+// wkv7_recurrent.hip -- token-serial WKV7 kernels: decode (T = 1), speculative verify (short T) with per-token
 // state snapshots, in-place rollback replay (n_keep), and the short rows of a ragged batch.
 //
 // Replaces the reference's fused recurrent Triton program _wkv7_raw (rwkv_next/kernels/wkv7.py:38-79) for
 // these cases.  Work decomposition (MI355X, wave64):
-//   * one wavefront per (sequence, head) pair at a time.  wkv7_recurrent_kernel: at most two waves per SIMD;
-//     each wave walks pairs gw, gw + nwaves, ... and issues the next pair's state loads before working on the
-//     current pair, so state reads, the recurrence math and state writes of different pairs overlap.
-//     wkv7_decode_kernel (single-token rows, at least three pairs per SIMD): one wave per SIMD issues the loads of
-//     four pairs before updating and storing the first, so the grid's state reads run ahead of its writes;
-//   * lane L = 16 g + c owns state rows k = 4 i + g (i = 0..15) and columns v = 4 c .. 4 c + 3: 64 fp32 in VGPRs.
-//     Load instruction i of a wave reads rows 4i .. 4i+3, i.e. 1 KB contiguous, so a 16 KB state arrives in 16
-//     coalesced dwordx4 instructions.  State traffic is streamed with non-temporal loads and stores (each state
-//     is touched once per call);
+//   * wkv7_recurrent_kernel (every row shape): one wavefront per (sequence, head) pair at a time, at most two waves
+//     per SIMD; each wave walks pairs gw, gw + nwaves, ... and issues the next pair's state loads before working on
+//     the current pair, so state reads, the recurrence math and state writes of different pairs overlap.  Lane
+//     L = 16 g + c owns state rows k = 4 i + g (i = 0..15) and columns v = 4 c .. 4 c + 3 (the per-pair code of
+//     wkv7_token.h);
+//   * wkv7_decode_kernel (dense single-token rows without snapshots): half-pair units (32 columns of one pair), one
+//     wave per SIMD holding up to eight units, all of their loads issued before the first update, so that across the
+//     grid the state reads run ahead of the writes;
 //   * the per-token k-side vectors (decay, a, b, k, r) are computed by lane i for channel i and broadcast through
-//     a per-wave LDS slab, stored permuted (channel 4 i + g at slot 16 g + i) so each lane group reads its 16
-//     channels with four ds_read_b128; v is read per lane;
-//   * sa = a^T S and y = S^T r are lane-local sums over the lane's 16 rows followed by a two-step xor butterfly
-//     over the four row groups.  Every lane ends with bitwise identical sums (fp add is commutative), so all
-//     lanes hold the same update.  Updated rows are stored as soon as they are final.
+//     a per-wave LDS slab; v is read per lane; sa = a^T S and y = S^T r are lane-local sums over the lane's rows
+//     followed by an xor butterfly over the row groups.  Every lane ends with bitwise identical sums (fp add is
+//     commutative), so all lanes hold the same update.  State traffic is streamed with non-temporal loads and
+//     stores (each state is touched once per call).
 // Decode is HBM-bound: 16 KB state read + 16 KB written per pair, plus 896 B of operands and output.
 //
-// The per-token arithmetic is one fixed instruction sequence with explicit fmaf (the file is built with
+// The per-token arithmetic of a kernel is one fixed instruction sequence with explicit fmaf (the file is built with
 // -ffp-contract=off), so a snapshot taken after token t is bit-identical to a re-run over the first t+1 tokens.
+#include <algorithm>
+
 #include "wkv7_device.h"
 #include "wkv7_launch.h"
 #include "wkv7_token.h"
@@ -69,35 +69,185 @@ __global__ __launch_bounds__(64 * kWaves, kWavesPerSimd) void wkv7_recurrent_ker
     }
 }
 
-// Single-token rows (decode): one wavefront per SIMD; each wave issues the state loads of up to kGroup pairs
-// (w, w + nwaves, ...) before updating and storing the first of them, so that across the grid the state reads run
-// ahead of the state writes instead of mixing with them (a decode-shaped streaming probe: 64 MiB in place in
-// 22.9 us this way, 25.0 us with two pairs per wave and two waves per SIMD).
-constexpr int kGroup = 4;
+// Dense single-token rows (decode) without snapshots: half-pair units.  Unit u is pair u >> 1, columns
+// 32 (u & 1) .. + 31.  The recurrence is column-local (sa_j = a^T S[:, j] and y_j = r^T S[:, j] read column j only),
+// so the two halves of a pair are independent.  One wavefront per SIMD holds G units, u = w, w + nwaves, ..., so
+// 2 B H units spread evenly over the SIMDs (B = 64, H = 40: five per SIMD, where whole pairs would leave some SIMDs
+// three and some two), and all of a wave's state loads are in flight before its first update.  Measured per launch
+// at B = 64 (pool slots, HIP graph of 32 layers): H = 64 24.7 us (whole pairs, four per wave: 25.3), H = 40 16.2 us
+// (17.5), H = 8 5.3 us (5.9).
+// Lane L = 8 g + c owns rows k = 8 i + g (i = 0..7) and columns 32 half + 4 c .. + 3: 32 fp32 per unit.  Load
+// instruction i of a unit reads rows 8 i .. 8 i + 7, 128 contiguous bytes each.  sa and y are lane-local sums over
+// 8 rows and a three-step butterfly over the row groups (so their rounding differs from the 16-row sums of
+// wkv7_recurrent_kernel; the two kernels are never mixed within a call).
+// State rows go through buffer resources that cover the 16 KB state or nothing (num_records = 0: loads return zeros,
+// stores are dropped), so a zero initial state or an unstored final state needs no branch around the loads.
+constexpr int kDecodeMaxUnits = 8;
 
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t state_rsrc(const float* base, bool live) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, live ? HS2 * (int)sizeof(float) : 0,
+                                             0x00020000 /* raw 32-bit buffer, gfx9 family */);
+}
+
+constexpr int kCachePolicyNT = 2;  // buffer-instruction cache policy: non-temporal
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Sum over the eight row groups g = lane >> 3 (lanes L, L ^ 8, L ^ 16, ... ^ 56), without LDS: DPP row_ror:8 pairs
+// the halves of each 16-lane row, v_permlane16_swap pairs rows 0-1 and 2-3, v_permlane32_swap the wave's halves.
+// Every lane adds the same partial sums in the same order, so all lanes end with the same float.  (Cross-lane reads
+// need their source lanes active: every lane runs this.)
+__device__ __forceinline__ float butterfly8(float x) {
+    float r = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128 /* row_ror:8 */, 0xf, 0xf, false));
+    x += r;
+    const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    float e = __uint_as_float(pr[0]), o = __uint_as_float(pr[1]);  // the even row's value, the odd row's
+    x = e + o;
+    const auto hv = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    float lo = __uint_as_float(hv[0]), hi = __uint_as_float(hv[1]);  // rows 0-1, rows 2-3
+    return lo + hi;
+}
+
+template <int G>
 __global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Params p) {
-    __shared__ __attribute__((aligned(16))) float slab[kWaves][5 * HS];
+    __shared__ __attribute__((aligned(16))) float slab[kWaves][5 * HS];  // decay, a, b, k, r (permuted)
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int g = lane >> 4, c = lane & 15;
-    const uint32_t npairs = (uint32_t)p.num_seqs * (uint32_t)p.H;
+    const int g = lane >> 3, c = lane & 7;
+    const uint64_t nunits = 2ull * (uint64_t)p.num_seqs * (uint64_t)p.H;  // pair indices u >> 1 fit 31 bits
     const uint32_t nwaves = gridDim.x * kWaves;
-    for (uint32_t base = blockIdx.x * kWaves + wv; base < npairs; base += kGroup * nwaves) {
-        f4 S[kGroup][16];
-        TokenIn x[kGroup];
-        Pair q[kGroup];
+    float* const dvec = slab[wv];
+    float* const avec = dvec + HS;
+    float* const bvec = dvec + 2 * HS;
+    float* const kvec = dvec + 3 * HS;
+    float* const rvec = dvec + 4 * HS;
+    const int slot = (lane & 7) * 8 + (lane >> 3);  // LDS position of channel `lane` (channel 8 i + g at 8 g + i)
+    const int rowoff = g * HS + 4 * c;               // this lane's offset (floats) in rows 0 .. 7
+    auto lane64 = [](int64_t x, int j) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, j);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)x >> 32), j);
+        return (int64_t)(((uint64_t)hi << 32) | lo);
+    };
+
+    for (uint64_t base = blockIdx.x * kWaves + wv; base < nunits; base += (uint64_t)G * nwaves) {
+        // Unit j's state rows and token count, gathered in lane j (j < G).  Dense single-token rows: the row of
+        // sequence n is token n, its length min(1, max(n_keep[n], 0)).
+        const uint64_t mu = base + (uint64_t)lane * nwaves;
+        const bool mvalid = lane < G && mu < nunits;
+        const uint32_t mpr = (uint32_t)((mvalid ? mu : 0) >> 1);
+        const int mn = (int)(mpr / (uint32_t)p.H), mh = (int)(mpr % (uint32_t)p.H);
+        int64_t nk = 1, hi = mn, ti = mn;
+        uint8_t fr = 0;
+        if (p.n_keep) nk = p.n_keep[mn];
+        if (p.fresh) fr = p.fresh[mn];
+        if (p.h0_idx) hi = p.h0_idx[mn];
+        if (p.ht_idx) ti = p.ht_idx[mn];
+        // The token operands depend on no index: their loads go out while the index loads are in flight (units past
+        // nunits read token 0, which always exists).
+        TokenIn x[G];
+        int col0[G];
 #pragma unroll
-        for (int j = 0; j < kGroup; ++j) {
-            const uint32_t pj = base + j * nwaves;
-            q[j] = Pair{};
-            if (pj < npairs) {
-                q[j] = pair_of(p, pj);
-                prefetch_pair(p, q[j], lane, g, c, S[j], x[j]);
-            }
+        for (int j = 0; j < G; ++j) {
+            const uint64_t u = base + (uint64_t)j * nwaves;
+            const uint32_t pr = (uint32_t)((u < nunits ? u : 0) >> 1);
+            const int n = (int)(pr / (uint32_t)p.H), h = (int)(pr % (uint32_t)p.H);
+            col0[j] = 32 * (int)(u & 1);
+            const int64_t off = (int64_t)n * p.in_tok_stride + (int64_t)h * HS;
+            x[j].w = uniform_ptr(p.w + off)[lane];
+            x[j].a = uniform_ptr(p.a + off)[lane];
+            x[j].b = uniform_ptr(p.b + off)[lane];
+            x[j].k = uniform_ptr(p.k + off)[lane];
+            x[j].r = uniform_ptr(p.r + off)[lane];
+            x[j].v = uniform_ptr(reinterpret_cast<const uint2*>(p.v + off + col0[j]))[c];
         }
+        __builtin_amdgcn_sched_barrier(0);  // the index values are first used below, after the token loads
+        const int mlen = mvalid && nk >= 1 ? 1 : 0;
+        const int64_t msrc = (mvalid && p.h0 && !fr && hi >= 0 && hi < p.h0_rows) ? (hi * p.H + mh) * (int64_t)HS2 : -1;
+        const int64_t mdst = (mvalid && p.ht && ti >= 0 && ti < p.ht_rows) ? (ti * p.H + mh) * (int64_t)HS2 : -1;
+        f4 S[G][8];
+        int len[G];
+        __amdgpu_buffer_rsrc_t dst[G];
 #pragma unroll
-        for (int j = 0; j < kGroup; ++j)
-            if (base + j * nwaves < npairs) run_pair(p, q[j], lane, g, c, S[j], x[j], slab[wv]);
+        for (int j = 0; j < G; ++j) {
+            const int64_t s = lane64(msrc, j), d = lane64(mdst, j);
+            len[j] = __builtin_amdgcn_readlane(mlen, j);
+            // a row another launch owns (rec_max_len) is neither read nor written here
+            const bool mine = base + (uint64_t)j * nwaves < nunits && (p.rec_max_len < 0 || len[j] <= p.rec_max_len);
+            const __amdgpu_buffer_rsrc_t src = state_rsrc(s >= 0 ? p.h0 + s : nullptr, mine && s >= 0);
+            dst[j] = state_rsrc(d >= 0 ? p.ht + d : nullptr, mine && d >= 0);
+            if (!mine) len[j] = -1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                S[j][i] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(
+                            src, (int)((rowoff + 8 * i * HS + col0[j]) * sizeof(float)), 0, kCachePolicyNT));
+        }
+
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            if (len[j] < 0) continue;  // wave-uniform
+            if (len[j] == 1) {
+                const TokenIn cur = x[j];
+                dvec[slot] = decay(bf16_to_f32(cur.w));
+                avec[slot] = bf16_to_f32(cur.a);
+                bvec[slot] = bf16_to_f32(cur.b);
+                kvec[slot] = bf16_to_f32(cur.k);
+                rvec[slot] = bf16_to_f32(cur.r);
+                float vj[4];
+                bf16x2_to_f32(cur.v.x, vj[0], vj[1]);
+                bf16x2_to_f32(cur.v.y, vj[2], vj[3]);
+                wave_lds_sync();
+                // sa[q] = sum_k a_k S[k][q] over the old state (wkv7.py:75)
+                float sa[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i2 = 0; i2 < 2; ++i2) {
+                    const f4 av = *reinterpret_cast<const f4*>(avec + 8 * g + 4 * i2);
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) {
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) sa[q] = fmaf(av[ii], S[j][4 * i2 + ii][q], sa[q]);
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) sa[q] = butterfly8(sa[q]);
+                // S[k][q] = d_k S[k][q] + b_k sa[q] + k_k v_q;  y[q] = sum_k r_k S[k][q] (updated state, wkv7.py:75-77)
+                float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int i2 = 0; i2 < 2; ++i2) {
+                    const f4 dv = *reinterpret_cast<const f4*>(dvec + 8 * g + 4 * i2);
+                    const f4 bv = *reinterpret_cast<const f4*>(bvec + 8 * g + 4 * i2);
+                    const f4 kv = *reinterpret_cast<const f4*>(kvec + 8 * g + 4 * i2);
+                    const f4 rv = *reinterpret_cast<const f4*>(rvec + 8 * g + 4 * i2);
+#pragma unroll
+                    for (int ii = 0; ii < 4; ++ii) {
+                        const int i = 4 * i2 + ii;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            S[j][i][q] = fmaf(dv[ii], S[j][i][q], fmaf(bv[ii], sa[q], kv[ii] * vj[q]));
+                            y[q] = fmaf(rv[ii], S[j][i][q], y[q]);
+                        }
+                    }
+                }
+#pragma unroll
+                for (int q = 0; q < 4; ++q) y[q] = butterfly8(y[q]);
+                if (p.o && g == 0) {
+                    const uint32_t pr = (uint32_t)((base + (uint64_t)j * nwaves) >> 1);
+                    const int n = (int)(pr / (uint32_t)p.H), h = (int)(pr % (uint32_t)p.H);
+                    uint2 pk;
+                    pk.x = pack_bf16x2(y[0], y[1]);
+                    pk.y = pack_bf16x2(y[2], y[3]);
+                    uniform_ptr(reinterpret_cast<uint2*>(p.o + (int64_t)n * p.o_tok_stride + (int64_t)h * HS +
+                                                         col0[j]))[c] = pk;
+                }
+                wave_lds_sync();  // this unit's LDS reads precede the next unit's writes
+            }
+            // the updated state, or for a row with no tokens the initial state passed through (dropped when not
+            // stored)
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, S[j][i]), dst[j],
+                                                       (int)((rowoff + 8 * i * HS + col0[j]) * sizeof(float)), 0,
+                                                       kCachePolicyNT);
+        }
     }
 }
 
@@ -107,14 +257,24 @@ hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
     if (pairs == 0) return hipSuccess;
     const int cus = device_cu_count();
-    // Dense single-token rows (decode) with at least three pairs per SIMD: the grouped kernel.  Measured per launch
-    // (B x H pairs; this kernel / the double-buffered one): 3072 pairs 20.0 / 20.6 us, 4096 25.2 / 27.1, 6144
-    // 40.1 / 41.0, 8192 50.8 / 53.6; fewer pairs do not fill its groups (2560: 19.5 / 17.6 us).
     const int64_t simds = (int64_t)cus * 4;
-    if (p.T == 1 && !p.cu && pairs >= 3 * simds) {
-        const int64_t waves = simds;  // one wavefront per SIMD
-        const int64_t blocks = (waves + kWaves - 1) / kWaves;
-        hipLaunchKernelGGL(wkv7_decode_kernel, dim3((unsigned)blocks), dim3(64 * kWaves), 0, stream, p);
+    // Dense single-token rows without snapshots: the decode kernel, one wavefront per SIMD (or one per unit when
+    // there are fewer units than SIMDs), ceil(units / waves) units per wave up to eight, then further rounds.
+    if (p.T == 1 && !p.cu && !p.snap) {
+        const int64_t units = 2 * pairs;
+        const int64_t waves = std::min<int64_t>(units, simds);
+        const int G = (int)std::min<int64_t>((units + waves - 1) / waves, kDecodeMaxUnits);
+        const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves)), block(64 * kWaves);
+        switch (G) {
+            case 1: hipLaunchKernelGGL(wkv7_decode_kernel<1>, grid, block, 0, stream, p); break;
+            case 2: hipLaunchKernelGGL(wkv7_decode_kernel<2>, grid, block, 0, stream, p); break;
+            case 3: hipLaunchKernelGGL(wkv7_decode_kernel<3>, grid, block, 0, stream, p); break;
+            case 4: hipLaunchKernelGGL(wkv7_decode_kernel<4>, grid, block, 0, stream, p); break;
+            case 5: hipLaunchKernelGGL(wkv7_decode_kernel<5>, grid, block, 0, stream, p); break;
+            case 6: hipLaunchKernelGGL(wkv7_decode_kernel<6>, grid, block, 0, stream, p); break;
+            case 7: hipLaunchKernelGGL(wkv7_decode_kernel<7>, grid, block, 0, stream, p); break;
+            default: hipLaunchKernelGGL(wkv7_decode_kernel<8>, grid, block, 0, stream, p); break;
+        }
         return hipGetLastError();
     }
     const int64_t max_waves = (int64_t)cus * 4 * kWavesPerSimd;  // 4 SIMDs per CU
