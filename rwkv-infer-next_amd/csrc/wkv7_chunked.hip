@@ -155,29 +155,6 @@ __device__ __forceinline__ bf8 ld8_tr(const __bf16* M, int kb, int n0) {
     return __builtin_bit_cast(bf8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// mma with the Y operand stored contraction-major (Y[y][kappa] = Yt[kappa][y]).
-template <int TERMS>
-__device__ __forceinline__ f4 mma_ty(f4 acc, BM X, int x0, BM Yt, int y0) {
-    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        const int xo = (x0 + i) * PB + 32 * kb + 8 * q;
-        const bf8 xh = ld8(X.h + xo), yh = ld8_tr(Yt.h, kb, y0);
-        if constexpr (TERMS == 3) acc = mfma_bf16(xh, ld8_tr(Yt.l, kb, y0), acc);
-        if constexpr (TERMS >= 2) acc = mfma_bf16(ld8(X.l + xo), yh, acc);
-        acc = mfma_bf16(xh, yh, acc);
-    }
-    return acc;
-}
-
-// mma with the X operand stored contraction-major (X[x][kappa] = Xt[kappa][x]), one term.
-__device__ __forceinline__ f4 mma_tx1(f4 acc, BM Xt, int x0, BM Y, int y0) {
-    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) acc = mfma_bf16(ld8_tr(Xt.h, kb, x0), ld8(Y.h + (y0 + i) * PB + 32 * kb + 8 * q), acc);
-    return acc;
-}
-
 // Natural stores of a tile (element (x0 + 4q + v, y0 + i) at M[(y0 + i) * pitch + x0 + 4q + v]): 4 consecutive
 // elements per lane.
 __device__ __forceinline__ void st_hi(__bf16* M, int pitch, int x0, int y0, f4 acc) {
@@ -390,7 +367,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 //   4-5   Bk hi/lo                  6-7   Kk hi/lo
 //   8     Rq hi
 //   10-11 beta hi/lo -> G hi/lo     12 rho    13 sigma    14 E
-//   15    V (row-major, exact)
+//   15    V^T ([v][s], exact)
 // The products that contract over tokens (W = T A0, A = Bh^T W, F = Kh^T + Bh^T G, H = F V, O_intra = E V) read Aq,
 // Bk, Kk and V where they lie, through transposing LDS reads, and apply the per-channel decay factors that separate
 // A0, Bh, Kh from Aq, Bk, Kk (2^m, 2^{g_C - m}) to their fp32 results.
@@ -416,7 +393,7 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     const BM Rho{sm.slot[12], nullptr};
     const BM Sig{sm.slot[13], nullptr};
     const BM Em{sm.slot[14], nullptr};
-    const BM Vr{sm.slot[15], nullptr};
+    const BM Vt{sm.slot[15], nullptr};  // V transposed: [v][s]
     const BM Wm{sm.slot[0], sm.slot[1]}, Gm = Be;   // after step 7: W^T [k][t], G^T [s'][t]
     const BM Fm{sm.slot[2], sm.slot[3]};            // step 8 (Aq is dead after step 7)
     char* const rec = LDS_REC ? reinterpret_cast<char*>(sm.slot[kRecSlot]) : wsc + it.rec * (int64_t)kChunkBytes;
@@ -428,7 +405,8 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
     //         lanes 8 r + channel group, so a scan over lanes with stride 8), then across waves through the wave
     //         totals.  Every g below is (in-wave scan) + (sum of the earlier waves' totals, in wave order), so the
     //         previous row's g, the midpoint (row 31) and the chunk total (row 63) are the same floats wherever
-    //         they are formed.  V (row-major, exact) -> Vr.
+    //         they are formed.  V (exact) -> Vt transposed, [v][s]: both of its products (step 9) contract over
+    //         tokens, so stored this way they read it with ordinary row reads instead of transposing ones.
     float lam[8], gin[8], gprev[8];
     {
         const uint32_t ww[4] = {raw.w.x, raw.w.y, raw.w.z, raw.w.w};
@@ -445,7 +423,14 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             *reinterpret_cast<f4*>(&sm.bsum[wv][cb]) = f4{gin[0], gin[1], gin[2], gin[3]};
             *reinterpret_cast<f4*>(&sm.bsum[wv][cb + 4]) = f4{gin[4], gin[5], gin[6], gin[7]};
         }
-        *reinterpret_cast<uint4*>(Vr.h + row * PB + cb) = valid ? raw.v : make_uint4(0u, 0u, 0u, 0u);
+        const uint4 vv = valid ? raw.v : make_uint4(0u, 0u, 0u, 0u);
+        const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+        uint16_t* const vt = reinterpret_cast<uint16_t*>(Vt.h) + row;
+#pragma unroll
+        for (int e2 = 0; e2 < 4; ++e2) {
+            vt[(cb + 2 * e2) * PB] = (uint16_t)(vw[e2] & 0xffffu);
+            vt[(cb + 2 * e2 + 1) * PB] = (uint16_t)(vw[e2] >> 16);
+        }
     }
     __syncthreads();
     next.w = *reinterpret_cast<const uint4*>(p.w + noff);
@@ -812,9 +797,9 @@ __device__ __forceinline__ void prep_item(const Params& p, const Item& it, const
             const int x0 = 16 * bx, y0 = 16 * by;
             if (prod == 0) {
                 *reinterpret_cast<f4*>(rec + REC_HT + ((by * 4 + bx) * 64 + lane) * 16) =
-                    mma_ty<2>(zero4(), Fm, x0, Vr, y0);  // H^T[v][k]: v tile by, k tile bx
+                    mma<2>(zero4(), Fm, x0, Vt, y0, 0, 2);  // H^T[v][k]: v tile by, k tile bx
             } else {
-                const f4 acc = mma_tx1(zero4(), Vr, x0, Em, y0);  // E is zero for s' > t
+                const f4 acc = mma<1>(zero4(), Vt, x0, Em, y0, 0, 2);  // O[t][v] = sum_s' Vt[v][s'] E[t][s']
                 bf4 hv;
 #pragma unroll
                 for (int v = 0; v < 4; ++v) hv[v] = (__bf16)acc[v];
