@@ -23,9 +23,10 @@
 //     exact, assembled for two values with one v_perm_b32 against a register of 0x43 bytes.  One extra MFMA pair
 //     per chunk and M tile against a constant B of -160 removes the bias (128 + u - 160 = q) exactly;
 //   * the dequantised operand serves all MT M tiles; each chunk's fp32 tile is scaled by s (fp16) and accumulated.
-// Split-K partials are reduced inside the kernel: every split stores its tile (fp32, in register order) and
-// increments the tile's arrival counter; the split that arrives last sums the partials in split order (a fixed
-// order: the result does not depend on which split arrives last), stores the result and resets the counter to zero.
+// Split-K partials are reduced inside the kernel: every split stores its tile (fp32, in register order) and the
+// workgroup increments its tiles' arrival counters after one agent-scope release; the split that arrives last sums
+// the partials in split order (a fixed order: the result does not depend on which split arrives last), stores the
+// result and resets the counter to zero.
 // Rows m >= M and columns n >= N are clamped on load (they only feed outputs that are not stored).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -276,44 +277,34 @@ __device__ __forceinline__ void reduce_rows(const Args& p, const float* part, in
     }
 }
 
-// Stores the wavefront's tile, or (split-K) publishes it and, in the split that completes the tile last, reduces the
-// partials in split order and stores the result.
+// Split-K: this split's partial tile of `tile`, row-major [16 MT rows][128 columns] fp32 per (tile, split); rows >= M
+// are not written.
 template <int MT>
-__device__ __forceinline__ void finish_tile(const Args& p, int b, int mg, int strip, int split, int m0, int n0,
-                                            f4 (&acc)[MT][kTiles]) {
+__device__ __forceinline__ void publish_partials(const Args& p, int64_t tile, int split, int m0,
+                                                 const f4 (&acc)[MT][kTiles]) {
     const int lane = threadIdx.x & 63, q = lane >> 4;
-    if (p.split_k == 1) {
-        store_tile<MT>(p, b, m0, n0, acc);
-        return;
-    }
-    // Split-K: publish this split's tile, count arrivals; the last split to arrive reduces in split order.
-    // Partial tiles are row-major [16 MT rows][128 columns] fp32 per (tile, split); rows >= M are not written.
-    const int64_t tile = ((int64_t)b * p.m_groups + mg) * p.n_strips + strip;
     constexpr int kTileFloats = 16 * MT * kTileN;
-    float* const part = p.part + tile * p.split_k * kTileFloats;
     const int rows = min(16 * MT, p.M - m0);  // valid rows of this tile
-    {
-        float* const mine = part + (int64_t)split * kTileFloats + (lane & 15);
+    float* const mine = p.part + (tile * p.split_k + split) * kTileFloats + (lane & 15);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int t = 0; t < kTiles; ++t)
+        for (int t = 0; t < kTiles; ++t)
 #pragma unroll
-                for (int v = 0; v < 4; ++v) {
-                    const int r = 16 * mt + 4 * q + v;
-                    if (r < rows) coherent_store(mine + r * kTileN + 16 * t, acc[mt][t][v]);
-                }
-    }
-    // Hand-off (memory model, agent scope): every lane releases its partial stores with a release fence, then one
-    // lane counts the wavefront in; the last arriver's acquire fence makes all splits' partials visible before it
-    // reads them.  The partials themselves are agent-scope atomic stores, so the release finds little dirty data to
-    // write back.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-    uint32_t arrived = 0;
-    if (lane == 0) arrived = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    arrived = __builtin_amdgcn_readfirstlane(arrived);
-    if (arrived != (uint32_t)p.split_k - 1) return;
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            for (int v = 0; v < 4; ++v) {
+                const int r = 16 * mt + 4 * q + v;
+                if (r < rows) coherent_store(mine + r * kTileN + 16 * t, acc[mt][t][v]);
+            }
+}
+
+// Split-K, in the split that completed `tile`: sum the partials in split order (a fixed order: the result does not
+// depend on which split arrived last), store the result, reset the tile's counter.
+template <int MT>
+__device__ __forceinline__ void reduce_tile(const Args& p, int64_t tile, int b, int m0, int n0) {
+    const int lane = threadIdx.x & 63;
+    constexpr int kTileFloats = 16 * MT * kTileN;
+    const float* const part = p.part + tile * p.split_k * kTileFloats;
+    const int rows = min(16 * MT, p.M - m0);
     if (rows == 1)
         reduce_rows<1>(p, part, kTileFloats, 0, 1, b, m0, n0);
     else
@@ -479,16 +470,45 @@ __global__ __launch_bounds__(64 * kStrips * KS) void w6a16_kernel(const Args p) 
                 for (int t = 0; t < kTiles; ++t) r[(part - 1) * kPartStride + (mt * kTiles + t) * 64] = acc[mt][t];
         }
         __syncthreads();
-        if (part > 0) return;
+        if (part == 0) {
 #pragma unroll
-        for (int k = 1; k < KS; ++k)
+            for (int k = 1; k < KS; ++k)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int t = 0; t < kTiles; ++t) acc[mt][t] += r[(k - 1) * kPartStride + (mt * kTiles + t) * 64];
+                    for (int t = 0; t < kTiles; ++t) acc[mt][t] += r[(k - 1) * kPartStride + (mt * kTiles + t) * 64];
+        }
     }
-    if (!live) return;
-    finish_tile<MT>(p, b, mg, strip, split, m0, n0, acc);
+    const bool owner = live && part == 0;  // this wavefront finishes its strip's tile
+    if (p.split_k == 1) {  // uniform over the grid
+        if (owner) store_tile<MT>(p, b, m0, n0, acc);
+        return;
+    }
+    // Split-K hand-off, one agent-scope release per workgroup.  An agent-scope release fence writes back the XCD's L2
+    // (a walk whose cost grows with the number of releases, not with the dirty data): issued by every wavefront it
+    // cost 6 us per call at M = 1 and 42 us at M = 128.  Here every wavefront stores its strip's partials and waits
+    // for them; the workgroup barrier orders those stores before wavefront 0's release fence, which then counts all
+    // of the workgroup's strips in with relaxed atomic increments; if a strip completed, wavefront 0's acquire fence
+    // follows, and the second barrier orders it before the reducing wavefronts' reads.
+    const int64_t tile0 = ((int64_t)b * p.m_groups + mg) * p.n_strips;
+    if (owner) publish_partials<MT>(p, tile0 + strip, split, m0, acc);
+    __builtin_amdgcn_s_waitcnt(0);  // this wavefront's partial stores have completed
+    __shared__ uint32_t completed[kStrips];
+    __syncthreads();
+    if (wv == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        bool done = false;
+        if (lane < kStrips) {
+            const int st = blockIdx.x * kStrips + lane;
+            if (st < p.n_strips)
+                done = __hip_atomic_fetch_add(p.cnt + tile0 + st, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                       (uint32_t)p.split_k - 1;
+            completed[lane] = done ? 1u : 0u;
+        }
+        if (__builtin_amdgcn_ballot_w64(done)) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    __syncthreads();
+    if (owner && completed[sw]) reduce_tile<MT>(p, tile0 + strip, b, m0, n0);
 }
 
 // Dequantise the packed layout: one thread per (b, strip, chunk, lane) writes its 16 rows x 8 columns (rows
@@ -740,12 +760,13 @@ int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
     const int chunks = K / 64;
     const int64_t cus = w6::cu_count();
     // The smallest power of two that gives every CU a workgroup (every range keeps at least one chunk); then doubled
-    // while ranges keep at least 16 chunks and the launch stays within two workgroups per CU.  Measured at K = 4096,
-    // N = 16384: M = 128 is faster at split 4 than 2 (49.4 vs 51.1 us packed, 56.0 vs 61.4 planes), while M = 32 and
-    // M = 64 lose with ranges of eight chunks (split 8: 28.4 vs 24.3 us, 40.7 vs 33.9 us).
+    // while ranges keep at least 16 chunks and the launch stays within one workgroup per CU (each workgroup's
+    // split-K hand-off costs one agent-scope release).  Measured at K = 4096, N = 16384 (us, planes / packed): M = 128
+    // split 2 63.5 / 53.9, split 4 64.0 / 60.6; M = 64 split 4 41.7 / 37.1, split 8 51.3 / 49.1; M = 16 split 8
+    // 23.6 / 23.4, split 4 29.1 / 25.3.
     int sk = 1;
     while (groups * sk < cus && sk * 2 <= 64 && chunks / (sk * 2) >= 1) sk *= 2;
-    while (chunks / (sk * 2) >= 16 && groups * sk * 2 <= 2 * cus && sk * 2 <= 64) sk *= 2;
+    while (chunks / (sk * 2) >= 16 && groups * sk * 2 <= cus && sk * 2 <= 64) sk *= 2;
     return sk;
 }
 

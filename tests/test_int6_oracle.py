@@ -332,7 +332,7 @@ def test_split_rule():
     # without a GPU the CU count is taken as 256: K = 4096, N = 16384 has 32 groups of four 128-column strips
     assert lib.w6a16_plan_split(1, 1, 16384, 4096) == 8
     assert lib.w6a16_plan_split(1, 64, 16384, 4096) == 4        # two M groups of 32 rows: 64 groups
-    assert lib.w6a16_plan_split(1, 128, 16384, 4096) == 4       # 128 groups: 2 fills the chip, 4 keeps 16 chunks
+    assert lib.w6a16_plan_split(1, 128, 16384, 4096) == 2       # 128 groups: 2 fills the chip, one workgroup per CU
     assert lib.w6a16_plan_split(1, 1, 1024, 16384) == 64        # 2 groups, 256 chunks: capped at 64
     assert lib.w6a16_plan_split(1, 1, 4096, 16384) == 32
     assert I6.plan_int6(1, 4096, 4096, 1) == (lib.w6a16_plan_split(1, 1, 4096, 4096), False)
