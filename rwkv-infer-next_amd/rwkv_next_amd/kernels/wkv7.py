@@ -251,10 +251,10 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
     snapshots: optional (N, T, H, K, K) fp32 receiving the state after every token (dense only); rolling back to
     an accepted prefix of n tokens is `restore_snapshots_(pool, slots, snapshots, n)`.
     max_len: ragged calls may pass an upper bound on any row's length (sizes the workspace; 0 = sumT).
-    status: optional int32 device tensor (one element, see new_status) into which the kernels OR WKV7_STATUS_*
-    bits when a slot index lies outside the pool, cu_seqlens is malformed or an n_keep entry is negative; the
-    kernels skip such reads and writes and go on.  Nothing synchronises: read it with check_status when
-    convenient.
+    status: optional int32 device tensor (one element, see new_status): a check launched ahead of the recurrence
+    ORs WKV7_STATUS_* bits into it when a slot index lies outside the pool, cu_seqlens is malformed or an n_keep
+    entry is negative; the kernels skip such reads and writes and go on.  Nothing synchronises: read it with
+    check_status when convenient.
     Returns o like v (or None when store_o=False).  Runs as the registered op rwkv_next_amd::wkv7_pool_."""
     if r.dim() not in (3, 4):
         raise ValueError(f"operands must be (B, T, H*K) or (B, T, H, K), got {tuple(r.shape)}")
