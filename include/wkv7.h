@@ -49,6 +49,13 @@ extern "C" {
 #define WKV7_STATUS_HT_SLOT 2   /* an ht index outside [0, ht_rows): that final state was not stored */
 #define WKV7_STATUS_SEQLENS 4   /* cu_seqlens entries not non-decreasing within [0, total_tokens]: extents clamped */
 #define WKV7_STATUS_NKEEP 8     /* a negative n_keep entry: treated as 0 */
+#define WKV7_STATUS_DECAY 16    /* the call runs the chunked or chain kernels and some w exceeds WKV7_CHUNK_W_MAX:
+                                 * the chunked rows' results are not finite; run such calls with WKV7_ALGO_RECURRENT */
+
+/* Largest raw w the chunked form handles.  It references each chunk's decay factors to the chunk midpoint, so factors
+ * up to exp(32 exp(w)) must fit fp32: w <= 1.0 (32 e^1.0 = 87 < 88.7).  RWKV-7 produces w = -softplus(-x) - 0.5
+ * <= -0.5 (rwkv_next/model.py:142-144).  The token-serial kernels take any w. */
+#define WKV7_CHUNK_W_MAX 1.0f
 
 /* Algorithm selection (wkv7_args.algo). */
 #define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens, chunked otherwise; a
@@ -65,7 +72,7 @@ extern "C" {
  */
 typedef struct wkv7_args {
     /* operands, bf16: r, w (raw log-log decay), k, v, a, b -- rwkv_next/kernels/wkv7.py:39, 60-73 */
-    const uint16_t *r, *w, *k, *v, *a, *b;
+    const uint16_t *r, *w, *k, *v, *a, *b;  /* chunked / chain paths: w <= WKV7_CHUNK_W_MAX (see above) */
     int64_t in_tok_stride;        /* elements between consecutive tokens (multiple of 8) */
     uint16_t *o;                  /* output o, bf16, or NULL for STORE_O = False (wkv7.py:76-77, 93) */
     int64_t o_tok_stride;         /* elements between consecutive output tokens (multiple of 8) */

@@ -147,10 +147,13 @@ Params to_params(const wkv7_args* a) {
 // The optional status word: one pass over the call's sequences, launched before the recurrence only when the
 // caller passes a status pointer (so calls without one keep their single dispatch and pay nothing).  It checks
 // exactly what the kernels skip: an h0 slot outside [0, h0_rows) on a row that reads it (not fresh), an ht slot
-// outside [0, ht_rows), cu_seqlens entries that are not non-decreasing within [0, total_tokens], a negative n_keep.
-__global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, int32_t* __restrict__ status) {
+// outside [0, ht_rows), cu_seqlens entries that are not non-decreasing within [0, total_tokens], a negative n_keep;
+// and, when the call runs the chunked or chain kernels, every w against WKV7_CHUNK_W_MAX (16 bytes per thread).
+__global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, int32_t* __restrict__ status,
+                                                          bool check_w) {
     int bits = 0;
-    for (int n = blockIdx.x * blockDim.x + threadIdx.x; n < p.num_seqs; n += gridDim.x * blockDim.x) {
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nthr = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t n = tid; n < p.num_seqs; n += nthr) {
         if (p.h0 && !(p.fresh && p.fresh[n])) {
             const int64_t s = p.h0_idx ? p.h0_idx[n] : n;
             if (s < 0 || s >= p.h0_rows) bits |= WKV7_STATUS_H0_SLOT;
@@ -164,6 +167,20 @@ __global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, 
             if (b < 0 || e < b || e > p.total_tokens) bits |= WKV7_STATUS_SEQLENS;
         }
         if (p.n_keep && p.n_keep[n] < 0) bits |= WKV7_STATUS_NKEEP;
+    }
+    if (check_w) {
+        const int64_t per_tok = (int64_t)p.H * (wkv7::HS / 8);  // 16-byte pieces of one token's w
+        for (int64_t i = tid; i < p.total_tokens * per_tok; i += nthr) {
+            const int64_t t = i / per_tok, j = (i - t * per_tok) * 8;
+            const uint4 x = *reinterpret_cast<const uint4*>(p.w + t * p.in_tok_stride + j);
+            const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float lo, hi;
+                wkv7::bf16x2_to_f32(wd[e], lo, hi);
+                if (!(lo <= WKV7_CHUNK_W_MAX) || !(hi <= WKV7_CHUNK_W_MAX)) bits |= WKV7_STATUS_DECAY;  // NaN too
+            }
+        }
     }
     if (bits) __hip_atomic_fetch_or(status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -227,8 +244,10 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     hipStream_t s = static_cast<hipStream_t>(stream);
     Params p = to_params(args);
     if (args->status) {
-        const int blocks = (int)std::min<int64_t>(((int64_t)args->num_seqs + 255) / 256, 1024);
-        hipLaunchKernelGGL(wkv7_status_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, args->status);
+        const bool check_w = pl.run_chunked || pl.run_chain;
+        const int64_t work = std::max<int64_t>(args->num_seqs, check_w ? args->total_tokens * args->H * 8 : 0);
+        const int blocks = (int)std::min<int64_t>((work + 255) / 256, 1024);
+        hipLaunchKernelGGL(wkv7_status_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, args->status, check_w);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);
     }

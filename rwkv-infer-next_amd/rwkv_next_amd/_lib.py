@@ -24,6 +24,8 @@ WKV7_STATUS_H0_SLOT = 1
 WKV7_STATUS_HT_SLOT = 2
 WKV7_STATUS_SEQLENS = 4
 WKV7_STATUS_NKEEP = 8
+WKV7_STATUS_DECAY = 16
+WKV7_CHUNK_W_MAX = 1.0
 
 ALGO_AUTO = 0
 ALGO_RECURRENT = 1

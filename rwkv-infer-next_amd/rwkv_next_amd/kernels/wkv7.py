@@ -162,6 +162,8 @@ wkv7_fwd_reference_name = _register_reference_name()
 def wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True, *, algo: int = _lib.ALGO_AUTO):
     """o, final_state = recurrence over (B, T, H*K) inputs from `state` (B|N, H, K, K) fp32 or None.
     w is RAW (decay = exp(-exp(w))).  cu_seqlens (N+1,) int32: packed varlen (B must be 1).
+    Rows longer than 32 tokens run the chunked form, which needs w <= 1.0 (RWKV-7's w = -softplus(-x) - 0.5 is
+    always below -0.5); larger w needs algo=ALGO_RECURRENT (the status word of wkv7_pool_ reports it).
     Mirrors rwkv_next/kernels/wkv7.py:126-138."""
     if cu_seqlens is None:
         if algo == _lib.ALGO_AUTO:
@@ -253,8 +255,9 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
     max_len: ragged calls may pass an upper bound on any row's length (sizes the workspace; 0 = sumT).
     status: optional int32 device tensor (one element, see new_status): a check launched ahead of the recurrence
     ORs WKV7_STATUS_* bits into it when a slot index lies outside the pool, cu_seqlens is malformed or an n_keep
-    entry is negative; the kernels skip such reads and writes and go on.  Nothing synchronises: read it with
-    check_status when convenient.
+    entry is negative (the kernels skip such reads and writes and go on), or when a call that runs the chunked
+    kernels has w above 1.0 (their results are not finite: the chunked form needs w <= 1.0, which RWKV-7's
+    w = -softplus(-x) - 0.5 always meets).  Nothing synchronises: read it with check_status when convenient.
     Returns o like v (or None when store_o=False).  Runs as the registered op rwkv_next_amd::wkv7_pool_."""
     if r.dim() not in (3, 4):
         raise ValueError(f"operands must be (B, T, H*K) or (B, T, H, K), got {tuple(r.shape)}")
@@ -300,7 +303,9 @@ def new_status(device) -> torch.Tensor:
 STATUS_REASONS = {_lib.WKV7_STATUS_H0_SLOT: "initial-state slot index outside the pool",
                   _lib.WKV7_STATUS_HT_SLOT: "final-state slot index outside the pool",
                   _lib.WKV7_STATUS_SEQLENS: "cu_seqlens not non-decreasing within [0, total tokens]",
-                  _lib.WKV7_STATUS_NKEEP: "negative n_keep"}
+                  _lib.WKV7_STATUS_NKEEP: "negative n_keep",
+                  _lib.WKV7_STATUS_DECAY: f"w above {_lib.WKV7_CHUNK_W_MAX} on a call that runs the chunked kernels "
+                                          "(their results are not finite): run it with algo=ALGO_RECURRENT"}
 
 
 def check_status(status: torch.Tensor) -> None:

@@ -119,3 +119,56 @@ def test_chunk_factors_stay_bounded_for_model_decays():
     g = np.cumsum(-np.exp(w), axis=0)
     m = g[31]
     assert np.max(np.abs(g - m)) < 20.0
+
+
+def chunk_prep_fp32(r, w, k, v, a, b):
+    """chunk_prep in float32 (the kernels' range: bf16 hi/lo splits carry fp32's exponent range); the triangular
+    solve stays float64 (only the range of the midpoint-referenced factors is at stake here)."""
+    f = np.float32
+    L = r.shape[0]
+    pad = lambda x: np.vstack([x.astype(f), np.zeros((C - L, x.shape[1]), f)])
+    r, k, v, a, b = (pad(x) for x in (r, k, v, a, b))
+    lam = pad(-np.exp(w.astype(f)))
+    g = np.cumsum(lam, axis=0, dtype=f)
+    g_ex = np.vstack([np.zeros((1, g.shape[1]), f), g[:-1]])
+    m, gL = g[31], g[-1]
+    with np.errstate(over="ignore", invalid="ignore"):
+        Aq, Rq = a * np.exp(g_ex - m), r * np.exp(g - m)
+        Bk, Kk = b * np.exp(m - g), k * np.exp(m - g)
+        alpha, beta = np.tril(Aq @ Bk.T, -1), np.tril(Aq @ Kk.T, -1)
+        rho, sigma = np.tril(Rq @ Bk.T), np.tril(Rq @ Kk.T)
+        A0, R0 = Aq * np.exp(m), Rq * np.exp(m)
+        Bh, Kh = Bk * np.exp(gL - m), Kk * np.exp(gL - m)
+        X = block_forward_substitution(alpha.astype(np.float64), np.hstack([A0, beta]).astype(np.float64)).astype(f)
+        W, G = X[:, :64], X[:, 64:]
+        Q, E = R0 + rho @ W, sigma + rho @ G
+        A = np.diag(np.exp(gL)) + Bh.T @ W
+        F = Bh.T @ G + Kh.T
+    return A, F @ v, Q, E @ v
+
+
+def test_chunked_form_range_of_w():
+    """WKV7_CHUNK_W_MAX = 1.0: with every w at the bound the fp32 chunk factors (up to exp(32 e^w) = e^87) stay finite
+    and the chunked form matches the fp64 recurrence; just above it (w = 1.05: e^91 > FLT_MAX) they overflow."""
+    import rwkv_next_amd.synth as synth
+    from rwkv_next_amd import _lib
+    assert 32 * np.exp(_lib.WKV7_CHUNK_W_MAX) < np.log(np.finfo(np.float32).max) < 32 * np.exp(1.05)
+    T_ = 128
+    ops = synth.operands_np((1, T_, 1, 64), seed=7)
+    ins = [ops[n] for n in synth.OPERAND_NAMES]
+    s0 = synth.state_np((1, 1, 64, 64), seed=8, std=0.3)
+    for wv, ok in ((-0.5, True), (0.0, True), (0.5, True), (_lib.WKV7_CHUNK_W_MAX, True), (1.05, False)):
+        x = list(ins)
+        x[1] = np.full_like(ins[1], wv)
+        o_ref, S_ref, _ = wkv7_ref(*x, s0)
+        S = s0[0, 0].astype(np.float32)
+        o = np.zeros((T_, 64), np.float32)
+        for c0 in range(0, T_, C):
+            sl = slice(c0, c0 + C)
+            A, Hm, Q, Oi = chunk_prep_fp32(*(t[0, sl, 0] for t in x))
+            o[sl] = Q @ S + Oi
+            S = A @ S + Hm
+        finite = bool(np.isfinite(S).all() and np.isfinite(o).all())
+        assert finite == ok, wv
+        if ok:
+            assert rel_max(S, S_ref[0, 0]) < 1e-5 and rel_max(o, o_ref[0, :, 0]) < 1e-5, wv

@@ -215,3 +215,39 @@ def test_status_word_reports_bad_slots_without_fault(dev, K):
                  status=status)
     torch.cuda.synchronize()
     assert int(status.item()) & _lib.WKV7_STATUS_SEQLENS
+
+
+def test_status_word_reports_w_outside_the_chunked_range(dev, K):
+    """A dense T = 100 call runs the chunked kernels: with the model's w (<= -0.5) the word stays zero; one w above
+    WKV7_CHUNK_W_MAX sets WKV7_STATUS_DECAY (every kernel still exits normally); a token-serial call with the same w
+    does not, since those kernels take any w, and its rows match the oracle."""
+    from oracle import wkv7_ref
+    import rwkv_next_amd.synth as synth
+    from rwkv_next_amd import _lib
+    B, T, S_slots = 2, 100, 4
+    say("status word, w range")
+    ops = operands(B, T, H8, seed=73)
+    pool0 = synth.state_np((S_slots, H8, 64, 64), seed=74)
+    slots = torch.tensor([3, 0], device=dev)
+    status = K.new_status(dev)
+    x = to_dev(ops, dev)
+    K.wkv7_pool_(*x, torch.from_numpy(pool0).to(dev), slots, H8, 64, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    w_hi = x[1].clone()
+    w_hi[1, 57, 5] = 1.25                                            # one channel of one token of row 1
+    xs = [x[0], w_hi] + list(x[2:])
+    K.wkv7_pool_(*xs, torch.from_numpy(pool0).to(dev), slots, H8, 64, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == _lib.WKV7_STATUS_DECAY
+    with pytest.raises(ValueError, match="ALGO_RECURRENT"):
+        K.check_status(status)
+    status.zero_()
+    pool = torch.from_numpy(pool0).to(dev)
+    o = K.wkv7_pool_(*xs, pool, slots, H8, 64, algo=_lib.ALGO_RECURRENT, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    npo = np_list(ops)
+    npo[1] = as_np(w_hi).reshape(npo[1].shape).astype(npo[1].dtype)
+    o_ref, S_ref, _ = wkv7_ref(*npo, pool0[[3, 0]])
+    check(o, o_ref, as_np(pool)[[3, 0]], S_ref)
