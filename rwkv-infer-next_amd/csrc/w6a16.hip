@@ -722,16 +722,22 @@ int validate(const w6a16_args* a) {
     return WKV7_OK;
 }
 
-constexpr int kParts = 1;  // wavefronts per strip (KS); 2 was measured: no gain at M = 1, slower at M = 64
+// Wavefronts per strip (KS): two for the two-tile (M > 32) kernels -- each strip's chunk range split in two inside the
+// workgroup and summed through LDS, so twice the waves stream the weight without more split-K hand-offs.  Measured at
+// K = 4096, N = 16384 (us, planes / packed, at each M's best split): M = 64 41.9 / 37.2 -> 38.0 / 35.5, M = 128
+// 63.4 / 54.1 -> 52.5 / 49.1, M = 256 95.8 / 81.9 -> 71.7 / 63.3.  One wavefront per strip for M <= 32 (two: no gain).
+template <int MT>
+constexpr int parts_for() { return MT >= 2 ? 2 : 1; }
 
 template <int MT, int D>
 void launch(const Args& p, const Layout& l, bool packed, hipStream_t s) {
+    constexpr int KS = parts_for<MT>();
     const dim3 grid((l.n_strips + kStrips - 1) / kStrips, p.split_k, p.B * l.m_groups);
-    const dim3 block(64 * kStrips * kParts);
+    const dim3 block(64 * kStrips * KS);
     if (packed)
-        hipLaunchKernelGGL((w6a16_kernel<MT, D, kParts, true>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((w6a16_kernel<MT, D, KS, true>), grid, block, 0, s, p);
     else
-        hipLaunchKernelGGL((w6a16_kernel<MT, D, kParts, false>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((w6a16_kernel<MT, D, KS, false>), grid, block, 0, s, p);
 }
 
 }  // namespace

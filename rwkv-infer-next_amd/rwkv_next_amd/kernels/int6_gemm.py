@@ -38,7 +38,7 @@ from .. import _lib
 CHUNK = 64
 QMIN, QMAX = -32, 31
 # Largest M that the W6A16 kernel serves; larger M dequantises once and runs the library GEMM.
-MAX_M = int(os.environ.get("RWKV_INT6_MAX_M", "128"))
+MAX_M = int(os.environ.get("RWKV_INT6_MAX_M", "256"))
 _RATIOS = (1.0, 0.97, 0.94, 0.91, 0.88, 0.85)
 
 
