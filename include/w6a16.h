@@ -41,9 +41,10 @@ typedef struct w6a16_args {
     int64_t scales_batch_stride;       /* elements */
     void *out;                         /* [B][M][N] bf16 or fp32 (out_dtype) */
     int64_t out_batch_stride, out_row_stride;      /* elements */
-    void *workspace;                   /* split_k > 1: w6a16_workspace_size bytes, 256-byte aligned, see below */
+    void *workspace;                   /* split_k > 1 or M > 32: w6a16_workspace_size bytes, 256-byte aligned */
     size_t workspace_bytes;
-    int32_t B, M, N, K;                /* K % 64 == 0, N % 16 == 0, B * ceil(M / 16) <= 65535 */
+    int32_t B, M, N, K;                /* K % 64 == 0, N % 16 == 0; M <= 32: B * ceil(M / 16) <= 65535,
+                                          M > 32: B <= 65535 */
     int32_t group_k;                   /* % 64 == 0, divides K */
     int32_t split_k;                   /* 1 .. 256: K is cut into split_k ranges of 64-row chunks */
     int32_t out_dtype;                 /* W6A16_OUT_BF16 or W6A16_OUT_F32 */
@@ -53,9 +54,10 @@ typedef struct w6a16_args {
 /* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
 size_t w6a16_args_size(void);
 
-/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1): a fixed 1 MiB region of u32 arrival counters (one
- * per output tile; a call with more than 262144 tiles is refused with WKV7_ERR_SHAPE), then fp32 partial tiles.  The
- * split that completes a tile last reduces it inside the kernel, so no second launch is made.  Contract: the counter
+/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1 and M <= 32): a fixed 1 MiB region of u32 arrival
+ * counters (one per output tile; a call with more than 262144 tiles is refused with WKV7_ERR_SHAPE), then fp32
+ * partial tiles (split_k > 1), then, for M > 32, the per-row sums of A that a small first launch computes and the
+ * GEMM kernel reads.  The split that completes a tile last reduces it inside the kernel.  Contract: the counter
  * region (the first 1 MiB) must be zero before the workspace's first use; every completed call leaves it zero again
  * and never writes partials into it, so one workspace serves any number of calls of any shapes issued one after
  * another (stream order).  Calls that can run at the same time (different streams) need different workspaces. */

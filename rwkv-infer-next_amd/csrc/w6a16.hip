@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <type_traits>
+#include <utility>
 
 #include "w6a16.h"
 #include "wkv7_launch.h"
@@ -70,7 +71,9 @@ struct Args {
     int64_t so_b, so_m;
     uint32_t* cnt;  // split_k > 1: arrival counters, one per (batch, M group, column strip); zero between calls
     float* part;    // split_k > 1: partial tiles [tile][split][16 MT rows][128 columns]
+    float* rsum;    // wide kernel: row-sum bias per chain of 64 CG k, [batch][chain][mpad]
     int32_t B, M, N, K, group_k, split_k, out_dtype, m_groups, n_strips, chunks_per_split;
+    int32_t mpad, chain_k, nchains, chains_per_split;  // wide kernel
 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -511,6 +514,524 @@ __global__ __launch_bounds__(64 * kStrips * KS) void w6a16_kernel(const Args p) 
     if (owner && completed[sw]) reduce_tile<MT>(p, tile0 + strip, b, m0, n0);
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Wide kernel (M > 32).  A workgroup of 4 KP wavefronts covers one 128-column strip for 16 MTW rows of A: wavefront
+// w owns column tiles 2 (w & 3) and 2 (w & 3) + 1 for all the workgroup's rows, over K part w >> 2 (the workgroup's
+// chunk range cut into KP contiguous parts, summed through LDS at the end).  Each dequantised weight operand serves
+// MTW M tiles, each A operand two column tiles.  The M groups of one strip are 8 blocks apart in dispatch order (the
+// same XCD, one after the other), so the weight bytes come from HBM once per strip and hit that XCD's L2 for the
+// other groups.
+//   * A's chunk of every part ([16 MTW rows][64 k] bf16) is staged in LDS, double-buffered, one workgroup barrier
+//     per step.  16-byte piece j of row r sits at slot 8 r + (j ^ ((r >> 1) & 7)): the 16 lanes of an MFMA operand
+//     read (rows r0 .. r0 + 15, one j) touch all 64 banks once, and so do the writes.
+//   * Chains: the products of CG consecutive chunks (CG = 2 when the quantisation group holds two chunks, else 1)
+//     accumulate in one MFMA chain whose accumulator starts at the chain's bias -160 sum_k A[m][k] (the row sums of
+//     w6a16_rowsum_kernel, computed once per call instead of once per strip), then are scaled once: acc += s * chain.
+//   * Packed weights are loaded straight into registers (16 + 8 bytes per lane and chunk: the lane's records of its
+//     two tiles), D steps ahead; planes are staged in LDS with A (48 rows x 128 columns) and read back transposed as
+//     in the narrow kernel.
+// Split-K (when used): one partial tile per (tile, split) in the accumulators' register layout, one release per
+// workgroup; the last split adds the others to its own registers in split order.
+constexpr int kCachePolicySC1 = 16;  // buffer instructions' cache-policy bit sc1: device-scope write-through
+constexpr int kRowSumBias = -160;    // 128 + u - 160 = q
+constexpr int kPlaneBytes = kBuf;    // planes: the chunk's 48 plane rows and 128 scales, as in the narrow kernel
+
+template <int MTW>
+constexpr int part_a_bytes() { return 16 * MTW * 128; }
+
+// One K part's share of an LDS stage: A slots, the chain's row sums (16 MTW fp32), then (planes) the plane rows.
+template <int MTW, bool PACKED>
+constexpr int part_bytes() { return part_a_bytes<MTW>() + 16 * MTW * 4 + (PACKED ? 0 : kPlaneBytes); }
+
+__device__ __forceinline__ int a_slot(int r, int j) { return 8 * r + (j ^ ((r >> 1) & 7)); }
+
+// f(std::integral_constant<int, 0>{}), .., f(std::integral_constant<int, N - 1>{})
+template <typename F, int... J>
+__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll(F&& f) { unroll_seq(f, std::make_integer_sequence<int, N>{}); }
+
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+
+// (1, 1) as a bf16 pair held in a register (an empty asm keeps the compiler from folding the pair into an inline
+// constant, which the packed bf16 dot product would read differently).
+__device__ __forceinline__ bf2 ones_bf16x2() {
+    uint32_t bits = 0x3F803F80u;
+    asm("" : "+v"(bits));
+    return __builtin_bit_cast(bf2, bits);
+}
+
+__device__ __forceinline__ float sum8_bf16(const u4 v, bf2 one) {
+    float x = 0.f;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+        // the element is copied out first: bit-casting a vector element in place (v[d]) compiled to a read of
+        // element 0 for every d
+        const uint32_t word = v[d];
+        x = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, word), one, x, false);
+    }
+    return x;
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float x) {  // x + x of the lane DPP control CTRL selects (all lanes active)
+    return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+
+// Row sums of A per chain of 64 CG k: rsum[b][chain][m] = -160 sum A[b][m][chain 64 CG .. + 64 CG - 1], zero for
+// rows M <= m < mpad.  One wavefront per (row, 512-element segment of K; 8 bf16 per lane, coalesced); the 8 CG lanes
+// of a chain add their sums with DPP in a fixed order.
+__global__ __launch_bounds__(256) void w6a16_rowsum_kernel(const Args p) {
+    const int lane = threadIdx.x & 63;
+    const int m = blockIdx.x * 4 + (threadIdx.x >> 6), k = blockIdx.y * 512 + 8 * lane, b = blockIdx.z;
+    if (m >= p.mpad) return;  // uniform over the wavefront
+    const int lanes_per_chain = 8 * p.chain_k / 64;  // 8 or 16
+    const uint16_t* const row = p.a + (int64_t)b * p.sa_b + (int64_t)min(m, p.M - 1) * p.sa_m;
+    // K is a multiple of 64 CG: a chain's lanes are all inside K or all past it
+    float x = (m < p.M && k < p.K) ? sum8_bf16(*reinterpret_cast<const u4*>(row + k), ones_bf16x2()) : 0.f;
+    x = dpp_add<0xB1>(x);   // lanes ^ 1
+    x = dpp_add<0x4E>(x);   // lanes ^ 2: each lane holds its quad's sum
+    x = dpp_add<0x141>(x);  // half-row mirror: lane 7 - l of the 8-lane group, in the other quad
+    if (lanes_per_chain == 16) x = dpp_add<0x140>(x);  // row mirror: lane 15 - l, in the other half
+    if ((lane & (lanes_per_chain - 1)) == 0 && k < p.K)
+        p.rsum[((int64_t)b * p.nchains + k / p.chain_k) * p.mpad + m] = (float)kRowSumBias * x;
+}
+
+// The chunk schedule of one workgroup: its split's range of chains, cut into KP contiguous parts.
+struct Sched {
+    int cg, c_s, per, n_s, nchunks;  // chunks per chain, first chunk of the split, chunks per part, split's chunks
+    __device__ __forceinline__ int part_n(int kq) const { return max(0, min(per, n_s - kq * per)); }
+    // chunk of part kq at step s, clamped into the part and the matrix (steps past a part's end re-load its last
+    // chunk; a part with no chunk loads a valid one)
+    __device__ __forceinline__ int chunk(int kq, int s) const {
+        return min(c_s + kq * per + max(0, min(s, part_n(kq) - 1)), nchunks - 1);
+    }
+};
+
+// What one thread loads per step into the LDS stage: MTW / 2 pieces of A, four row sums (threads 0 .. 4 MTW - 1
+// of each part's 256) and (planes) 16 bytes of a lo-plane row, 16 bytes of a hi-plane row (threads 0..127 of each
+// part's 256) or two scales (threads 128..191).
+template <int MTW, bool PACKED>
+struct WideLds {
+    u4 a[MTW / 2];
+    u4 rs;
+    u4 pl[2];
+    uint32_t sc;
+};
+
+// The packed weights of one chunk in one lane's registers: R[4 cp .. 4 cp + 3] (lo plane bytes of tiles 2 cp and
+// 2 cp + 1), R[16 + 2 cp], R[17 + 2 cp] (their top bits) and the two tiles' scales of column i.
+struct WideW {
+    u4 lo;
+    uint2 hd;
+    uint32_t sc;
+};
+
+// Buffer resources and per-lane offsets of the wide kernel's loads, fixed for the whole call: inside the loop only
+// the chunk-dependent part changes, and it is the same for a whole wavefront (its K part's chunk), so it goes into the
+// instructions' scalar offset and the loop's address arithmetic runs on the scalar unit.
+// A raw buffer over [base, base + bytes) (capped at 2 GB; the validation keeps every range the kernel addresses below
+// it).  The base and size are passed through readfirstlane so that the descriptor is provably wave-uniform: a
+// descriptor the compiler cannot prove uniform is used through a per-lane loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(uint64_t base, int64_t bytes) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+    const int n = __builtin_amdgcn_readfirstlane(bytes < 0x7FFFFFFF ? (int)bytes : 0x7FFFFFFF);
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0, n,
+                                             0x00020000 /* raw 32-bit buffer, gfx9 family */);
+}
+
+// A wave-uniform scalar offset (held in an SGPR, as buffer instructions need it).
+__device__ __forceinline__ int soff(int x) { return __builtin_amdgcn_readfirstlane(x); }
+
+template <int MTW>
+struct WideSrc {
+    uint64_t a, rs, lo, hi, sc;                 // buffer bases (wave-uniform)
+    int64_t na, nrs, nlo, nhi, nsc;             // and sizes in bytes
+    uint32_t va[MTW / 2], vrs, vlo, vhi, vsc;  // per-lane byte offsets
+    int kq[MTW / 2], kq_t, kp;                 // wave-uniform K parts: of each A piece, of the row-sum / plane loads,
+                                               // of this wavefront
+};
+
+template <int MTW, int KP, bool PACKED>
+__device__ __forceinline__ void wide_src(const Args& p, int b, int m0, int strip, WideSrc<MTW>& x) {
+    const int tid = threadIdx.x, lane = tid & 63, t = tid & 255, i = lane & 15, cp = (tid >> 6) & 3;
+    const int n0 = strip * kTileN;
+    x.a = reinterpret_cast<uint64_t>(p.a + (int64_t)b * p.sa_b);
+    x.na = ((int64_t)(p.M - 1) * p.sa_m + p.K) * 2;
+#pragma unroll
+    for (int e = 0; e < MTW / 2; ++e) {
+        const int piece = tid + 256 * KP * e, w = piece % (128 * MTW);
+        x.kq[e] = __builtin_amdgcn_readfirstlane(piece / (128 * MTW));  // one K part per wavefront and e
+        const int m = min(m0 + (w >> 3), p.M - 1);
+        x.va[e] = (uint32_t)(((int64_t)m * p.sa_m + 8 * (w & 7)) * 2);
+    }
+    x.kq_t = __builtin_amdgcn_readfirstlane(tid >> 8);
+    x.kp = __builtin_amdgcn_readfirstlane(tid >> 8);
+    x.rs = reinterpret_cast<uint64_t>(p.rsum + (int64_t)b * p.nchains * p.mpad);
+    x.nrs = (int64_t)p.nchains * p.mpad * 4;
+    x.vrs = (m0 + 4 * min(t, 4 * MTW - 1)) * 4;
+    if constexpr (PACKED) {
+        const int nchunks = p.K / 64, groups = p.K / p.group_k;
+        x.lo = reinterpret_cast<uint64_t>(p.lo + (int64_t)b * p.sl_b + (int64_t)strip * nchunks * kPackBytes);
+        x.nlo = (int64_t)nchunks * kPackBytes;
+        x.vlo = 16 * lane + 1024 * cp;
+        x.vhi = 4096 + 1024 * (cp >> 1) + 8 * (cp & 1) + 16 * lane;
+        x.sc = reinterpret_cast<uint64_t>(p.sc + (int64_t)b * p.ss_b + (int64_t)strip * groups * kTileN);
+        x.nsc = (int64_t)groups * kTileN * 2;
+        x.vsc = (8 * i + 2 * cp) * 2;
+    } else {
+        const int row = t >> 3, n = min(n0 + 16 * (t & 7), p.N - 16);  // lo row 0..31; hi row (row & 15)
+        x.lo = reinterpret_cast<uint64_t>(p.lo + (int64_t)b * p.sl_b);
+        x.nlo = (int64_t)(p.K / 2) * p.N;
+        x.vlo = row * p.N + n;
+        x.hi = reinterpret_cast<uint64_t>(p.hi + (int64_t)b * p.sh_b);
+        x.nhi = (int64_t)(p.K / 4) * p.N;
+        x.vhi = (row & 15) * p.N + n;
+        x.sc = reinterpret_cast<uint64_t>(p.sc + (int64_t)b * p.ss_b);
+        x.nsc = (int64_t)(p.K / p.group_k) * p.N * 2;
+        x.vsc = min(n0 + 2 * (t & 63), p.N - 2) * 2;
+    }
+}
+
+template <int MTW, int KP, bool PACKED>
+__device__ __forceinline__ void wide_load_lds(const Args& p, const Sched& S, const WideSrc<MTW>& src, int s,
+                                              WideLds<MTW, PACKED>& x) {
+#pragma unroll
+    for (int e = 0; e < MTW / 2; ++e)
+        x.a[e] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src.a, src.na), src.va[e], soff(S.chunk(src.kq[e], s) * 128), 0);
+    const int c = soff(S.chunk(src.kq_t, s));
+    x.rs = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src.rs, src.nrs), src.vrs, soff((c / S.cg) * p.mpad * 4), 0);
+    if constexpr (!PACKED) {
+        x.pl[0] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src.lo, src.nlo), src.vlo, soff(c * 32 * p.N), 0);
+        x.pl[1] = __builtin_amdgcn_raw_buffer_load_b128(rsrc(src.hi, src.nhi), src.vhi, soff(c * 16 * p.N), 0);
+        x.sc = __builtin_amdgcn_raw_buffer_load_b32(rsrc(src.sc, src.nsc), src.vsc, soff((c * 64 / p.group_k) * p.N * 2), 0);
+    }
+}
+
+template <int MTW, int KP, bool PACKED>
+__device__ __forceinline__ void wide_store_lds(const WideLds<MTW, PACKED>& x, uint8_t* st) {
+    constexpr int PB = part_bytes<MTW, PACKED>();
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int e = 0; e < MTW / 2; ++e) {
+        const int piece = tid + 256 * KP * e, kq = piece / (128 * MTW), w = piece % (128 * MTW);
+        *reinterpret_cast<u4*>(st + kq * PB + 16 * a_slot(w >> 3, w & 7)) = x.a[e];
+    }
+    const int kq = tid >> 8, t = tid & 255;
+    uint8_t* const ps = st + kq * PB;
+    if (t < 4 * MTW) *reinterpret_cast<u4*>(ps + part_a_bytes<MTW>() + 16 * t) = x.rs;
+    if constexpr (!PACKED) {
+        uint8_t* const pl = ps + part_a_bytes<MTW>() + 16 * MTW * 4;
+        uint8_t* dst = pl + (t >> 3) * kPitch + 16 * (t & 7);
+        *reinterpret_cast<uint2*>(dst) = uint2{x.pl[0][0], x.pl[0][1]};
+        *reinterpret_cast<uint2*>(dst + 8) = uint2{x.pl[0][2], x.pl[0][3]};
+        if (t < 128) {
+            dst += 32 * kPitch;
+            *reinterpret_cast<uint2*>(dst) = uint2{x.pl[1][0], x.pl[1][1]};
+            *reinterpret_cast<uint2*>(dst + 8) = uint2{x.pl[1][2], x.pl[1][3]};
+        } else if (t < 192) {
+            *reinterpret_cast<uint32_t*>(pl + kScaleOff + 4 * (t & 63)) = x.sc;
+        }
+    }
+}
+
+template <int MTW>
+__device__ __forceinline__ void wide_load_w(const Args& p, const WideSrc<MTW>& src, int c, WideW& w) {
+    const __amdgpu_buffer_rsrc_t lo = rsrc(src.lo, src.nlo);
+    const int off = soff(c * kPackBytes);
+    w.lo = __builtin_amdgcn_raw_buffer_load_b128(lo, src.vlo, off, 0);
+    w.hd = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(lo, src.vhi, off, 0));
+    w.sc = __builtin_amdgcn_raw_buffer_load_b32(rsrc(src.sc, src.nsc), src.vsc, soff((c * 64 / p.group_k) * kTileN * 2), 0);
+}
+
+// x s + a per element, written as a whole vector (stores into the components of an accumulator passed by reference
+// kept the accumulators in scratch memory)
+__device__ __forceinline__ f4 fma4(const f4 x, float s, const f4 a) {
+    return f4{fmaf(x[0], s, a[0]), fmaf(x[1], s, a[1]), fmaf(x[2], s, a[2]), fmaf(x[3], s, a[3])};
+}
+
+// Dequantise the wavefront's two column tiles of one chunk into B operands w0 (rows 0..31 of the chunk) and w1
+// (rows 32..63), and their scales.
+template <int MTW, bool PACKED>
+__device__ __forceinline__ void wide_dequant(const uint8_t* ps, const WideW& w, bf8 (&w0)[2], bf8 (&w1)[2],
+                                             float (&sv)[2]) {
+    const int lane = threadIdx.x & 63, cp = (threadIdx.x >> 6) & 3;
+    const int i = lane & 15, q = lane >> 4;
+    if constexpr (PACKED) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const uint32_t L0 = w.lo[2 * tt], L1 = w.lo[2 * tt + 1], Hd = tt ? w.hd.y : w.hd.x;
+            const uint32_t u0a = (L0 & 0x0F0F0F0Fu) | ((Hd & 0x03030303u) << 4);         // rows 8 q + 0..3
+            const uint32_t u0b = (L1 & 0x0F0F0F0Fu) | (Hd & 0x30303030u);                // rows 8 q + 4..7
+            const uint32_t u1a = ((L0 >> 4) & 0x0F0F0F0Fu) | ((Hd & 0x0C0C0C0Cu) << 2);  // rows 32 + 8 q + 0..3
+            const uint32_t u1b = ((L1 >> 4) & 0x0F0F0F0Fu) | ((Hd >> 2) & 0x30303030u);  // rows 32 + 8 q + 4..7
+            uint32_t o0[4], o1[4];
+            codes_to_bf16(u0a, o0[0], o0[1]);
+            codes_to_bf16(u0b, o0[2], o0[3]);
+            codes_to_bf16(u1a, o1[0], o1[1]);
+            codes_to_bf16(u1b, o1[2], o1[3]);
+            w0[tt] = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
+            w1[tt] = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+            sv[tt] = h2f((uint16_t)(w.sc >> (16 * tt)));
+        }
+    } else {
+        const uint8_t* const pl = ps + part_a_bytes<MTW>() + 16 * MTW * 4;
+        const int sel = 2 * (q >> 1), r = lane & 15;
+        const int off = (r >> 1) * kPitch + 8 * (r & 1);
+        v2i lo_t[2], hi_t[2];
+        uint16_t sh[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = 2 * cp + tt;
+            lo_t[tt] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(pl + (8 * q) * kPitch + off + 16 * t));
+            hi_t[tt] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i*)(pl + (32 + 8 * (q & 1)) * kPitch + off + 16 * t));
+            sh[tt] = *reinterpret_cast<const uint16_t*>(pl + kScaleOff + 2 * (16 * t + i));
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            uint32_t o0[4], o1[4];
+#pragma unroll
+            for (int d = 0; d < 2; ++d) {
+                const uint32_t L = (uint32_t)lo_t[tt][d], Hs = (uint32_t)hi_t[tt][d] >> sel;
+                const uint32_t u0 = (L & 0x0F0F0F0Fu) | ((Hs & 0x03030303u) << 4);   // rows 8 q + e
+                const uint32_t u1 = ((L >> 4) & 0x0F0F0F0Fu) | (Hs & 0x30303030u);   // rows 32 + 8 q + e
+                codes_to_bf16(u0, o0[2 * d], o0[2 * d + 1]);
+                codes_to_bf16(u1, o1[2 * d], o1[2 * d + 1]);
+            }
+            w0[tt] = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
+            w1[tt] = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+            sv[tt] = h2f(sh[tt]);
+        }
+    }
+}
+
+// One chunk of the wavefront's part: two MFMAs per (M tile, column tile) into the chain accumulators tc; FIRST starts
+// the chain at the row sums' bias, LAST scales it into acc.  The LDS reads are issued in batches of up to four M tiles
+// ahead of the work that hides them (the first batch ahead of the dequantisation, each further batch ahead of the
+// previous batch's MFMAs), with scheduling barriers keeping that order: left to itself the compiler reused a few
+// operand registers and waited on the LDS once per M tile.
+template <int MTW, bool PACKED, bool FIRST, bool LAST>
+__device__ __forceinline__ void wide_compute(const uint8_t* ps, const WideW& w, f4 (&tc)[MTW][2], f4 (&acc)[MTW][2]) {
+    constexpr int MB = MTW < 4 ? MTW : 4;  // M tiles per batch of LDS reads
+    const int lane = threadIdx.x & 63;
+    const int i = lane & 15, q = lane >> 4;
+    const float* const rsum = reinterpret_cast<const float*>(ps + part_a_bytes<MTW>());
+    bf8 a0[MB], a1[MB], w0[2], w1[2];
+    f4 nc[MB];
+    float sv[2];
+    auto read = [&](int mb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < MB; ++k) {
+            const int mt = mb + k;
+            a0[k] = *reinterpret_cast<const bf8*>(ps + 16 * a_slot(16 * mt + i, q));
+            a1[k] = *reinterpret_cast<const bf8*>(ps + 16 * a_slot(16 * mt + i, 4 + q));
+            if constexpr (FIRST) nc[k] = *reinterpret_cast<const f4*>(rsum + 16 * mt + 4 * q);  // rows 16 mt + 4 q + v
+        }
+    };
+    read(0);
+    wide_dequant<MTW, PACKED>(ps, w, w0, w1, sv);
+#pragma unroll
+    for (int mb = 0; mb < MTW; mb += MB) {
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k = 0; k < MB; ++k)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const f4 c = mfma(a0[k], w0[tt], FIRST ? nc[k] : tc[mb + k][tt]);
+                tc[mb + k][tt] = mfma(a1[k], w1[tt], c);
+            }
+        if (mb + MB < MTW) read(mb + MB);
+    }
+    if constexpr (LAST) {
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) acc[mt][tt] = fma4(tc[mt][tt], sv[tt], acc[mt][tt]);
+    }
+}
+
+// lane (i, q) of wavefront cp holds C[m0 + 16 mt + 4 q + v][n0 + 16 (2 cp + tt) + i]
+template <int MTW>
+__device__ __forceinline__ void wide_store(const Args& p, int b, int m0, int n0, const f4 (&acc)[MTW][2]) {
+    const int lane = threadIdx.x & 63, cp = (threadIdx.x >> 6) & 3;
+    const int i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int n = n0 + 16 * (2 * cp + tt) + i;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int m = m0 + 16 * mt + 4 * q + v;
+                if (n >= p.N || m >= p.M) continue;
+                const int64_t o = (int64_t)b * p.so_b + (int64_t)m * p.so_m + n;
+                if (p.out_dtype == W6A16_OUT_F32)
+                    reinterpret_cast<float*>(p.out)[o] = acc[mt][tt][v];
+                else
+                    reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)acc[mt][tt][v];
+            }
+        }
+}
+
+template <int MTW, int KP, int CG, int D, int NL, bool PACKED>
+__global__ __launch_bounds__(256 * KP) void w6a16_wide_kernel(const Args p) {
+    constexpr int PB = part_bytes<MTW, PACKED>(), kStage = KP * PB;
+    constexpr int kRed = (KP - 1) * 4 * MTW * 2 * 64 * 16;  // K-part partials in LDS
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kStage > kRed ? 2 * kStage : kRed];
+    __shared__ uint32_t completed;
+    static_assert(D % CG == 0 && D % 2 == 0 && D % NL == 0, "a group of D steps holds whole chains, buffer pairs and rings");
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, kp = wv >> 2;
+    // XCD-aware order: the M groups of one strip are 8 blocks apart (same XCD, consecutive in its dispatch order)
+    const int bx = blockIdx.x, rest = bx >> 3;
+    const int mg = rest % p.m_groups, strip = (rest / p.m_groups) * 8 + (bx & 7);
+    if (strip >= p.n_strips) return;  // uniform over the workgroup
+    const int n0 = strip * kTileN;
+    const int split = blockIdx.y, b = blockIdx.z;
+    const int m0 = mg * 16 * MTW;
+    Sched S;
+    S.cg = CG;
+    S.nchunks = p.K / 64;
+    {
+        const int nch = p.K / (64 * CG);  // chains
+        const int h0 = split * p.chains_per_split, h1 = min(nch, h0 + p.chains_per_split);
+        const int nh = max(0, h1 - h0);
+        S.c_s = h0 * CG;
+        S.n_s = nh * CG;
+        S.per = (nh + KP - 1) / KP * CG;
+    }
+    const int steps = S.per;        // uniform over the workgroup
+    WideSrc<MTW> src;
+    wide_src<MTW, KP, PACKED>(p, b, m0, strip, src);
+    const int mine_n = S.part_n(src.kp);  // this wavefront's chunks (uniform over the wavefront)
+
+    f4 acc[MTW][2], tc[MTW][2];
+#pragma unroll
+    for (int mt = 0; mt < MTW; ++mt) acc[mt][0] = acc[mt][1] = f4{0.f, 0.f, 0.f, 0.f};
+
+    if (steps > 0) {
+        // The LDS stage of step s is written in step s - 1 (after its reads of the other buffer have passed that
+        // step's barrier) from a ring of NL register stages loaded NL - 1 steps earlier; packed weights are loaded D
+        // steps ahead of their use.  Loads past a part's range re-load its last chunk (a cache hit), so every load is
+        // unconditional; whole groups of D steps run unconditionally with a scheduling barrier after each step's
+        // loads, and the remainder (fewer than D steps, already loaded, whole chains) follows.
+        WideLds<MTW, PACKED> ls[NL];
+        WideW ws[D];
+#pragma unroll
+        for (int j = 0; j < NL; ++j) wide_load_lds<MTW, KP, PACKED>(p, S, src, j, ls[j]);
+        if constexpr (PACKED) {
+#pragma unroll
+            for (int j = 0; j < D; ++j) wide_load_w(p, src, S.chunk(src.kp, j), ws[j]);
+        }
+        wide_store_lds<MTW, KP, PACKED>(ls[0], lds);
+        wide_load_lds<MTW, KP, PACKED>(p, S, src, NL, ls[0]);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        // step s = base + j (base a multiple of D, so s = j modulo 2 and NL): compute from buffer j & 1, write step
+        // s + 1 into buffer (j + 1) & 1 from ls[(j + 1) % NL], refill that register stage with step s + 1 + NL, and
+        // (packed) ws[j] with step s + D.  Every register index is a compile-time constant (a run-time one put the
+        // stages in scratch memory).
+        auto step = [&](int base, auto J) __attribute__((always_inline)) {
+            constexpr int j = decltype(J)::value;
+            const int s = base + j;
+            const uint8_t* const ps = lds + (j & 1) * kStage + kp * PB;
+            if (s < mine_n) wide_compute<MTW, PACKED, j % CG == 0, j % CG == CG - 1>(ps, ws[j], tc, acc);
+            if constexpr (PACKED) wide_load_w(p, src, S.chunk(src.kp, s + D), ws[j]);
+            wide_store_lds<MTW, KP, PACKED>(ls[(j + 1) % NL], lds + ((j + 1) & 1) * kStage);
+            wide_load_lds<MTW, KP, PACKED>(p, S, src, s + 1 + NL, ls[(j + 1) % NL]);
+            __builtin_amdgcn_sched_barrier(0);
+            __syncthreads();
+        };
+        const int full = steps / D * D;
+        for (int base = 0; base < full; base += D) unroll<D>([&](auto J) __attribute__((always_inline)) { step(base, J); });
+        unroll<D - 1>([&](auto J) __attribute__((always_inline)) {
+            if (full + decltype(J)::value < steps) step(full, J);
+        });
+    }
+
+    if constexpr (KP > 1) {  // sum the K parts through LDS in part order 0, 1, ..
+        f4* const red = reinterpret_cast<f4*>(lds) + (wv & 3) * MTW * 2 * 64 + lane;
+        constexpr int kPartF4 = 4 * MTW * 2 * 64;
+        __syncthreads();  // the last step's LDS reads are done
+        if (kp > 0) {
+#pragma unroll
+            for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) red[(kp - 1) * kPartF4 + (mt * 2 + tt) * 64] = acc[mt][tt];
+        }
+        __syncthreads();
+        if (kp == 0) {
+#pragma unroll
+            for (int k = 1; k < KP; ++k)
+#pragma unroll
+                for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+                    for (int tt = 0; tt < 2; ++tt) acc[mt][tt] += red[(k - 1) * kPartF4 + (mt * 2 + tt) * 64];
+        }
+    }
+
+    if (p.split_k == 1) {  // uniform over the grid
+        if (kp == 0) wide_store<MTW>(p, b, m0, n0, acc);
+        return;
+    }
+    // Split-K hand-off, one release per workgroup.  Partials are kept in the accumulators' own layout
+    // ([wavefront][mt][tt][lane] f4, 16 bytes per lane and store) and written through the L2 (sc1 stores: written
+    // back, the release fence's L2 walk has nothing of theirs left to write; with plain stores it cost 10 us per call
+    // at M = 128); the release fence orders them before the arrival count, and the last split's acquire fence orders
+    // its loads after it.  The last split keeps its own tile in registers and adds the others' in split order 0, 1, ..
+    // (a fixed order: the result does not depend on which split arrives last).
+    const int64_t tile = ((int64_t)b * p.m_groups + mg) * p.n_strips + strip;
+    constexpr int kTileF4 = 4 * MTW * 2 * 64;  // f4 per partial tile
+    f4* const tbase = reinterpret_cast<f4*>(p.part) + tile * p.split_k * kTileF4;
+    const int cp = wv & 3;
+    if (kp == 0) {
+        const __amdgpu_buffer_rsrc_t prs =
+            __builtin_amdgcn_make_buffer_rsrc(tbase, 0, p.split_k * kTileF4 * 16, 0x00020000);
+        const int mine = split * kTileF4 + cp * MTW * 2 * 64 + lane;
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[mt][tt]), prs,
+                                                       (mine + (mt * 2 + tt) * 64) * 16, 0, kCachePolicySC1);
+    }
+    // Each wavefront waits for its own stores (wavefront 0's release fence waits only for wavefront 0's), then the
+    // barrier puts all of them before that fence.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (wv == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        bool done = false;
+        if (lane == 0) {
+            done = __hip_atomic_fetch_add(p.cnt + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                   (uint32_t)p.split_k - 1;
+            completed = done ? 1u : 0u;
+        }
+        if (__builtin_amdgcn_ballot_w64(done)) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            if (lane == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    __syncthreads();  // wavefront 0's acquire precedes every wavefront's loads
+    if (!completed || kp != 0) return;
+    const f4* const part = tbase + cp * MTW * 2 * 64 + lane;
+    f4 tot[MTW][2];
+    for (int sp = 0; sp < p.split_k; ++sp) {
+#pragma unroll
+        for (int mt = 0; mt < MTW; ++mt)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const f4 x = sp == split ? acc[mt][tt] : part[sp * kTileF4 + (mt * 2 + tt) * 64];
+                tot[mt][tt] = sp == 0 ? x : tot[mt][tt] + x;
+            }
+    }
+    wide_store<MTW>(p, b, m0, n0, tot);
+}
+
 // Dequantise the packed layout: one thread per (b, strip, chunk, lane) writes its 16 rows x 8 columns (rows
 // 8 q + e and 32 + 8 q + e, columns 128 strip + 16 t + i); for each (row, tile) the 16 lanes of a row group store
 // 16 consecutive columns.
@@ -668,28 +1189,52 @@ int cu_count() { return wkv7::device_cu_count(); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// M tiles per wavefront: above 32 rows two 16-row tiles share each dequantised weight operand (measured at
-// K = 4096, N = 16384: M = 32 is faster with one tile per wavefront and two M groups, M = 64 with two; four tiles
-// per wavefront leave one wavefront per SIMD and lose at every split).  Measured and not kept: a mode in which the
-// four wavefronts of a workgroup share one strip's dequantised chunk through LDS (each wavefront dequantising two
-// of the eight tiles, one barrier per chunk) -- 8 % faster at M = 64, no faster at M = 128, slower below 64 rows.
-int m_tiles_per_wave(int M) { return M <= 32 ? 1 : 2; }
+// Narrow kernel (M <= 32 rows): one 16-row tile per wavefront, one M group per 16 rows (measured at K = 4096,
+// N = 16384: M = 32 is faster with one tile per wavefront and two M groups).  Wide kernel (M > 32): MTW 16-row tiles
+// per wavefront, KP K parts per workgroup, chains of CG chunks.
+bool wide_rows(int M) { return M > 32; }
+
+struct WideCfg {
+    int mtw, kp;
+};
+// Measured at K = 4096, N = 16384 (us per call, packed / planes): M = 64 (2, 2) 27.2 / 33.0, (4, 2) 31.3 / 32.4,
+// (2, 1) 32.8 / 44.9; M = 128 (4, 2) 36.2 / 40.9, (2, 2) 46.2 / 54.8, (4, 1) 43.7 / 53.5; M = 256 (4, 1) 54.1 / 71.9,
+// (8, 2) 57.5 / 72.8, (8, 1) 94.4 / 103.5, (4, 2) 64.1 / 73.2.
+WideCfg wide_cfg(int M) {
+    if (M <= 64) return {2, 2};
+    if (M <= 128) return {4, 2};
+    return {4, 1};
+}
 
 struct Layout {
-    int mt, m_groups, n_strips;
-    size_t tiles, counter_bytes, partial_bytes;
+    bool wide;
+    int mt, kp, cg, m_groups, n_strips, mpad, nchains;
+    size_t tiles, counter_bytes, partial_bytes, rsum_offset, rsum_bytes;
 };
 
 Layout layout(const w6a16_args* a) {
     Layout l{};
-    l.mt = m_tiles_per_wave(a->M);
-    l.m_groups = (a->M + 16 * l.mt - 1) / (16 * l.mt);
+    l.wide = wide_rows(a->M);
     l.n_strips = (a->N + kTileN - 1) / kTileN;
-    if (a->split_k > 1) {
-        const size_t tiles = (size_t)a->B * l.m_groups * l.n_strips;
-        l.tiles = tiles;
+    if (l.wide) {
+        const WideCfg c = wide_cfg(a->M);
+        l.mt = c.mtw;
+        l.kp = c.kp;
+        l.cg = (a->group_k % 128 == 0) ? 2 : 1;
+        l.nchains = a->K / (64 * l.cg);
+    } else {
+        l.mt = 1;
+        l.kp = 1;
+    }
+    const int rows_per_group = 16 * l.mt;  // A rows per workgroup (wide) or per wavefront (narrow)
+    l.m_groups = (a->M + rows_per_group - 1) / rows_per_group;
+    l.mpad = l.m_groups * rows_per_group;
+    if (a->split_k > 1 || l.wide) {
+        l.tiles = (size_t)a->B * l.m_groups * l.n_strips;
         l.counter_bytes = kCounterRegion;
-        l.partial_bytes = tiles * a->split_k * (size_t)l.mt * kTiles * 4 * 64 * 4;
+        l.partial_bytes = a->split_k > 1 ? l.tiles * a->split_k * (size_t)rows_per_group * kTileN * 4 : 0;
+        l.rsum_offset = l.counter_bytes + l.partial_bytes;
+        l.rsum_bytes = l.wide ? (size_t)a->B * l.nchains * l.mpad * 4 : 0;
     }
     return l;
 }
@@ -713,10 +1258,11 @@ int validate(const w6a16_args* a) {
         return WKV7_ERR_ALIGN;
     if (a->a_row_stride < a->K || a->out_row_stride < a->N) return WKV7_ERR_SHAPE;
     const Layout l = layout(a);
-    if ((int64_t)a->B * l.m_groups > 65535) return WKV7_ERR_SHAPE;  // grid z: batch x M groups
-    if (a->split_k > 1) {
-        if (l.tiles * 4 > kCounterRegion) return WKV7_ERR_SHAPE;  // more tiles than counters
-        if (!a->workspace || a->workspace_bytes < l.counter_bytes + l.partial_bytes) return WKV7_ERR_WORKSPACE;
+    if ((int64_t)a->B * (l.wide ? 1 : l.m_groups) > 65535) return WKV7_ERR_SHAPE;  // grid z: batch (x M groups)
+    if (l.wide && (int64_t)l.m_groups * ((l.n_strips + 7) / 8) * 8 > 0x7FFFFFFF) return WKV7_ERR_SHAPE;
+    if (a->split_k > 1 && l.tiles * 4 > kCounterRegion) return WKV7_ERR_SHAPE;  // more tiles than counters
+    if (a->split_k > 1 || l.wide) {
+        if (!a->workspace || a->workspace_bytes < l.rsum_offset + l.rsum_bytes) return WKV7_ERR_WORKSPACE;
         if (reinterpret_cast<uintptr_t>(a->workspace) % kCounterAlign) return WKV7_ERR_ALIGN;
     }
     return WKV7_OK;
@@ -740,6 +1286,25 @@ void launch(const Args& p, const Layout& l, bool packed, hipStream_t s) {
         hipLaunchKernelGGL((w6a16_kernel<MT, D, KS, false>), grid, block, 0, s, p);
 }
 
+template <int MTW, int KP, int CG>
+void launch_wide(const Args& p, const Layout& l, bool packed, hipStream_t s) {
+    constexpr int D = 4, NL = 4;  // packed weights D steps ahead; NL register stages of the LDS ring
+    hipLaunchKernelGGL(w6a16_rowsum_kernel, dim3(l.mpad / 4, (p.K + 511) / 512, p.B), dim3(256), 0, s, p);
+    const dim3 grid(8 * l.m_groups * ((l.n_strips + 7) / 8), p.split_k, p.B);
+    if (packed)
+        hipLaunchKernelGGL((w6a16_wide_kernel<MTW, KP, CG, D, NL, true>), grid, dim3(256 * KP), 0, s, p);
+    else
+        hipLaunchKernelGGL((w6a16_wide_kernel<MTW, KP, CG, D, NL, false>), grid, dim3(256 * KP), 0, s, p);
+}
+
+template <int MTW, int KP>
+void launch_wide_cg(const Args& p, const Layout& l, bool packed, hipStream_t s) {
+    if (l.cg == 2)
+        launch_wide<MTW, KP, 2>(p, l, packed, s);
+    else
+        launch_wide<MTW, KP, 1>(p, l, packed, s);
+}
+
 }  // namespace
 }  // namespace w6
 
@@ -749,22 +1314,29 @@ size_t w6a16_args_size(void) { return sizeof(w6a16_args); }
 
 int w6a16_workspace_size(const w6a16_args* a, size_t* bytes) {
     if (!a || !bytes) return WKV7_ERR_NULL;
-    if (a->split_k <= 1 || a->M <= 0 || a->B < 1 || a->N < 1) {
+    if (a->M <= 0 || a->B < 1 || a->N < 1 || a->K < 64 || a->group_k < 64 || (a->split_k <= 1 && !w6::wide_rows(a->M))) {
         *bytes = 0;
         return WKV7_OK;
     }
     const w6::Layout l = w6::layout(a);
-    *bytes = l.counter_bytes + l.partial_bytes;
+    *bytes = l.rsum_offset + l.rsum_bytes;
     return WKV7_OK;
 }
 
 int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
     if (B < 1 || M < 1 || N < 1 || K < 64) return 1;
-    const int mt = w6::m_tiles_per_wave(M);
-    const int64_t strips = (N + w6::kTileN - 1) / w6::kTileN;
-    const int64_t groups = (int64_t)B * ((M + 16 * mt - 1) / (16 * mt)) * ((strips + w6::kStrips - 1) / w6::kStrips);
-    const int chunks = K / 64;
-    const int64_t cus = w6::cu_count();
+    w6a16_args shape{};
+    shape.B = B;
+    shape.M = M;
+    shape.N = N;
+    shape.K = K;
+    shape.group_k = K % 128 == 0 ? 128 : 64;  // chains of two chunks where K allows them
+    const w6::Layout l = w6::layout(&shape);
+    // workgroups per split: narrow, four strips per workgroup; wide, one strip per workgroup
+    const int64_t groups = (int64_t)B * l.m_groups * (l.wide ? l.n_strips : (l.n_strips + w6::kStrips - 1) / w6::kStrips);
+    const int chunks = l.wide ? l.nchains : K / 64;  // the units a split range holds
+    // narrow: one workgroup per CU; wide (4 KP wavefronts per workgroup): eight wavefronts per CU
+    const int64_t cus = l.wide ? w6::cu_count() * 2 / l.kp : w6::cu_count();
     // The smallest power of two that gives every CU a workgroup (every range keeps at least one chunk); then doubled
     // while ranges keep at least 16 chunks and the launch stays within one workgroup per CU (each workgroup's
     // split-K hand-off costs one agent-scope release).  Measured at K = 4096, N = 16384 (us, planes / packed): M = 128
@@ -793,9 +1365,10 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     p.out = a->out;
     p.so_b = a->out_batch_stride;
     p.so_m = a->out_row_stride;
-    if (a->split_k > 1) {
+    if (a->split_k > 1 || l.wide) {
         p.cnt = static_cast<uint32_t*>(a->workspace);
         p.part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + l.counter_bytes);
+        p.rsum = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + l.rsum_offset);
     }
     p.B = a->B;
     p.M = a->M;
@@ -808,12 +1381,22 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     p.n_strips = l.n_strips;
     const int chunks = a->K / 64;
     p.chunks_per_split = (chunks + a->split_k - 1) / a->split_k;
+    if (l.wide) {
+        p.mpad = l.mpad;
+        p.chain_k = 64 * l.cg;
+        p.nchains = l.nchains;
+        p.chains_per_split = (l.nchains + a->split_k - 1) / a->split_k;
+    }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const bool packed = a->format == W6A16_FORMAT_PACKED;
-    switch (l.mt) {
-        case 1: w6::launch<1, 2>(p, l, packed, s); break;
-        default: w6::launch<2, 2>(p, l, packed, s); break;
-    }
+    if (!l.wide)
+        w6::launch<1, 2>(p, l, packed, s);
+    else if (l.mt == 2)
+        w6::launch_wide_cg<2, 2>(p, l, packed, s);
+    else if (l.kp == 2)
+        w6::launch_wide_cg<4, 2>(p, l, packed, s);
+    else
+        w6::launch_wide_cg<4, 1>(p, l, packed, s);
     return static_cast<int>(hipGetLastError());
 }
 

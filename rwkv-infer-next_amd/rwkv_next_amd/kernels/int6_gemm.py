@@ -271,9 +271,9 @@ def _impl(a, w: _W, split_k, out_dtype=None):
     args.split_k = max(1, int(split_k))
     args.out_dtype = _lib.W6A16_OUT_F32 if odt == torch.float32 else _lib.W6A16_OUT_BF16
     lib = _lib.load()
-    if args.split_k > 1:
-        n = ctypes.c_size_t(0)
-        _lib.check(lib.w6a16_workspace_size(args, ctypes.byref(n)))
+    n = ctypes.c_size_t(0)
+    _lib.check(lib.w6a16_workspace_size(args, ctypes.byref(n)))
+    if n.value:  # split-K counters and partials, and the wide kernel's row sums (M > 32)
         ws = _workspace(A.device, int(n.value))
         args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     _lib.check(lib.w6a16_matmul(args, torch.cuda.current_stream(A.device).cuda_stream))
@@ -303,7 +303,7 @@ def _capture_id(stream: int) -> int:
 
 
 def _workspace(device, nbytes):
-    """The split-K workspace (a fixed counter region, then partials) of the current stream on `device`.  The
+    """The workspace (a fixed counter region, then split-K partials and row sums) of the current stream on `device`.  The
     counters must be zero when a call starts; every completed call leaves them zero, so the calls of one stream
     (which run in order) share the workspace, and calls on different streams, which may overlap, never do.
 

@@ -235,7 +235,7 @@ def base_args(**kw):
     ("group_k", 96, _lib.WKV7_ERR_SHAPE),
     ("group_k", 1024, _lib.WKV7_ERR_SHAPE),
     ("B", 0, _lib.WKV7_ERR_SHAPE),
-    ("M", 64 * 65536, _lib.WKV7_ERR_SHAPE),           # grid z = batch x 64-row groups
+    ("B", 65536, _lib.WKV7_ERR_SHAPE),                # grid z = batch (x 16-row groups for M <= 32)
     ("a_row_stride", 256, _lib.WKV7_ERR_SHAPE),       # < K
     ("out_row_stride", 128, _lib.WKV7_ERR_SHAPE),     # < N
     ("split_k", 0, _lib.WKV7_ERR_ARG),
@@ -265,12 +265,22 @@ def test_matmul_empty_and_workspace_size():
     # 16 x 128 fp32 partial tile
     tiles = 2 * 1 * 2
     assert n.value == (1 << 20) + tiles * 8 * 16 * 128 * 4
-    # M = 40 takes two 16-row tiles per wavefront: two M groups of 32 rows, two strips (N = 256): four tiles
+    # M > 32 runs the wide kernel: after the counters and partials, the row sums of A per chain of two 64-row chunks
+    # (group_k = 128), [B][K / 128][rows padded to the M groups]
+    # M = 40: two 16-row tiles per wavefront, two M groups of 32 rows, two strips (N = 256): four tiles
     assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=2, M=40)), ctypes.byref(n)) == 0
-    assert n.value == (1 << 20) + (2 * 2) * 2 * 32 * 128 * 4
-    # M = 100 takes two 16-row tiles per wavefront: four M groups of 32 rows, two strips: eight tiles
+    assert n.value == (1 << 20) + 4 * 2 * 32 * 128 * 4 + 4 * 64 * 4
+    # M = 100: four 16-row tiles per wavefront, two M groups of 64 rows, two strips
     assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=2, M=100)), ctypes.byref(n)) == 0
-    assert n.value == (1 << 20) + (4 * 2) * 2 * 32 * 128 * 4
+    assert n.value == (1 << 20) + 4 * 2 * 64 * 128 * 4 + 4 * 128 * 4
+    # M = 200: four M groups of 64 rows
+    assert lib.w6a16_workspace_size(ctypes.byref(base_args(split_k=2, M=200)), ctypes.byref(n)) == 0
+    assert n.value == (1 << 20) + 8 * 2 * 64 * 128 * 4 + 4 * 256 * 4
+    # without split-K the wide kernel still needs the counter region's place and the row sums
+    assert lib.w6a16_workspace_size(ctypes.byref(base_args(M=40)), ctypes.byref(n)) == 0
+    assert n.value == (1 << 20) + 4 * 64 * 4
+    wide = base_args(M=40, a_batch_stride=40 * 512, out_batch_stride=40 * 256)
+    assert lib.w6a16_matmul(ctypes.byref(wide), None) == _lib.WKV7_ERR_WORKSPACE
     small = base_args(split_k=8, B=2, M=3, workspace=0x10000, workspace_bytes=(1 << 20) + tiles * 8 * 16 * 128 * 4 - 4)
     assert lib.w6a16_matmul(ctypes.byref(small), None) == _lib.WKV7_ERR_WORKSPACE
     # at most 262144 tiles (the counter region's u32 counters): 40000 x 1 x 8 tiles are refused, 30000 x 1 x 8 reach
@@ -331,8 +341,12 @@ def test_split_rule():
         assert (K // 64) // sk >= 1
     # without a GPU the CU count is taken as 256: K = 4096, N = 16384 has 32 groups of four 128-column strips
     assert lib.w6a16_plan_split(1, 1, 16384, 4096) == 8
-    assert lib.w6a16_plan_split(1, 64, 16384, 4096) == 4        # two M groups of 32 rows: 64 groups
-    assert lib.w6a16_plan_split(1, 128, 16384, 4096) == 2       # 128 groups: 2 fills the chip, one workgroup per CU
+    # M > 32: the wide kernel, one 128-column strip per workgroup; two M groups of eight wavefronts (M = 64, 128) or
+    # four M groups of four (M = 256) put eight wavefronts on every CU without split-K
+    assert lib.w6a16_plan_split(1, 64, 16384, 4096) == 1
+    assert lib.w6a16_plan_split(1, 128, 16384, 4096) == 1
+    assert lib.w6a16_plan_split(1, 256, 16384, 4096) == 1
+    assert lib.w6a16_plan_split(1, 128, 4096, 4096) == 4        # 32 strips x 2 M groups: split 4 fills the chip
     assert lib.w6a16_plan_split(1, 1, 1024, 16384) == 64        # 2 groups, 256 chunks: capped at 64
     assert lib.w6a16_plan_split(1, 1, 4096, 16384) == 32
     assert I6.plan_int6(1, 4096, 4096, 1) == (lib.w6a16_plan_split(1, 1, 4096, 4096), False)
