@@ -8,9 +8,10 @@
 //                       | (u[.. + j + 48] >> 4) << 6                                                 j < 16
 // C[b][m][n] = sum_k A[b][m][k] s[k / group_k][n] q[k][n] with fp32 accumulation (int6_gemm.py:156-215).
 //
-// A workgroup of four wavefronts covers four adjacent 128-column strips (512 columns: neighbouring strips share DRAM
-// pages, which the four wavefronts read at about the same time) for one range of 64-row chunks (split-K over chunk
-// ranges) and up to 64 rows of A.  Each wavefront computes MT 16 (M) x 128 (N) tiles:
+// Narrow kernel (M <= 32, the decode GEMV): a workgroup of four wavefronts covers four adjacent 128-column strips
+// (512 columns: neighbouring strips share DRAM pages, which the four wavefronts read at about the same time) for one
+// range of 64-row chunks (split-K over chunk ranges) and one 16-row tile of A.  Each wavefront computes a 16 (M) x
+// 128 (N) tile:
 //   * the chunk's 48 plane rows x 128 columns (6 KB) are loaded coalesced (16 bytes per lane, 8 lanes per row), with
 //     the next chunk's loads in flight, and written to the wave's own LDS buffer (no workgroup barrier: a wave's LDS
 //     operations execute in order);
@@ -21,12 +22,12 @@
 //     32-row halves of the chunk (low and high nibbles), one read of the hi plane supplies the top 2 bits;
 //   * the 6-bit code u becomes a bf16 operand without conversion instructions: 0x4300 | u is the bf16 of 128 + u,
 //     exact, assembled for two values with one v_perm_b32 against a register of 0x43 bytes.  One extra MFMA pair
-//     per chunk and M tile against a constant B of -160 removes the bias (128 + u - 160 = q) exactly;
-//   * the dequantised operand serves all MT M tiles; each chunk's fp32 tile is scaled by s (fp16) and accumulated.
-// Split-K partials are reduced inside the kernel: every split stores its tile (fp32, in register order) and the
-// workgroup increments its tiles' arrival counters after one agent-scope release; the split that arrives last sums
-// the partials in split order (a fixed order: the result does not depend on which split arrives last), stores the
-// result and resets the counter to zero.
+//     per chunk against a constant B of -160 removes the bias (128 + u - 160 = q) exactly;
+//   * each chunk's fp32 tile is scaled by s (fp16) and accumulated.
+// Split-K partials are reduced inside the kernel: every split stores its tile (fp32) and the workgroup increments its
+// tiles' arrival counters after one agent-scope release; the split that arrives last sums the partials in split
+// order (a fixed order: the result does not depend on which split arrives last), stores the result and resets the
+// counter to zero.  The wide kernel (M > 32) is described where it is defined.
 // Rows m >= M and columns n >= N are clamped on load (they only feed outputs that are not stored).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -390,17 +391,13 @@ __device__ __forceinline__ void process_pstage(const PStage<MT>& s, f4 (&acc)[MT
     }
 }
 
-// One kernel for both weight formats.  A workgroup holds KS x 4 wavefronts: four adjacent 128-column strips, and
-// for each strip KS wavefronts splitting the workgroup's chunk range in KS parts (more loads in flight per CU at the
-// same global split).  The KS partial tiles of a strip are summed through LDS in part order 0, 1, .. (fixed), then
-// the tile is finished as a whole (stored, or split-K published and reduced).
-template <int MT, int D, int KS, bool PACKED>
-__global__ __launch_bounds__(64 * kStrips * KS) void w6a16_kernel(const Args p) {
-    constexpr int kStage = PACKED ? 16 : kStrips * KS * kBuf;  // planes: each wavefront's staging buffer
+// Narrow kernel (M <= 32), both weight formats: a workgroup of four wavefronts, one per 128-column strip.
+template <int MT, int D, bool PACKED>
+__global__ __launch_bounds__(64 * kStrips) void w6a16_kernel(const Args p) {
+    constexpr int kStage = PACKED ? 16 : kStrips * kBuf;  // planes: each wavefront's staging buffer
     __shared__ __attribute__((aligned(16))) uint8_t lds[kStage];
-    __shared__ __attribute__((aligned(16))) f4 red[KS > 1 ? (KS - 1) * kStrips * MT * kTiles * 64 : 1];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int sw = wv % kStrips, part = wv / kStrips;
+    const int sw = wv;
     const int strip = blockIdx.x * kStrips + sw;
     const bool live = strip < p.n_strips;
     const int n0 = strip * kTileN;
@@ -408,9 +405,7 @@ __global__ __launch_bounds__(64 * kStrips * KS) void w6a16_kernel(const Args p) 
     const int b = blockIdx.z / p.m_groups, mg = blockIdx.z % p.m_groups;
     const int m0 = mg * 16 * MT;
     const int nchunks = p.K / 64;
-    const int s0 = split * p.chunks_per_split, s1 = min(nchunks, s0 + p.chunks_per_split);
-    const int per = (max(0, s1 - s0) + KS - 1) / KS;
-    const int c0 = s0 + part * per, c1 = min(s1, c0 + per);
+    const int c0 = split * p.chunks_per_split, c1 = min(nchunks, c0 + p.chunks_per_split);
     uint8_t* const buf = lds + (PACKED ? 0 : wv * kBuf);
 
     f4 acc[MT][kTiles];
@@ -463,26 +458,7 @@ __global__ __launch_bounds__(64 * kStrips * KS) void w6a16_kernel(const Args p) 
         }
     }
 
-    if constexpr (KS > 1) {
-        f4* const r = red + (int64_t)sw * MT * kTiles * 64 + lane;
-        constexpr int kPartStride = kStrips * MT * kTiles * 64;
-        if (part > 0) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int t = 0; t < kTiles; ++t) r[(part - 1) * kPartStride + (mt * kTiles + t) * 64] = acc[mt][t];
-        }
-        __syncthreads();
-        if (part == 0) {
-#pragma unroll
-            for (int k = 1; k < KS; ++k)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                    for (int t = 0; t < kTiles; ++t) acc[mt][t] += r[(k - 1) * kPartStride + (mt * kTiles + t) * 64];
-        }
-    }
-    const bool owner = live && part == 0;  // this wavefront finishes its strip's tile
+    const bool owner = live;  // this wavefront finishes its strip's tile
     if (p.split_k == 1) {  // uniform over the grid
         if (owner) store_tile<MT>(p, b, m0, n0, acc);
         return;
@@ -527,6 +503,8 @@ __global__ __launch_bounds__(64 * kStrips * KS) void w6a16_kernel(const Args p) 
 //   * Chains: the products of CG consecutive chunks (CG = 2 when the quantisation group holds two chunks, else 1)
 //     accumulate in one MFMA chain whose accumulator starts at the chain's bias -160 sum_k A[m][k] (the row sums of
 //     w6a16_rowsum_kernel, computed once per call instead of once per strip), then are scaled once: acc += s * chain.
+//     (Measured against row sums taken by the staging threads with per-chunk scaling, which saves that launch: M = 64
+//     1 us faster, M = 128 3 us and M = 256 18 us slower per call -- the per-step VALU work decides at four M tiles.)
 //   * Packed weights are loaded straight into registers (16 + 8 bytes per lane and chunk: the lane's records of its
 //     two tiles), D steps ahead; planes are staged in LDS with A (48 rows x 128 columns) and read back transposed as
 //     in the narrow kernel.
@@ -1268,22 +1246,13 @@ int validate(const w6a16_args* a) {
     return WKV7_OK;
 }
 
-// Wavefronts per strip (KS): two for the two-tile (M > 32) kernels -- each strip's chunk range split in two inside the
-// workgroup and summed through LDS, so twice the waves stream the weight without more split-K hand-offs.  Measured at
-// K = 4096, N = 16384 (us, planes / packed, at each M's best split): M = 64 41.9 / 37.2 -> 38.0 / 35.5, M = 128
-// 63.4 / 54.1 -> 52.5 / 49.1, M = 256 95.8 / 81.9 -> 71.7 / 63.3.  One wavefront per strip for M <= 32 (two: no gain).
-template <int MT>
-constexpr int parts_for() { return MT >= 2 ? 2 : 1; }
-
 template <int MT, int D>
 void launch(const Args& p, const Layout& l, bool packed, hipStream_t s) {
-    constexpr int KS = parts_for<MT>();
     const dim3 grid((l.n_strips + kStrips - 1) / kStrips, p.split_k, p.B * l.m_groups);
-    const dim3 block(64 * kStrips * KS);
     if (packed)
-        hipLaunchKernelGGL((w6a16_kernel<MT, D, KS, true>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((w6a16_kernel<MT, D, true>), grid, dim3(64 * kStrips), 0, s, p);
     else
-        hipLaunchKernelGGL((w6a16_kernel<MT, D, KS, false>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((w6a16_kernel<MT, D, false>), grid, dim3(64 * kStrips), 0, s, p);
 }
 
 template <int MTW, int KP, int CG>
