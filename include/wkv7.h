@@ -51,6 +51,11 @@ extern "C" {
 #define WKV7_STATUS_NKEEP 8     /* a negative n_keep entry: treated as 0 */
 #define WKV7_STATUS_DECAY 16    /* the call runs the chunked or chain kernels and some w exceeds WKV7_CHUNK_W_MAX:
                                  * the chunked rows' results are not finite; run such calls with WKV7_ALGO_RECURRENT */
+#define WKV7_STATUS_SLOT_CLASH 32  /* (calls of at most WKV7_STATUS_CLASH_MAX_SEQS sequences) two sequences store their
+                                    * final states to the same ht slot, or, with h0 and ht one pool, a sequence stores
+                                    * to a slot another sequence reads its initial state from: the result depends on
+                                    * the order in which the kernels reach them */
+#define WKV7_STATUS_CLASH_MAX_SEQS 1024
 
 /* Largest raw w the chunked form handles.  It references each chunk's decay factors to the chunk midpoint, so factors
  * up to exp(32 exp(w)) must fit fp32: w <= 1.0 (32 e^1.0 = 87 < 88.7).  RWKV-7 produces w = -softplus(-x) - 0.5

@@ -182,6 +182,40 @@ __global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, 
             }
         }
     }
+    // Slot clashes (uniform over the grid): every workgroup stages the call's in-range final-state slots and, for an
+    // in-place pool, initial-state slots in LDS; workgroup b then compares each final-state slot j = b, b + G, ..
+    // with every other sequence's slots, each thread holding the entries n = threadIdx.x + 256 k in registers.
+    constexpr int kMax = WKV7_STATUS_CLASH_MAX_SEQS, kPer = kMax / 256;
+    const int N = p.num_seqs;
+    if (p.ht && N >= 2 && N <= kMax) {
+        __shared__ int64_t dst[kMax], src[kMax];
+        const bool same_pool = static_cast<const void*>(p.h0) == static_cast<const void*>(p.ht);
+        for (int n = threadIdx.x; n < N; n += blockDim.x) {
+            const int64_t d = p.ht_idx ? p.ht_idx[n] : n;
+            dst[n] = (d >= 0 && d < p.ht_rows) ? d : -1;
+            int64_t s = -1;
+            if (same_pool && !(p.fresh && p.fresh[n])) {
+                const int64_t x = p.h0_idx ? p.h0_idx[n] : n;
+                if (x >= 0 && x < p.h0_rows) s = x;
+            }
+            src[n] = s;
+        }
+        __syncthreads();
+        int64_t md[kPer], ms[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int n = threadIdx.x + 256 * k;
+            md[k] = n < N ? dst[n] : -1;
+            ms[k] = n < N ? src[n] : -1;
+        }
+        for (int j = blockIdx.x; j < N; j += gridDim.x) {
+            const int64_t dj = dst[j];
+            if (dj < 0) continue;
+#pragma unroll
+            for (int k = 0; k < kPer; ++k)
+                if (threadIdx.x + 256 * k != j && (md[k] == dj || ms[k] == dj)) bits |= WKV7_STATUS_SLOT_CLASH;
+        }
+    }
     if (bits) __hip_atomic_fetch_or(status, bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -246,7 +280,9 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     if (args->status) {
         const bool check_w = pl.run_chunked || pl.run_chain;
         const int64_t work = std::max<int64_t>(args->num_seqs, check_w ? args->total_tokens * args->H * 8 : 0);
-        const int blocks = (int)std::min<int64_t>((work + 255) / 256, 1024);
+        int blocks = (int)std::min<int64_t>((work + 255) / 256, 1024);
+        // the slot-clash comparison (up to 1024 x 1024 slot pairs) is spread over at least 16 workgroups
+        if (args->ht && args->num_seqs >= 2 && args->num_seqs <= WKV7_STATUS_CLASH_MAX_SEQS) blocks = std::max(blocks, 16);
         hipLaunchKernelGGL(wkv7_status_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, args->status, check_w);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);

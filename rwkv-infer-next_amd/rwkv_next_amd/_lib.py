@@ -25,6 +25,8 @@ WKV7_STATUS_HT_SLOT = 2
 WKV7_STATUS_SEQLENS = 4
 WKV7_STATUS_NKEEP = 8
 WKV7_STATUS_DECAY = 16
+WKV7_STATUS_SLOT_CLASH = 32
+WKV7_STATUS_CLASH_MAX_SEQS = 1024
 WKV7_CHUNK_W_MAX = 1.0
 
 ALGO_AUTO = 0

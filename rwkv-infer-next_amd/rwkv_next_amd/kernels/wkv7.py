@@ -255,9 +255,10 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
     max_len: ragged calls may pass an upper bound on any row's length (sizes the workspace; 0 = sumT).
     status: optional int32 device tensor (one element, see new_status): a check launched ahead of the recurrence
     ORs WKV7_STATUS_* bits into it when a slot index lies outside the pool, cu_seqlens is malformed or an n_keep
-    entry is negative (the kernels skip such reads and writes and go on), or when a call that runs the chunked
+    entry is negative (the kernels skip such reads and writes and go on), when a call that runs the chunked
     kernels has w above 1.0 (their results are not finite: the chunked form needs w <= 1.0, which RWKV-7's
-    w = -softplus(-x) - 0.5 always meets).  Nothing synchronises: read it with check_status when convenient.
+    w = -softplus(-x) - 0.5 always meets), or, for calls of at most 1024 rows, when two rows share a slot (their
+    states race).  Nothing synchronises: read it with check_status when convenient.
     Returns o like v (or None when store_o=False).  Runs as the registered op rwkv_next_amd::wkv7_pool_."""
     if r.dim() not in (3, 4):
         raise ValueError(f"operands must be (B, T, H*K) or (B, T, H, K), got {tuple(r.shape)}")
@@ -305,7 +306,9 @@ STATUS_REASONS = {_lib.WKV7_STATUS_H0_SLOT: "initial-state slot index outside th
                   _lib.WKV7_STATUS_SEQLENS: "cu_seqlens not non-decreasing within [0, total tokens]",
                   _lib.WKV7_STATUS_NKEEP: "negative n_keep",
                   _lib.WKV7_STATUS_DECAY: f"w above {_lib.WKV7_CHUNK_W_MAX} on a call that runs the chunked kernels "
-                                          "(their results are not finite): run it with algo=ALGO_RECURRENT"}
+                                          "(their results are not finite): run it with algo=ALGO_RECURRENT",
+                  _lib.WKV7_STATUS_SLOT_CLASH: "two sequences share a state slot (a final state stored where another "
+                                               "sequence stores or reads its state): the result depends on timing"}
 
 
 def check_status(status: torch.Tensor) -> None:

@@ -217,6 +217,53 @@ def test_status_word_reports_bad_slots_without_fault(dev, K):
     assert int(status.item()) & _lib.WKV7_STATUS_SEQLENS
 
 
+def test_status_word_reports_slot_clashes(dev, K):
+    """Two rows of an in-place pool call on one slot set WKV7_STATUS_SLOT_CLASH, and so does, with h0 and ht one
+    pool, a row storing where another reads its initial state; distinct slots, a row reading and writing its own
+    slot, and fresh rows reading nothing leave the word at zero.  Every kernel exits normally."""
+    from rwkv_next_amd import _lib
+    import rwkv_next_amd.synth as synth
+    B, T, S_slots = 4, 2, 8
+    say("status word, slot clashes")
+    ops = operands(B, T, H8, seed=75)
+    x = to_dev(ops, dev)
+    pool0 = synth.state_np((S_slots, H8, 64, 64), seed=76)
+    status = K.new_status(dev)
+    K.wkv7_pool_(*x, torch.from_numpy(pool0).to(dev), torch.tensor([6, 1, 4, 3], device=dev), H8, 64, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    K.wkv7_pool_(*x, torch.from_numpy(pool0).to(dev), torch.tensor([6, 1, 6, 3], device=dev), H8, 64, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == _lib.WKV7_STATUS_SLOT_CLASH
+    with pytest.raises(ValueError, match="share a state slot"):
+        K.check_status(status)
+    # the C ABI with separate index lists on one pool: row 2 stores into slot 5, which row 0 reads from (unless row 0
+    # starts fresh)
+    import importlib
+    W = importlib.import_module("rwkv_next_amd.kernels.wkv7")  # the package re-exports the function of that name
+    pool = torch.from_numpy(pool0).to(dev)
+    h0_idx = torch.tensor([5, 1, 2, 3], device=dev)
+    ht_idx = torch.tensor([0, 1, 5, 3], device=dev)
+    ops_p, Bp, Tp = W._prep_operands(*x, H8, 64)
+    for fresh0, expect in ((False, _lib.WKV7_STATUS_SLOT_CLASH), (True, 0)):
+        status.zero_()
+        fresh = torch.tensor([fresh0, False, False, False], device=dev, dtype=torch.uint8)
+        W._launch(ops_p, H=H8, num_seqs=Bp, T=Tp, total=Bp * Tp, o=torch.empty_like(ops_p[3]), h0=pool,
+                  h0_idx=h0_idx, h0_rows=S_slots, ht=pool, ht_idx=ht_idx, ht_rows=S_slots, fresh=fresh,
+                  status=status)
+        torch.cuda.synchronize()
+        assert int(status.item()) == expect, (fresh0, int(status.item()))
+    # more rows than the check covers: not checked (no bit), and the call still runs
+    n = _lib.WKV7_STATUS_CLASH_MAX_SEQS + 1
+    big = operands(n, 1, H8, seed=77)
+    status.zero_()
+    slots = torch.arange(n, device=dev)
+    slots[7] = 3
+    K.wkv7_pool_(*to_dev(big, dev), torch.zeros(n, H8, 64, 64, device=dev), slots, H8, 64, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+
+
 def test_status_word_reports_w_outside_the_chunked_range(dev, K):
     """A dense T = 100 call runs the chunked kernels: with the model's w (<= -0.5) the word stays zero; one w above
     WKV7_CHUNK_W_MAX sets WKV7_STATUS_DECAY (every kernel still exits normally); a token-serial call with the same w
