@@ -85,6 +85,31 @@ def test_matmul_matches_oracle(B, M, N, K, g, split):
     _check(Cb[None], a, lo, hi, sc, g, KERNEL_TOL, bf16_out=True)
 
 
+@pytest.mark.parametrize("B,M,N,K,g,shared,split", [
+    (1, 80, 384, 640, 64, True, None),      # chains of one chunk (group_k = 64), two M groups of 64 rows
+    (3, 70, 272, 512, 128, True, None),     # a batch sharing one weight; N not a multiple of 128
+    (2, 150, 640, 1024, 256, False, None),  # four 16-row tiles per wavefront, one K part, three M groups
+    (1, 96, 1024, 2048, 128, True, 3),      # split-K with uneven ranges of chains
+])
+def test_wide_kernel_matches_oracle(B, M, N, K, g, shared, split):
+    """M > 32 runs the wide kernel (row-sum pre-pass, K parts, chains per quantisation group); planes and packed give
+    the same bits."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    say("int6_matmul wide kernel", dict(B=B, M=M, N=N, K=K, g=g, shared=shared, split=split))
+    rng = np.random.default_rng(300 + M + N + K)
+    lo, hi, sc = _weights(rng, 1 if shared else B, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    if shared:
+        Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    C = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
+    pk = I6.prepack_int6(Ld, Hd, Sd, g)
+    Cp = I6.int6_matmul(a.to(DEV), pk, split_k=split, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(C, Cp)
+    _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=shared)
+
+
 @pytest.mark.parametrize("shared", [True, False])
 def test_batched(shared):
     from rwkv_next_amd.kernels import int6_gemm as I6
