@@ -110,6 +110,36 @@ def test_wide_kernel_matches_oracle(B, M, N, K, g, shared, split):
     _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=shared)
 
 
+@pytest.mark.parametrize("seed", range(8))
+def test_random_shapes_match_oracle(seed):
+    """Seeded random shapes across both kernels: M in [1, 256] (weighted to the 16/32/64/128 tile edges), N a
+    multiple of 16 up to 1280, K a multiple of 64 up to 2560, group_k in {64, 128, 256} dividing K, one or two
+    batches with a shared or per-batch weight, automatic or forced split-K; planes and packed weights give the same
+    bits, and the fp32 result is within KERNEL_TOL of the oracle."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    rng = np.random.default_rng(7000 + seed)
+    M = int(rng.choice([1, 2, 15, 16, 17, 31, 32, 33, 63, 64, 65, 127, 128, 129, 200, 256])) if rng.random() < 0.6 \
+        else int(rng.integers(1, 257))
+    N = 16 * int(rng.integers(1, 81))
+    g = int(rng.choice([64, 128, 256]))
+    K = g * int(rng.integers(1, 2560 // g + 1))
+    B = int(rng.integers(1, 3))
+    shared = bool(rng.random() < 0.5)
+    split = None if rng.random() < 0.5 else int(rng.integers(1, 9))
+    say("int6_matmul random", dict(seed=seed, B=B, M=M, N=N, K=K, g=g, shared=shared, split=split))
+    lo, hi, sc = _weights(rng, 1 if shared else B, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    if shared:
+        Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    C = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
+    Cp = I6.int6_matmul(a.to(DEV), I6.prepack_int6(Ld, Hd, Sd, g), split_k=split, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert C.shape == (B, M, N)
+    assert torch.equal(C, Cp)
+    _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=shared)
+
+
 @pytest.mark.parametrize("shared", [True, False])
 def test_batched(shared):
     from rwkv_next_amd.kernels import int6_gemm as I6

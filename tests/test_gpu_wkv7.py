@@ -190,6 +190,54 @@ def test_chain_kernel_many_chains(dev, K):
     assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
 
 
+@pytest.mark.parametrize("algo", list(ALGOS))
+@pytest.mark.parametrize("seed", [2, 4, 5, 6, 7, 10])
+def test_random_ragged_batches(dev, K, algo, seed):
+    """Seeded random ragged batches on every algorithm: 1 to 12 rows whose lengths are drawn with weight on the
+    token-serial bound and the chunk edges (0, 1, 31, 32, 33, 63, 64, 65, 127, 128, 129) and otherwise uniform in
+    [0, 300), 1 to 12 heads, distinct random pool slots, fresh rows, n_keep limits and a tight or absent max_len.
+    Every kept output and every state against the oracle, the status word clean, other slots untouched."""
+    from oracle import rel_max, wkv7_ref
+    import rwkv_next_amd.synth as synth
+    rng = np.random.default_rng(4000 + seed)
+    H = int(rng.choice([1, 3, 8, 12]))
+    B = int(rng.integers(1, 13))
+    edges = [0, 1, 31, 32, 33, 63, 64, 65, 127, 128, 129]
+    lens = [int(rng.choice(edges)) if rng.random() < 0.6 else int(rng.integers(0, 300)) for _ in range(B)]
+    if sum(lens) == 0:
+        lens[0] = 65
+    S_slots = B + 5
+    slots = rng.permutation(S_slots)[:B].astype(np.int64)
+    fresh = rng.random(B) < 0.25
+    n_keep = np.array([L if rng.random() < 0.7 else int(rng.integers(0, L + 1)) for L in lens], np.int64)
+    max_len = max(lens) if seed % 2 else 0
+    say("random ragged", seed, algo, "H", H, "lens", lens, "n_keep", n_keep.tolist(), "max_len", max_len)
+    seqs = [operands(1, L, H, seed=500 + 13 * seed + i) for i, L in enumerate(lens)]
+    cat = {n: np.concatenate([s[n] for s in seqs], axis=1) for n in seqs[0]}
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool0 = synth.state_np((S_slots, H, 64, 64), seed=600 + seed)
+    pool_in = pool0.copy()
+    pool_in[slots[fresh]] = 0.0
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(cat), pool_in, cu_seqlens=cu, state_idx=slots, n_keep=n_keep)
+    pool = torch.from_numpy(pool0).to(dev)
+    status = K.new_status(dev)
+    o = K.wkv7_pool_(*to_dev(cat, dev), pool, torch.from_numpy(slots).to(dev), H, 64,
+                     cu_seqlens=torch.from_numpy(cu).to(dev), n_keep=torch.from_numpy(n_keep).to(dev),
+                     fresh=torch.from_numpy(fresh).to(dev), max_len=max_len, algo=ALGOS[algo], status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    keep = np.zeros(sum(lens), bool)
+    for i in range(B):
+        keep[cu[i]:cu[i] + min(lens[i], n_keep[i])] = True
+    if keep.any():
+        eo = rel_max(as_np(o).reshape(o_ref.shape)[:, keep], o_ref[:, keep])
+        assert eo <= Y_TOL, f"y max-rel {eo:.3e}"
+    es = rel_max(as_np(pool), pool_ref)
+    assert es <= S_TOL, f"state max-rel {es:.3e}"
+    untouched = np.setdiff1d(np.arange(S_slots), slots)
+    assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
+
+
 def test_pool_final_false_leaves_pool_untouched(dev, K):
     from oracle import wkv7_ref
     import rwkv_next_amd.synth as synth
