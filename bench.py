@@ -186,7 +186,12 @@ def mixed_bench(torch, kernels, synth, dev, steps, warmup):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    return {"ms": ms, "tokens": total, "tok_s": total / (ms * 1e-3), "prefill_lens": sorted(v for v in lens if v > 1)}
+    # HBM roofline: every (row, head) reads and writes its 16 KB state once, and every head-token moves 896 B of
+    # operands and output
+    nbytes = H * (len(lens) * 2 * 64 * 64 * 4 + total * 896)
+    t_roof_us = nbytes / (HBM_PEAK_GBS * 1e3)
+    return {"ms": ms, "tokens": total, "tok_s": total / (ms * 1e-3), "prefill_lens": sorted(v for v in lens if v > 1),
+            "algorithmic_bytes": nbytes, "t_roof_us": t_roof_us, "frac": t_roof_us / (ms * 1e3)}
 
 
 def graph_us(torch, fns, steps, warmup):
