@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""WKV7 recurrence benchmark on one MI355X (BASELINE.json metric: decode GB/s at B=64, H=64; prefill tok/s at
+"""WKV7 recurrence benchmark on one MI355X (headline metric: decode GB/s at B=64, H=64; prefill tok/s at
 T=4096).  Prints ONE JSON line.
 
 Headline step ("value"): one decode token for B = 64 sequences drawn from a 128-slot fp32 pool, H = 64, through 32
@@ -516,7 +516,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
-        "data": "synthetic (seeded; BASELINE distributions), bf16 operands, fp32 state pools",
+        "data": "synthetic (seeded; the reference test's input distributions), bf16 operands, fp32 state pools",
         "config": {"workload": "decode B=64 H=64 T=1 over 32 layer slices of a [128,64,64,64] fp32 pool, "
                                "one HIP graph of 32 launches per step",
                    "B": 64, "H": 64, "head_size": 64, "slots": 128, "layers": 32},

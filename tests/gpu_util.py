@@ -5,7 +5,7 @@ import numpy as np
 
 import rwkv_next_amd.synth as synth
 
-# Tolerances (BASELINE: y <= 2e-2, final state <= 1e-4, both max|x - y| / max|y| against the fp64 recurrence on
+# Tolerances (the parity bar: y <= 2e-2, final state <= 1e-4, both max|x - y| / max|y| against the fp64 recurrence on
 # the same bf16-rounded inputs).
 Y_TOL = 2e-2
 S_TOL = 1e-4

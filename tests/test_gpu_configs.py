@@ -1,4 +1,5 @@
-"""Parity at BASELINE.json's full sizes (seeded synthetic inputs, seed = 1000 + config index):
+"""Parity at the full sizes of the five benchmark configurations (seeded synthetic inputs, seed = 1000 +
+config index):
 
   config 0  the reference's CPU-runnable case, B = 1, T = 512, H = 12 (fp32 on the CPU there; here the same
             operands rounded to bf16, the kernels' input type), on every algorithm

@@ -139,7 +139,7 @@ def test_model_wrapper_casts_and_reshapes(dev, K):
 
 
 def test_speculative_verify_and_rollback_across_layers(dev, K):
-    """BASELINE config 4 wired through the pool: every layer verifies T tokens (pool untouched, snapshots taken),
+    """Configuration 4 (speculative verify, B=64, T=5) wired through the pool: every layer verifies T tokens (pool untouched, snapshots taken),
     then rollback_ restores each row's accepted prefix in every layer.  The result equals, bit for bit, the
     reference's method -- wkv7_replay of the first n[b] tokens per layer from the incoming states (model.py:498-503)
     -- eagerly and inside one captured HIP graph replayed three times (the pool reset eagerly between replays)."""

@@ -255,7 +255,7 @@ def test_pool_final_false_leaves_pool_untouched(dev, K):
 
 
 def test_snapshots_are_bit_identical_to_a_rerun(dev, K):
-    """BASELINE config 4 contract at a small size: after a verify of T tokens with snapshots, restoring the state
+    """The speculative-verify contract (configuration 4) at a small size: after a verify of T tokens with snapshots, restoring the state
     after n accepted tokens equals, bit for bit, re-running the first n tokens."""
     import rwkv_next_amd.synth as synth
     say("snapshots")

@@ -272,7 +272,7 @@ def test_exact_rational_brute_force_on_tiny_inputs():
 
 
 def test_fp32_vs_fp64_gap_on_config0():
-    """Calibrates the tolerances: the fp32 recurrence's own distance from fp64 on BASELINE config 0
+    """Calibrates the tolerances: the fp32 recurrence's own distance from fp64 on configuration 0
     (B=1, T=512, H=12; synthetic distributions).  The GPU is held to y <= 2e-2 and state <= 1e-4 (max-relative)."""
     import rwkv_next_amd.synth as synth
     ops = synth.operands_np((1, 512, 12, 64), seed=1000)
