@@ -523,13 +523,7 @@ constexpr int part_bytes() { return part_a_bytes<MTW>() + 16 * MTW * 4 + (PACKED
 
 __device__ __forceinline__ int a_slot(int r, int j) { return 8 * r + (j ^ ((r >> 1) & 7)); }
 
-// f(std::integral_constant<int, 0>{}), .., f(std::integral_constant<int, N - 1>{})
-template <typename F, int... J>
-__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, J...>) {
-    (f(std::integral_constant<int, J>{}), ...);
-}
-template <int N, typename F>
-__device__ __forceinline__ void unroll(F&& f) { unroll_seq(f, std::make_integer_sequence<int, N>{}); }
+using wkv7::unroll;  // f(integral_constant<0>), .., f(integral_constant<N - 1>)
 
 typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
 

@@ -914,28 +914,86 @@ __device__ __forceinline__ void state_operand_block(const f4& X, const f4& Y, bf
 
 constexpr int kPlanSortRows = 4096;    // ragged calls: longest-first ordering of up to this many chunked rows
 constexpr int kScanRaggedGrid = 2048;  // ragged calls: scan workgroups (about two rounds of residency)
-constexpr int kScanDepth = 2;  // chunk records in flight per lane (register ring)
+constexpr int kScanDepth = 4;  // chunk record register sets per lane (three in flight, one in use)
+// Chunks per pass of the scan's main loop, fully unrolled: the compiler counts outstanding loads exactly only within
+// straight-line code and drains them all at a loop header, so a long body keeps the record loads in flight across
+// most chunks (the remaining chunks run in passes of kScanDepth).
+constexpr int kScanUnroll = 16;
 
-// A workgroup of two wavefronts owns one (row, head, 16-column group vg); block b -> XCD b % 8, and the 4 groups of a
-// (row, head) share an XCD, so 3 of the 4 reads of a chunk's A and Q hit that XCD's L2.  Wavefront hf holds row
-// tiles 2 hf, 2 hf + 1 of the state: lane (i, q) holds S[16 r + 4 q + e][16 vg + i] -- the layout of a 16x16 MFMA
-// result -- so the state stays in registers from chunk to chunk.  Each chunk the wavefront re-forms its two tiles as
-// the 16x16x32 operand of contraction block hf with two lane swaps per register (state_operand_block), the two
-// operand halves are exchanged through LDS (double-buffered: one barrier per chunk), and it runs
-//     S <- A S + H   for its row tiles (12 MFMAs: 2 row tiles x 2 contraction blocks, 3 terms on the hi/lo split)
-//     y^T = S^T Q^T + O_intra^T   for token tiles 2 hf, 2 hf + 1 (4 MFMAs on S hi).
-// (One wavefront holding all four row tiles needs no exchange but issues 32 MFMAs per chunk on one SIMD: measured
-// 61 us for one row of T = 4096, H = 64 against 56 us for this split.)
-// Chunk records stream through a ring of kScanDepth register sets.  Every step issues the same memory operations
-// (the refill index is clamped to the last chunk; stores that must not land go to the workspace's trash record), so
-// the compiler counts the outstanding loads exactly and waits only for the record about to be used.
+// The shares of a chunk record in the scan: state wavefront r (row tile r) reads A's row tile r (hi, lo, both
+// contraction blocks) and H^T's k tile r; output wavefront t reads Q's token tile t and the O_intra pair holding it.
+struct ScanRecS {
+    s8 ah[2], al[2];  // [k block c]
+    f4 h;
+};
+struct ScanRecY {
+    s8 q[2];  // [k block c]
+    s8 o;     // token tile pair t / 2
+};
+
+// The record loads go through a buffer resource at the record (wave-uniform) with the lane's 16-byte slot as the
+// vector offset and the share's offset as the scalar one, so a refill costs no vector address arithmetic.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rec_rsrc(const char* rec) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(uniform_ptr(rec)), 0, kChunkBytes,
+                                             0x00020000 /* raw 32-bit buffer, gfx9 family */);
+}
+__device__ __forceinline__ s8 rec_s8(__amdgpu_buffer_rsrc_t r, int lo, int off) {
+    return __builtin_bit_cast(s8, __builtin_amdgcn_raw_buffer_load_b128(r, lo, off, 0));
+}
+
+__device__ __forceinline__ void scan_load_s(ScanRecS& r, const char* rec, int vg, int t, int lane) {
+    const __amdgpu_buffer_rsrc_t rs = rec_rsrc(rec);
+    const int lo = lane * 16;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+        r.ah[c] = rec_s8(rs, lo, REC_AH + (t * 2 + c) * 1024);
+        r.al[c] = rec_s8(rs, lo, REC_AL + (t * 2 + c) * 1024);
+    }
+    r.h = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(rs, lo, REC_HT + (vg * 4 + t) * 1024, 0));
+}
+
+__device__ __forceinline__ void scan_load_y(ScanRecY& r, const char* rec, int vg, int t, int lane) {
+    const __amdgpu_buffer_rsrc_t rs = rec_rsrc(rec);
+    const int lo = lane * 16;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) r.q[c] = rec_s8(rs, lo, REC_Q + (t * 2 + c) * 1024);
+    r.o = rec_s8(rs, lo, REC_OT + (vg * 2 + (t >> 1)) * 1024);
+}
+
+// The state of one column group as published each chunk for the 16x16x32 operands: [row tile][column][row in tile]
+// bf16, hi and lo (column-major within a tile, so that the 8 consecutive rows an operand lane needs are 16 contiguous
+// bytes, and the 4 rows a result lane holds are 8).
+struct ScanEx {
+    __bf16 v[2][2][4][16][16];  // [buffer][hi, lo][row tile][column][row]
+};
+
+// A workgroup of eight wavefronts owns one (row, head, 16-column group vg); block b -> XCD b % 8, and the 4 groups
+// of a (row, head) share an XCD, so 3 of the 4 reads of a chunk's A and Q hit that XCD's L2.
+//   * State wavefront r = 0..3 holds row tile r of the state in the 16x16 MFMA result layout -- lane (i, q) holds
+//     S[16 r + 4 q + e][16 vg + i], e = 0..3 -- so the state stays in registers from chunk to chunk.  Each chunk it
+//     runs  S_r <- A_r S + H_r  (6 MFMAs: 2 contraction blocks, 3 terms on the hi/lo split), splits the new tile hi/lo
+//     and publishes it in LDS (one 8-byte store per lane and part; double-buffered, one workgroup barrier per chunk);
+//     after the barrier every wavefront reads the operand of contraction block c (rows 32 c + 8 q .. + 7 of column
+//     i) as one 16-byte load per part.
+//   * Output wavefront 4 + t computes  y_t^T = S^T Q_t^T + O_intra,t^T  for token tile t (2 MFMAs on S hi) from the
+//     same published operands, off the state's dependency chain.
+// Chunk records stream through a ring of kScanDepth register sets per wavefront (each loads only its share).  Every
+// step issues the same memory operations (the refill index is clamped to the last chunk; stores that must not land
+// go to the workspace's trash record), so within a pass the compiler counts the outstanding loads exactly and waits
+// only for the record about to be used.
+// Measured for one row of T = 4096, H = 64 (cycle stamps per phase in an instrumented copy): a chunk step is bound by
+// the CU's vector-memory pipeline, not by the MFMA chain -- each workgroup streams about 30 KB of record per chunk
+// (all of A and Q, its slices of H and O_intra), and issuing a 16-byte-per-lane load waits about 110 cycles for the
+// pipeline.  This layout takes 51 us; two wavefronts each holding two row tiles, re-forming operands with lane swaps
+// and computing y themselves, 56 us; one wavefront holding all four row tiles, 61 us.
 // One work item b of the scan: (row, head) pair (b >> 5) * 8 + (b & 7) of the rows the call chunks, column group
 // (b >> 3) & 3 -- numbered so that, with a grid (or grid stride) that is a multiple of 8, the 4 column groups of a
 // pair run on one XCD and share its L2.  `rows` is the number of chunked rows; `row_of` lists them (ragged calls) or
 // is null (dense calls: every row).  `buf` is the exchange buffer index, carried across a workgroup's items.
+constexpr int kScanWaves = 8;
 __device__ __forceinline__ void scan_item(const Params& p, char* __restrict__ wsc, const int32_t* __restrict__ plan,
                                           int64_t max_chunks, int ncps, int64_t b, int64_t rows,
-                                          const int32_t* row_of, bf8 (&ex)[2][2][2][64], int& buf) {
+                                          const int32_t* row_of, ScanEx& ex, int& buf) {
     const int xcd = (int)(b & 7), rsl = (int)(b >> 3), vg = rsl & 3;
     const int64_t pair = (int64_t)(rsl >> 2) * 8 + xcd;
     if (pair >= rows * p.H) return;  // uniform over the workgroup, as are the returns below
@@ -947,7 +1005,9 @@ __device__ __forceinline__ void scan_item(const Params& p, char* __restrict__ ws
     if (!owns_row(p, L)) return;
 
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
-    const int hf = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int t = wv & 3;        // row tile (state wavefronts) or token tile (output wavefronts)
+    const bool ywave = wv >= 4;  // wave-uniform role
     const int64_t j0 = p.cu ? (int64_t)plan[2 * max_chunks + n] : (int64_t)n * ncps;
     // the chunk table never exceeds max_chunks for valid cu_seqlens; the clamp keeps invalid ones in bounds
     const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((L + C - 1) / C, max_chunks - j0));
@@ -955,118 +1015,127 @@ __device__ __forceinline__ void scan_item(const Params& p, char* __restrict__ ws
     float* dst = state_dst(p, n, h);
     const int col = 16 * vg + i;  // the state column this lane holds
 
-    f4 S[2];  // row tiles 2 hf, 2 hf + 1
+    f4 S;  // state wavefronts: row tile t
+    if (!ywave) {
 #pragma unroll
-    for (int x = 0; x < 2; ++x) {
+        for (int e = 0; e < 4; ++e) S[e] = src ? src[(16 * t + 4 * q + e) * HS + col] : 0.f;
+        if (nch == 0 && dst) {  // no chunks (length 0): the state passes through
 #pragma unroll
-        for (int e = 0; e < 4; ++e) S[x][e] = src ? src[(16 * (2 * hf + x) + 4 * q + e) * HS + col] : 0.f;
-    }
-    if (nch == 0) {  // no chunks (length 0): the state passes through
-        if (dst) {
-#pragma unroll
-            for (int x = 0; x < 2; ++x) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) dst[(16 * (2 * hf + x) + 4 * q + e) * HS + col] = S[x][e];
-            }
+            for (int e = 0; e < 4; ++e) dst[(16 * t + 4 * q + e) * HS + col] = S[e];
         }
-        return;
     }
+    if (nch == 0) return;
+    // state operands of the chunk about to run, as 16x16x32 blocks c = 0, 1 (the output wavefronts use only hi)
     bf8 Bh[2], Bl[2];
-    auto exchange = [&]() {  // this half's operand block out, the other half's in
-        bf8 oh, ol;
-        state_operand_block(S[0], S[1], oh, ol);
-        ex[buf][hf][0][lane] = oh;
-        ex[buf][hf][1][lane] = ol;
-        __syncthreads();
-        const bf8 th = ex[buf][1 - hf][0][lane], tl = ex[buf][1 - hf][1][lane];
-        // whole-vector selects on the wave-uniform hf (an element index into Bh would become per-element selects)
-        Bh[0] = hf ? th : oh;
-        Bl[0] = hf ? tl : ol;
-        Bh[1] = hf ? oh : th;
-        Bl[1] = hf ? ol : tl;
-        buf ^= 1;  // the next writes go to the other buffer: the partner has read this one before the next barrier
+    auto publish = [&]() {  // state wavefronts: rows 4 q .. 4 q + 3 of column i of tile t, hi and lo
+        s4 hv, lv;
+        split4(S, hv, lv);
+        *reinterpret_cast<s4*>(&ex.v[buf][0][t][i][4 * q]) = hv;
+        *reinterpret_cast<s4*>(&ex.v[buf][1][t][i][4 * q]) = lv;
     };
-    exchange();
+    auto collect = [&]() {  // after the barrier: rows 32 c + 8 q .. + 7 (tile 2 c + q / 2, rows 8 (q & 1) ..) of column i
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            Bh[c] = *reinterpret_cast<const bf8*>(&ex.v[buf][0][2 * c + (q >> 1)][i][8 * (q & 1)]);
+            if (!ywave) Bl[c] = *reinterpret_cast<const bf8*>(&ex.v[buf][1][2 * c + (q >> 1)][i][8 * (q & 1)]);
+        }
+        buf ^= 1;  // the next writes go to the other buffer: every wavefront reads this one before the next barrier
+    };
+    if (!ywave) publish();
+    __syncthreads();
+    collect();
 
     const char* const rec0 = wsc + (j0 * p.H + h) * (int64_t)kChunkBytes;
     const int64_t rec_stride = (int64_t)p.H * kChunkBytes;
-    // stores that must not land go to the trash record, 2 KB per block slot (24 slots) so that blocks do not all hit
-    // the same lines
-    char* const trash = wsc + max_chunks * p.H * (int64_t)kChunkBytes + (int)(b % 24) * 2048 + lane * 8;
-    uint16_t* const obase = p.o ? p.o + bos * p.o_tok_stride + (int64_t)h * HS + 16 * vg + 4 * q : nullptr;
-
-    ScanRecH ring[kScanDepth];
+    if (!ywave) {
+        ScanRecS ring[kScanDepth];
 #pragma unroll
-    for (int d = 0; d < kScanDepth; ++d) scan_load_half(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, vg, hf, lane);
+        for (int d = 0; d < kScanDepth - 1; ++d) scan_load_s(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, vg, t, lane);
+        // chunk cc (ring set d = cc % kScanDepth, a compile-time index in every unrolled copy)
+        auto step = [&](int cc, auto D) __attribute__((always_inline)) {
+            constexpr int d = decltype(D)::value;
+            // the set used one chunk ago takes the record kScanDepth - 1 chunks ahead; its loads issue while the
+            // exchange's LDS reads are in flight
+            scan_load_s(ring[(d + kScanDepth - 1) % kScanDepth],
+                        rec0 + std::min(cc + kScanDepth - 1, nch - 1) * rec_stride, vg, t, lane);
+            const ScanRecS& R = ring[d];
+            // two accumulators (one per contraction block), interleaved so that no MFMA waits on the one before
+            f4 n0 = R.h, n1 = zero4();
+            const bf8 ah0 = __builtin_bit_cast(bf8, R.ah[0]), al0 = __builtin_bit_cast(bf8, R.al[0]);
+            const bf8 ah1 = __builtin_bit_cast(bf8, R.ah[1]), al1 = __builtin_bit_cast(bf8, R.al[1]);
+            n0 = mfma_bf16(ah0, Bl[0], n0);
+            n1 = mfma_bf16(ah1, Bl[1], n1);
+            n0 = mfma_bf16(al0, Bh[0], n0);
+            n1 = mfma_bf16(al1, Bh[1], n1);
+            n0 = mfma_bf16(ah0, Bh[0], n0);
+            n1 = mfma_bf16(ah1, Bh[1], n1);
+            if (cc < nch) {  // wave-uniform
 #pragma unroll
-    for (int d = 0; d < kScanDepth; ++d) settle(ring[d]);
-    for (int c0 = 0; c0 < nch; c0 += kScanDepth) {
-#pragma unroll
-        for (int d = 0; d < kScanDepth; ++d) {
-            const int cc = c0 + d;
-            const bool live = cc < nch;  // wave-uniform
-            ScanRecH& R = ring[d];
-            f4 nS[2];
-#pragma unroll
-            for (int x = 0; x < 2; ++x) nS[x] = R.h[x];
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-#pragma unroll
-                for (int x = 0; x < 2; ++x) {
-                    const bf8 ah = __builtin_bit_cast(bf8, R.ah[x][c]), al = __builtin_bit_cast(bf8, R.al[x][c]);
-                    nS[x] = mfma_bf16(ah, Bl[c], nS[x]);
-                    nS[x] = mfma_bf16(al, Bh[c], nS[x]);
-                    nS[x] = mfma_bf16(ah, Bh[c], nS[x]);
-                }
+                for (int e = 0; e < 4; ++e) S[e] = n0[e] + n1[e];
             }
-            f4 y[2];
+            publish();
+            __syncthreads();
+            collect();
+        };
+        int c0 = 0;
+        for (; c0 + kScanUnroll <= nch; c0 += kScanUnroll)
+            unroll<kScanUnroll>([&](auto J) __attribute__((always_inline)) {
+                step(c0 + decltype(J)::value, std::integral_constant<int, decltype(J)::value % kScanDepth>{});
+            });
+        for (; c0 < nch; c0 += kScanDepth)
+            unroll<kScanDepth>([&](auto J) __attribute__((always_inline)) { step(c0 + decltype(J)::value, J); });
+        if (dst) {
 #pragma unroll
-            for (int x = 0; x < 2; ++x) {
-                const s4 o4 = half4(R.o, x);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) y[x][e] = bf16_to_f32((uint16_t)o4[e]);
-#pragma unroll
-                for (int c = 0; c < 2; ++c) y[x] = mfma_bf16(Bh[c], __builtin_bit_cast(bf8, R.q[x][c]), y[x]);
-            }
-            // the refill reuses the slot's registers only if it is not scheduled above the slot's last use
-            __builtin_amdgcn_sched_barrier(0);
-            scan_load_half(R, rec0 + std::min(cc + kScanDepth, nch - 1) * rec_stride, vg, hf, lane);
-#pragma unroll
-            for (int x = 0; x < 2; ++x) {
-                // lane (i, q) holds y[token 16 t + i][columns 16 vg + 4 q .. + 3], t = 2 hf + x
-                const int t = 2 * hf + x;
-                const int tok = cc * C + 16 * t + i;
-                uint2 pk;
-                pk.x = pack_bf16x2(y[x][0], y[x][1]);
-                pk.y = pack_bf16x2(y[x][2], y[x][3]);
-                char* const out = (live && tok < L && obase)
-                                      ? reinterpret_cast<char*>(obase + (int64_t)tok * p.o_tok_stride)
-                                      : trash + t * 512;
-                *reinterpret_cast<uint2*>(out) = pk;
-            }
-            if (live) {
-#pragma unroll
-                for (int x = 0; x < 2; ++x) S[x] = nS[x];
-            }
-            exchange();
+            for (int e = 0; e < 4; ++e) dst[(16 * t + 4 * q + e) * HS + col] = S[e];
         }
-    }
-    if (dst) {
+    } else {
+        // stores that must not land go to the trash record, 2 KB per block slot (24 slots) so that blocks do not all
+        // hit the same lines
+        char* const trash = wsc + max_chunks * p.H * (int64_t)kChunkBytes + (int)(b % 24) * 2048 + lane * 8;
+        uint16_t* const obase = p.o ? p.o + bos * p.o_tok_stride + (int64_t)h * HS + 16 * vg + 4 * q : nullptr;
+        ScanRecY ring[kScanDepth];
 #pragma unroll
-        for (int x = 0; x < 2; ++x) {
+        for (int d = 0; d < kScanDepth - 1; ++d) scan_load_y(ring[d], rec0 + std::min(d, nch - 1) * rec_stride, vg, t, lane);
+        auto step = [&](int cc, auto D) __attribute__((always_inline)) {
+            constexpr int d = decltype(D)::value;
+            scan_load_y(ring[(d + kScanDepth - 1) % kScanDepth],
+                        rec0 + std::min(cc + kScanDepth - 1, nch - 1) * rec_stride, vg, t, lane);
+            const ScanRecY& R = ring[d];
+            f4 y;
+            const s4 o4 = half4(R.o, t & 1);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) dst[(16 * (2 * hf + x) + 4 * q + e) * HS + col] = S[x][e];
-        }
+            for (int e = 0; e < 4; ++e) y[e] = bf16_to_f32((uint16_t)o4[e]);
+#pragma unroll
+            for (int c = 0; c < 2; ++c) y = mfma_bf16(Bh[c], __builtin_bit_cast(bf8, R.q[c]), y);
+            // lane (i, q) holds y[token 16 t + i][columns 16 vg + 4 q .. + 3]
+            const int tok = cc * C + 16 * t + i;
+            uint2 pk;
+            pk.x = pack_bf16x2(y[0], y[1]);
+            pk.y = pack_bf16x2(y[2], y[3]);
+            char* const out = (cc < nch && tok < L && obase)
+                                  ? reinterpret_cast<char*>(obase + (int64_t)tok * p.o_tok_stride)
+                                  : trash + t * 512;
+            *reinterpret_cast<uint2*>(out) = pk;
+            __syncthreads();  // the state wavefronts have published the next chunk's operands
+            collect();
+        };
+        int c0 = 0;
+        for (; c0 + kScanUnroll <= nch; c0 += kScanUnroll)
+            unroll<kScanUnroll>([&](auto J) __attribute__((always_inline)) {
+                step(c0 + decltype(J)::value, std::integral_constant<int, decltype(J)::value % kScanDepth>{});
+            });
+        for (; c0 < nch; c0 += kScanDepth)
+            unroll<kScanDepth>([&](auto J) __attribute__((always_inline)) { step(c0 + decltype(J)::value, J); });
     }
 }
 
 // Dense calls: one item per workgroup.  Ragged calls: a bounded grid walks the items of the rows the plan marked as
 // chunked (a grid over every row would be almost all empty workgroups when decode rows dominate, and their dispatch
 // costs more than the work).
-__global__ __launch_bounds__(128) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
-                                                              const int32_t* __restrict__ plan, int64_t max_chunks,
-                                                              int ncps) {
-    __shared__ bf8 ex[2][2][2][64];  // [buffer][half][hi, lo][lane]
+__global__ __launch_bounds__(64 * kScanWaves) void wkv7_chunk_scan_kernel(const Params p, char* __restrict__ wsc,
+                                                                          const int32_t* __restrict__ plan,
+                                                                          int64_t max_chunks, int ncps) {
+    __shared__ __attribute__((aligned(16))) ScanEx ex;
     int buf = 0;
     if (!p.cu) {
         scan_item(p, wsc, plan, max_chunks, ncps, blockIdx.x, p.num_seqs, nullptr, ex, buf);
@@ -1175,7 +1244,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 // Chain kernel: a whole ragged step (token-serial rows and chunked rows) in one dispatch, with no workspace.
 // Each workgroup takes whole (row, head) chains of chunked rows and walks their chunks in order: prep_item builds
 // the chunk's record in LDS and chain_step applies it at once to the state, which stays in the registers of the
-// eight wavefronts (wavefront wv: column group wv >> 1, rows half wv & 1, the scan's layout).  So the 48 KB record
+// eight wavefronts (wavefront wv: column group wv >> 1, row tiles 2 (wv & 1), 2 (wv & 1) + 1).  So the 48 KB record
 // never leaves the CU, and no second kernel, plan kernel or cross-workgroup synchronisation is needed.  The price is
 // that a chain's chunks are serial on one CU: the launcher picks this kernel when the rows are short enough for that
 // not to set the call's length (many chains, few chunks each -- a continuous-batching step of prefill rows and
@@ -1184,7 +1253,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // One chunk of a chain on the LDS record `rec`: y <- Q S + O_intra for this wavefront's token tiles 2 hf, 2 hf + 1
 // (column group vg), S <- A S + H for its row tiles, then the new state's operand halves are exchanged through
-// `ex` (one barrier).  (Bh, Bl) hold the state at the chunk start as 16x16x32 operands, as in scan_item.
+// `ex` (one barrier).  (Bh, Bl) hold the state at the chunk start as the 16x16x32 operands of contraction blocks 0, 1.
 __device__ __forceinline__ void chain_step(const Params& p, const char* rec, f4 (&S)[2], bf8 (&Bh)[2], bf8 (&Bl)[2],
                                            bf8 (*ex)[2][64], int vg, int hf, int lane, int64_t bos, int c, int L,
                                            int h) {
@@ -1485,7 +1554,7 @@ hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* works
     const int64_t pairs = (int64_t)p.num_seqs * p.H;
     int64_t blocks = ((pairs + 7) / 8) * 8 * 4;
     if (p.cu) blocks = std::min<int64_t>(blocks, kScanRaggedGrid);  // a multiple of 8: see scan_item
-    hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(128), 0, stream, p, wsc, plan,
+    hipLaunchKernelGGL(wkv7_chunk_scan_kernel, dim3((unsigned)blocks), dim3(64 * kScanWaves), 0, stream, p, wsc, plan,
                        ws.max_chunks, ncps);
     return hipGetLastError();
 }

@@ -8,10 +8,22 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+#include <utility>
+
 namespace wkv7 {
 
 constexpr int HS = 64;          // head size, K == V
 constexpr int HS2 = HS * HS;    // state elements per (sequence, head)
+
+// f(std::integral_constant<int, 0>{}), .., f(std::integral_constant<int, N - 1>{}): straight-line copies of a step
+// whose register-array indices must be compile-time constants.
+template <typename F, int... J>
+__device__ __forceinline__ void unroll_seq(F&& f, std::integer_sequence<int, J...>) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll(F&& f) { unroll_seq(f, std::make_integer_sequence<int, N>{}); }
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
