@@ -928,7 +928,7 @@ struct ScanRecS {
 };
 struct ScanRecY {
     s8 q[2];  // [k block c]
-    s8 o;     // token tile pair t / 2
+    s4 o;     // token tile t's half of the O_intra piece of pair t / 2
 };
 
 // The record loads go through a buffer resource at the record (wave-uniform) with the lane's 16-byte slot as the
@@ -957,7 +957,7 @@ __device__ __forceinline__ void scan_load_y(ScanRecY& r, const char* rec, int vg
     const int lo = lane * 16;
 #pragma unroll
     for (int c = 0; c < 2; ++c) r.q[c] = rec_s8(rs, lo, REC_Q + (t * 2 + c) * 1024);
-    r.o = rec_s8(rs, lo, REC_OT + (vg * 2 + (t >> 1)) * 1024);
+    r.o = __builtin_bit_cast(s4, __builtin_amdgcn_raw_buffer_load_b64(rs, lo + 8 * (t & 1), REC_OT + (vg * 2 + (t >> 1)) * 1024, 0));
 }
 
 // The state of one column group as published each chunk for the 16x16x32 operands: [row tile][column][row in tile]
@@ -1102,7 +1102,7 @@ __device__ __forceinline__ void scan_item(const Params& p, char* __restrict__ ws
                         rec0 + std::min(cc + kScanDepth - 1, nch - 1) * rec_stride, vg, t, lane);
             const ScanRecY& R = ring[d];
             f4 y;
-            const s4 o4 = half4(R.o, t & 1);
+            const s4 o4 = R.o;
 #pragma unroll
             for (int e = 0; e < 4; ++e) y[e] = bf16_to_f32((uint16_t)o4[e]);
 #pragma unroll
