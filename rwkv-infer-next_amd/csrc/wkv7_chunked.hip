@@ -984,7 +984,7 @@ struct ScanEx {
 // Measured for one row of T = 4096, H = 64 (cycle stamps per phase in an instrumented copy): a chunk step is bound by
 // the CU's vector-memory pipeline, not by the MFMA chain -- each workgroup streams about 30 KB of record per chunk
 // (all of A and Q, its slices of H and O_intra), and issuing a 16-byte-per-lane load waits about 110 cycles for the
-// pipeline.  This layout takes 51 us; two wavefronts each holding two row tiles, re-forming operands with lane swaps
+// pipeline.  This layout takes 50 us; two wavefronts each holding two row tiles, re-forming operands with lane swaps
 // and computing y themselves, 56 us; one wavefront holding all four row tiles, 61 us.
 // One work item b of the scan: (row, head) pair (b >> 5) * 8 + (b & 7) of the rows the call chunks, column group
 // (b >> 3) & 3 -- numbered so that, with a grid (or grid stride) that is a multiple of 8, the 4 column groups of a
