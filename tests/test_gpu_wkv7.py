@@ -238,6 +238,48 @@ def test_random_ragged_batches(dev, K, algo, seed):
     assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
 
 
+def test_chunked_rows_across_scan_passes(dev, K):
+    """The chunked path's scan walks a row's chunks in unrolled passes of 16 and then passes of 4: rows of 17 to 63
+    chunks use both.  Dense T = 1100 (18 chunks, the last partial) and a ragged batch on the chunked algorithm with
+    rows of 1030, 2100, 64, 5 and 0 tokens (17, 33, 1, 1, 0 chunks), fresh rows and an n_keep limit, against the
+    oracle."""
+    from oracle import rel_max, wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H = 4
+    say("chunked scan passes: dense T=1100")
+    ops = operands(2, 1100, H, seed=91)
+    s0 = (0.3 * np.random.default_rng(92).standard_normal((2, H, 64, 64))).astype(np.float32)
+    o_ref, S_ref, _ = wkv7_ref(*np_list(ops), s0)
+    o, S = K.wkv7(*to_dev(ops, dev), torch.from_numpy(s0).to(dev), H, 64, algo=ALGOS["chunked"])
+    torch.cuda.synchronize()
+    check(o, o_ref, S, S_ref)
+
+    lens = [1030, 2100, 64, 5, 0]
+    say("chunked scan passes: ragged", lens)
+    seqs = [operands(1, L, H, seed=93 + i) for i, L in enumerate(lens)]
+    cat = {n: np.concatenate([s[n] for s in seqs], axis=1) for n in seqs[0]}
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool0 = synth.state_np((8, H, 64, 64), seed=94)
+    slots = np.array([6, 1, 3, 7, 0], np.int64)
+    fresh = np.array([0, 1, 0, 0, 1], bool)
+    n_keep = np.array([1030, 1500, 64, 5, 0], np.int64)
+    pool_in = pool0.copy()
+    pool_in[slots[fresh]] = 0.0
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(cat), pool_in, cu_seqlens=cu, state_idx=slots, n_keep=n_keep)
+    pool = torch.from_numpy(pool0).to(dev)
+    o = K.wkv7_pool_(*to_dev(cat, dev), pool, torch.from_numpy(slots).to(dev), H, 64,
+                     cu_seqlens=torch.from_numpy(cu).to(dev), n_keep=torch.from_numpy(n_keep).to(dev),
+                     fresh=torch.from_numpy(fresh).to(dev), max_len=2100, algo=ALGOS["chunked"])
+    torch.cuda.synchronize()
+    keep = np.zeros(sum(lens), bool)
+    for i in range(len(lens)):
+        keep[cu[i]:cu[i] + min(lens[i], n_keep[i])] = True
+    eo = rel_max(as_np(o).reshape(o_ref.shape)[:, keep], o_ref[:, keep])
+    es = rel_max(as_np(pool), pool_ref)
+    say(f"y max-rel {eo:.3e}  state max-rel {es:.3e}")
+    assert eo <= Y_TOL and es <= S_TOL
+
+
 def test_pool_final_false_leaves_pool_untouched(dev, K):
     from oracle import wkv7_ref
     import rwkv_next_amd.synth as synth
