@@ -1329,11 +1329,18 @@ __device__ __forceinline__ Item chain_item(int h, int64_t bos, int L, int c) {
 // keeps a CU busy for about 10 us; with a few workgroups on the token-serial rows at a time, about 24 pairs take as
 // long as a chunk-item.
 constexpr int kPairsPerItem = 24;
+// Chain assignment: when the workgroups come in whole groups of H (G % H == 0, at most kChainLptGroups groups) and
+// there are at most kChainLptRows chained rows, longest row first, each row's H chains to the group with the least
+// chain work so far; otherwise the snake.  For the mixed step's eight prefill rows (28, 22, 19, 16, 10, 10, 9, 7
+// chunks over 4 groups of 64) that is 28 | 22 + 9 | 19 + 10 | 16 + 10 + 7, the busiest workgroup 33 chunk-items
+// against 35 for the snake's pairs.
+constexpr int kChainLptRows = 64;    // the list of one workgroup's chains holds at most this many
+constexpr int kChainLptGroups = 64;
 
 __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
     __shared__ __attribute__((aligned(16))) PrepSmem sm;
     __shared__ int32_t wave_count[8], wave_count2[8];
-    __shared__ int32_t max_load;
+    __shared__ int32_t max_load, list_len;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int G = (int)gridDim.x, b = (int)blockIdx.x;
@@ -1348,7 +1355,9 @@ __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
     int32_t* const cnch = crow + kChainMaxSeqs;
     int32_t* const srow = cnch + kChainMaxSeqs;
     int32_t* const start = srow + kChainMaxSeqs;                     // [G + 1]
+    int32_t* const list = start + kChainMaxSeqs + 1;                 // [kChainLptRows]: chains j (lpt)
     int nrows, nshort;
+    bool lpt;
     {
         int32_t* const tmp_row = reinterpret_cast<int32_t*>(sm.slot[0]);
         int32_t* const tmp_nch = tmp_row + kChainMaxSeqs;
@@ -1393,12 +1402,37 @@ __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
             crow[rank] = tmp_row[tid];
             cnch[rank] = mine;
         }
-        if (tid == 0) max_load = 0;
+        if (tid == 0) {
+            max_load = 0;
+            list_len = 0;
+        }
         __syncthreads();
-        // chain load (chunk-items) of workgroup tid under the snake assignment
+        // chain load (chunk-items) of workgroup tid; with lpt, this workgroup's chains are listed in `list`
         const int64_t nchains = (int64_t)nrows * p.H;
+        lpt = nrows > 0 && nrows <= kChainLptRows && G % p.H == 0 && G / p.H <= kChainLptGroups;
         int load = 0;
-        if (tid < G) {
+        if (lpt) {
+            // Workgroups g H .. g H + H - 1 form group g.  Each row's H chains go to the least-loaded group (the
+            // lowest index on ties), workgroup g H + h taking head h, so a group's workgroups always carry equal work
+            // and this is exactly the assignment that gives each chain to a least-loaded workgroup.  One thread
+            // deals the rows (rows x groups steps), then every workgroup reads its group's rows.
+            const int groups = G / p.H, gb = b / p.H;
+            int32_t* const gl = reinterpret_cast<int32_t*>(sm.slot[1]);  // [groups] chain work per group, scratch
+            if (tid == 0) {
+                for (int g = 0; g < groups; ++g) gl[g] = 0;
+                for (int r = 0; r < nrows; ++r) {
+                    int best = 0;
+                    for (int g = 1; g < groups; ++g) best = gl[g] < gl[best] ? g : best;
+                    gl[best] += cnch[r];
+                    if (best == gb) list[list_len++] = r * p.H + (b - gb * p.H);
+                }
+            }
+            __syncthreads();
+            if (tid < G) {
+                load = gl[tid / p.H];
+                atomicMax(&max_load, load);
+            }
+        } else if (tid < G) {  // snake
             for (int64_t k = 0;; ++k) {
                 const int64_t j = k * G + ((k & 1) ? G - 1 - tid : tid);
                 if (j >= nchains) break;
@@ -1427,17 +1461,25 @@ __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
         __syncthreads();
     }
 
-    // ---- 2. chains j = rank * H + h, snake-assigned: pass k covers chains [k G, (k + 1) G); workgroup b takes
-    //         k G + b on even passes and k G + G - 1 - b on odd ones (the longest chains are spread over all
-    //         workgroups, and a workgroup with a long chain in one pass gets a short one in the next)
+    // ---- 2. chains j = rank * H + h: this workgroup's list (lpt), or snake-assigned: pass k covers chains
+    //         [k G, (k + 1) G); workgroup b takes k G + b on even passes and k G + G - 1 - b on odd ones (the
+    //         longest chains are spread over all workgroups, and a workgroup with a long chain in one pass gets a
+    //         short one in the next)
     const int64_t nchains = (int64_t)nrows * p.H;
     const int vg = wv >> 1, hf = wv & 1;
     bf8 (*const ex)[2][64] = reinterpret_cast<bf8 (*)[2][64]>(sm.slot[12]) + 2 * vg;  // [hf][hi, lo][lane]
     const int trow = tid >> 3, cb = (tid & 7) * 8;
     const int i = lane & 15, q = lane >> 4, col = 16 * vg + i;
+    const int nlist = list_len;
     auto chain_at = [&](int64_t k, int& n, int& h) {
-        const int64_t j = k * G + ((k & 1) ? G - 1 - b : b);
-        if (j >= nchains) return false;
+        int64_t j;
+        if (lpt) {
+            if (k >= nlist) return false;
+            j = list[k];
+        } else {
+            j = k * G + ((k & 1) ? G - 1 - b : b);
+            if (j >= nchains) return false;
+        }
         n = crow[j / p.H];
         h = (int)(j % p.H);
         return true;
