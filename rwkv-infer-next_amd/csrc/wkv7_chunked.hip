@@ -1326,9 +1326,10 @@ __device__ __forceinline__ Item chain_item(int h, int64_t bos, int L, int c) {
 }
 
 // Token-serial pairs per chunk-item of chain work, for balancing: a pair moves 33.7 KB (HBM-bound), a chunk-item
-// keeps a CU busy for about 10 us; with a few workgroups on the token-serial rows at a time, about 24 pairs take as
-// long as a chunk-item.
-constexpr int kPairsPerItem = 24;
+// keeps a CU busy for about 10 us; with a few workgroups on the token-serial rows at a time, the eight wavefronts of
+// one take about as long for 48 pairs as for a chunk-item (measured on the mixed step: 24, 48, 96 gave 365, 362 and
+// 362-368 us).
+constexpr int kPairsPerItem = 48;
 // Chain assignment: when the workgroups come in whole groups of H (G % H == 0, at most kChainLptGroups groups) and
 // there are at most kChainLptRows chained rows, longest row first, each row's H chains to the group with the least
 // chain work so far; otherwise the snake.  For the mixed step's eight prefill rows (28, 22, 19, 16, 10, 10, 9, 7
