@@ -913,7 +913,7 @@ __device__ __forceinline__ void state_operand_block(const f4& X, const f4& Y, bf
 }
 
 constexpr int kPlanSortRows = 4096;    // ragged calls: longest-first ordering of up to this many chunked rows
-constexpr int kScanRaggedGrid = 2048;  // ragged calls: scan workgroups (about two rounds of residency)
+constexpr int kScanRaggedGrid = 2048;  // ragged calls: scan workgroups (four rounds of residency at two per CU)
 constexpr int kScanDepth = 4;  // chunk record register sets per lane (three in flight, one in use)
 // Chunks per pass of the scan's main loop, fully unrolled: the compiler counts outstanding loads exactly only within
 // straight-line code and drains them all at a loop header, so a long body keeps the record loads in flight across
