@@ -54,7 +54,9 @@ typedef struct w6a16_args {
 /* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
 size_t w6a16_args_size(void);
 
-/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1 and M <= 32): a fixed 1 MiB region of u32 arrival
+/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1 and M <= 32, and for M <= 32 with split_k 2..8 where the
+ * in-workgroup split-K kernel runs: always for W6A16_FORMAT_PACKED, and for the planes when B * ceil(M / 16) *
+ * ceil(N / 128) reaches the device's CU count; that kernel sums its split_k partial tiles in LDS): a fixed 1 MiB region of u32 arrival
  * counters (one per output tile; a call with more than 262144 tiles is refused with WKV7_ERR_SHAPE), then fp32
  * partial tiles (split_k > 1), then, for M > 32, the per-row sums of A that a small first launch computes and the
  * GEMM kernel reads.  The split that completes a tile last reduces it inside the kernel.  Contract: the counter

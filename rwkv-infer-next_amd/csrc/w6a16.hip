@@ -490,6 +490,92 @@ __global__ __launch_bounds__(64 * kStrips) void w6a16_kernel(const Args p) {
     if (owner && completed[sw]) reduce_tile<MT>(p, tile0 + strip, b, m0, n0);
 }
 
+// In-workgroup split-K (M <= 32, 2 <= split_k <= kGemvMaxSplit): the split_k ranges of one 128-column strip run as
+// the wavefronts of one workgroup -- wavefront w takes exactly the chunks split w of w6a16_kernel takes -- and their
+// partial tiles are summed through LDS in split order 0, 1, ..., the same fp32 sums as w6a16_kernel's hand-off
+// (bit-identical results) with no cross-workgroup hand-off, counter or workspace traffic.  One workgroup per strip
+// and 16-row M group.
+constexpr int kGemvMaxSplit = 8;
+constexpr int kGemvPart = kGemvMaxSplit * 16 * kTileN * 4;  // fp32 partial tiles [split][16 rows][128 columns]
+constexpr int kGemvLds = kGemvMaxSplit * kBuf > kGemvPart ? kGemvMaxSplit * kBuf : kGemvPart;
+
+template <int D, bool PACKED>
+__global__ __launch_bounds__(64 * kGemvMaxSplit) void w6a16_gemv_kernel(const Args p) {
+    constexpr int MT = 1;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kGemvLds];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int strip = blockIdx.x;
+    const int n0 = strip * kTileN;
+    const int b = blockIdx.z / p.m_groups, mg = blockIdx.z % p.m_groups;
+    const int m0 = mg * 16;
+    const int nchunks = p.K / 64;
+    const int c0 = wv * p.chunks_per_split, c1 = min(nchunks, c0 + p.chunks_per_split);
+    uint8_t* const buf = lds + (PACKED ? 0 : wv * kBuf);
+
+    f4 acc[MT][kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) acc[0][t] = f4{0.f, 0.f, 0.f, 0.f};
+
+    if (c0 < c1) {  // the loop of w6a16_kernel, for this wavefront's range
+        typedef typename std::conditional<PACKED, PStage<MT>, Stage<MT>>::type S;
+        S st[D];
+        auto load = [&](int c, S& x) {
+            if constexpr (PACKED) load_pstage<MT>(p, b, m0, strip, c, x);
+            else load_stage<MT>(p, b, m0, n0, c, x);
+        };
+        auto work = [&](const S& x) {
+            if constexpr (PACKED) process_pstage<MT>(x, acc);
+            else process_stage<MT>(x, buf, acc);
+        };
+#pragma unroll
+        for (int j = 0; j < D; ++j) load(min(c0 + j, c1 - 1), st[j]);
+        if constexpr (PACKED) {
+            const int full = c0 + (c1 - c0) / D * D;
+            for (int c = c0; c < full; c += D) {
+#pragma unroll
+                for (int j = 0; j < D; ++j) {
+                    work(st[j]);
+                    load(min(c + j + D, c1 - 1), st[j]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+#pragma unroll
+            for (int j = 0; j + 1 < D; ++j)
+                if (full + j < c1) work(st[j]);
+        } else {
+            for (int c = c0; c < c1; c += D) {
+#pragma unroll
+                for (int j = 0; j < D; ++j) {
+                    if (c + j < c1) work(st[j]);
+                    load(min(c + j + D, c1 - 1), st[j]);
+                }
+            }
+        }
+    }
+    __syncthreads();  // the staging buffers are dead: the partial tiles reuse the LDS
+    float* const part = reinterpret_cast<float*>(lds);
+    {
+        const int i = lane & 15, q = lane >> 4;  // lane (i, q) holds rows 4 q + v of column 16 t + i
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v) part[(wv * 16 + 4 * q + v) * kTileN + 16 * t + i] = acc[0][t][v];
+    }
+    __syncthreads();
+    const int rows = min(16, p.M - m0), ks = p.split_k;
+    for (int e = threadIdx.x; e < rows * kTileN; e += blockDim.x) {
+        const int r = e / kTileN, col = e % kTileN, n = n0 + col;
+        float sum = 0.f;
+        for (int w = 0; w < ks; ++w) sum += part[(w * 16 + r) * kTileN + col];
+        if (n >= p.N) continue;
+        const int64_t o = (int64_t)b * p.so_b + (int64_t)(m0 + r) * p.so_m + n;
+        if (p.out_dtype == W6A16_OUT_F32)
+            reinterpret_cast<float*>(p.out)[o] = sum;
+        else
+            reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)sum;
+    }
+}
+
 // ---------------------------------------------------------------------------------------------------------------
 // Wide kernel (M > 32).  A workgroup of 4 KP wavefronts covers one 128-column strip for 16 MTW rows of A: wavefront
 // w owns column tiles 2 (w & 3) and 2 (w & 3) + 1 for all the workgroup's rows, over K part w >> 2 (the workgroup's
@@ -1179,7 +1265,7 @@ WideCfg wide_cfg(int M) {
 }
 
 struct Layout {
-    bool wide;
+    bool wide, gemv;  // gemv: the in-workgroup split-K kernel (no workspace)
     int mt, kp, cg, m_groups, n_strips, mpad, nchains;
     size_t tiles, counter_bytes, partial_bytes, rsum_offset, rsum_bytes;
 };
@@ -1201,7 +1287,13 @@ Layout layout(const w6a16_args* a) {
     const int rows_per_group = 16 * l.mt;  // A rows per workgroup (wide) or per wavefront (narrow)
     l.m_groups = (a->M + rows_per_group - 1) / rows_per_group;
     l.mpad = l.m_groups * rows_per_group;
-    if (a->split_k > 1 || l.wide) {
+    // In-workgroup split-K for the packed layout, and for the planes once its grid (one workgroup per strip and M
+    // group) fills the chip.  Measured at K = 4096, N = 16384 (us per call, planes / packed, split 8): M = 1 split-K
+    // across workgroups 17.2 / 16.4, in-workgroup 20.6 / 16.1; M = 16 22.4 / 23.1 against 22.6 / 18.6; M = 32 (split 4
+    // across workgroups) 30.1 / 26.5 against 22.0 / 18.6.
+    l.gemv = !l.wide && a->split_k >= 2 && a->split_k <= kGemvMaxSplit &&
+             (a->format == W6A16_FORMAT_PACKED || (int64_t)a->B * l.m_groups * l.n_strips >= cu_count());
+    if ((a->split_k > 1 && !l.gemv) || l.wide) {
         l.tiles = (size_t)a->B * l.m_groups * l.n_strips;
         l.counter_bytes = kCounterRegion;
         l.partial_bytes = a->split_k > 1 ? l.tiles * a->split_k * (size_t)rows_per_group * kTileN * 4 : 0;
@@ -1232,12 +1324,21 @@ int validate(const w6a16_args* a) {
     const Layout l = layout(a);
     if ((int64_t)a->B * (l.wide ? 1 : l.m_groups) > 65535) return WKV7_ERR_SHAPE;  // grid z: batch (x M groups)
     if (l.wide && (int64_t)l.m_groups * ((l.n_strips + 7) / 8) * 8 > 0x7FFFFFFF) return WKV7_ERR_SHAPE;
-    if (a->split_k > 1 && l.tiles * 4 > kCounterRegion) return WKV7_ERR_SHAPE;  // more tiles than counters
-    if (a->split_k > 1 || l.wide) {
+    if (a->split_k > 1 && l.tiles * 4 > kCounterRegion) return WKV7_ERR_SHAPE;  // more tiles than counters (0: gemv)
+    if ((a->split_k > 1 && !l.gemv) || l.wide) {
         if (!a->workspace || a->workspace_bytes < l.rsum_offset + l.rsum_bytes) return WKV7_ERR_WORKSPACE;
         if (reinterpret_cast<uintptr_t>(a->workspace) % kCounterAlign) return WKV7_ERR_ALIGN;
     }
     return WKV7_OK;
+}
+
+template <int D>
+void launch_gemv(const Args& p, const Layout& l, bool packed, hipStream_t s) {
+    const dim3 grid(l.n_strips, 1, p.B * l.m_groups), block(64 * p.split_k);
+    if (packed)
+        hipLaunchKernelGGL((w6a16_gemv_kernel<D, true>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((w6a16_gemv_kernel<D, false>), grid, block, 0, s, p);
 }
 
 template <int MT, int D>
@@ -1308,6 +1409,10 @@ int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
     int sk = 1;
     while (groups * sk < cus && sk * 2 <= 64 && chunks / (sk * 2) >= 1) sk *= 2;
     while (chunks / (sk * 2) >= 16 && groups * sk * 2 <= cus && sk * 2 <= 64) sk *= 2;
+    // Narrow, split, and one workgroup per (strip, M group) fills the chip: the in-workgroup split-K kernel takes the
+    // split, and its deepest split is the fastest (M = 32 above: split 4 24.1 / 19.5 us, split 8 22.0 / 18.6).
+    if (!l.wide && sk >= 2 && (int64_t)B * l.m_groups * l.n_strips >= cus)
+        while (sk * 2 <= w6::kGemvMaxSplit && chunks / (sk * 2) >= 1) sk *= 2;
     return sk;
 }
 
@@ -1328,7 +1433,7 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     p.out = a->out;
     p.so_b = a->out_batch_stride;
     p.so_m = a->out_row_stride;
-    if (a->split_k > 1 || l.wide) {
+    if ((a->split_k > 1 && !l.gemv) || l.wide) {
         p.cnt = static_cast<uint32_t*>(a->workspace);
         p.part = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + l.counter_bytes);
         p.rsum = reinterpret_cast<float*>(static_cast<char*>(a->workspace) + l.rsum_offset);
@@ -1352,7 +1457,9 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const bool packed = a->format == W6A16_FORMAT_PACKED;
-    if (!l.wide)
+    if (l.gemv)
+        w6::launch_gemv<2>(p, l, packed, s);
+    else if (!l.wide)
         w6::launch<1, 2>(p, l, packed, s);
     else if (l.mt == 2)
         w6::launch_wide_cg<2, 2>(p, l, packed, s);

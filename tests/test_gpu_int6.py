@@ -140,6 +140,25 @@ def test_random_shapes_match_oracle(seed):
     _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=shared)
 
 
+@pytest.mark.parametrize("split", [2, 4, 8, 16])
+def test_in_workgroup_split_on_planes(split):
+    """B x ceil(M / 16) x N / 128 = 4 x 2 x 32 = 256 workgroups fill the chip, so split 2..8 runs the in-workgroup
+    split-K kernel on the planes as well as on the packed layout (split 16: the cross-workgroup hand-off on both);
+    the two layouts give the same bits, within KERNEL_TOL of the oracle."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    B, M, N, K, g = 4, 20, 4096, 1024, 128
+    say("int6_matmul in-workgroup split", dict(B=B, M=M, N=N, K=K, split=split))
+    rng = np.random.default_rng(60 + split)
+    lo, hi, sc = _weights(rng, B, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    C = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
+    Cp = I6.int6_matmul(a.to(DEV), I6.prepack_int6(Ld, Hd, Sd, g), split_k=split, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(C, Cp)
+    _check(C, a, lo, hi, sc, g, KERNEL_TOL)
+
+
 @pytest.mark.parametrize("shared", [True, False])
 def test_batched(shared):
     from rwkv_next_amd.kernels import int6_gemm as I6

@@ -283,9 +283,15 @@ def test_matmul_empty_and_workspace_size():
     assert lib.w6a16_matmul(ctypes.byref(wide), None) == _lib.WKV7_ERR_WORKSPACE
     small = base_args(split_k=8, B=2, M=3, workspace=0x10000, workspace_bytes=(1 << 20) + tiles * 8 * 16 * 128 * 4 - 4)
     assert lib.w6a16_matmul(ctypes.byref(small), None) == _lib.WKV7_ERR_WORKSPACE
+    # the in-workgroup split-K kernel (packed layout, split 2..8; or planes once one workgroup per strip and M group
+    # fills the chip) sums its partials in LDS: no workspace
+    packed = dict(format=_lib.W6A16_FORMAT_PACKED, split_k=8, B=2, M=3)
+    assert lib.w6a16_workspace_size(ctypes.byref(base_args(**packed)), ctypes.byref(n)) == 0 and n.value == 0
+    assert lib.w6a16_workspace_size(ctypes.byref(base_args(**dict(packed, split_k=16))), ctypes.byref(n)) == 0
+    assert n.value == (1 << 20) + tiles * 16 * 16 * 128 * 4
     # at most 262144 tiles (the counter region's u32 counters): 40000 x 1 x 8 tiles are refused, 30000 x 1 x 8 reach
-    # the workspace check
-    many = dict(split_k=2, N=1024, out_row_stride=1024, out_batch_stride=4 * 1024, workspace=0x10000, workspace_bytes=1)
+    # the workspace check (split 16: the cross-workgroup hand-off)
+    many = dict(split_k=16, N=1024, out_row_stride=1024, out_batch_stride=4 * 1024, workspace=0x10000, workspace_bytes=1)
     assert lib.w6a16_matmul(ctypes.byref(base_args(B=40000, **many)), None) == _lib.WKV7_ERR_SHAPE
     assert lib.w6a16_matmul(ctypes.byref(base_args(B=30000, **many)), None) == _lib.WKV7_ERR_WORKSPACE
     odd = base_args(split_k=8, B=2, M=3, workspace=0x10080, workspace_bytes=1 << 24)
