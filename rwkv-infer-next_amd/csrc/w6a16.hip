@@ -490,41 +490,99 @@ __global__ __launch_bounds__(64 * kStrips) void w6a16_kernel(const Args p) {
     if (owner && completed[sw]) reduce_tile<MT>(p, tile0 + strip, b, m0, n0);
 }
 
+// Half a strip of the packed layout (tiles 4 h .. 4 h + 3 of the 128-column strip, one 16-row tile of A): load
+// instructions 2 h, 2 h + 1 (the low bits) and 4 + h (the top bits) of the chunk's 6 KB block, scale dwords 2 h and
+// 2 h + 1.  Tile t of the half computes exactly what process_pstage computes for tile 4 h + t.
+struct PHalf {
+    u4 w[3];
+    u4 a[2];
+    uint2 sc;
+};
+
+__device__ __forceinline__ void load_phalf(const Args& p, int b, int m0, int strip, int h, int c, PHalf& s) {
+    const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int nchunks = p.K / 64;
+    const uint8_t* const blk =
+        p.lo + (int64_t)b * p.sl_b + ((int64_t)strip * nchunks + c) * kPackBytes + 16 * lane;
+    s.w[0] = *reinterpret_cast<const u4*>(blk + 1024 * (2 * h));
+    s.w[1] = *reinterpret_cast<const u4*>(blk + 1024 * (2 * h + 1));
+    s.w[2] = *reinterpret_cast<const u4*>(blk + 1024 * (4 + h));
+    const int m = min(m0 + i, p.M - 1);
+    const uint16_t* const arow = p.a + (int64_t)b * p.sa_b + (int64_t)m * p.sa_m + (int64_t)c * 64 + 8 * q;
+    s.a[0] = *reinterpret_cast<const u4*>(arow);
+    s.a[1] = *reinterpret_cast<const u4*>(arow + 32);
+    const int g = (c * 64) / p.group_k, groups = p.K / p.group_k;
+    s.sc = *reinterpret_cast<const uint2*>(p.sc + (int64_t)b * p.ss_b + ((int64_t)strip * groups + g) * kTileN + 8 * i +
+                                           4 * h);
+}
+
+__device__ __forceinline__ void process_phalf(const PHalf& s, f4 (&acc)[1][4]) {
+    const bf8 bias = __builtin_bit_cast(bf8, u4{0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u});  // -160
+    f4 corr = mfma(__builtin_bit_cast(bf8, s.a[0]), bias, f4{0.f, 0.f, 0.f, 0.f});
+    corr = mfma(__builtin_bit_cast(bf8, s.a[1]), bias, corr);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t L0 = s.w[t >> 1][2 * (t & 1)], L1 = s.w[t >> 1][2 * (t & 1) + 1];
+        const uint32_t Hd = s.w[2][t];
+        const uint32_t u0a = (L0 & 0x0F0F0F0Fu) | ((Hd & 0x03030303u) << 4);
+        const uint32_t u0b = (L1 & 0x0F0F0F0Fu) | (Hd & 0x30303030u);
+        const uint32_t u1a = ((L0 >> 4) & 0x0F0F0F0Fu) | ((Hd & 0x0C0C0C0Cu) << 2);
+        const uint32_t u1b = ((L1 >> 4) & 0x0F0F0F0Fu) | ((Hd >> 2) & 0x30303030u);
+        uint32_t o0[4], o1[4];
+        codes_to_bf16(u0a, o0[0], o0[1]);
+        codes_to_bf16(u0b, o0[2], o0[3]);
+        codes_to_bf16(u1a, o1[0], o1[1]);
+        codes_to_bf16(u1b, o1[2], o1[3]);
+        const bf8 w0 = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
+        const bf8 w1 = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+        const float sv = h2f((uint16_t)((t >> 1 ? s.sc.y : s.sc.x) >> (16 * (t & 1))));
+        f4 tc = mfma(__builtin_bit_cast(bf8, s.a[0]), w0, corr);
+        tc = mfma(__builtin_bit_cast(bf8, s.a[1]), w1, tc);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) acc[0][t][v] += tc[v] * sv;
+    }
+}
+
 // In-workgroup split-K (M <= 32, 2 <= split_k <= kGemvMaxSplit): the split_k ranges of one 128-column strip run as
 // the wavefronts of one workgroup -- wavefront w takes exactly the chunks split w of w6a16_kernel takes -- and their
 // partial tiles are summed through LDS in split order 0, 1, ..., the same fp32 sums as w6a16_kernel's hand-off
 // (bit-identical results) with no cross-workgroup hand-off, counter or workspace traffic.  One workgroup per strip
-// and 16-row M group.
+// and 16-row M group, or (NT = 4, packed layout) per half strip, which doubles the workgroups where strips are fewer
+// than CUs.
 constexpr int kGemvMaxSplit = 8;
 constexpr int kGemvPart = kGemvMaxSplit * 16 * kTileN * 4;  // fp32 partial tiles [split][16 rows][128 columns]
 constexpr int kGemvLds = kGemvMaxSplit * kBuf > kGemvPart ? kGemvMaxSplit * kBuf : kGemvPart;
 
-template <int D, bool PACKED>
+template <int D, bool PACKED, int NT>
 __global__ __launch_bounds__(64 * kGemvMaxSplit) void w6a16_gemv_kernel(const Args p) {
-    constexpr int MT = 1;
+    static_assert(NT == kTiles || (NT == 4 && PACKED), "half strips: packed layout only");
+    constexpr int MT = 1, NC = 16 * NT;  // NC: columns per workgroup
     __shared__ __attribute__((aligned(16))) uint8_t lds[kGemvLds];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int strip = blockIdx.x;
-    const int n0 = strip * kTileN;
+    const int strip = blockIdx.x / (kTiles / NT), h = blockIdx.x % (kTiles / NT);
+    const int n0 = strip * kTileN + h * NC;
     const int b = blockIdx.z / p.m_groups, mg = blockIdx.z % p.m_groups;
     const int m0 = mg * 16;
     const int nchunks = p.K / 64;
     const int c0 = wv * p.chunks_per_split, c1 = min(nchunks, c0 + p.chunks_per_split);
     uint8_t* const buf = lds + (PACKED ? 0 : wv * kBuf);
 
-    f4 acc[MT][kTiles];
+    f4 acc[MT][NT];
 #pragma unroll
-    for (int t = 0; t < kTiles; ++t) acc[0][t] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < NT; ++t) acc[0][t] = f4{0.f, 0.f, 0.f, 0.f};
 
     if (c0 < c1) {  // the loop of w6a16_kernel, for this wavefront's range
-        typedef typename std::conditional<PACKED, PStage<MT>, Stage<MT>>::type S;
+        typedef typename std::conditional<PACKED, typename std::conditional<NT == 4, PHalf, PStage<MT>>::type,
+                                          Stage<MT>>::type S;
         S st[D];
         auto load = [&](int c, S& x) {
-            if constexpr (PACKED) load_pstage<MT>(p, b, m0, strip, c, x);
+            if constexpr (PACKED && NT == 4) load_phalf(p, b, m0, strip, h, c, x);
+            else if constexpr (PACKED) load_pstage<MT>(p, b, m0, strip, c, x);
             else load_stage<MT>(p, b, m0, n0, c, x);
         };
         auto work = [&](const S& x) {
-            if constexpr (PACKED) process_pstage<MT>(x, acc);
+            if constexpr (PACKED && NT == 4) process_phalf(x, acc);
+            else if constexpr (PACKED) process_pstage<MT>(x, acc);
             else process_stage<MT>(x, buf, acc);
         };
 #pragma unroll
@@ -557,16 +615,16 @@ __global__ __launch_bounds__(64 * kGemvMaxSplit) void w6a16_gemv_kernel(const Ar
     {
         const int i = lane & 15, q = lane >> 4;  // lane (i, q) holds rows 4 q + v of column 16 t + i
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t)
+        for (int t = 0; t < NT; ++t)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) part[(wv * 16 + 4 * q + v) * kTileN + 16 * t + i] = acc[0][t][v];
+            for (int v = 0; v < 4; ++v) part[(wv * 16 + 4 * q + v) * NC + 16 * t + i] = acc[0][t][v];
     }
     __syncthreads();
     const int rows = min(16, p.M - m0), ks = p.split_k;
-    for (int e = threadIdx.x; e < rows * kTileN; e += blockDim.x) {
-        const int r = e / kTileN, col = e % kTileN, n = n0 + col;
+    for (int e = threadIdx.x; e < rows * NC; e += blockDim.x) {
+        const int r = e / NC, col = e % NC, n = n0 + col;
         float sum = 0.f;
-        for (int w = 0; w < ks; ++w) sum += part[(w * 16 + r) * kTileN + col];
+        for (int w = 0; w < ks; ++w) sum += part[(w * 16 + r) * NC + col];
         if (n >= p.N) continue;
         const int64_t o = (int64_t)b * p.so_b + (int64_t)(m0 + r) * p.so_m + n;
         if (p.out_dtype == W6A16_OUT_F32)
@@ -1265,7 +1323,7 @@ WideCfg wide_cfg(int M) {
 }
 
 struct Layout {
-    bool wide, gemv;  // gemv: the in-workgroup split-K kernel (no workspace)
+    bool wide, gemv, gemv_half;  // gemv: the in-workgroup split-K kernel (no workspace); gemv_half: per half strip
     int mt, kp, cg, m_groups, n_strips, mpad, nchains;
     size_t tiles, counter_bytes, partial_bytes, rsum_offset, rsum_bytes;
 };
@@ -1293,6 +1351,7 @@ Layout layout(const w6a16_args* a) {
     // across workgroups) 30.1 / 26.5 against 22.0 / 18.6.
     l.gemv = !l.wide && a->split_k >= 2 && a->split_k <= kGemvMaxSplit &&
              (a->format == W6A16_FORMAT_PACKED || (int64_t)a->B * l.m_groups * l.n_strips >= cu_count());
+    l.gemv_half = l.gemv && a->format == W6A16_FORMAT_PACKED && (int64_t)a->B * l.m_groups * l.n_strips < cu_count();
     if ((a->split_k > 1 && !l.gemv) || l.wide) {
         l.tiles = (size_t)a->B * l.m_groups * l.n_strips;
         l.counter_bytes = kCounterRegion;
@@ -1332,13 +1391,18 @@ int validate(const w6a16_args* a) {
     return WKV7_OK;
 }
 
-template <int D>
+template <int D, int DH>
 void launch_gemv(const Args& p, const Layout& l, bool packed, hipStream_t s) {
-    const dim3 grid(l.n_strips, 1, p.B * l.m_groups), block(64 * p.split_k);
-    if (packed)
-        hipLaunchKernelGGL((w6a16_gemv_kernel<D, true>), grid, block, 0, s, p);
+    const dim3 block(64 * p.split_k);
+    if (packed && l.gemv_half)
+        hipLaunchKernelGGL((w6a16_gemv_kernel<DH, true, 4>), dim3(2 * l.n_strips, 1, p.B * l.m_groups), block, 0, s,
+                           p);
+    else if (packed)
+        hipLaunchKernelGGL((w6a16_gemv_kernel<D, true, kTiles>), dim3(l.n_strips, 1, p.B * l.m_groups), block, 0, s,
+                           p);
     else
-        hipLaunchKernelGGL((w6a16_gemv_kernel<D, false>), grid, block, 0, s, p);
+        hipLaunchKernelGGL((w6a16_gemv_kernel<D, false, kTiles>), dim3(l.n_strips, 1, p.B * l.m_groups), block, 0, s,
+                           p);
 }
 
 template <int MT, int D>
@@ -1458,7 +1522,7 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const bool packed = a->format == W6A16_FORMAT_PACKED;
     if (l.gemv)
-        w6::launch_gemv<2>(p, l, packed, s);
+        w6::launch_gemv<2, 2>(p, l, packed, s);
     else if (!l.wide)
         w6::launch<1, 2>(p, l, packed, s);
     else if (l.mt == 2)
