@@ -345,17 +345,20 @@ def int6_bench(torch, kernels, dev, steps, warmup):
         a = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
         sk, ud = I6.plan_int6(M, N, K, 1, dev)
         us = graph_time(lambda: [I6.int6_matmul_op(a, lo[i], hi[i], sc[i], G, sk, ud) for i in range(SETS)], steps)
-        us_pk = graph_time(lambda: [I6.int6_matmul_packed_op(a, pk[i].weight, pk[i].scales, 0, K, N, G, sk)
+        sk_pk = I6.plan_int6_packed(M, N, K, 1, dev)
+        us_pk = graph_time(lambda: [I6.int6_matmul_packed_op(a, pk[i].weight, pk[i].scales, 0, K, N, G, sk_pk)
                                     for i in range(SETS)], steps)
         us_bf = graph_time(lambda: [torch.matmul(a, wbf[i]) for i in range(SETS)], steps)
         byts = weight_bytes + M * K * 2 + M * N * 2
         path = "w6a16 kernel" if M <= I6.MAX_M else "dequantize + library GEMM"
-        rows.append({"M": M, "path": path, "split_k": sk if M <= I6.MAX_M else None, "us": us,
+        rows.append({"M": M, "path": path, "split_k": sk if M <= I6.MAX_M else None,
+                     "packed_split_k": sk_pk if M <= I6.MAX_M else None, "us": us,
                      "GBps": byts / (us * 1e-6) / 1e9, "frac_hbm": byts / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
                      "packed_us": us_pk, "packed_GBps": byts / (us_pk * 1e-6) / 1e9,
                      "packed_frac_hbm": byts / (us_pk * 1e-6) / 1e9 / HBM_PEAK_GBS,
                      "bf16_matmul_us": us_bf, "speedup_vs_bf16": us_bf / us, "packed_speedup_vs_bf16": us_bf / us_pk})
-        log(f"int6 M={M} ({path}, split {sk}): {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), packed {us_pk:.2f} us "
+        log(f"int6 M={M} ({path}, split {sk}): {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), "
+            f"packed (split {sk_pk}) {us_pk:.2f} us "
             f"({rows[-1]['packed_GBps']:.0f} GB/s), bf16 matmul {us_bf:.2f} us")
     # prefill-sized M: dequantise once, then the library GEMM
     M = 4096

@@ -70,6 +70,12 @@ int w6a16_workspace_size(const w6a16_args *args, size_t *bytes);
  * within two workgroups per CU.  Replaces the split-K rule of plan_int6 (rwkv_next/kernels/int6_gemm.py:239-250). */
 int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K);
 
+/* split_k for the packed layout (W6A16_FORMAT_PACKED), whose in-workgroup kernel prefers a shallower split where it
+ * runs half strips; otherwise equal to w6a16_plan_split.  No counterpart in the reference (its weights come only as
+ * planes); for callers that pass packed weights.  Results depend on split_k: a packed call gives the planes' bits
+ * only at the same split_k. */
+int w6a16_plan_split_packed(int32_t B, int32_t M, int32_t N, int32_t K);
+
 /* C = A @ dequant(W) on `stream` (hipStream_t).  Replaces `_impl` + `_w6a16` (int6_gemm.py:253-287, 156-215). */
 int w6a16_matmul(const w6a16_args *args, void *stream);
 

@@ -1480,6 +1480,25 @@ int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K) {
     return sk;
 }
 
+int w6a16_plan_split_packed(int32_t B, int32_t M, int32_t N, int32_t K) {
+    const int sk = w6a16_plan_split(B, M, N, K);
+    if (sk != 8) return sk;
+    w6a16_args shape{};
+    shape.B = B;
+    shape.M = M;
+    shape.N = N;
+    shape.K = K;
+    shape.group_k = K % 128 == 0 ? 128 : 64;
+    shape.split_k = sk;
+    shape.format = W6A16_FORMAT_PACKED;
+    const w6::Layout l = w6::layout(&shape);
+    // Half strips (the in-workgroup kernel where strips are fewer than CUs) run fastest at split 4 with three chunks
+    // in flight, given at least 8 chunks per range.  Measured at K = 4096, N = 16384 (us per call): M = 1 split 4
+    // 11.9, split 8 12.4; M = 16 14.1 / 14.7.
+    if (l.gemv_half && K / 64 / 4 >= 8) return 4;
+    return sk;
+}
+
 int w6a16_matmul(const w6a16_args* a, void* stream) {
     const int rc = w6::validate(a);
     if (rc != WKV7_OK || a->M == 0) return rc;
@@ -1521,7 +1540,9 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const bool packed = a->format == W6A16_FORMAT_PACKED;
-    if (l.gemv)
+    if (l.gemv && l.gemv_half && p.split_k <= 4)  // half strips, split <= 4: three chunks in flight
+        w6::launch_gemv<2, 3>(p, l, packed, s);
+    else if (l.gemv)
         w6::launch_gemv<2, 2>(p, l, packed, s);
     else if (!l.wide)
         w6::launch<1, 2>(p, l, packed, s);

@@ -38,7 +38,8 @@ EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_versio
             "wkv7_args_layout", "wkv7_run_noalloc",
             "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore", "wkv7_timemix_prologue",
             "wkv7_timemix_epilogue")
-W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split", "w6a16_matmul",
+W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split", "w6a16_plan_split_packed",
+                  "w6a16_matmul",
                   "w6a16_dequantize", "w6a16_packed_size", "w6a16_pack", "w6a16_dequantize_packed")
 W6A16_FORMAT_PLANES = 0
 W6A16_FORMAT_PACKED = 1
@@ -158,6 +159,8 @@ def load(path: str = LIB_PATH):
     lib.w6a16_workspace_size.argtypes = [ctypes.POINTER(W6a16Args), ctypes.POINTER(ctypes.c_size_t)]
     lib.w6a16_plan_split.restype = ctypes.c_int
     lib.w6a16_plan_split.argtypes = [i32, i32, i32, i32]
+    lib.w6a16_plan_split_packed.restype = ctypes.c_int
+    lib.w6a16_plan_split_packed.argtypes = [i32, i32, i32, i32]
     lib.w6a16_matmul.restype = ctypes.c_int
     lib.w6a16_matmul.argtypes = [ctypes.POINTER(W6a16Args), _vp]
     lib.w6a16_dequantize.restype = ctypes.c_int

@@ -11,6 +11,7 @@ quantised there load unchanged:
 plus a load-time re-layout with no counterpart in the reference:
     prepack_int6(lo, hi, s, group_k) -> Int6Packed      accepted by int6_matmul in place of lo, and by
     int6_matmul_packed_op(a, weight, scales, batches, K, N, group_k, split_k)   op rwkv_next_amd::int6_matmul_packed
+    plan_int6_packed(M, N, K, n_batch, device)      -> split_k for a packed weight
 
 Format: a (K, N) weight (N contiguous) is quantised to q in [-32, 31] per (group of group_k rows, column) with an
 fp16 scale, w ~ s q; the code u = q + 32 is split into bit planes per 64-row chunk c:
@@ -151,6 +152,17 @@ def plan_int6(M, N, K, n_batch, device=None):
     else:
         sk = _lib.load().w6a16_plan_split(n_batch, M, N, K)
     return int(sk), M > 1
+
+
+def plan_int6_packed(M, N, K, n_batch, device=None):
+    """split_k for a packed weight (w6a16_plan_split_packed; no counterpart in the reference): plan_int6's split, made
+    shallower where the packed kernel runs half strips.  A packed call equals the planes' bit for bit only at the same
+    split_k."""
+    lib = _lib.load()
+    if device is not None and torch.device(device).type == "cuda":
+        with torch.cuda.device(device):
+            return int(lib.w6a16_plan_split_packed(n_batch, M, N, K))
+    return int(lib.w6a16_plan_split_packed(n_batch, M, N, K))
 
 
 class Int6Packed(NamedTuple):
@@ -339,11 +351,12 @@ def int6_matmul(a, lo, hi=None, s=None, group_k=None, split_k=None, use_dot=None
     out_dtype: bfloat16 / float32).  The weight is the planes (lo, hi, s, group_k) or an Int6Packed passed as `lo`
     (hi, s, group_k then unused).  A single weight (K, N) is shared by every batch row.  Eager entry point; the
     model-facing functional ops are int6_matmul_op and int6_matmul_packed_op."""
-    w = _packed(lo) if isinstance(lo, Int6Packed) else _planes(lo, hi, s, group_k)
+    packed = isinstance(lo, Int6Packed)
+    w = _packed(lo) if packed else _planes(lo, hi, s, group_k)
     B = a.shape[0] if a.dim() == 3 else 1
     M = a.shape[-2]
     if split_k is None:
-        split_k, _ = plan_int6(M, w.N, w.K, B, a.device)
+        split_k = plan_int6_packed(M, w.N, w.K, B, a.device) if packed else plan_int6(M, w.N, w.K, B, a.device)[0]
     with torch.cuda.device(a.device):
         return _impl(a, w, split_k, out_dtype)
 

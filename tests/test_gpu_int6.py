@@ -38,6 +38,12 @@ def _dev(*xs):
     return [torch.from_numpy(np.ascontiguousarray(x)).to(DEV) for x in xs]
 
 
+def _split(split, B, M, N, K):
+    """The split_k a planes-vs-packed comparison uses for both calls: the given one, else plan_int6's."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    return split if split is not None else I6.plan_int6(M, N, K, B, torch.device(DEV))[0]
+
+
 def _check(C, a_bf, lo, hi, sc, g, tol, bf16_out=False, shared=False):
     a64 = a_bf.float().numpy().astype(np.float64)
     L, H, S = (lo[0], hi[0], sc[0]) if shared else (lo, hi, sc)
@@ -102,6 +108,7 @@ def test_wide_kernel_matches_oracle(B, M, N, K, g, shared, split):
     Ld, Hd, Sd = _dev(lo, hi, sc)
     if shared:
         Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    split = _split(split, B, M, N, K)
     C = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
     pk = I6.prepack_int6(Ld, Hd, Sd, g)
     Cp = I6.int6_matmul(a.to(DEV), pk, split_k=split, out_dtype=torch.float32)
@@ -132,6 +139,7 @@ def test_random_shapes_match_oracle(seed):
     Ld, Hd, Sd = _dev(lo, hi, sc)
     if shared:
         Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    split = _split(split, B, M, N, K)
     C = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
     Cp = I6.int6_matmul(a.to(DEV), I6.prepack_int6(Ld, Hd, Sd, g), split_k=split, out_dtype=torch.float32)
     torch.cuda.synchronize()
@@ -339,6 +347,10 @@ def test_packed_matmul_equals_planes(B, M, N, K, g, split, shared):
         Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
     pk = I6.prepack_int6(Ld, Hd, Sd, g)
     ad = a.to(DEV) if B > 1 else a[0].to(DEV)
+    if split is None:  # the packed default plan, given to the planes too (results depend on split_k)
+        split = I6.plan_int6_packed(M, N, K, B, torch.device(DEV))
+        Cd = I6.int6_matmul(ad, pk, out_dtype=torch.float32)
+        assert torch.equal(Cd, I6.int6_matmul(ad, pk, split_k=split, out_dtype=torch.float32))
     for odt in (torch.float32, torch.bfloat16):
         Cp = I6.int6_matmul(ad, pk, split_k=split, out_dtype=odt)
         Cq = I6.int6_matmul(ad, Ld, Hd, Sd, g, split_k=split, out_dtype=odt)
@@ -346,8 +358,7 @@ def test_packed_matmul_equals_planes(B, M, N, K, g, split, shared):
         assert torch.equal(Cp, Cq), odt
     _check(Cp.float() if B > 1 else Cp.float()[None], a, lo, hi, sc, g, KERNEL_TOL, bf16_out=True, shared=shared)
     # the functional op
-    sk = split if split is not None else I6.plan_int6(M, N, K, B, torch.device(DEV))[0]
-    Co = I6.int6_matmul_packed_op(ad, pk.weight, pk.scales, pk.batches, K, N, g, sk)
+    Co = I6.int6_matmul_packed_op(ad, pk.weight, pk.scales, pk.batches, K, N, g, split)
     torch.cuda.synchronize()
     assert torch.equal(Co, Cp)
 

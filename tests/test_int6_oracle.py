@@ -357,3 +357,18 @@ def test_split_rule():
     assert lib.w6a16_plan_split(1, 1, 4096, 16384) == 32
     assert I6.plan_int6(1, 4096, 4096, 1) == (lib.w6a16_plan_split(1, 1, 4096, 4096), False)
     assert I6.plan_int6(8, 4096, 4096, 1)[1] is True
+    # M = 32: two M groups x 128 strips = 256 in-workgroup blocks fill the chip, so the deepest split
+    assert lib.w6a16_plan_split(1, 32, 16384, 4096) == 8
+
+
+def test_split_rule_packed():
+    """The packed layout takes split 4 instead of 8 where its kernel runs half strips (fewer strips x M groups than
+    CUs) and the ranges keep at least 8 chunks; everywhere else it takes the planes' split."""
+    lib = _lib.load()
+    assert lib.w6a16_plan_split_packed(1, 1, 16384, 4096) == 4
+    assert lib.w6a16_plan_split_packed(1, 16, 16384, 4096) == 4
+    assert lib.w6a16_plan_split_packed(1, 32, 16384, 4096) == 8      # 256 blocks: whole strips
+    assert lib.w6a16_plan_split_packed(1, 1, 16384, 1024) == 8       # 16 chunks: 4 per range at split 4
+    for B, M, N, K in [(1, 64, 16384, 4096), (1, 1, 1024, 16384), (4, 1, 2048, 2048), (1, 1, 256, 128)]:
+        assert lib.w6a16_plan_split_packed(B, M, N, K) == lib.w6a16_plan_split(B, M, N, K), (B, M, N, K)
+    assert I6.plan_int6_packed(1, 16384, 4096, 1) == 4
