@@ -167,19 +167,20 @@ def test_in_workgroup_split_on_planes(split):
     _check(C, a, lo, hi, sc, g, KERNEL_TOL)
 
 
-@pytest.mark.parametrize("N,M", [(80, 1), (80, 17), (208, 5), (16, 32)])
-def test_half_strips_ragged_n(N, M):
-    """Packed layout, split 4, few strips: each workgroup takes half a 128-column strip, so at N = 80 the second half
-    (columns 64..127) holds 16 valid columns, at N = 16 none; planes (the cross-workgroup kernel) give the same bits."""
+@pytest.mark.parametrize("N,M,split", [(80, 1, 4), (80, 17, 3), (208, 5, 2), (16, 32, 4), (208, 2, 8)])
+def test_half_strips_ragged_n(N, M, split):
+    """Packed layout, few strips: each workgroup takes half a 128-column strip (three chunks in flight at split <= 4,
+    two at 8), so at N = 80 the second half (columns 64..127) holds 16 valid columns, at N = 16 none; split 3 leaves
+    uneven ranges; planes (the cross-workgroup kernel) give the same bits."""
     from rwkv_next_amd.kernels import int6_gemm as I6
     K, g = 768, 64
-    say("int6_matmul half strips", dict(M=M, N=N, K=K))
+    say("int6_matmul half strips", dict(M=M, N=N, K=K, split=split))
     rng = np.random.default_rng(90 + N + M)
     lo, hi, sc = _weights(rng, 1, K, N, g)
     a = _act(rng, 1, M, K)
     Ld, Hd, Sd = _dev(lo, hi, sc)
-    C = I6.int6_matmul(a.to(DEV), Ld[0], Hd[0], Sd[0], g, split_k=4, out_dtype=torch.float32)
-    Cp = I6.int6_matmul(a.to(DEV), I6.prepack_int6(Ld[0], Hd[0], Sd[0], g), split_k=4, out_dtype=torch.float32)
+    C = I6.int6_matmul(a.to(DEV), Ld[0], Hd[0], Sd[0], g, split_k=split, out_dtype=torch.float32)
+    Cp = I6.int6_matmul(a.to(DEV), I6.prepack_int6(Ld[0], Hd[0], Sd[0], g), split_k=split, out_dtype=torch.float32)
     torch.cuda.synchronize()
     assert torch.equal(C, Cp)
     _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=True)
