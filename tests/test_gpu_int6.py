@@ -186,6 +186,26 @@ def test_half_strips_ragged_n(N, M, split):
     _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=True)
 
 
+@pytest.mark.parametrize("shared,split", [(False, 3), (True, 4), (False, 8)])
+def test_half_strips_batched(shared, split):
+    """Half strips over a batch (grid z = batch x M groups; per-batch or shared packed weights and scales): same bits
+    as the planes, within KERNEL_TOL of the oracle."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    B, M, N, K, g = 3, 21, 208, 768, 64
+    say("int6_matmul half strips batched", dict(B=B, M=M, N=N, K=K, shared=shared, split=split))
+    rng = np.random.default_rng(70 + split + shared)
+    lo, hi, sc = _weights(rng, 1 if shared else B, K, N, g)
+    a = _act(rng, B, M, K)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    if shared:
+        Ld, Hd, Sd = Ld[0], Hd[0], Sd[0]
+    C = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32)
+    Cp = I6.int6_matmul(a.to(DEV), I6.prepack_int6(Ld, Hd, Sd, g), split_k=split, out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert torch.equal(C, Cp)
+    _check(C, a, lo, hi, sc, g, KERNEL_TOL, shared=shared)
+
+
 @pytest.mark.parametrize("shared", [True, False])
 def test_batched(shared):
     from rwkv_next_amd.kernels import int6_gemm as I6
