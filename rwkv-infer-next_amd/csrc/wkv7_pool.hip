@@ -12,6 +12,7 @@
 
 #include "wkv7.h"
 #include "wkv7_device.h"
+#include "wkv7_launch.h"
 
 namespace wkv7 {
 namespace {
@@ -66,23 +67,40 @@ __global__ __launch_bounds__(kThreads) void pool_move_kernel(float* __restrict__
     }
 }
 
-// pool[slots[b]] := snaps[b][n[b] - 1] for n[b] in [1, T]; other rows keep the pool's state.  One workgroup per
-// (b, head).
+// pool[slots[b]] := snaps[b][n[b] - 1] for n[b] in [1, T]; other rows keep the pool's state.  One workgroup per UPW
+// consecutive (b, head) units: all their index loads, then all their states' loads, then the stores, so a workgroup
+// of two units waits for one index round trip where two workgroups of one would each wait for theirs (measured at
+// B = 64, H = 64, 4096 units: 24.9 us with one unit per workgroup, 24.2 with two; at H = 8, 512 units, two per
+// workgroup halve an already small grid: 5.0 against 5.2 us).
+template <int UPW>
 __global__ __launch_bounds__(kThreads) void snapshot_restore_kernel(float* __restrict__ pool, int64_t rows, int H,
                                                                     const int64_t* __restrict__ slots,
                                                                     const float* __restrict__ snaps, int T,
-                                                                    const int64_t* __restrict__ nacc) {
-    const int64_t b = blockIdx.x / H;
-    const int h = (int)(blockIdx.x % H);
-    const int64_t nb = nacc[b], s = slots[b];
-    if (nb < 1 || nb > T || s < 0 || s >= rows) return;
-    const float* from = snaps + ((b * T + (nb - 1)) * H + h) * (int64_t)HS2;
-    float* to = pool + (s * H + h) * (int64_t)HS2;
-    f4 x[4];
+                                                                    const int64_t* __restrict__ nacc, int64_t units) {
+    const float* from[UPW];
+    float* to[UPW];
+    bool ok[UPW];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) x[u] = ldg4(from + (u * kThreads + threadIdx.x) * 4);
+    for (int k = 0; k < UPW; ++k) {
+        const uint32_t u = UPW * blockIdx.x + k;  // < 2^32: at most 2^31 - 1 workgroups
+        const int64_t b = u / (uint32_t)H;
+        const int h = (int)(u % (uint32_t)H);
+        const int64_t nb = u < units ? nacc[b] : 0, s = u < units ? slots[b] : -1;
+        ok[k] = nb >= 1 && nb <= T && s >= 0 && s < rows;
+        from[k] = snaps + ((b * T + (ok[k] ? nb - 1 : 0)) * H + h) * (int64_t)HS2;
+        to[k] = pool + ((ok[k] ? s : 0) * H + h) * (int64_t)HS2;
+    }
+    f4 x[UPW][4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) stg4(to + (u * kThreads + threadIdx.x) * 4, x[u]);
+    for (int k = 0; k < UPW; ++k)
+        if (ok[k])
+#pragma unroll
+            for (int v = 0; v < 4; ++v) x[k][v] = ldg4(from[k] + (v * kThreads + threadIdx.x) * 4);
+#pragma unroll
+    for (int k = 0; k < UPW; ++k)
+        if (ok[k])
+#pragma unroll
+            for (int v = 0; v < 4; ++v) stg4(to[k] + (v * kThreads + threadIdx.x) * 4, x[k][v]);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -130,10 +148,18 @@ int wkv7_snapshot_restore(float* pool, int64_t rows, int32_t H, const int64_t* s
     if (num_seqs == 0 || rows == 0) return WKV7_OK;
     if (!pool || !slots || !snapshots || !n_accepted) return WKV7_ERR_NULL;
     if (!wkv7::aligned16(pool) || !wkv7::aligned16(snapshots)) return WKV7_ERR_ALIGN;
-    const int64_t blocks = (int64_t)num_seqs * H;
+    // two units per workgroup once there are at least four per CU
+    const int64_t units = (int64_t)num_seqs * H;
+    const bool two = units >= 4 * (int64_t)wkv7::device_cu_count();
+    const int64_t blocks = two ? (units + 1) / 2 : units;
     if (blocks > 0x7fffffffLL) return WKV7_ERR_SHAPE;
-    hipLaunchKernelGGL(wkv7::snapshot_restore_kernel, dim3((unsigned)blocks), dim3(wkv7::kThreads), 0,
-                       static_cast<hipStream_t>(stream), pool, rows, (int)H, slots, snapshots, (int)T, n_accepted);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (two)
+        hipLaunchKernelGGL(wkv7::snapshot_restore_kernel<2>, dim3((unsigned)blocks), dim3(wkv7::kThreads), 0, s, pool,
+                           rows, (int)H, slots, snapshots, (int)T, n_accepted, units);
+    else
+        hipLaunchKernelGGL(wkv7::snapshot_restore_kernel<1>, dim3((unsigned)blocks), dim3(wkv7::kThreads), 0, s, pool,
+                           rows, (int)H, slots, snapshots, (int)T, n_accepted, units);
     return static_cast<int>(hipGetLastError());
 }
 

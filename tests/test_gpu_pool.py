@@ -82,6 +82,25 @@ def test_snapshot_restore_matches_indexing(dev, K):
     assert torch.equal(pool, ref)
 
 
+def test_snapshot_restore_two_units_per_workgroup(dev, K):
+    """Enough (sequence, head) units (257 x 5 = 1285, odd) for the two-units-per-workgroup launch, with accepted
+    counts 0..T and a pool slot per sequence."""
+    say("snapshot restore, two units per workgroup")
+    N, T, H, S = 257, 3, 5, 300
+    g = torch.Generator(device=dev).manual_seed(5)
+    pool = torch.randn(S, H, 64, 64, device=dev, generator=g)
+    snaps = torch.randn(N, T, H, 64, 64, device=dev, generator=g)
+    slots = torch.randperm(S, device=dev, generator=g)[:N]
+    n = torch.randint(0, T + 1, (N,), device=dev, generator=g)
+    ref = pool.clone()
+    for b in range(N):
+        if int(n[b]) > 0:
+            ref[int(slots[b])] = snaps[b, int(n[b]) - 1]
+    K.restore_snapshots_(pool, slots, snaps, n)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, ref)
+
+
 def test_pool_ops_in_a_graph_replay_like_eager(dev, K):
     """reset + move + decode recorded into one HIP graph, replayed several times with eager work between the
     replays; every replay equals the same calls made eagerly."""
