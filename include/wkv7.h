@@ -56,6 +56,9 @@ extern "C" {
                                     * to a slot another sequence reads its initial state from: the result depends on
                                     * the order in which the kernels reach them */
 #define WKV7_STATUS_CLASH_MAX_SEQS 1024
+#define WKV7_STATUS_SEGMENT_WAIT 64  /* the segmented prefill kernel gave up a bounded wait (an internal hand-off did not
+                                      * arrive): that row's results are wrong and the workspace's hand-off flags must
+                                      * be zeroed again before the next call */
 
 /* Largest raw w the chunked form handles.  It references each chunk's decay factors to the chunk midpoint, so factors
  * up to exp(32 exp(w)) must fit fp32: w <= 1.0 (32 e^1.0 = 87 < 88.7).  RWKV-7 produces w = -softplus(-x) - 0.5
@@ -67,6 +70,8 @@ extern "C" {
                                 * ragged call whose rows are short enough runs as one chain-kernel dispatch */
 #define WKV7_ALGO_RECURRENT 1  /* token-serial kernel for every row */
 #define WKV7_ALGO_CHUNKED 2    /* chunked MFMA prefill for every row */
+#define WKV7_ALGO_SEGMENTED 4  /* every row through the segmented chunked kernel (32-token chunks, rows cut into
+                                * segments, one dispatch; needs a workspace) */
 #define WKV7_ALGO_CHAIN 3      /* one dispatch: rows of at most rec_max_len tokens token-serial, longer rows chunked with
                                 * each (row, head) chain walked by one workgroup (no workspace; num_seqs <= 512) */
 

@@ -40,9 +40,11 @@ struct Plan {
     bool run_recurrent = false;
     bool run_chunked = false;
     bool run_chain = false;
+    bool run_seg = false;
     int rec_len_rec = -1;    // Params.rec_max_len of the token-serial launch (-1: all rows)
     int rec_len_chunk = -1;  // Params.rec_max_len of the chunked launch (-1: all rows)
     wkv7::ChunkWorkspace ws{};
+    wkv7::SegWorkspace sws{};
 };
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -50,7 +52,10 @@ bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p
 int validate(const wkv7_args* a) {
     if (a->head_size != wkv7::HS) return WKV7_ERR_SHAPE;
     if (a->H < 1 || a->num_seqs < 0 || a->T < 0 || a->total_tokens < 0) return WKV7_ERR_SHAPE;
-    if (a->algo < WKV7_ALGO_AUTO || a->algo > WKV7_ALGO_CHAIN) return WKV7_ERR_ARG;
+    if (a->algo < WKV7_ALGO_AUTO || a->algo > WKV7_ALGO_SEGMENTED) return WKV7_ERR_ARG;
+    if (a->algo == WKV7_ALGO_SEGMENTED && a->snapshots) return WKV7_ERR_ARG;
+    if (a->algo == WKV7_ALGO_SEGMENTED && (a->cu_seqlens || a->n_keep) && a->num_seqs > wkv7::kSegMaxRows)
+        return WKV7_ERR_ARG;
     if (a->algo == WKV7_ALGO_CHAIN && (a->num_seqs > wkv7::kChainMaxSeqs || a->snapshots)) return WKV7_ERR_ARG;
     if (a->rec_max_len < -1) return WKV7_ERR_ARG;
     if ((int64_t)a->num_seqs * a->H > ((int64_t)1 << 31)) return WKV7_ERR_SHAPE;
@@ -101,6 +106,8 @@ Plan make_plan(const wkv7_args* a) {
     const int thr = a->rec_max_len >= 0 ? a->rec_max_len : kDefaultRecMaxLen;
     if (a->snapshots || a->algo == WKV7_ALGO_RECURRENT) {
         pl.run_recurrent = true;
+    } else if (a->algo == WKV7_ALGO_SEGMENTED) {
+        pl.run_seg = true;
     } else if (a->algo == WKV7_ALGO_CHAIN || chain_fits(a, bound, thr)) {
         pl.run_chain = true;
         pl.rec_len_rec = thr;
@@ -117,7 +124,18 @@ Plan make_plan(const wkv7_args* a) {
     }
     if (pl.run_chunked)
         pl.ws = wkv7::chunk_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen, pl.rec_len_chunk);
+    if (pl.run_seg)
+        pl.sws = wkv7::seg_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen || a->n_keep != nullptr,
+                                     pl.rec_len_chunk, wkv7::device_cu_count());
     return pl;
+}
+
+// Every path that uses a workspace leaves its first kSegFlagRegion bytes to the segmented kernel's hand-off flags, so
+// one workspace can serve calls of any path in stream order.
+size_t workspace_bytes(const Plan& pl) {
+    if (pl.run_seg) return pl.sws.total_bytes;
+    if (pl.run_chunked && pl.ws.total_bytes > 0) return wkv7::kSegFlagRegion + pl.ws.total_bytes;
+    return 0;
 }
 
 Params to_params(const wkv7_args* a) {
@@ -141,6 +159,7 @@ Params to_params(const wkv7_args* a) {
     p.T = a->T;
     p.H = a->H;
     p.rec_max_len = -1;
+    p.status = a->status;
     return p;
 }
 
@@ -261,7 +280,8 @@ int wkv7_workspace_size(const wkv7_args* args, size_t* bytes) {
     const int rc = validate(args);
     if (rc != WKV7_OK) return rc;
     const Plan pl = make_plan(args);
-    *bytes = pl.run_chunked ? pl.ws.total_bytes : 0;
+    if (pl.run_seg && pl.sws.units > (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t))) return WKV7_ERR_SHAPE;
+    *bytes = workspace_bytes(pl);
     return WKV7_OK;
 }
 
@@ -270,15 +290,17 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     const int rc = validate(args);
     if (rc != WKV7_OK) return rc;
     const Plan pl = make_plan(args);
-    if (pl.run_chunked && pl.ws.total_bytes > 0) {
-        if (!args->workspace || args->workspace_bytes < pl.ws.total_bytes) return WKV7_ERR_WORKSPACE;
+    if (pl.run_seg && pl.sws.units > (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t))) return WKV7_ERR_SHAPE;
+    const size_t need = workspace_bytes(pl);
+    if (need > 0) {
+        if (!args->workspace || args->workspace_bytes < need) return WKV7_ERR_WORKSPACE;
         if (!aligned(args->workspace, 256)) return WKV7_ERR_ALIGN;
     }
     if (args->num_seqs == 0) return WKV7_OK;
     hipStream_t s = static_cast<hipStream_t>(stream);
     Params p = to_params(args);
     if (args->status) {
-        const bool check_w = pl.run_chunked || pl.run_chain;
+        const bool check_w = pl.run_chunked || pl.run_chain || pl.run_seg;
         const int64_t work = std::max<int64_t>(args->num_seqs, check_w ? args->total_tokens * args->H * 8 : 0);
         int blocks = (int)std::min<int64_t>((work + 255) / 256, 1024);
         // the slot-clash comparison (up to 1024 x 1024 slot pairs) is spread over at least 16 workgroups
@@ -299,7 +321,12 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     }
     if (pl.run_chunked) {
         p.rec_max_len = pl.rec_len_chunk;
-        const hipError_t e = wkv7::launch_chunked(p, pl.ws, args->workspace, s);
+        const hipError_t e = wkv7::launch_chunked(p, pl.ws, static_cast<char*>(args->workspace) + wkv7::kSegFlagRegion, s);
+        if (e != hipSuccess) return static_cast<int>(e);
+    }
+    if (pl.run_seg) {
+        p.rec_max_len = pl.rec_len_chunk;
+        const hipError_t e = wkv7::launch_seg(p, pl.sws, args->workspace, s);
         if (e != hipSuccess) return static_cast<int>(e);
     }
     return WKV7_OK;

@@ -115,6 +115,7 @@ struct Params {
     int32_t T;                      // dense tokens per sequence; snapshot time stride
     int32_t H;
     int32_t rec_max_len;            // chunked launches: rows this short run the recurrent path instead
+    int32_t* status;                // nullable device status word (WKV7_STATUS_* bits)
 };
 
 // Extent of sequence n (rwkv_next/kernels/wkv7.py:46-54).

@@ -46,4 +46,22 @@ hipError_t launch_chain(const Params& p, hipStream_t stream);
 // (parallel over chunks), scan (sequential over chunks per (row, head, 16-column block)).
 hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* workspace, hipStream_t stream);
 
+// Segmented single-dispatch chunked prefill (wkv7_seg.hip).  Chunks of kSegChunk tokens; a row's chunks are cut into
+// segments of `seg` chunks, one workgroup per (row, head, segment) unit.  Ragged or n_keep calls build a row table
+// in LDS and take at most kSegMaxRows rows.
+constexpr int kSegChunk = 32;
+constexpr int kSegMaxRows = 4096;
+constexpr int kSegMinChunks = 8;
+// The workspace starts with one int32 hand-off flag per unit (at most kSegFlagRegion / 4 units).  The region must be
+// zero before a workspace's first call; every call that completes leaves it zero.  No other path writes it.
+constexpr size_t kSegFlagRegion = 256 * 1024;
+struct SegWorkspace {
+    int seg;             // chunks per segment
+    int64_t units;       // grid (an upper bound on the call's units)
+    size_t flag_bytes, x_bytes, qp_bytes, total_bytes;
+};
+SegWorkspace seg_workspace(int num_seqs, int H, int64_t total_tokens, int64_t max_len_bound, bool varlen,
+                           int rec_max_len, int cus);
+hipError_t launch_seg(const Params& p, const SegWorkspace& ws, void* workspace, hipStream_t stream);
+
 }  // namespace wkv7

@@ -1,0 +1,996 @@
+// wkv7_seg.hip -- chunked WKV7 prefill in one dispatch, with no chunk records in HBM (gfx950, bf16 MFMA).
+//
+// Replaces the reference's token-serial Triton program (rwkv_next/kernels/wkv7.py:65-77) for rows longer than the
+// token-serial threshold, dense or varlen (wkv7.py:46-54).  The reference walks every token of a row in one program,
+// so a B=1, T=4096, H=64 prefill has (64/BV)*64 programs and no parallelism over T.
+//
+// Decomposition.  A row is cut into chunks of C = 32 tokens and its chunks into segments of at most `seg` chunks.
+// One workgroup (a "unit") takes one (row, head, segment):
+//   * four prep wavefronts each build the transition of one chunk at a time, alone (no barrier inside a chunk):
+//     S_C = A S_0 + H,  y^T = S_0^T Q^T + O^T  (S_0 the state before the chunk);
+//     they hand the chunk's record (A, H, Q, O: 44 KB) to the state wavefronts through a three-slot LDS ring;
+//   * four state wavefronts each own 16 columns of the state (columns of S evolve independently) and apply the
+//     records in chunk order: y, then S <- A S + H.
+//   A segment after the first starts from zeros and also accumulates P = A_n .. A_1, the map from its true initial
+//   state S_in to its end state: S_end = S_local + P S_in, and every output gets Q_c P_{c-1} S_in added.  S_in is
+//   the previous segment's S_end, handed over through global memory (one flag per unit; the waiting unit always has
+//   the higher workgroup index, so the earliest unfinished unit never waits and every wait ends).
+//
+// Algebra of one chunk (per head; S is K x V, the reference's orientation, wkv7.py:4-7, 62-79).  With
+// g_t = sum_{u<=t} log2 d_u per channel (padding tokens count log2 d = 0), m = g_15 and c = g_31:
+//   Ah_t = a_t 2^{g_{t-1} - m},  Rh_t = r_t 2^{g_t - m},  Bp_t = b_t 2^{m - g_t},  Kp_t = k_t 2^{m - g_t}
+//   alpha[t][s] = Ah_t . Bp_s (s < t),  beta = Ah_t . Kp_s (s < t),  rho = Rh_t . Bp_s (s <= t),  sigma = Rh_t . Kp_s
+//   T = (I - alpha)^{-1},  W' = T Ah,  U0 = T beta V
+//   A = diag(2^c) + diag(2^{c-m}) Bp^T W' diag(2^m),   H = diag(2^{c-m}) (Bp^T U0 + Kp^T V)
+//   Q = (Rh + rho W') diag(2^m),                        O = sigma V + rho U0.
+// (U_t = a_t^T S_{t-1} satisfies (I - alpha) U = Ah 2^m S_0 + beta V; substituting gives the rest.)  Every decay
+// factor is one v_exp_f32 of a difference of the same partial sums, and |g_t - m| <= 16 max|log2 d| (<= 63 for
+// w <= WKV7_CHUNK_W_MAX), inside fp32 and bf16 range.
+//
+// Precision.  Products feeding the state (alpha, beta, T, W', U0, A, H, the state update and P) run as three bf16
+// MFMAs on hi/lo splits (x = hi + lo, relative error ~2^-17 per operand), two where one operand is exact bf16 (V);
+// products feeding only y (rho, sigma, Q, O, y, Q P, the correction) run as one.  fp32 accumulation throughout.
+//
+// Register layouts (lane l: i = l & 15, q = l >> 4).
+//   N layout of a token x channel matrix M, token tile tau (16 rows), channel block kb (32): lane holds
+//     M[16 tau + i][32 kb + 8 q + e], e = 0..7 -- one 16-byte global load.  Two N fragments as the A and B operands
+//     of v_mfma_f32_16x16x32_bf16 give the Gram tile M1 M2^T.
+//   RL layout of a 16 x 16 tile of X (the MFMA result layout): lane holds X[x0 + 4 q + v][y0 + i], v = 0..3.
+//     With RL(X) as the A operand and RL(Y) as the B operand, v_mfma_f32_16x16x16bf16_1k accumulates RL(X^T Y)
+//     (contraction over the 16 rows); two RL tiles stacked (rows 0-15 in elements 0-3, rows 16-31 in 4-7) are the
+//     16x16x32 operand of a 32-row contraction (the contraction order is permuted alike in both operands).
+//   An identity operand turns an N fragment into the RL tile of M or of M^T (one exact MFMA per tile).
+// The state S is held as RL tiles (k tile m, column tile j); a state wavefront j holds tiles (0..3, j).
+#include <algorithm>
+
+#include "wkv7.h"
+#include "wkv7_device.h"
+#include "wkv7_launch.h"
+
+namespace wkv7 {
+
+namespace {
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef short s4 __attribute__((ext_vector_type(4)));
+
+constexpr int SC = kSegChunk;          // 32 tokens per chunk
+constexpr int NREC = 3;                // LDS ring slots
+constexpr float kL2E = 1.4426950408889634f;
+constexpr int kSpinLimit = 1 << 22;    // LDS ring waits (s_sleep 1 each: a few hundred ms at most)
+constexpr int kFlagSpinLimit = 1 << 20;  // segment hand-off waits (s_sleep 8 each)
+
+// Record of one chunk in the LDS ring (byte offsets).  Pieces are lane-contiguous 16-byte words.
+constexpr int REC_A = 0;                       // A^T hi/lo as 16x16x32 A operands: [k tile mo][kb][hl][lane]
+constexpr int REC_H = REC_A + 4 * 2 * 2 * 1024;  // H, RL fp32: [column tile j][k tile m][lane]
+constexpr int REC_Q = REC_H + 16 * 1024;       // Q^T hi as 16x16x32 B operands: [token tile][kb][lane]
+constexpr int REC_O = REC_Q + 4 * 1024;        // O^T, RL fp32: [column tile j][token tile][lane]
+constexpr int REC_BYTES = REC_O + 8 * 1024;    // 45056
+
+struct SegSmem {
+    char ring[NREC][REC_BYTES];
+    float fac[4][3][HS];   // per prep wavefront: 2^m, 2^{c-m}, 2^c per channel of its current chunk
+    int ready[NREC];       // chunk index + 1 of the record a slot holds
+    int done[NREC][4];     // per state wavefront: uses of the slot it has finished reading
+    int fail;
+};
+
+__device__ __forceinline__ f4 z4() { return f4{0.f, 0.f, 0.f, 0.f}; }
+__device__ __forceinline__ f4 mma32(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
+__device__ __forceinline__ f4 mma16(s4 a, s4 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0); }
+
+struct T4 { s4 h, l; };   // hi/lo bf16 of an RL tile
+struct T8 { bf8 h, l; };  // hi/lo bf16 16x16x32 operand
+
+__device__ __forceinline__ T4 split_t(f4 x) {
+    uint32_t hw[2], lw[2];
+    split_pair(x[0], x[1], hw[0], lw[0]);
+    split_pair(x[2], x[3], hw[1], lw[1]);
+    return T4{__builtin_bit_cast(s4, hw), __builtin_bit_cast(s4, lw)};
+}
+__device__ __forceinline__ s4 hi_t(f4 x) {
+    const uint32_t hw[2] = {pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
+    return __builtin_bit_cast(s4, hw);
+}
+__device__ __forceinline__ bf8 cat(s4 a, s4 b) {
+    return __builtin_bit_cast(bf8, __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+__device__ __forceinline__ T8 cat(T4 a, T4 b) { return T8{cat(a.h, b.h), cat(a.l, b.l)}; }
+// RL(X^T Y) += ..., 16 contraction rows (small terms first)
+__device__ __forceinline__ f4 p16x3(T4 x, T4 y, f4 c) {
+    c = mma16(x.h, y.l, c);
+    c = mma16(x.l, y.h, c);
+    return mma16(x.h, y.h, c);
+}
+__device__ __forceinline__ f4 p16x2(T4 x, s4 y, f4 c) {  // y exact in bf16
+    c = mma16(x.l, y, c);
+    return mma16(x.h, y, c);
+}
+// 32 contraction rows
+__device__ __forceinline__ f4 p32x3(T8 x, T8 y, f4 c) {
+    c = mma32(x.h, y.l, c);
+    c = mma32(x.l, y.h, c);
+    return mma32(x.h, y.h, c);
+}
+__device__ __forceinline__ f4 p32x2(T8 x, bf8 y, f4 c) {
+    c = mma32(x.l, y, c);
+    return mma32(x.h, y, c);
+}
+
+// x + I for an RL tile on the diagonal
+__device__ __forceinline__ f4 plus_i(f4 x, int lane) {
+    const int i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) x[v] += (4 * q + v == i) ? 1.f : 0.f;
+    return x;
+}
+// RL(I) as a bf16 operand
+__device__ __forceinline__ s4 ident16(int lane) {
+    const int i = lane & 15, q = lane >> 4;
+    s4 r;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) r[v] = (4 * q + v == i) ? (short)0x3F80 : (short)0;
+    return r;
+}
+// Column selector of a 16x16x32 operand: element e of lane (i, q) is 1 iff 8 q + e == i + 16 par.  As the B operand
+// after an N fragment of block kb it yields the RL tile of columns 32 kb + 16 par ..; as the A operand before one, the
+// RL tile of the transpose.
+__device__ __forceinline__ bf8 isel(int par, int lane) {
+    const int i = lane & 15, q = lane >> 4;
+    s4 a, b;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        a[e] = (8 * q + e == i + 16 * par) ? (short)0x3F80 : (short)0;
+        b[e] = (8 * q + 4 + e == i + 16 * par) ? (short)0x3F80 : (short)0;
+    }
+    return cat(a, b);
+}
+
+// mask of an RL tile on the diagonal: keep row < column (strict) or row <= column
+__device__ __forceinline__ f4 keep_upper(f4 x, int lane, bool strict) {
+    const int i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+        const int r = 4 * q + v;
+        if (strict ? !(r < i) : !(r <= i)) x[v] = 0.f;
+    }
+    return x;
+}
+
+template <int CTRL, bool BC>
+__device__ __forceinline__ float dpp(float x) {
+    float r = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, BC));
+    asm volatile("" : "+v"(r));
+    return r;
+}
+// inclusive prefix sum over the 16 lanes of each row (Hillis-Steele on row_shr; lanes before the start read 0)
+__device__ __forceinline__ float row_scan16(float x) {
+    x = x + dpp<0x111, true>(x);
+    x = x + dpp<0x112, true>(x);
+    x = x + dpp<0x114, true>(x);
+    x = x + dpp<0x118, true>(x);
+    return x;
+}
+__device__ __forceinline__ float bcast15(float x) { return dpp<0x15F, false>(x); }  // row_newbcast:15
+__device__ __forceinline__ float shr1(float x) { return dpp<0x111, true>(x); }
+
+__device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+__device__ __forceinline__ void vmem_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Exchange between workgroups.  Every word of an exchange entry is written and read as a relaxed agent-scope atomic,
+// which is coherent across the device by itself (no cache maintenance); a writer waits for its stores to complete
+// before its flag store, and a reader issues its loads only after its flag load returned.  Agent-scope fences would
+// write back / invalidate a whole L2 per call and cost microseconds each.
+__device__ __forceinline__ void xstore(f4* dst, f4 x) {
+    uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+    const uint64_t a = __builtin_bit_cast(uint64_t, f2_t{x[0], x[1]}), b = __builtin_bit_cast(uint64_t, f2_t{x[2], x[3]});
+    __hip_atomic_store(d, a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(d + 1, b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f4 xload(const f4* src) {
+    const uint64_t* s = reinterpret_cast<const uint64_t*>(src);
+    const f2_t a = __builtin_bit_cast(f2_t, __hip_atomic_load(s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    const f2_t b = __builtin_bit_cast(f2_t, __hip_atomic_load(s + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    return f4{a[0], a[1], b[0], b[1]};
+}
+
+__device__ __forceinline__ bf8 as_bf8(uint4 x) { return __builtin_bit_cast(bf8, x); }
+__device__ __forceinline__ uint4 as_u4(bf8 x) { return __builtin_bit_cast(uint4, x); }
+
+// ------------------------------------------------------------------------------------------------------------------
+// Units
+// ------------------------------------------------------------------------------------------------------------------
+
+struct Unit {
+    bool ok;
+    int n, h, s, nseg;
+    int64_t bos;
+    int L, nch;       // row length and chunks of the row
+    int c0, c1;       // chunk range of the unit
+    int64_t u;        // unit index (exchange slot); the previous segment's is u - H
+    int64_t qp0;      // Q P slot of the row's chunk `seg` (chunks of later segments follow it)
+};
+
+// Rows this launch owns: every row when p.rec_max_len < 0, else rows longer than it (the token-serial kernel takes
+// the others).  An owned row has at least one unit: an empty row's unit passes its initial state to its final state.
+__device__ __forceinline__ bool owns(const Params& p, int L) { return p.rec_max_len < 0 || L > p.rec_max_len; }
+__device__ __forceinline__ int row_chunks(int L) { return (L + SC - 1) / SC; }
+__device__ __forceinline__ int row_units(const Params& p, int L, int seg) {
+    return owns(p, L) ? std::max(1, (row_chunks(L) + seg - 1) / seg) : 0;
+}
+
+// Row table of ragged / n_keep calls, built in LDS by every workgroup (rows <= kSegMaxRows):
+// tab[n] = units (segments) before row n, tab[kSegMaxRows + 1 + n] = Q P chunks before row n.
+__device__ Unit find_unit(const Params& p, int seg, int64_t blk, int* tab) {
+    Unit U{};
+    const int H = p.H;
+    const int64_t k = blk / H;
+    U.h = (int)(blk - k * H);
+    if (!p.cu && !p.n_keep) {
+        const int L = p.T;
+        const int nseg = row_units(p, L, seg);
+        if (nseg == 0) return U;
+        const int nch = row_chunks(L);
+        const int64_t n = k / nseg;
+        if (n >= p.num_seqs) return U;
+        U.n = (int)n;
+        U.s = (int)(k - n * nseg);
+        U.nseg = nseg;
+        U.L = L;
+        U.nch = nch;
+        U.bos = n * (int64_t)p.T;
+        U.qp0 = n * (int64_t)std::max(0, nch - seg);
+    } else {
+        const int N = p.num_seqs;
+        int* useg = tab;
+        int* uqp = tab + kSegMaxRows + 1;
+        // per-thread partial sums over a contiguous block of rows, then an exclusive scan over threads
+        int (*part)[512] = reinterpret_cast<int (*)[512]>(tab + 2 * (kSegMaxRows + 1));
+        const int tid = threadIdx.x, nt = blockDim.x;
+        const int per = (N + nt - 1) / nt;
+        const int r0 = min(N, tid * per), r1 = min(N, r0 + per);
+        int a = 0, b = 0;
+        for (int n = r0; n < r1; ++n) {
+            int64_t bos;
+            int L;
+            seq_extent(p, n, bos, L);
+            useg[n] = row_units(p, L, seg);
+            uqp[n] = useg[n] ? std::max(0, row_chunks(L) - seg) : 0;
+            a += useg[n];
+            b += uqp[n];
+        }
+        part[0][tid] = a;
+        part[1][tid] = b;
+        __syncthreads();
+        if (tid < 2) {
+            int acc = 0;
+            for (int t = 0; t < nt; ++t) {
+                const int x = part[tid][t];
+                part[tid][t] = acc;
+                acc += x;
+            }
+            if (tid == 0) useg[N] = acc; else uqp[N] = acc;
+        }
+        __syncthreads();
+        a = part[0][tid];
+        b = part[1][tid];
+        for (int n = r0; n < r1; ++n) {
+            const int x = useg[n], y = uqp[n];
+            useg[n] = a;
+            uqp[n] = b;
+            a += x;
+            b += y;
+        }
+        __syncthreads();
+        if (k >= useg[N]) {
+            __syncthreads();
+            return U;
+        }
+        int lo = 0, hi = N - 1;  // last n with useg[n] <= k
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (useg[mid] <= k) lo = mid; else hi = mid - 1;
+        }
+        U.n = lo;
+        U.s = (int)(k - useg[lo]);
+        U.nseg = useg[lo + 1] - useg[lo];
+        U.qp0 = uqp[lo];
+        seq_extent(p, lo, U.bos, U.L);
+        U.nch = row_chunks(U.L);
+        __syncthreads();  // the table lives in the ring
+    }
+    U.ok = true;
+    U.u = blk;
+    U.c0 = U.s * seg;
+    U.c1 = std::min(U.nch, U.c0 + seg);
+    return U;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Prep wavefront: one chunk -> record
+// ------------------------------------------------------------------------------------------------------------------
+
+struct Raw {
+    uint4 w[2][2], a[2][2], b[2][2], k[2][2], r[2][2], v[2][2];  // N layout [token tile][channel block]
+};
+
+__device__ __forceinline__ void load_raw(Raw& x, const Params& p, int64_t tok0, int Lc, int h, int lane) {
+    const int i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+        const int t = 16 * tau + i;
+        const int64_t tok = tok0 + (t < Lc ? t : 0);  // rows past the chunk read its first token and are zeroed
+        const int64_t off = tok * p.in_tok_stride + (int64_t)h * HS + 8 * q;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            x.w[tau][kb] = *reinterpret_cast<const uint4*>(p.w + off + 32 * kb);
+            x.a[tau][kb] = *reinterpret_cast<const uint4*>(p.a + off + 32 * kb);
+            x.b[tau][kb] = *reinterpret_cast<const uint4*>(p.b + off + 32 * kb);
+            x.k[tau][kb] = *reinterpret_cast<const uint4*>(p.k + off + 32 * kb);
+            x.r[tau][kb] = *reinterpret_cast<const uint4*>(p.r + off + 32 * kb);
+            x.v[tau][kb] = *reinterpret_cast<const uint4*>(p.v + off + 32 * kb);
+        }
+    }
+}
+
+__device__ __forceinline__ void unpack8(uint4 x, float (&f)[8]) {
+    bf16x2_to_f32(x.x, f[0], f[1]);
+    bf16x2_to_f32(x.y, f[2], f[3]);
+    bf16x2_to_f32(x.z, f[4], f[5]);
+    bf16x2_to_f32(x.w, f[6], f[7]);
+}
+// fp32 x 8 -> hi / lo bf16 x 8
+__device__ __forceinline__ void split8(const float (&f)[8], bf8& h, bf8& l) {
+    uint32_t hw[4], lw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) split_pair(f[2 * e], f[2 * e + 1], hw[e], lw[e]);
+    h = __builtin_bit_cast(bf8, hw);
+    l = __builtin_bit_cast(bf8, lw);
+}
+__device__ __forceinline__ bf8 hi8(const float (&f)[8]) {
+    uint32_t hw[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) hw[e] = pack_bf16x2(f[2 * e], f[2 * e + 1]);
+    return __builtin_bit_cast(bf8, hw);
+}
+
+// 2^m etc. of channel ch, this wavefront's chunk
+struct Fac {
+    const float* em;   // 2^m
+    const float* ecm;  // 2^{c-m}
+    const float* ec;   // 2^c
+};
+
+// The transition of one chunk into `rec` (an LDS ring slot), after waiting for that slot to be free.
+__device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, float (*fac)[HS], int lane,
+                                           const volatile int* done4, int use, int* fail) {
+    const int i = lane & 15, q = lane >> 4;
+
+    // ---- 1. log2-decays lam = log2 d = -e^w log2(e) and their running sums over the chunk's tokens.  Lanes i of
+    //         a row hold tokens 16 tau + i of the row's 8 channels; every sum is a fixed sequence of row_shr adds, so
+    //         the midpoint m (token 15) and the total c (token 31) equal the g of those tokens bit for bit.
+    float g[2][2][8];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+        const bool valid = 16 * tau + i < Lc;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            float w8[8];
+            unpack8(raw.w[tau][kb], w8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float lam = -__builtin_amdgcn_exp2f(w8[e] * kL2E) * kL2E;
+                g[tau][kb][e] = row_scan16(valid ? lam : 0.f);
+            }
+        }
+    }
+    float m[2][8], c[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            m[kb][e] = bcast15(g[0][kb][e]);
+            g[1][kb][e] += m[kb][e];
+            c[kb][e] = bcast15(g[1][kb][e]);
+        }
+    // per-channel factors for the products' row/column scalings (lanes i == 0 hold every channel once)
+    if (i == 0) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int ch = 32 * kb + 8 * q + e;
+                fac[0][ch] = __builtin_amdgcn_exp2f(m[kb][e]);
+                fac[1][ch] = __builtin_amdgcn_exp2f(c[kb][e] - m[kb][e]);
+                fac[2][ch] = __builtin_amdgcn_exp2f(c[kb][e]);
+            }
+    }
+    wave_lds_sync();
+
+    // ---- 2. operands referenced to the midpoint (N layout), split hi/lo
+    bf8 Ah[2][2], Al[2][2], Bh[2][2], Bl[2][2], Kh[2][2], Kl[2][2], Rh[2][2], Vn[2][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        float fr0[8];
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau) {
+            const uint32_t vm = (16 * tau + i < Lc) ? 0xffffffffu : 0u;
+            auto msk = [vm](uint4 x) { return make_uint4(x.x & vm, x.y & vm, x.z & vm, x.w & vm); };
+            float a8[8], b8[8], k8[8], r8[8];
+            unpack8(msk(raw.a[tau][kb]), a8);
+            unpack8(msk(raw.b[tau][kb]), b8);
+            unpack8(msk(raw.k[tau][kb]), k8);
+            unpack8(msk(raw.r[tau][kb]), r8);
+            float fa[8], fr[8], fb[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float d = g[tau][kb][e] - m[kb][e];
+                fr[e] = __builtin_amdgcn_exp2f(d);
+                fb[e] = __builtin_amdgcn_exp2f(-d);
+                const float prev = shr1(fr[e]);  // token t - 1 of the row (lane 0 reads 0)
+                const float first = tau == 0 ? __builtin_amdgcn_exp2f(-m[kb][e]) : bcast15(fr0[e]);
+                fa[e] = i == 0 ? first : prev;
+            }
+            if (tau == 0)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) fr0[e] = fr[e];
+            float x8[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x8[e] = a8[e] * fa[e];
+            split8(x8, Ah[tau][kb], Al[tau][kb]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x8[e] = b8[e] * fb[e];
+            split8(x8, Bh[tau][kb], Bl[tau][kb]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x8[e] = k8[e] * fb[e];
+            split8(x8, Kh[tau][kb], Kl[tau][kb]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) x8[e] = r8[e] * fr[e];
+            Rh[tau][kb] = hi8(x8);
+            Vn[tau][kb] = as_bf8(msk(raw.v[tau][kb]));
+        }
+    }
+
+    // ---- 3. Grams (RL tiles, rows s, columns t): alphaT = Bp Ah^T, betaT = Kp Ah^T (s < t), rhoT = Bp Rh^T,
+    //         sigmaT = Kp Rh^T (s <= t).  Tiles (s tile, t tile) = (0,0), (0,1), (1,1); (1,0) is zero.
+    f4 aT[3], bT[3], rT[3], sT[3];
+    {
+        const int st[3] = {0, 0, 1}, tt[3] = {0, 1, 1};
+#pragma unroll
+        for (int x = 0; x < 3; ++x) {
+            f4 a = z4(), b = z4(), r = z4(), s = z4();
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const bf8 bh = Bh[st[x]][kb], bl = Bl[st[x]][kb], kh = Kh[st[x]][kb], kl = Kl[st[x]][kb];
+                const bf8 ah = Ah[tt[x]][kb], al = Al[tt[x]][kb], rh = Rh[tt[x]][kb];
+                a = mma32(bh, al, a);
+                a = mma32(bl, ah, a);
+                a = mma32(bh, ah, a);
+                b = mma32(kh, al, b);
+                b = mma32(kl, ah, b);
+                b = mma32(kh, ah, b);
+                r = mma32(bh, rh, r);
+                s = mma32(kh, rh, s);
+            }
+            if (st[x] == tt[x]) {
+                a = keep_upper(a, lane, true);
+                b = keep_upper(b, lane, true);
+                r = keep_upper(r, lane, false);
+                s = keep_upper(s, lane, false);
+            }
+            aT[x] = a;
+            bT[x] = b;
+            rT[x] = r;
+            sT[x] = s;
+        }
+    }
+
+    // ---- 4. T^T = (I - alpha^T)^{-1} by 16 x 16 blocks: T_dd = (I + L)(I + L^2)(I + L^4)(I + L^8) with L = alpha_dd
+    //         strictly lower (L^16 = 0); products in the RL form X^T Y, so powers of L and L^T feed each other.
+    //         T10 = T11 alpha10 T00, so (T^T)_01 = T10^T = (alpha10 T00)^T T11^T.
+    const s4 Id = ident16(lane);
+    T4 tt00, tt01, tt11;
+    {
+        T4 TT[2], T00;
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+            const f4 LTf = aT[d == 0 ? 0 : 2];                                 // RL(L^T)
+            const T4 LT = split_t(LTf);
+            const f4 LLf = mma16(LT.l, Id, mma16(LT.h, Id, z4()));            // RL(L): transpose, exact
+            const T4 LL = split_t(LLf);
+            const f4 L2f = p16x3(LT, LL, z4()), L2tf = p16x3(LL, LT, z4());
+            const T4 L2 = split_t(L2f), L2t = split_t(L2tf);
+            const f4 L4f = p16x3(L2t, L2, z4()), L4tf = p16x3(L2, L2t, z4());
+            const T4 L4 = split_t(L4f), L4t = split_t(L4tf);
+            const f4 L8f = p16x3(L4t, L4, z4());
+            // T^T = (I + L^T)(I + L^2T)(I + L^4T)(I + L^8T) as X^T Y products with X = I + L^{2^k}; the diagonals of
+            // the powers are zero, so adding I is exact
+            T4 acc = split_t(p16x3(split_t(plus_i(LLf, lane)), split_t(plus_i(L2tf, lane)), z4()));
+            acc = split_t(p16x3(split_t(plus_i(L4f, lane)), acc, z4()));
+            TT[d] = split_t(p16x3(split_t(plus_i(L8f, lane)), acc, z4()));
+            if (d == 0) {  // T00 itself, for the off-diagonal block
+                const f4 L8tf = p16x3(L4, L4t, z4());
+                T4 t0 = split_t(p16x3(split_t(plus_i(LTf, lane)), split_t(plus_i(L2f, lane)), z4()));
+                t0 = split_t(p16x3(split_t(plus_i(L4tf, lane)), t0, z4()));
+                T00 = split_t(p16x3(split_t(plus_i(L8tf, lane)), t0, z4()));
+            }
+        }
+        const T4 Z = split_t(p16x3(split_t(aT[1]), T00, z4()));  // alpha10 T00
+        tt00 = TT[0];
+        tt11 = TT[1];
+        tt01 = split_t(p16x3(Z, TT[1], z4()));
+    }
+    const T8 ttp = cat(tt01, tt11);  // rows s 0-31 of (T^T)'s token tile 1
+
+    // ---- 5. token-row RL tiles (token tile tau, channel tile j) through identity MFMAs (exact): V now, the others
+    //         on the fly below.
+    const bf8 I0 = isel(0, lane), I1 = isel(1, lane);
+    s4 rV[2][4];
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) rV[tau][j] = hi_t(mma32(Vn[tau][j >> 1], (j & 1) ? I1 : I0, z4()));
+    auto rl = [&](const bf8 (&H8)[2][2], const bf8 (&L8)[2][2], int tau, int j) {
+        const bf8 I = (j & 1) ? I1 : I0;
+        return T4{hi_t(mma32(H8[tau][j >> 1], I, z4())), hi_t(mma32(L8[tau][j >> 1], I, z4()))};
+    };
+
+    // ---- 6. wait for the ring slot
+    {
+        bool ok = false;
+        for (int it = 0; it < kSpinLimit; ++it) {
+            const int d0 = done4[0], d1 = done4[1], d2 = done4[2], d3 = done4[3];
+            if (min(min(d0, d1), min(d2, d3)) >= use) {
+                ok = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (!ok) *fail = 1;
+        asm volatile("" ::: "memory");
+    }
+    uint4* const R = reinterpret_cast<uint4*>(rec);
+
+    // ---- 7. per channel tile j: W' = T Ah and U0 = T (beta V) (RL tiles (token tile, j), kept), then
+    //         Q^T = diag(2^m) (Rh^T + W'^T rho^T) and O^T = V^T sigma^T + U0^T rho^T (tiles (j, token tile), stored)
+    T4 Wt[2][4], U0t[2][4];
+    // per-lane factors, read in one batch per phase (ahead of that phase's record stores): 2^m of rows 16 j + 4 q + v
+    f4 emr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) emr[j] = *reinterpret_cast<const f4*>(&fac[0][16 * j + 4 * q]);
+    {
+        const T4 b00 = split_t(bT[0]);
+        const T8 bp = cat(split_t(bT[1]), split_t(bT[2]));
+        const s4 r00 = hi_t(rT[0]), s00 = hi_t(sT[0]);
+        const bf8 rp = cat(hi_t(rT[1]), hi_t(rT[2])), sp = cat(hi_t(sT[1]), hi_t(sT[2]));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const T4 a0 = rl(Ah, Al, 0, j), a1 = rl(Ah, Al, 1, j);
+            Wt[0][j] = split_t(p16x3(tt00, a0, z4()));
+            Wt[1][j] = split_t(p32x3(ttp, cat(a0, a1), z4()));
+            const T4 bv0 = split_t(p16x2(b00, rV[0][j], z4()));
+            const T4 bv1 = split_t(p32x2(bp, cat(rV[0][j], rV[1][j]), z4()));
+            U0t[0][j] = split_t(p16x3(tt00, bv0, z4()));
+            U0t[1][j] = split_t(p32x3(ttp, cat(bv0, bv1), z4()));
+            const bf8 I = (j & 1) ? I1 : I0;
+            f4 q0 = mma16(Wt[0][j].h, r00, mma32(I, Rh[0][j >> 1], z4()));
+            f4 q1 = mma32(cat(Wt[0][j].h, Wt[1][j].h), rp, mma32(I, Rh[1][j >> 1], z4()));
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                q0[v] *= emr[j][v];
+                q1[v] *= emr[j][v];
+            }
+            // Q^T pieces [token tile][kb]: tiles j = 2 kb, 2 kb + 1 in the low / high 8 bytes
+            reinterpret_cast<uint2*>(R + (REC_Q / 16) + (0 * 2 + (j >> 1)) * 64 + lane)[j & 1] = __builtin_bit_cast(uint2, hi_t(q0));
+            reinterpret_cast<uint2*>(R + (REC_Q / 16) + (1 * 2 + (j >> 1)) * 64 + lane)[j & 1] = __builtin_bit_cast(uint2, hi_t(q1));
+            const f4 o0 = mma16(rV[0][j], s00, mma16(U0t[0][j].h, r00, z4()));
+            const f4 o1 = mma32(cat(rV[0][j], rV[1][j]), sp, mma32(cat(U0t[0][j].h, U0t[1][j].h), rp, z4()));
+            R[(REC_O / 16) + (j * 2 + 0) * 64 + lane] = __builtin_bit_cast(uint4, o0);
+            R[(REC_O / 16) + (j * 2 + 1) * 64 + lane] = __builtin_bit_cast(uint4, o1);
+        }
+    }
+
+    // ---- 8. A^T tiles (k' tile mr, k tile j) = 2^{m_k'} (W'^T Bp)[k'][k] 2^{c_k - m_k} + [k' = k] 2^{c_k}; the scan's
+    //         A operand for output tile j and contraction block kb stacks k' tiles 2 kb and 2 kb + 1.
+    float cfj[4], dgj[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        cfj[j] = fac[1][16 * j + i];
+        dgj[j] = fac[2][16 * j + i];
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const float cf = cfj[j], dg = dgj[j];
+        const T8 bpj = cat(rl(Bh, Bl, 0, j), rl(Bh, Bl, 1, j));
+        T4 at[4];
+#pragma unroll
+        for (int mr = 0; mr < 4; ++mr) {
+            f4 x = p32x3(cat(Wt[0][mr], Wt[1][mr]), bpj, z4());
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                x[v] = x[v] * emr[mr][v] * cf;
+                if (mr == j && 4 * q + v == i) x[v] += dg;
+            }
+            at[mr] = split_t(x);
+        }
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+            const T8 pc = cat(at[2 * kb], at[2 * kb + 1]);
+            R[(REC_A / 16) + ((j * 2 + kb) * 2 + 0) * 64 + lane] = as_u4(pc.h);
+            R[(REC_A / 16) + ((j * 2 + kb) * 2 + 1) * 64 + lane] = as_u4(pc.l);
+        }
+    }
+    // ---- 9. H tiles (k tile mr, column tile j) = 2^{c_k - m_k} (Bp^T U0 + Kp^T V)
+    f4 ecr[4];
+#pragma unroll
+    for (int mr = 0; mr < 4; ++mr) ecr[mr] = *reinterpret_cast<const f4*>(&fac[1][16 * mr + 4 * q]);
+#pragma unroll
+    for (int mr = 0; mr < 4; ++mr) {
+        const T8 bpm = cat(rl(Bh, Bl, 0, mr), rl(Bh, Bl, 1, mr)), kpm = cat(rl(Kh, Kl, 0, mr), rl(Kh, Kl, 1, mr));
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            f4 x = p32x3(bpm, cat(U0t[0][j], U0t[1][j]), z4());
+            x = p32x2(kpm, cat(rV[0][j], rV[1][j]), x);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) x[v] *= ecr[mr][v];
+            R[(REC_H / 16) + (j * 4 + mr) * 64 + lane] = __builtin_bit_cast(uint4, x);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// State wavefront
+// ------------------------------------------------------------------------------------------------------------------
+
+// the state's 16x16x32 operands: contraction block kb stacks k tiles 2 kb and 2 kb + 1 of column tile j
+__device__ __forceinline__ void state_ops(const f4 (&S)[4], T8 (&o)[2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) o[kb] = cat(split_t(S[2 * kb]), split_t(S[2 * kb + 1]));
+}
+
+__device__ __forceinline__ void store_y(const Params& p, int64_t tok0, int Lc, int h, int j, int lane, const f4 (&y)[2]) {
+    const int i = lane & 15, q = lane >> 4;
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+        const int t = 16 * tau + i;
+        if (t < Lc) {
+            uint2 pk;
+            pk.x = pack_bf16x2(y[tau][0], y[tau][1]);
+            pk.y = pack_bf16x2(y[tau][2], y[tau][3]);
+            *reinterpret_cast<uint2*>(p.o + (tok0 + t) * p.o_tok_stride + (int64_t)h * HS + 16 * j + 4 * q) = pk;
+        }
+    }
+}
+
+}  // namespace
+
+// xbuf: one 32 KB entry per unit (its local end state, then its P^T, RL tiles); flags: one per unit, set to the number
+// of later segments of the row that read the entry and counted down by them.
+__global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, int32_t* __restrict__ flags,
+                                                       float* __restrict__ xbuf, char* __restrict__ qpbuf) {
+    __shared__ SegSmem sm;
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int i = lane & 15, q = lane >> 4;
+    const Unit U = find_unit(p, seg, (int64_t)blockIdx.x, reinterpret_cast<int*>(&sm.ring[0][0]));
+    if (!U.ok) return;
+    const int H = p.H, h = U.h;
+    if (tid < NREC) sm.ready[tid] = 0;
+    if (tid < NREC * 4) (&sm.done[0][0])[tid] = 0;
+    if (tid == 0) sm.fail = 0;
+    __syncthreads();
+    const int nloc = U.c1 - U.c0;  // chunks of this unit
+    // Q P slot of local chunk cl (segments after the first): the row's chunks c >= seg are numbered from U.qp0
+    auto qp_slot = [&](int cl) -> uint4* {
+        const int64_t slot = U.qp0 + (int64_t)(U.c0 + cl - seg);
+        return reinterpret_cast<uint4*>(qpbuf + (slot * H + h) * (int64_t)(4 * 1024));
+    };
+
+    f4 S[4], P[4];  // state wavefronts: column tile j of S and of P
+    if (wv < 4) {
+        // ---------------- prep wavefronts: chunks cl = wv, wv + 4, ..
+        for (int cl = wv; cl < nloc; cl += 4) {
+            const int ci = U.c0 + cl;
+            const int64_t tok0 = U.bos + (int64_t)ci * SC;
+            const int Lc = min(SC, U.L - ci * SC);
+            Raw raw;
+            load_raw(raw, p, tok0, Lc, h, lane);
+            const int slot = cl % NREC;
+            prep_chunk(raw, Lc, sm.ring[slot], sm.fac[wv], lane, sm.done[slot], cl / NREC, &sm.fail);
+            lds_wait_all();
+            if (lane == 0) *reinterpret_cast<volatile int*>(&sm.ready[slot]) = cl + 1;
+        }
+    } else {
+        // ---------------- state wavefronts: columns 16 j .. 16 j + 15
+        const int j = wv - 4;
+        const float* src = U.s == 0 ? state_src(p, U.n, h) : nullptr;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) S[m][v] = src ? src[(16 * m + 4 * q + v) * HS + 16 * j + i] : 0.f;
+            P[m] = (m == j) ? plus_i(z4(), lane) : z4();
+        }
+        const bool acc_p = U.s > 0 && p.o;  // P S_in enters the outputs and the end state
+        const bool acc_pp = U.s > 0;
+        for (int cl = 0; cl < nloc; ++cl) {
+            const int slot = cl % NREC;
+            {
+                bool ok = false;
+                for (int it = 0; it < kSpinLimit; ++it) {
+                    if (*reinterpret_cast<volatile int*>(&sm.ready[slot]) == cl + 1) {
+                        ok = true;
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                }
+                if (!ok) sm.fail = 1;
+                asm volatile("" ::: "memory");
+            }
+            const uint4* const R = reinterpret_cast<const uint4*>(sm.ring[slot]);
+            uint4 ra[4][2][2], rq[2][2];
+            f4 rh[4], ro[2];
+#pragma unroll
+            for (int mo = 0; mo < 4; ++mo)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                    for (int hl = 0; hl < 2; ++hl) ra[mo][kb][hl] = R[(REC_A / 16) + ((mo * 2 + kb) * 2 + hl) * 64 + lane];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) rh[m] = __builtin_bit_cast(f4, R[(REC_H / 16) + (j * 4 + m) * 64 + lane]);
+#pragma unroll
+            for (int tau = 0; tau < 2; ++tau) {
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) rq[tau][kb] = R[(REC_Q / 16) + (tau * 2 + kb) * 64 + lane];
+                ro[tau] = __builtin_bit_cast(f4, R[(REC_O / 16) + (j * 2 + tau) * 64 + lane]);
+            }
+            lds_wait_all();
+            if (lane == 0) *reinterpret_cast<volatile int*>(&sm.done[slot][j]) = cl / NREC + 1;
+
+            const int ci = U.c0 + cl;
+            const int64_t tok0 = U.bos + (int64_t)ci * SC;
+            const int Lc = min(SC, U.L - ci * SC);
+            T8 so[2];
+            state_ops(S, so);
+            // y^T = S^T Q^T + O^T  (token tiles 0, 1)
+            f4 y[2];
+#pragma unroll
+            for (int tau = 0; tau < 2; ++tau) {
+                y[tau] = ro[tau];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) y[tau] = mma32(so[kb].h, as_bf8(rq[tau][kb]), y[tau]);
+            }
+            if (p.o) store_y(p, tok0, Lc, h, j, lane, y);
+            T8 po[2];
+            if (acc_p) {
+                state_ops(P, po);
+                // (Q P)^T rows k' in column tile j, for the correction once S_in is known
+                uint4* const dst = qp_slot(cl);
+#pragma unroll
+                for (int tau = 0; tau < 2; ++tau) {
+                    f4 x = z4();
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) x = mma32(po[kb].h, as_bf8(rq[tau][kb]), x);
+                    // piece [tau][kb = j >> 1], half j & 1
+                    uint2* d2 = reinterpret_cast<uint2*>(dst + (tau * 2 + (j >> 1)) * 64 + lane) + (j & 1);
+                    *d2 = __builtin_bit_cast(uint2, hi_t(x));
+                }
+            }
+            // S <- A S + H,  P <- A P
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                f4 x = rh[m];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+                    x = p32x3(T8{as_bf8(ra[m][kb][0]), as_bf8(ra[m][kb][1])}, so[kb], x);
+                S[m] = x;
+            }
+            if (acc_pp) {
+                if (!acc_p) state_ops(P, po);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    f4 x = z4();
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+                        x = p32x3(T8{as_bf8(ra[m][kb][0]), as_bf8(ra[m][kb][1])}, po[kb], x);
+                    P[m] = x;
+                }
+            }
+        }
+    }
+    __syncthreads();  // every main loop done: the ring is free
+    // ---------------- end phase: all eight wavefronts.  LDS (ring space): local end state, this unit's P^T, S_in.
+    f4* const Sx = reinterpret_cast<f4*>(sm.ring[0]);  // S_local, [column tile j][k tile m][lane]
+    f4* const Ptx = Sx + 16 * 64;                      // P^T, RL tiles [k' tile][k tile][lane]
+    f4* const Sin = Ptx + 16 * 64;                     // S_in, [k tile m][column tile j][lane]
+    const bool last = U.s == U.nseg - 1;
+    // exchange entry of a unit: its local end state [m][j][lane], then (segments after the first) its P^T
+    auto xs_of = [&](int64_t u) { return reinterpret_cast<f4*>(xbuf + u * (int64_t)(2 * HS2)); };
+    if (wv >= 4) {
+        const int j = wv - 4;
+        const s4 Id = ident16(lane);
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            Sx[(j * 4 + m) * 64 + lane] = S[m];
+            if (U.s > 0) {
+                const T4 x = split_t(P[m]);
+                Ptx[(j * 4 + m) * 64 + lane] = mma16(x.l, Id, mma16(x.h, Id, z4()));  // RL(P^T) tile (j, m)
+            }
+        }
+        if (!last) {  // publish for the later segments of the row
+            f4* const xd = xs_of(U.u);
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                xstore(xd + (m * 4 + j) * 64 + lane, S[m]);
+                if (U.s > 0) xstore(xd + 16 * 64 + (j * 4 + m) * 64 + lane, Ptx[(j * 4 + m) * 64 + lane]);
+            }
+            vmem_wait_all();
+        }
+    }
+    __syncthreads();
+    // every later segment of the row reads this entry once: the flag counts its readers down to zero
+    if (!last && tid == 0)
+        __hip_atomic_store(flags + U.u, U.nseg - 1 - U.s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    if (U.s > 0) {
+        // S_in = S_end(s - 1) by Horner over the earlier segments: X = S_end(0); X <- P_jj X + S_local(jj), jj = 1 ..
+        if (tid < U.s) {
+            int* const f = flags + (U.u - (int64_t)(U.s - tid) * H);
+            bool ok = false;
+            for (int it = 0; it < kFlagSpinLimit; ++it) {
+                if (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) > 0) {
+                    ok = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (!ok) sm.fail = 1;
+        }
+        __syncthreads();
+        if (wv >= 4) {
+            const int j = wv - 4;
+            const int64_t u0 = U.u - (int64_t)U.s * H;
+            f4 X[4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m) X[m] = xload(xs_of(u0) + (m * 4 + j) * 64 + lane);
+            for (int jj = 1; jj < U.s; ++jj) {
+                const f4* const e = xs_of(u0 + (int64_t)jj * H);
+                T8 xo[2];
+                state_ops(X, xo);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    f4 x = xload(e + (m * 4 + j) * 64 + lane);
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+                        x = p32x3(cat(split_t(xload(e + 16 * 64 + ((2 * kb) * 4 + m) * 64 + lane)),
+                                      split_t(xload(e + 16 * 64 + ((2 * kb + 1) * 4 + m) * 64 + lane))), xo[kb], x);
+                    X[m] = x;
+                }
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m) Sin[(m * 4 + j) * 64 + lane] = X[m];
+            if (last) {  // the row's final state S_end = P_s S_in + S_local(s)
+                T8 xo[2];
+                state_ops(X, xo);
+                float* const dst = state_dst(p, U.n, h);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    f4 x = Sx[(j * 4 + m) * 64 + lane];
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+                        x = p32x3(cat(split_t(Ptx[((2 * kb) * 4 + m) * 64 + lane]),
+                                      split_t(Ptx[((2 * kb + 1) * 4 + m) * 64 + lane])), xo[kb], x);
+                    if (dst)
+#pragma unroll
+                        for (int v = 0; v < 4; ++v) dst[(16 * m + 4 * q + v) * HS + 16 * j + i] = x[v];
+                }
+            }
+        }
+        __syncthreads();
+        // the earlier segments' entries are read: count this unit out of their flags
+        if (tid < U.s)
+            __hip_atomic_fetch_add(flags + (U.u - (int64_t)(U.s - tid) * H), -1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+        // correction of this segment's outputs: y_c^T += S_in^T (Q_c P_{c-1})^T; wavefront w takes column tile
+        // w & 3 of the chunks cl = w >> 2, + 2, ..; two chunks per round with their loads issued together
+        if (p.o) {
+            const int j = wv & 3;
+            bf8 sh[2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb)
+                sh[kb] = cat(hi_t(Sin[((2 * kb) * 4 + j) * 64 + lane]), hi_t(Sin[((2 * kb + 1) * 4 + j) * 64 + lane]));
+            constexpr int RB = 4;  // chunks per round (their loads issued together)
+            for (int cl0 = wv >> 2; cl0 < nloc; cl0 += 2 * RB) {
+                uint4 qp[RB][4];
+                uint2 old[RB][2];
+                int64_t tok0[RB];
+                int Lc[RB];
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    const int cl = min(cl0 + 2 * r, nloc - 1);  // a duplicate of the last chunk is not stored
+                    const int ci = U.c0 + cl;
+                    tok0[r] = U.bos + (int64_t)ci * SC;
+                    Lc[r] = (cl0 + 2 * r < nloc) ? min(SC, U.L - ci * SC) : 0;
+                    const uint4* const src = qp_slot(cl);
+#pragma unroll
+                    for (int x = 0; x < 4; ++x) qp[r][x] = src[x * 64 + lane];
+#pragma unroll
+                    for (int tau = 0; tau < 2; ++tau) {
+                        const int t = 16 * tau + i;
+                        old[r][tau] = *reinterpret_cast<const uint2*>(
+                            p.o + (tok0[r] + (t < Lc[r] ? t : 0)) * p.o_tok_stride + (int64_t)h * HS + 16 * j + 4 * q);
+                    }
+                }
+#pragma unroll
+                for (int r = 0; r < RB; ++r) {
+                    f4 y[2];
+#pragma unroll
+                    for (int tau = 0; tau < 2; ++tau) {
+                        float y0, y1, y2, y3;
+                        bf16x2_to_f32(old[r][tau].x, y0, y1);
+                        bf16x2_to_f32(old[r][tau].y, y2, y3);
+                        y[tau] = f4{y0, y1, y2, y3};
+#pragma unroll
+                        for (int kb = 0; kb < 2; ++kb) y[tau] = mma32(sh[kb], as_bf8(qp[r][tau * 2 + kb]), y[tau]);
+                    }
+                    store_y(p, tok0[r], Lc[r], h, j, lane, y);
+                }
+            }
+        }
+    } else if (last && wv >= 4) {
+        // a single-segment row: the local end state is the final state
+        const int j = wv - 4;
+        float* const dst = state_dst(p, U.n, h);
+        if (dst) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const f4 x = S[m];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) dst[(16 * m + 4 * q + v) * HS + 16 * j + i] = x[v];
+            }
+        }
+    }
+    if (tid == 0 && sm.fail && p.status)
+        __hip_atomic_fetch_or(p.status, WKV7_STATUS_SEGMENT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+SegWorkspace seg_workspace(int num_seqs, int H, int64_t total_tokens, int64_t max_len_bound, bool varlen,
+                           int rec_max_len, int cus) {
+    SegWorkspace ws{};
+    // rows the launch owns: all of them, or those longer than rec_max_len
+    const int64_t long_rows = rec_max_len < 0 ? num_seqs
+                                              : std::min<int64_t>(num_seqs, total_tokens / ((int64_t)rec_max_len + 1));
+    int64_t chunks;
+    if (!varlen) {
+        chunks = (int64_t)num_seqs * ((max_len_bound + SC - 1) / SC);
+    } else {
+        chunks = std::min<int64_t>((int64_t)num_seqs * ((max_len_bound + SC - 1) / SC),
+                                   (total_tokens + SC - 1) / SC + long_rows);
+    }
+    ws.seg = (int)std::max<int64_t>(kSegMinChunks, (chunks * H + cus - 1) / std::max(1, cus));
+    int64_t units;
+    if (!varlen) {
+        const int64_t nch = (max_len_bound + SC - 1) / SC;
+        units = (int64_t)num_seqs * std::max<int64_t>(1, (nch + ws.seg - 1) / ws.seg);
+    } else {
+        units = (chunks + ws.seg - 1) / ws.seg + long_rows;
+    }
+    ws.units = units * H;
+    const int64_t qp_chunks = std::max<int64_t>(0, chunks - (varlen ? (int64_t)ws.seg - 1 : 0));
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    ws.flag_bytes = al(sizeof(int32_t) * (size_t)ws.units);
+    ws.x_bytes = al((size_t)ws.units * 2 * HS2 * sizeof(float));  // local end state + P^T per unit
+    ws.qp_bytes = al((size_t)qp_chunks * H * 4096);
+    ws.total_bytes = kSegFlagRegion + ws.x_bytes + ws.qp_bytes;
+    return ws;
+}
+
+hipError_t launch_seg(const Params& p, const SegWorkspace& ws, void* workspace, hipStream_t stream) {
+    if (p.num_seqs == 0 || ws.units == 0) return hipSuccess;
+    char* base = static_cast<char*>(workspace);
+    int32_t* flags = reinterpret_cast<int32_t*>(base);
+    float* xbuf = reinterpret_cast<float*>(base + kSegFlagRegion);
+    char* qp = base + kSegFlagRegion + ws.x_bytes;
+    hipLaunchKernelGGL(wkv7_seg_kernel, dim3((unsigned)ws.units), dim3(512), 0, stream, p, ws.seg, flags, xbuf, qp);
+    return hipGetLastError();
+}
+
+}  // namespace wkv7

@@ -21,7 +21,7 @@ LIB_NAME = "librwkv7_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 BUILD_DIR = os.path.join(PROJECT_DIR, "_build")
 
-SOURCES = ("wkv7_recurrent.hip", "wkv7_chunked.hip", "wkv7_pool.hip", "wkv7_timemix.hip", "w6a16.hip", "wkv7_capi.hip",
+SOURCES = ("wkv7_recurrent.hip", "wkv7_chunked.hip", "wkv7_seg.hip", "wkv7_pool.hip", "wkv7_timemix.hip", "w6a16.hip", "wkv7_capi.hip",
            "wkv7_noalloc.hip")
 HEADERS = ("wkv7_device.h", "wkv7_launch.h", "wkv7_token.h")
 

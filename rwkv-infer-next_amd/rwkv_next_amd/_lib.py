@@ -26,6 +26,7 @@ WKV7_STATUS_SEQLENS = 4
 WKV7_STATUS_NKEEP = 8
 WKV7_STATUS_DECAY = 16
 WKV7_STATUS_SLOT_CLASH = 32
+WKV7_STATUS_SEGMENT_WAIT = 64
 WKV7_STATUS_CLASH_MAX_SEQS = 1024
 WKV7_CHUNK_W_MAX = 1.0
 
@@ -33,6 +34,8 @@ ALGO_AUTO = 0
 ALGO_RECURRENT = 1
 ALGO_CHUNKED = 2
 ALGO_CHAIN = 3
+ALGO_SEGMENTED = 4
+WKV7_FLAG_REGION_BYTES = 256 << 10  # leading workspace region of hand-off flags (zero between calls)
 
 EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
             "wkv7_args_layout", "wkv7_run_noalloc",

@@ -35,6 +35,7 @@ from typing import NamedTuple
 import torch
 
 from .. import _lib
+from ._workspace import stream_workspace
 
 CHUNK = 64
 QMIN, QMAX = -32, 31
@@ -294,56 +295,12 @@ def _impl(a, w: _W, split_k, out_dtype=None):
 
 _COUNTER_BYTES = 1 << 20   # the workspace's arrival-counter region (include/w6a16.h, w6a16_workspace_size)
 _WORKSPACES: dict = {}     # (device index, stream handle) -> [buffer, counters zeroed in stream order, capture id]
-_RETIRED: list = []
-_HIP = None
-
-
-def _capture_id(stream: int) -> int:
-    """The id of the HIP graph capture in progress on `stream` (hipStreamGetCaptureInfo)."""
-    global _HIP
-    if _HIP is None:
-        hip = ctypes.CDLL("libamdhip64.so")
-        hip.hipStreamGetCaptureInfo.restype = ctypes.c_int
-        hip.hipStreamGetCaptureInfo.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int),
-                                                ctypes.POINTER(ctypes.c_ulonglong)]
-        _HIP = hip
-    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
-    rc = _HIP.hipStreamGetCaptureInfo(ctypes.c_void_p(stream), ctypes.byref(status), ctypes.byref(cid))
-    if rc != 0:
-        raise RuntimeError(f"hipStreamGetCaptureInfo failed ({rc})")
-    return int(cid.value)
 
 
 def _workspace(device, nbytes):
-    """The workspace (a fixed counter region, then split-K partials and row sums) of the current stream on `device`.  The
-    counters must be zero when a call starts; every completed call leaves them zero, so the calls of one stream
-    (which run in order) share the workspace, and calls on different streams, which may overlap, never do.
-
-    A workspace created eagerly is zero-filled there.  One created during a HIP graph capture is zero-filled by a
-    node of that graph only, so until an eager call has zeroed it in stream order, every further capture that uses
-    it starts with a fill of its counter region (a graph may be replayed before the one that created the buffer).
-    A larger request replaces the buffer; the old one is kept alive, since a captured graph may still address it."""
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    stream = torch.cuda.current_stream(idx).cuda_stream
-    capturing = torch.cuda.is_current_stream_capturing()
-    key = (idx, stream)
-    entry = _WORKSPACES.get(key)
-    if entry is None or entry[0].numel() < nbytes:
-        if entry is not None:
-            _RETIRED.append(entry[0])
-        ws = torch.zeros(max(nbytes, 2 * _COUNTER_BYTES), dtype=torch.uint8, device=torch.device("cuda", idx))
-        entry = [ws, not capturing, _capture_id(stream) if capturing else None]
-        _WORKSPACES[key] = entry
-    if not entry[1]:
-        if capturing:
-            cid = _capture_id(stream)
-            if entry[2] != cid:
-                entry[0][:_COUNTER_BYTES].zero_()
-                entry[2] = cid
-        else:
-            entry[0][:_COUNTER_BYTES].zero_()
-            entry[1] = True
-    return entry[0]
+    """The workspace (a fixed counter region, then split-K partials and row sums) of the current stream on `device`;
+    see `_workspace.stream_workspace`."""
+    return stream_workspace(_WORKSPACES, device, nbytes, _COUNTER_BYTES)
 
 
 def int6_matmul(a, lo, hi=None, s=None, group_k=None, split_k=None, use_dot=None, *, out_dtype=None):

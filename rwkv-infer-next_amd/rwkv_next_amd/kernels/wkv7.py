@@ -28,6 +28,14 @@ import torch
 from torch import Tensor
 
 from .. import _lib
+from ._workspace import stream_workspace
+
+_WORKSPACES: dict = {}  # (device index, stream handle) -> [workspace, flags zeroed in stream order, capture id]
+
+
+def reset_workspaces() -> None:
+    """Drop the cached per-stream workspaces (the next call creates a zeroed one)."""
+    _WORKSPACES.clear()
 
 HEAD_SIZE = 64
 OPERANDS = ("r", "w", "k", "v", "a", "b")
@@ -97,8 +105,9 @@ def _launch(ops, *, H, num_seqs, T, total, o=None, h0=None, h0_idx=None, h0_rows
     nbytes = _lib.workspace_size(args)
     ws = None
     if nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)  # caching allocator (graph pool under capture)
-        args.workspace, args.workspace_bytes = ws.data_ptr(), nbytes
+        # one workspace per (device, stream): its leading flag region starts zero and every call leaves it zero
+        ws = stream_workspace(_WORKSPACES, dev, nbytes, _lib.WKV7_FLAG_REGION_BYTES)
+        args.workspace, args.workspace_bytes = ws.data_ptr(), ws.numel()
     with torch.cuda.device(dev):
         _lib.run(args, torch.cuda.current_stream(dev).cuda_stream)
     return ws
@@ -144,14 +153,24 @@ wkv7_fwd = torch.library.custom_op("rwkv_next_amd::wkv7_fwd", _wkv7_fwd, mutates
 wkv7_fwd.register_fake(_wkv7_fwd_fake)
 
 
+def _op_registered(namespace: str, name: str) -> bool:
+    """Whether torch.ops.<namespace>.<name> exists in this process (any registration: custom_op, triton_op, a
+    schema from torch.library.define)."""
+    try:
+        getattr(getattr(torch.ops, namespace), name)
+    except (AttributeError, RuntimeError):
+        return False
+    return True
+
+
 def _register_reference_name():
     """The same op under the reference's name, rwkv_next::wkv7_fwd, so that callers binding torch.ops.rwkv_next
     find it.  Skipped (returns None) when that name is already registered in this process, e.g. by the reference
-    package itself."""
-    try:
-        op = torch.library.custom_op("rwkv_next::wkv7_fwd", _wkv7_fwd, mutates_args=())
-    except RuntimeError:
+    package itself: registering again would silently replace that op (torch accepts a second registration of a
+    name and dispatches to the later one)."""
+    if _op_registered("rwkv_next", "wkv7_fwd"):
         return None
+    op = torch.library.custom_op("rwkv_next::wkv7_fwd", _wkv7_fwd, mutates_args=())
     op.register_fake(_wkv7_fwd_fake)
     return op
 
@@ -184,12 +203,25 @@ def wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True, *, algo: in
     return o, ht
 
 
+def _require(t: Tensor, name: str, dtype, shape) -> None:
+    """Raise ValueError unless `t` is a contiguous tensor of `dtype` and `shape` (None entries match any size).
+    The registered ops hand raw pointers to the C ABI, so a strided or mis-shaped buffer would be read and written
+    at the wrong elements instead of failing."""
+    if t.dtype != dtype or not t.is_contiguous() or t.dim() != len(shape) or \
+            any(want is not None and got != want for got, want in zip(t.shape, shape)):
+        want = ", ".join("*" if x is None else str(x) for x in shape)
+        raise ValueError(f"{name} must be a contiguous {dtype} ({want}) tensor, got {t.dtype} {tuple(t.shape)} "
+                         f"{'contiguous' if t.is_contiguous() else 'strided'}")
+
+
 @torch.library.custom_op("rwkv_next_amd::wkv7_replay_", mutates_args=("state",))
 def wkv7_replay_(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tensor, state: Tensor, n_keep: Tensor,
                  H: int, K: int) -> None:
     """In-place rollback as a registered op: state (B, H, K, K) fp32 := the recurrence over the first n_keep[b]
     steps of row b.  The body of the reference's wkv7_replay (rwkv_next/kernels/wkv7.py:141-147)."""
     ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
+    _require(state, "state", torch.float32, (B, H, K, K))
+    _require(n_keep, "n_keep", torch.int64, (B,))
     _launch(ops, H=H, num_seqs=B, T=T, total=B * T, h0=state, h0_rows=B, ht=state, ht_rows=B, n_keep=n_keep,
             algo=_lib.ALGO_RECURRENT)
 
@@ -224,9 +256,22 @@ def wkv7_pool_op(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tenso
     Returns o, or an empty tensor when store_o is False."""
     ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
     if cu_seqlens is not None:
+        _require(cu_seqlens, "cu_seqlens", torch.int32, (None,))
         N, Tn, total = cu_seqlens.numel() - 1, max_len, T
     else:
         N, Tn, total = B, T, B * T
+    _require(pool, "pool", torch.float32, (None, H, K, K))
+    _require(slots, "slots", torch.int64, (N,))
+    if n_keep is not None:
+        _require(n_keep, "n_keep", torch.int64, (N,))
+    if fresh is not None:
+        _require(fresh, "fresh", torch.uint8, (N,))
+    if snapshots is not None:
+        _require(snapshots, "snapshots", torch.float32, (N, T, H, K, K))
+    if status is not None:
+        _require(status, "status", torch.int32, (None,))
+        if status.numel() < 1:
+            raise ValueError("status must hold at least one int32")
     o = torch.empty_like(ops[3]) if store_o else ops[3].new_empty(0)
     _launch(ops, H=H, num_seqs=N, T=Tn, total=total, o=o if store_o else None, h0=pool, h0_idx=slots,
             h0_rows=pool.shape[0], ht=pool if final else None, ht_idx=slots if final else None,
@@ -308,7 +353,10 @@ STATUS_REASONS = {_lib.WKV7_STATUS_H0_SLOT: "initial-state slot index outside th
                   _lib.WKV7_STATUS_DECAY: f"w above {_lib.WKV7_CHUNK_W_MAX} on a call that runs the chunked kernels "
                                           "(their results are not finite): run it with algo=ALGO_RECURRENT",
                   _lib.WKV7_STATUS_SLOT_CLASH: "two sequences share a state slot (a final state stored where another "
-                                               "sequence stores or reads its state): the result depends on timing"}
+                                               "sequence stores or reads its state): the result depends on timing",
+                  _lib.WKV7_STATUS_SEGMENT_WAIT: "the segmented prefill gave up waiting for a segment hand-off: "
+                                                 "the results are wrong and the stream's workspace flags must be "
+                                                 "zeroed (reset_workspaces())"}
 
 
 def check_status(status: torch.Tensor) -> None:

@@ -119,7 +119,7 @@ def test_grouped_decode_fresh_rows_snapshots_and_no_write_back(dev, K):
     assert np.array_equal(as_np(pool), pool0)
 
 
-@pytest.mark.parametrize("algo", [2, 1])
+@pytest.mark.parametrize("algo", [4, 2, 1])
 def test_config2_prefill_T4096(dev, K, algo):
     from oracle import wkv7_ref
     say("config 2", "algo", algo)

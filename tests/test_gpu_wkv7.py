@@ -14,7 +14,7 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 H8 = 8
-ALGOS = {"auto": 0, "recurrent": 1, "chunked": 2, "chain": 3}
+ALGOS = {"auto": 0, "recurrent": 1, "chunked": 2, "chain": 3, "seg": 4}
 
 
 @pytest.fixture(scope="module")

@@ -82,10 +82,13 @@ def test_wkv7_args_field_order_and_offsets():
 
 def test_status_bits_match_header():
     text = open(os.path.join(REPO, "include", "wkv7.h")).read()
-    for name in ("H0_SLOT", "HT_SLOT", "SEQLENS", "NKEEP", "DECAY", "SLOT_CLASH", "CLASH_MAX_SEQS"):
+    for name in ("H0_SLOT", "HT_SLOT", "SEQLENS", "NKEEP", "DECAY", "SLOT_CLASH", "CLASH_MAX_SEQS", "SEGMENT_WAIT"):
         value = int(re.search(rf"#define WKV7_STATUS_{name} (\d+)", text).group(1))
         assert value == getattr(_lib, f"WKV7_STATUS_{name}")
     from rwkv_next_amd.kernels.wkv7 import STATUS_REASONS
-    assert set(STATUS_REASONS) == {1, 2, 4, 8, 16, 32}
+    assert set(STATUS_REASONS) == {1, 2, 4, 8, 16, 32, 64}
+    for name in ("AUTO", "RECURRENT", "CHUNKED", "CHAIN", "SEGMENTED"):
+        value = int(re.search(rf"#define WKV7_ALGO_{name} (\d+)", text).group(1))
+        assert value == getattr(_lib, f"ALGO_{name}")
     w_max = float(re.search(r"#define WKV7_CHUNK_W_MAX ([0-9.]+)f", text).group(1))
     assert w_max == _lib.WKV7_CHUNK_W_MAX
