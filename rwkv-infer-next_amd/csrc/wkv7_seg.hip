@@ -6,13 +6,14 @@
 //
 // Decomposition.  A row is cut into chunks of C = 32 tokens and its chunks into segments of at most `seg` chunks.
 // One workgroup (a "unit") takes one (row, head, segment):
-//   * four prep wavefronts each build the transition of one chunk at a time, alone (no barrier inside a chunk):
-//     S_C = A S_0 + H,  y^T = S_0^T Q^T + O^T  (S_0 the state before the chunk);
-//     they hand the chunk's record (A, H, Q, O: 44 KB) to the state wavefronts through a three-slot LDS ring;
+//   * four prep wavefronts each build the transition of one chunk at a time, alone (no barrier inside a chunk), in
+//     factored form (below), and hand the chunk's record (44 KB) to the state wavefronts through a three-slot LDS
+//     ring;
 //   * four state wavefronts each own 16 columns of the state (columns of S evolve independently) and apply the
-//     records in chunk order: y, then S <- A S + H.
-//   A segment after the first starts from zeros and also accumulates P = A_n .. A_1, the map from its true initial
-//   state S_in to its end state: S_end = S_local + P S_in, and every output gets Q_c P_{c-1} S_in added.  S_in is
+//     records in chunk order: U = W S + U0, y, then S <- Gamma S + Bt^T U + Kt^T V.
+//   A segment after the first starts from zeros and also accumulates P = A_n .. A_1 (A_c = Gamma + Bt^T W, the
+//   chunk's linear part), the map from its true initial state S_in to its end state: S_end = S_local + P S_in, and
+//   every output of chunk c gets (R0 + rho W)_c P_{c-1} S_in added.  S_in is
 //   the previous segment's S_end, handed over through global memory (one flag per unit; the waiting unit always has
 //   the higher workgroup index, so the earliest unfinished unit never waits and every wait ends).
 //
@@ -20,16 +21,16 @@
 // g_t = sum_{u<=t} log2 d_u per channel (padding tokens count log2 d = 0), m = g_15 and c = g_31:
 //   Ah_t = a_t 2^{g_{t-1} - m},  Rh_t = r_t 2^{g_t - m},  Bp_t = b_t 2^{m - g_t},  Kp_t = k_t 2^{m - g_t}
 //   alpha[t][s] = Ah_t . Bp_s (s < t),  beta = Ah_t . Kp_s (s < t),  rho = Rh_t . Bp_s (s <= t),  sigma = Rh_t . Kp_s
-//   T = (I - alpha)^{-1},  W' = T Ah,  U0 = T beta V
-//   A = diag(2^c) + diag(2^{c-m}) Bp^T W' diag(2^m),   H = diag(2^{c-m}) (Bp^T U0 + Kp^T V)
-//   Q = (Rh + rho W') diag(2^m),                        O = sigma V + rho U0.
-// (U_t = a_t^T S_{t-1} satisfies (I - alpha) U = Ah 2^m S_0 + beta V; substituting gives the rest.)  Every decay
-// factor is one v_exp_f32 of a difference of the same partial sums, and |g_t - m| <= 16 max|log2 d| (<= 63 for
-// w <= WKV7_CHUNK_W_MAX), inside fp32 and bf16 range.
+//   T = (I - alpha)^{-1},  W = T Ah diag(2^m),  U0 = T beta V,  Bt = Bp diag(2^{c-m}),  Kt = Kp diag(2^{c-m}),
+//   R0 = Rh diag(2^m),  Gamma = diag(2^c):
+//   U = W S_0 + U0 (U_t = a_t^T S_{t-1}, from (I - alpha) U = Ah 2^m S_0 + beta V),
+//   S_C = Gamma S_0 + Bt^T U + Kt^T V,   y^T = S_0^T R0^T + U^T rho^T + V^T sigma^T.
+// Every decay factor is one v_exp_f32 of a difference of the same partial sums, and |g_t - m| <= 16 max|log2 d|
+// (<= 63 for w <= WKV7_CHUNK_W_MAX), inside fp32 and bf16 range.
 //
-// Precision.  Products feeding the state (alpha, beta, T, W', U0, A, H, the state update and P) run as three bf16
+// Precision.  Products feeding the state (alpha, beta, T, W, U0, U, the state update and P) run as three bf16
 // MFMAs on hi/lo splits (x = hi + lo, relative error ~2^-17 per operand), two where one operand is exact bf16 (V);
-// products feeding only y (rho, sigma, Q, O, y, Q P, the correction) run as one.  fp32 accumulation throughout.
+// products feeding only y (rho, sigma, R0, y, the P terms of y, the correction) run as one.  fp32 accumulation.
 //
 // Register layouts (lane l: i = l & 15, q = l >> 4).
 //   N layout of a token x channel matrix M, token tile tau (16 rows), channel block kb (32): lane holds
@@ -61,11 +62,21 @@ constexpr int kSpinLimit = 1 << 22;    // LDS ring waits (s_sleep 1 each: a few 
 constexpr int kFlagSpinLimit = 1 << 20;  // segment hand-off waits (s_sleep 8 each)
 
 // Record of one chunk in the LDS ring (byte offsets).  Pieces are lane-contiguous 16-byte words.
-constexpr int REC_A = 0;                       // A^T hi/lo as 16x16x32 A operands: [k tile mo][kb][hl][lane]
-constexpr int REC_H = REC_A + 4 * 2 * 2 * 1024;  // H, RL fp32: [column tile j][k tile m][lane]
-constexpr int REC_Q = REC_H + 16 * 1024;       // Q^T hi as 16x16x32 B operands: [token tile][kb][lane]
-constexpr int REC_O = REC_Q + 4 * 1024;        // O^T, RL fp32: [column tile j][token tile][lane]
-constexpr int REC_BYTES = REC_O + 8 * 1024;    // 45056
+// The chunk transition is kept in factored form (Bt = Bp diag(2^{c-m}), Kt = Kp diag(2^{c-m}), W = W' diag(2^m),
+// R0 = Rh diag(2^m)): the state wavefronts apply
+//   U = W S + U0,   S <- Gamma S + Bt^T U + Kt^T V,   y^T = S^T R0^T + U^T rho^T + V^T sigma^T
+// per 16-column tile, which costs them about as many MFMAs as a dense A S + H would and saves the prep wavefront
+// forming A, H and O (its critical path; the state wavefronts have slack).
+constexpr int REC_W = 0;                       // W^T hi/lo as 16x16x32 A operands: [token tile][kb][hl][lane]
+constexpr int REC_B = REC_W + 8 * 1024;        // Bt hi/lo as 16x16x32 A operands: [k tile m][hl][lane]
+constexpr int REC_K = REC_B + 8 * 1024;        // Kt hi/lo, same
+constexpr int REC_R = REC_K + 8 * 1024;        // R0^T hi as 16x16x32 B operands: [token tile][kb][lane]
+constexpr int REC_U = REC_R + 4 * 1024;        // U0, RL fp32: [column tile j][token tile][lane]
+constexpr int REC_V = REC_U + 8 * 1024;        // V (exact), RL tiles (0, j), (1, j) stacked: [column tile j][lane]
+constexpr int REC_RHO = REC_V + 4 * 1024;      // rho^T hi: tile (0,0) (low 8 bytes), then tiles (0,1), (1,1) stacked
+constexpr int REC_SIG = REC_RHO + 2 * 1024;    // sigma^T hi, same
+constexpr int REC_G = REC_SIG + 2 * 1024;      // Gamma = 2^c per channel, fp32 [64]
+constexpr int REC_BYTES = REC_G + 256;         // 45312
 
 struct SegSmem {
     char ring[NREC][REC_BYTES];
@@ -157,11 +168,15 @@ __device__ __forceinline__ f4 keep_upper(f4 x, int lane, bool strict) {
     return x;
 }
 
+// Cross-lane moves.  prep_chunk runs them in straight-line code with every lane active (its lane-dependent choices
+// are bit selects, never branches), so no move can read a lane that is switched off.
 template <int CTRL, bool BC>
 __device__ __forceinline__ float dpp(float x) {
-    float r = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, BC));
-    asm volatile("" : "+v"(r));
-    return r;
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xf, 0xf, BC));
+}
+// a where mask is all ones, b where it is zero (v_bfi_b32)
+__device__ __forceinline__ float bitsel(uint32_t mask, float a, float b) {
+    return __uint_as_float((__float_as_uint(a) & mask) | (__float_as_uint(b) & ~mask));
 }
 // inclusive prefix sum over the 16 lanes of each row (Hillis-Steele on row_shr; lanes before the start read 0)
 __device__ __forceinline__ float row_scan16(float x) {
@@ -175,6 +190,13 @@ __device__ __forceinline__ float bcast15(float x) { return dpp<0x15F, false>(x);
 __device__ __forceinline__ float shr1(float x) { return dpp<0x111, true>(x); }
 
 __device__ __forceinline__ void lds_wait_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// Ring flags, read and written as LDS accesses (ds_read / ds_write).  Through a generic volatile pointer they would
+// compile to flat accesses that also count on vmcnt, so every flag store would wait for the wavefront's outstanding
+// global stores.
+typedef __attribute__((address_space(3))) volatile int lds_vint;
+__device__ __forceinline__ int lds_load(const int* p) { return *(const lds_vint*)(p); }
+__device__ __forceinline__ void lds_store(int* p, int v) { *(lds_vint*)(p) = v; }
 __device__ __forceinline__ void vmem_wait_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Exchange between workgroups.  Every word of an exchange entry is written and read as a relaxed agent-scope atomic,
@@ -363,7 +385,7 @@ struct Fac {
 
 // The transition of one chunk into `rec` (an LDS ring slot), after waiting for that slot to be free.
 __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, float (*fac)[HS], int lane,
-                                           const volatile int* done4, int use, int* fail) {
+                                           const int* done4, int use, int* fail) {
     const int i = lane & 15, q = lane >> 4;
 
     // ---- 1. log2-decays lam = log2 d = -e^w log2(e) and their running sums over the chunk's tokens.  Lanes i of
@@ -429,7 +451,7 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
                 fb[e] = __builtin_amdgcn_exp2f(-d);
                 const float prev = shr1(fr[e]);  // token t - 1 of the row (lane 0 reads 0)
                 const float first = tau == 0 ? __builtin_amdgcn_exp2f(-m[kb][e]) : bcast15(fr0[e]);
-                fa[e] = i == 0 ? first : prev;
+                fa[e] = bitsel(i == 0 ? 0xffffffffu : 0u, first, prev);
             }
             if (tau == 0)
 #pragma unroll
@@ -539,7 +561,7 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
     {
         bool ok = false;
         for (int it = 0; it < kSpinLimit; ++it) {
-            const int d0 = done4[0], d1 = done4[1], d2 = done4[2], d3 = done4[3];
+            const int d0 = lds_load(done4 + 0), d1 = lds_load(done4 + 1), d2 = lds_load(done4 + 2), d3 = lds_load(done4 + 3);
             if (min(min(d0, d1), min(d2, d3)) >= use) {
                 ok = true;
                 break;
@@ -551,11 +573,10 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
     }
     uint4* const R = reinterpret_cast<uint4*>(rec);
 
-    // ---- 7. per channel tile j: W' = T Ah and U0 = T (beta V) (RL tiles (token tile, j), kept), then
-    //         Q^T = diag(2^m) (Rh^T + W'^T rho^T) and O^T = V^T sigma^T + U0^T rho^T (tiles (j, token tile), stored)
-    T4 Wt[2][4], U0t[2][4];
-    // per-lane factors, read in one batch per phase (ahead of that phase's record stores): 2^m of rows 16 j + 4 q + v
-    f4 emr[4];
+    // ---- 7. per channel tile j: W^T = diag(2^m) (T Ah)^T (RL tiles (j, token tile): the record's X = W S operand),
+    //         U0 = T (beta V) and V (RL tiles (token tile, j)), R0^T = diag(2^m) Rh^T (tiles (j, token tile)), all
+    //         stored
+    f4 emr[4];  // 2^m of rows 16 j + 4 q + v, read in one batch ahead of the record stores
 #pragma unroll
     for (int j = 0; j < 4; ++j) emr[j] = *reinterpret_cast<const f4*>(&fac[0][16 * j + 4 * q]);
     {
@@ -563,78 +584,74 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
         const T8 bp = cat(split_t(bT[1]), split_t(bT[2]));
         const s4 r00 = hi_t(rT[0]), s00 = hi_t(sT[0]);
         const bf8 rp = cat(hi_t(rT[1]), hi_t(rT[2])), sp = cat(hi_t(sT[1]), hi_t(sT[2]));
+        T4 Wtt[4][2];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const T4 a0 = rl(Ah, Al, 0, j), a1 = rl(Ah, Al, 1, j);
-            Wt[0][j] = split_t(p16x3(tt00, a0, z4()));
-            Wt[1][j] = split_t(p32x3(ttp, cat(a0, a1), z4()));
+            f4 w0 = p16x3(a0, tt00, z4()), w1 = p32x3(cat(a0, a1), ttp, z4());
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                w0[v] *= emr[j][v];
+                w1[v] *= emr[j][v];
+            }
+            Wtt[j][0] = split_t(w0);
+            Wtt[j][1] = split_t(w1);
             const T4 bv0 = split_t(p16x2(b00, rV[0][j], z4()));
             const T4 bv1 = split_t(p32x2(bp, cat(rV[0][j], rV[1][j]), z4()));
-            U0t[0][j] = split_t(p16x3(tt00, bv0, z4()));
-            U0t[1][j] = split_t(p32x3(ttp, cat(bv0, bv1), z4()));
+            const f4 u0f = p16x3(tt00, bv0, z4()), u1f = p32x3(ttp, cat(bv0, bv1), z4());
             const bf8 I = (j & 1) ? I1 : I0;
-            f4 q0 = mma16(Wt[0][j].h, r00, mma32(I, Rh[0][j >> 1], z4()));
-            f4 q1 = mma32(cat(Wt[0][j].h, Wt[1][j].h), rp, mma32(I, Rh[1][j >> 1], z4()));
+            f4 q0 = mma32(I, Rh[0][j >> 1], z4()), q1 = mma32(I, Rh[1][j >> 1], z4());
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
                 q0[v] *= emr[j][v];
                 q1[v] *= emr[j][v];
             }
-            // Q^T pieces [token tile][kb]: tiles j = 2 kb, 2 kb + 1 in the low / high 8 bytes
-            reinterpret_cast<uint2*>(R + (REC_Q / 16) + (0 * 2 + (j >> 1)) * 64 + lane)[j & 1] = __builtin_bit_cast(uint2, hi_t(q0));
-            reinterpret_cast<uint2*>(R + (REC_Q / 16) + (1 * 2 + (j >> 1)) * 64 + lane)[j & 1] = __builtin_bit_cast(uint2, hi_t(q1));
-            const f4 o0 = mma16(rV[0][j], s00, mma16(U0t[0][j].h, r00, z4()));
-            const f4 o1 = mma32(cat(rV[0][j], rV[1][j]), sp, mma32(cat(U0t[0][j].h, U0t[1][j].h), rp, z4()));
-            R[(REC_O / 16) + (j * 2 + 0) * 64 + lane] = __builtin_bit_cast(uint4, o0);
-            R[(REC_O / 16) + (j * 2 + 1) * 64 + lane] = __builtin_bit_cast(uint4, o1);
+            // R0^T pieces [token tile][kb]: k tiles j = 2 kb, 2 kb + 1 in the low / high 8 bytes
+            reinterpret_cast<uint2*>(R + (REC_R / 16) + (0 * 2 + (j >> 1)) * 64 + lane)[j & 1] = __builtin_bit_cast(uint2, hi_t(q0));
+            reinterpret_cast<uint2*>(R + (REC_R / 16) + (1 * 2 + (j >> 1)) * 64 + lane)[j & 1] = __builtin_bit_cast(uint2, hi_t(q1));
+            R[(REC_U / 16) + (j * 2 + 0) * 64 + lane] = __builtin_bit_cast(uint4, u0f);
+            R[(REC_U / 16) + (j * 2 + 1) * 64 + lane] = __builtin_bit_cast(uint4, u1f);
+            R[(REC_V / 16) + j * 64 + lane] = as_u4(cat(rV[0][j], rV[1][j]));
         }
+        // W^T pieces [token tile][kb][hl]: k tiles 2 kb, 2 kb + 1 stacked
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const T8 pc = cat(Wtt[2 * kb][tau], Wtt[2 * kb + 1][tau]);
+                R[(REC_W / 16) + ((tau * 2 + kb) * 2 + 0) * 64 + lane] = as_u4(pc.h);
+                R[(REC_W / 16) + ((tau * 2 + kb) * 2 + 1) * 64 + lane] = as_u4(pc.l);
+            }
+        // rho^T and sigma^T pieces for y's U^T rho^T and V^T sigma^T terms
+        R[(REC_RHO / 16) + lane] = as_u4(cat(r00, s4{0, 0, 0, 0}));
+        R[(REC_RHO / 16) + 64 + lane] = as_u4(rp);
+        R[(REC_SIG / 16) + lane] = as_u4(cat(s00, s4{0, 0, 0, 0}));
+        R[(REC_SIG / 16) + 64 + lane] = as_u4(sp);
+        // Gamma per channel
+        if (lane < 16)
+            reinterpret_cast<f4*>(rec + REC_G)[lane] = *reinterpret_cast<const f4*>(&fac[2][4 * lane]);
     }
 
-    // ---- 8. A^T tiles (k' tile mr, k tile j) = 2^{m_k'} (W'^T Bp)[k'][k] 2^{c_k - m_k} + [k' = k] 2^{c_k}; the scan's
-    //         A operand for output tile j and contraction block kb stacks k' tiles 2 kb and 2 kb + 1.
-    float cfj[4], dgj[4];
+    // ---- 8. per k tile m: Bt = Bp diag(2^{c-m}) and Kt = Kp diag(2^{c-m}) (token-row RL tiles, rescaled and split
+    //         again), stored
+    float cfm[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        cfj[j] = fac[1][16 * j + i];
-        dgj[j] = fac[2][16 * j + i];
-    }
+    for (int m = 0; m < 4; ++m) cfm[m] = fac[1][16 * m + i];
+    auto scaled = [&](const bf8 (&H8)[2][2], const bf8 (&L8)[2][2], int tau, int m) {
+        const bf8 I = (m & 1) ? I1 : I0;
+        f4 x = mma32(L8[tau][m >> 1], I, mma32(H8[tau][m >> 1], I, z4()));  // hi + lo, exact
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const float cf = cfj[j], dg = dgj[j];
-        const T8 bpj = cat(rl(Bh, Bl, 0, j), rl(Bh, Bl, 1, j));
-        T4 at[4];
+        for (int v = 0; v < 4; ++v) x[v] *= cfm[m];
+        return split_t(x);
+    };
 #pragma unroll
-        for (int mr = 0; mr < 4; ++mr) {
-            f4 x = p32x3(cat(Wt[0][mr], Wt[1][mr]), bpj, z4());
-#pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                x[v] = x[v] * emr[mr][v] * cf;
-                if (mr == j && 4 * q + v == i) x[v] += dg;
-            }
-            at[mr] = split_t(x);
-        }
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const T8 pc = cat(at[2 * kb], at[2 * kb + 1]);
-            R[(REC_A / 16) + ((j * 2 + kb) * 2 + 0) * 64 + lane] = as_u4(pc.h);
-            R[(REC_A / 16) + ((j * 2 + kb) * 2 + 1) * 64 + lane] = as_u4(pc.l);
-        }
-    }
-    // ---- 9. H tiles (k tile mr, column tile j) = 2^{c_k - m_k} (Bp^T U0 + Kp^T V)
-    f4 ecr[4];
-#pragma unroll
-    for (int mr = 0; mr < 4; ++mr) ecr[mr] = *reinterpret_cast<const f4*>(&fac[1][16 * mr + 4 * q]);
-#pragma unroll
-    for (int mr = 0; mr < 4; ++mr) {
-        const T8 bpm = cat(rl(Bh, Bl, 0, mr), rl(Bh, Bl, 1, mr)), kpm = cat(rl(Kh, Kl, 0, mr), rl(Kh, Kl, 1, mr));
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            f4 x = p32x3(bpm, cat(U0t[0][j], U0t[1][j]), z4());
-            x = p32x2(kpm, cat(rV[0][j], rV[1][j]), x);
-#pragma unroll
-            for (int v = 0; v < 4; ++v) x[v] *= ecr[mr][v];
-            R[(REC_H / 16) + (j * 4 + mr) * 64 + lane] = __builtin_bit_cast(uint4, x);
-        }
+    for (int m = 0; m < 4; ++m) {
+        const T8 btm = cat(scaled(Bh, Bl, 0, m), scaled(Bh, Bl, 1, m));
+        R[(REC_B / 16) + (m * 2 + 0) * 64 + lane] = as_u4(btm.h);
+        R[(REC_B / 16) + (m * 2 + 1) * 64 + lane] = as_u4(btm.l);
+        const T8 ktm = cat(scaled(Kh, Kl, 0, m), scaled(Kh, Kl, 1, m));
+        R[(REC_K / 16) + (m * 2 + 0) * 64 + lane] = as_u4(ktm.h);
+        R[(REC_K / 16) + (m * 2 + 1) * 64 + lane] = as_u4(ktm.l);
     }
 }
 
@@ -697,7 +714,7 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             const int slot = cl % NREC;
             prep_chunk(raw, Lc, sm.ring[slot], sm.fac[wv], lane, sm.done[slot], cl / NREC, &sm.fail);
             lds_wait_all();
-            if (lane == 0) *reinterpret_cast<volatile int*>(&sm.ready[slot]) = cl + 1;
+            if (lane == 0) lds_store(&sm.ready[slot], cl + 1);
         }
     } else {
         // ---------------- state wavefronts: columns 16 j .. 16 j + 15
@@ -716,7 +733,7 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             {
                 bool ok = false;
                 for (int it = 0; it < kSpinLimit; ++it) {
-                    if (*reinterpret_cast<volatile int*>(&sm.ready[slot]) == cl + 1) {
+                    if (lds_load(&sm.ready[slot]) == cl + 1) {
                         ok = true;
                         break;
                     }
@@ -726,74 +743,106 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
                 asm volatile("" ::: "memory");
             }
             const uint4* const R = reinterpret_cast<const uint4*>(sm.ring[slot]);
-            uint4 ra[4][2][2], rq[2][2];
-            f4 rh[4], ro[2];
+            uint4 rw[2][2][2], rb[4][2], rk[4][2], rr[2][2], rho[2], sig[2], rv;
+            f4 ru[2], gm[4];
 #pragma unroll
-            for (int mo = 0; mo < 4; ++mo)
+            for (int tau = 0; tau < 2; ++tau)
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-                    for (int hl = 0; hl < 2; ++hl) ra[mo][kb][hl] = R[(REC_A / 16) + ((mo * 2 + kb) * 2 + hl) * 64 + lane];
+                    for (int hl = 0; hl < 2; ++hl) rw[tau][kb][hl] = R[(REC_W / 16) + ((tau * 2 + kb) * 2 + hl) * 64 + lane];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) rh[m] = __builtin_bit_cast(f4, R[(REC_H / 16) + (j * 4 + m) * 64 + lane]);
+            for (int m = 0; m < 4; ++m) {
+#pragma unroll
+                for (int hl = 0; hl < 2; ++hl) {
+                    rb[m][hl] = R[(REC_B / 16) + (m * 2 + hl) * 64 + lane];
+                    rk[m][hl] = R[(REC_K / 16) + (m * 2 + hl) * 64 + lane];
+                }
+                gm[m] = reinterpret_cast<const f4*>(sm.ring[slot] + REC_G)[4 * m + q];  // 2^c of rows 16 m + 4 q + v
+            }
 #pragma unroll
             for (int tau = 0; tau < 2; ++tau) {
 #pragma unroll
-                for (int kb = 0; kb < 2; ++kb) rq[tau][kb] = R[(REC_Q / 16) + (tau * 2 + kb) * 64 + lane];
-                ro[tau] = __builtin_bit_cast(f4, R[(REC_O / 16) + (j * 2 + tau) * 64 + lane]);
+                for (int kb = 0; kb < 2; ++kb) rr[tau][kb] = R[(REC_R / 16) + (tau * 2 + kb) * 64 + lane];
+                ru[tau] = __builtin_bit_cast(f4, R[(REC_U / 16) + (j * 2 + tau) * 64 + lane]);
+                rho[tau] = R[(REC_RHO / 16) + tau * 64 + lane];
+                sig[tau] = R[(REC_SIG / 16) + tau * 64 + lane];
             }
+            rv = R[(REC_V / 16) + j * 64 + lane];
             lds_wait_all();
-            if (lane == 0) *reinterpret_cast<volatile int*>(&sm.done[slot][j]) = cl / NREC + 1;
+            if (lane == 0) lds_store(&sm.done[slot][j], cl / NREC + 1);
 
             const int ci = U.c0 + cl;
             const int64_t tok0 = U.bos + (int64_t)ci * SC;
             const int Lc = min(SC, U.L - ci * SC);
-            T8 so[2];
-            state_ops(S, so);
-            // y^T = S^T Q^T + O^T  (token tiles 0, 1)
-            f4 y[2];
-#pragma unroll
-            for (int tau = 0; tau < 2; ++tau) {
-                y[tau] = ro[tau];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) y[tau] = mma32(so[kb].h, as_bf8(rq[tau][kb]), y[tau]);
-            }
-            if (p.o) store_y(p, tok0, Lc, h, j, lane, y);
-            T8 po[2];
-            if (acc_p) {
-                state_ops(P, po);
-                // (Q P)^T rows k' in column tile j, for the correction once S_in is known
-                uint4* const dst = qp_slot(cl);
+            // X = W M (token tiles 0, 1; columns 16 j ..) for M = S or P
+            auto wmul = [&](const T8 (&mo)[2], f4 (&X)[2]) {
 #pragma unroll
                 for (int tau = 0; tau < 2; ++tau) {
                     f4 x = z4();
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb) x = mma32(po[kb].h, as_bf8(rq[tau][kb]), x);
-                    // piece [tau][kb = j >> 1], half j & 1
-                    uint2* d2 = reinterpret_cast<uint2*>(dst + (tau * 2 + (j >> 1)) * 64 + lane) + (j & 1);
-                    *d2 = __builtin_bit_cast(uint2, hi_t(x));
+                    for (int kb = 0; kb < 2; ++kb)
+                        x = p32x3(T8{as_bf8(rw[tau][kb][0]), as_bf8(rw[tau][kb][1])}, mo[kb], x);
+                    X[tau] = x;
                 }
-            }
-            // S <- A S + H,  P <- A P
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                f4 x = rh[m];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb)
-                    x = p32x3(T8{as_bf8(ra[m][kb][0]), as_bf8(ra[m][kb][1])}, so[kb], x);
-                S[m] = x;
-            }
-            if (acc_pp) {
-                if (!acc_p) state_ops(P, po);
+            };
+            // M <- Gamma M + Bt^T X (+ Kt^T V for the state)
+            auto apply = [&](f4 (&M)[4], const f4 (&X)[2], bool state) {
+                const T8 xo = cat(split_t(X[0]), split_t(X[1]));
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     f4 x = z4();
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-                        x = p32x3(T8{as_bf8(ra[m][kb][0]), as_bf8(ra[m][kb][1])}, po[kb], x);
-                    P[m] = x;
+                    for (int v = 0; v < 4; ++v) x[v] = gm[m][v] * M[m][v];
+                    if (state) x = p32x2(T8{as_bf8(rk[m][0]), as_bf8(rk[m][1])}, as_bf8(rv), x);
+                    M[m] = p32x3(T8{as_bf8(rb[m][0]), as_bf8(rb[m][1])}, xo, x);
                 }
+            };
+            // (R0 M + rho X)^T tiles (column tile j, token tile): y^T for M = S, X = U, (Q P)^T for M = P, X = W P
+            auto qmul = [&](const T8 (&mo)[2], const f4 (&X)[2], f4 (&Y)[2]) {
+                const s4 x0 = hi_t(X[0]), x1 = hi_t(X[1]);
+                Y[0] = mma16(x0, __builtin_bit_cast(s4, uint2{rho[0].x, rho[0].y}), Y[0]);  // tile (0, 0): low 8 bytes
+                Y[1] = mma32(cat(x0, x1), as_bf8(rho[1]), Y[1]);
+#pragma unroll
+                for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) Y[tau] = mma32(mo[kb].h, as_bf8(rr[tau][kb]), Y[tau]);
+            };
+            T8 so[2];
+            state_ops(S, so);
+            f4 X[2];
+            wmul(so, X);
+#pragma unroll
+            for (int tau = 0; tau < 2; ++tau) X[tau] += ru[tau];  // U = W S + U0
+            f4 y[2] = {z4(), z4()};
+            {  // V^T sigma^T
+                const bf8 vp = as_bf8(rv);
+                const s4 v0 = __builtin_bit_cast(s4, uint2{rv.x, rv.y});
+                y[0] = mma16(v0, __builtin_bit_cast(s4, uint2{sig[0].x, sig[0].y}), y[0]);
+                y[1] = mma32(vp, as_bf8(sig[1]), y[1]);
             }
+            qmul(so, X, y);
+            if (p.o) store_y(p, tok0, Lc, h, j, lane, y);
+            if (acc_pp) {
+                T8 po[2];
+                state_ops(P, po);
+                f4 XP[2];
+                wmul(po, XP);
+                if (acc_p) {
+                    // (Q P)^T rows k' in column tile j, for the correction once S_in is known
+                    f4 qp[2] = {z4(), z4()};
+                    qmul(po, XP, qp);
+                    uint4* const dst = qp_slot(cl);
+#pragma unroll
+                    for (int tau = 0; tau < 2; ++tau) {
+                        // piece [tau][kb = j >> 1], half j & 1
+                        uint2* d2 = reinterpret_cast<uint2*>(dst + (tau * 2 + (j >> 1)) * 64 + lane) + (j & 1);
+                        *d2 = __builtin_bit_cast(uint2, hi_t(qp[tau]));
+                    }
+                }
+                apply(P, XP, false);
+            }
+            apply(S, X, true);
         }
     }
     __syncthreads();  // every main loop done: the ring is free
