@@ -46,12 +46,23 @@ hipError_t launch_chain(const Params& p, hipStream_t stream);
 // (parallel over chunks), scan (sequential over chunks per (row, head, 16-column block)).
 hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* workspace, hipStream_t stream);
 
-// Segmented single-dispatch chunked prefill (wkv7_seg.hip).  Chunks of kSegChunk tokens; a row's chunks are cut into
-// segments of `seg` chunks, one workgroup per (row, head, segment) unit.  Ragged or n_keep calls build a row table
-// in LDS and take at most kSegMaxRows rows.
+// Segmented single-dispatch chunked prefill (wkv7_seg.hip).  Chunks of kSegChunk tokens; a row of nch chunks is cut
+// into nseg = ceil(nch / seg) segments, one workgroup per (row, head, segment) unit.  Ragged or n_keep calls build a
+// row table in LDS and take at most kSegMaxRows rows.
 constexpr int kSegChunk = 32;
 constexpr int kSegMaxRows = 4096;
 constexpr int kSegMinChunks = 8;
+// First chunk of segment s.  Segments after the first also carry the map from the row's initial state and finish
+// with a correction pass, so the first segment takes a longer share, round(7 nch / (6 nseg + 1)) chunks (the measured
+// per-chunk cost ratio of the two kinds is about 1.2); the later ones split the rest evenly, the last ones (with the
+// longest hand-off chains) taking the shorter shares.
+__host__ __device__ inline int seg_start(int nch, int nseg, int s) {
+    if (s <= 0) return 0;
+    const int64_t den = 6 * (int64_t)nseg + 1;
+    const int first = (int)((7 * (int64_t)nch + den / 2) / den);
+    if (nseg <= 1) return nch;
+    return first + (int)(((int64_t)(s - 1) * (nch - first) + nseg - 2) / (nseg - 1));  // later ones no longer
+}
 // The workspace starts with one int32 hand-off flag per unit (at most kSegFlagRegion / 4 units).  The region must be
 // zero before a workspace's first call; every call that completes leaves it zero.  No other path writes it.
 constexpr size_t kSegFlagRegion = 256 * 1024;

@@ -229,8 +229,9 @@ struct Unit {
     int64_t bos;
     int L, nch;       // row length and chunks of the row
     int c0, c1;       // chunk range of the unit
+    int first;        // chunks of the row's first segment
     int64_t u;        // unit index (exchange slot); the previous segment's is u - H
-    int64_t qp0;      // Q P slot of the row's chunk `seg` (chunks of later segments follow it)
+    int64_t qp0;      // Q P slot of the row's chunk `first` (chunks of later segments follow it)
 };
 
 // Rows this launch owns: every row when p.rec_max_len < 0, else rows longer than it (the token-serial kernel takes
@@ -261,7 +262,7 @@ __device__ Unit find_unit(const Params& p, int seg, int64_t blk, int* tab) {
         U.L = L;
         U.nch = nch;
         U.bos = n * (int64_t)p.T;
-        U.qp0 = n * (int64_t)std::max(0, nch - seg);
+        U.qp0 = n * (int64_t)(nch - seg_start(nch, nseg, 1));
     } else {
         const int N = p.num_seqs;
         int* useg = tab;
@@ -277,7 +278,7 @@ __device__ Unit find_unit(const Params& p, int seg, int64_t blk, int* tab) {
             int L;
             seq_extent(p, n, bos, L);
             useg[n] = row_units(p, L, seg);
-            uqp[n] = useg[n] ? std::max(0, row_chunks(L) - seg) : 0;
+            uqp[n] = useg[n] ? row_chunks(L) - seg_start(row_chunks(L), useg[n], 1) : 0;
             a += useg[n];
             b += uqp[n];
         }
@@ -323,8 +324,9 @@ __device__ Unit find_unit(const Params& p, int seg, int64_t blk, int* tab) {
     }
     U.ok = true;
     U.u = blk;
-    U.c0 = U.s * seg;
-    U.c1 = std::min(U.nch, U.c0 + seg);
+    U.c0 = seg_start(U.nch, U.nseg, U.s);
+    U.c1 = seg_start(U.nch, U.nseg, U.s + 1);
+    U.first = seg_start(U.nch, U.nseg, 1);
     return U;
 }
 
@@ -696,9 +698,9 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
     if (tid == 0) sm.fail = 0;
     __syncthreads();
     const int nloc = U.c1 - U.c0;  // chunks of this unit
-    // Q P slot of local chunk cl (segments after the first): the row's chunks c >= seg are numbered from U.qp0
+    // Q P slot of local chunk cl (segments after the first): the row's chunks c >= U.first are numbered from U.qp0
     auto qp_slot = [&](int cl) -> uint4* {
-        const int64_t slot = U.qp0 + (int64_t)(U.c0 + cl - seg);
+        const int64_t slot = U.qp0 + (int64_t)(U.c0 + cl - U.first);
         return reinterpret_cast<uint4*>(qpbuf + (slot * H + h) * (int64_t)(4 * 1024));
     };
 
@@ -900,18 +902,32 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             f4 X[4];
 #pragma unroll
             for (int m = 0; m < 4; ++m) X[m] = xload(xs_of(u0) + (m * 4 + j) * 64 + lane);
-            for (int jj = 1; jj < U.s; ++jj) {
-                const f4* const e = xs_of(u0 + (int64_t)jj * H);
-                T8 xo[2];
-                state_ops(X, xo);
+            // entries two at a time, both loaded before either is applied (one memory round trip per pair)
+            for (int jj = 1; jj < U.s; jj += 2) {
+                f4 es[2][4], ep[2][4][4];
 #pragma unroll
-                for (int m = 0; m < 4; ++m) {
-                    f4 x = xload(e + (m * 4 + j) * 64 + lane);
+                for (int x = 0; x < 2; ++x) {
+                    const f4* const e = xs_of(u0 + (int64_t)min(jj + x, U.s - 1) * H);
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
-                        x = p32x3(cat(split_t(xload(e + 16 * 64 + ((2 * kb) * 4 + m) * 64 + lane)),
-                                      split_t(xload(e + 16 * 64 + ((2 * kb + 1) * 4 + m) * 64 + lane))), xo[kb], x);
-                    X[m] = x;
+                    for (int m = 0; m < 4; ++m) {
+                        es[x][m] = xload(e + (m * 4 + j) * 64 + lane);
+#pragma unroll
+                        for (int kk = 0; kk < 4; ++kk) ep[x][m][kk] = xload(e + 16 * 64 + (kk * 4 + m) * 64 + lane);
+                    }
+                }
+#pragma unroll
+                for (int x = 0; x < 2; ++x) {
+                    if (jj + x >= U.s) break;
+                    T8 xo[2];
+                    state_ops(X, xo);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        f4 acc = es[x][m];
+#pragma unroll
+                        for (int kb = 0; kb < 2; ++kb)
+                            acc = p32x3(cat(split_t(ep[x][m][2 * kb]), split_t(ep[x][m][2 * kb + 1])), xo[kb], acc);
+                        X[m] = acc;
+                    }
                 }
             }
 #pragma unroll
@@ -938,49 +954,57 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
         if (tid < U.s)
             __hip_atomic_fetch_add(flags + (U.u - (int64_t)(U.s - tid) * H), -1, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_AGENT);
-        // correction of this segment's outputs: y_c^T += S_in^T (Q_c P_{c-1})^T; wavefront w takes column tile
-        // w & 3 of the chunks cl = w >> 2, + 2, ..; two chunks per round with their loads issued together
+        // correction of this segment's outputs: y_c^T += S_in^T (Q_c P_{c-1})^T.  Wavefront w takes the chunks
+        // cl = w, w + 8, .. whole (all four column tiles: one Q P read per chunk, full 128-byte rows of y), RB chunks
+        // per round with their loads issued together
         if (p.o) {
-            const int j = wv & 3;
-            bf8 sh[2];
+            bf8 sh[4][2];  // S_in hi, [column tile j][k block]
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb)
-                sh[kb] = cat(hi_t(Sin[((2 * kb) * 4 + j) * 64 + lane]), hi_t(Sin[((2 * kb + 1) * 4 + j) * 64 + lane]));
-            constexpr int RB = 4;  // chunks per round (their loads issued together)
-            for (int cl0 = wv >> 2; cl0 < nloc; cl0 += 2 * RB) {
+            for (int j = 0; j < 4; ++j)
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb)
+                    sh[j][kb] = cat(hi_t(Sin[((2 * kb) * 4 + j) * 64 + lane]), hi_t(Sin[((2 * kb + 1) * 4 + j) * 64 + lane]));
+            constexpr int RB = 4;
+            for (int cl0 = wv; cl0 < nloc; cl0 += 8 * RB) {
                 uint4 qp[RB][4];
-                uint2 old[RB][2];
+                uint2 old[RB][4][2];
                 int64_t tok0[RB];
                 int Lc[RB];
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
-                    const int cl = min(cl0 + 2 * r, nloc - 1);  // a duplicate of the last chunk is not stored
+                    const int cl = min(cl0 + 8 * r, nloc - 1);  // a duplicate of the last chunk is not stored
                     const int ci = U.c0 + cl;
                     tok0[r] = U.bos + (int64_t)ci * SC;
-                    Lc[r] = (cl0 + 2 * r < nloc) ? min(SC, U.L - ci * SC) : 0;
+                    Lc[r] = (cl0 + 8 * r < nloc) ? min(SC, U.L - ci * SC) : 0;
                     const uint4* const src = qp_slot(cl);
 #pragma unroll
                     for (int x = 0; x < 4; ++x) qp[r][x] = src[x * 64 + lane];
 #pragma unroll
                     for (int tau = 0; tau < 2; ++tau) {
                         const int t = 16 * tau + i;
-                        old[r][tau] = *reinterpret_cast<const uint2*>(
-                            p.o + (tok0[r] + (t < Lc[r] ? t : 0)) * p.o_tok_stride + (int64_t)h * HS + 16 * j + 4 * q);
+                        const uint16_t* const row =
+                            p.o + (tok0[r] + (t < Lc[r] ? t : 0)) * p.o_tok_stride + (int64_t)h * HS + 4 * q;
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) old[r][j][tau] = *reinterpret_cast<const uint2*>(row + 16 * j);
                     }
                 }
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
-                    f4 y[2];
 #pragma unroll
-                    for (int tau = 0; tau < 2; ++tau) {
-                        float y0, y1, y2, y3;
-                        bf16x2_to_f32(old[r][tau].x, y0, y1);
-                        bf16x2_to_f32(old[r][tau].y, y2, y3);
-                        y[tau] = f4{y0, y1, y2, y3};
+                    for (int j = 0; j < 4; ++j) {
+                        f4 y[2];
 #pragma unroll
-                        for (int kb = 0; kb < 2; ++kb) y[tau] = mma32(sh[kb], as_bf8(qp[r][tau * 2 + kb]), y[tau]);
+                        for (int tau = 0; tau < 2; ++tau) {
+                            float y0, y1, y2, y3;
+                            bf16x2_to_f32(old[r][j][tau].x, y0, y1);
+                            bf16x2_to_f32(old[r][j][tau].y, y2, y3);
+                            y[tau] = f4{y0, y1, y2, y3};
+#pragma unroll
+                            for (int kb = 0; kb < 2; ++kb)
+                                y[tau] = mma32(sh[j][kb], as_bf8(qp[r][tau * 2 + kb]), y[tau]);
+                        }
+                        store_y(p, tok0[r], Lc[r], h, j, lane, y);
                     }
-                    store_y(p, tok0[r], Lc[r], h, j, lane, y);
                 }
             }
         }
@@ -1023,7 +1047,13 @@ SegWorkspace seg_workspace(int num_seqs, int H, int64_t total_tokens, int64_t ma
         units = (chunks + ws.seg - 1) / ws.seg + long_rows;
     }
     ws.units = units * H;
-    const int64_t qp_chunks = std::max<int64_t>(0, chunks - (varlen ? (int64_t)ws.seg - 1 : 0));
+    // Q P slots: chunks after a row's first segment (for ragged calls, bounded by the chunks of all owned rows)
+    int64_t qp_chunks = chunks;
+    if (!varlen) {
+        const int nch = (int)((max_len_bound + SC - 1) / SC);
+        const int nseg = (int)std::max<int64_t>(1, (nch + ws.seg - 1) / ws.seg);
+        qp_chunks = (int64_t)num_seqs * (nch - seg_start(nch, nseg, 1));
+    }
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     ws.flag_bytes = al(sizeof(int32_t) * (size_t)ws.units);
     ws.x_bytes = al((size_t)ws.units * 2 * HS2 * sizeof(float));  // local end state + P^T per unit
