@@ -108,6 +108,10 @@ Plan make_plan(const wkv7_args* a) {
         pl.run_recurrent = true;
     } else if (a->algo == WKV7_ALGO_SEGMENTED) {
         pl.run_seg = true;
+        if (a->rec_max_len >= 0) {  // rows of at most rec_max_len tokens go to the token-serial kernel
+            pl.run_recurrent = true;
+            pl.rec_len_rec = pl.rec_len_chunk = a->rec_max_len;
+        }
     } else if (a->algo == WKV7_ALGO_CHAIN || chain_fits(a, bound, thr)) {
         pl.run_chain = true;
         pl.rec_len_rec = thr;

@@ -1541,7 +1541,7 @@ __global__ __launch_bounds__(512) void wkv7_chain_kernel(const Params p) {
     //         one pair per wavefront at a time, with the token-serial kernel's code
     {
         float* const slab = reinterpret_cast<float*>(sm.slot[14]) + wv * 5 * HS;
-        const int g = lane >> 4, c = lane & 15;
+        const int g = lane >> 3, c = lane & 7;
         for (int64_t u = start[b] + wv; u < start[b + 1]; u += 8) {
             const uint32_t pa = (uint32_t)srow[u / p.H] * (uint32_t)p.H + (uint32_t)(u % p.H);
             const Pair qp = pair_of(p, pa);

@@ -6,20 +6,21 @@
 //   * wkv7_recurrent_kernel (every row shape): one wavefront per (sequence, head) pair at a time, at most two waves
 //     per SIMD; each wave walks pairs gw, gw + nwaves, ... and issues the next pair's state loads before working on
 //     the current pair, so state reads, the recurrence math and state writes of different pairs overlap.  Lane
-//     L = 16 g + c owns state rows k = 4 i + g (i = 0..15) and columns v = 4 c .. 4 c + 3 (the per-pair code of
-//     wkv7_token.h);
+//     L = 8 g + c owns state rows k = 8 i + g (i = 0..7) and columns 32 hh + 4 c .. + 3 (hh = 0, 1; the per-pair
+//     code of wkv7_token.h);
 //   * wkv7_decode_kernel (dense single-token rows without snapshots): half-pair units (32 columns of one pair), one
 //     wave per SIMD holding up to eight units, all of their loads issued before the first update, so that across the
 //     grid the state reads run ahead of the writes;
 //   * the per-token k-side vectors (decay, a, b, k, r) are computed by lane i for channel i and broadcast through
-//     a per-wave LDS slab; v is read per lane; sa = a^T S and y = S^T r are lane-local sums over the lane's rows
-//     followed by an xor butterfly over the row groups.  Every lane ends with bitwise identical sums (fp add is
-//     commutative), so all lanes hold the same update.  State traffic is streamed with non-temporal loads and
-//     stores (each state is touched once per call).
+//     a per-wave LDS slab; v is read per lane; sa = a^T S and y = S^T r are lane-local sums over the lane's 8 rows
+//     followed by a butterfly over the 8 row groups, in the same order in both kernels.  Every lane ends with
+//     bitwise identical sums (fp add is commutative), so all lanes hold the same update.  State traffic is streamed
+//     with non-temporal loads and stores (each state is touched once per call).
 // Decode is HBM-bound: 16 KB state read + 16 KB written per pair, plus 896 B of operands and output.
 //
-// The per-token arithmetic of a kernel is one fixed instruction sequence with explicit fmaf (the file is built with
-// -ffp-contract=off), so a snapshot taken after token t is bit-identical to a re-run over the first t+1 tokens.
+// The per-token arithmetic is one fixed instruction sequence with explicit fmaf (the file is built with
+// -ffp-contract=off), shared by both kernels: a snapshot taken after token t is bit-identical to a re-run over the
+// first t+1 tokens, by either kernel (t + 1 single-token decode steps included).
 #include <algorithm>
 
 #include "wkv7_device.h"
@@ -37,7 +38,7 @@ __global__ __launch_bounds__(64 * kWaves, kWavesPerSimd) void wkv7_recurrent_ker
     __shared__ __attribute__((aligned(16))) float slab[kWaves][5 * HS];  // decay, a, b, k, r (permuted)
     const int lane = threadIdx.x & 63;
     const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: indices stay in SGPRs
-    const int g = lane >> 4, c = lane & 15;
+    const int g = lane >> 3, c = lane & 7;
     // pair indices fit 32 bits (wkv7_run validates num_seqs * H <= 2^31); 64-bit divisions are software-emulated
     const uint32_t npairs = (uint32_t)p.num_seqs * (uint32_t)p.H;
     const uint32_t nwaves = gridDim.x * kWaves;
@@ -78,11 +79,16 @@ __global__ __launch_bounds__(64 * kWaves, kWavesPerSimd) void wkv7_recurrent_ker
 // (17.5), H = 8 5.3 us (5.9).
 // Lane L = 8 g + c owns rows k = 8 i + g (i = 0..7) and columns 32 half + 4 c .. + 3: 32 fp32 per unit.  Load
 // instruction i of a unit reads rows 8 i .. 8 i + 7, 128 contiguous bytes each.  sa and y are lane-local sums over
-// 8 rows and a three-step butterfly over the row groups (so their rounding differs from the 16-row sums of
-// wkv7_recurrent_kernel; the two kernels are never mixed within a call).
+// 8 rows and a three-step butterfly over the row groups: the same arithmetic as wkv7_token.h's per-pair code, so a
+// decode step lands on the same bits as that token run inside a verify (snapshots) or a rollback replay.
 // State rows go through buffer resources that cover the 16 KB state or nothing (num_records = 0: loads return zeros,
 // stores are dropped), so a zero initial state or an unstored final state needs no branch around the loads.
 constexpr int kDecodeMaxUnits = 8;
+
+struct HalfIn {  // one token's operands for a half-pair unit
+    uint16_t w, a, b, k, r;
+    uint2 v;  // 4 bf16: v[32 half + 4c .. + 3]
+};
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t state_rsrc(const float* base, bool live) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(base), 0, live ? HS2 * (int)sizeof(float) : 0,
@@ -91,21 +97,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t state_rsrc(const float* base, 
 
 constexpr int kCachePolicyNT = 2;  // buffer-instruction cache policy: non-temporal
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-// Sum over the eight row groups g = lane >> 3 (lanes L, L ^ 8, L ^ 16, ... ^ 56), without LDS: DPP row_ror:8 pairs
-// the halves of each 16-lane row, v_permlane16_swap pairs rows 0-1 and 2-3, v_permlane32_swap the wave's halves.
-// Every lane adds the same partial sums in the same order, so all lanes end with the same float.  (Cross-lane reads
-// need their source lanes active: every lane runs this.)
-__device__ __forceinline__ float butterfly8(float x) {
-    float r = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128 /* row_ror:8 */, 0xf, 0xf, false));
-    x += r;
-    const auto pr = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    float e = __uint_as_float(pr[0]), o = __uint_as_float(pr[1]);  // the even row's value, the odd row's
-    x = e + o;
-    const auto hv = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-    float lo = __uint_as_float(hv[0]), hi = __uint_as_float(hv[1]);  // rows 0-1, rows 2-3
-    return lo + hi;
-}
 
 template <int G>
 __global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Params p) {
@@ -120,7 +111,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Param
     float* const bvec = dvec + 2 * HS;
     float* const kvec = dvec + 3 * HS;
     float* const rvec = dvec + 4 * HS;
-    const int slot = (lane & 7) * 8 + (lane >> 3);  // LDS position of channel `lane` (channel 8 i + g at 8 g + i)
+    const int slot = slab_slot(lane);  // LDS position of channel `lane` (channel 8 i + g at 8 g + i)
     const int rowoff = g * HS + 4 * c;               // this lane's offset (floats) in rows 0 .. 7
     auto lane64 = [](int64_t x, int j) {
         const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x, j);
@@ -143,7 +134,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Param
         if (p.ht_idx) ti = p.ht_idx[mn];
         // The token operands depend on no index: their loads go out while the index loads are in flight (units past
         // nunits read token 0, which always exists).
-        TokenIn x[G];
+        HalfIn x[G];
         int col0[G];
 #pragma unroll
         for (int j = 0; j < G; ++j) {
@@ -186,7 +177,7 @@ __global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Param
         for (int j = 0; j < G; ++j) {
             if (len[j] < 0) continue;  // wave-uniform
             if (len[j] == 1) {
-                const TokenIn cur = x[j];
+                const HalfIn cur = x[j];
                 dvec[slot] = decay(bf16_to_f32(cur.w));
                 avec[slot] = bf16_to_f32(cur.a);
                 bvec[slot] = bf16_to_f32(cur.b);

@@ -199,6 +199,28 @@ def test_config4_verify_snapshots_rollback(dev, K):
     assert eo <= Y_TOL and es <= S_TOL
 
 
+def test_config4_snapshots_equal_decode_steps(dev, K):
+    """Rollback bit-identity does not depend on which kernel re-runs the accepted tokens: the verify's snapshot
+    after token t (token-serial kernel) equals, bit for bit, the state after t + 1 dense single-token wkv7_pool_ calls
+    (the decode kernel), and each decode step's output equals the verify's output of that token.  B = 64, H = 64."""
+    import rwkv_next_amd.synth as synth
+    say("config 4: snapshots vs decode steps")
+    B, T, H = 64, 5, 64
+    ops = operands(B, T, H, seed=1014)
+    pool0 = synth.state_np((B, H, 64, 64), seed=1114)
+    slots = torch.arange(B, device=dev)
+    x = to_dev(ops, dev)
+    snaps = torch.empty(B, T, H, 64, 64, device=dev)
+    o_verify = K.wkv7_pool_(*x, torch.from_numpy(pool0).to(dev), slots, H, 64, final=False, snapshots=snaps)
+    step = torch.from_numpy(pool0).to(dev)
+    for t in range(T):
+        xt = [v[:, t:t + 1].contiguous() for v in x]
+        o_t = K.wkv7_pool_(*xt, step, slots, H, 64)
+        torch.cuda.synchronize()
+        assert torch.equal(step, snaps[:, t]), f"state after decode step {t} differs from the verify snapshot"
+        assert torch.equal(o_t[:, 0], o_verify[:, t]), f"decode step {t} output differs from the verify output"
+
+
 def test_tp_share_H8_decode(dev, K):
     """One TP-8 rank of the 7.2B model: H = 8, B = 64 of a 128-slot pool, T = 1 (512 pairs); untouched slots stay
     bit-identical."""

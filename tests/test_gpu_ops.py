@@ -96,6 +96,38 @@ def test_opcheck_wkv7_replay_(dev, K):
     opcheck(torch.ops.rwkv_next_amd.wkv7_replay_.default, (*to_dev(ops, dev), st, n, H8, 64))
 
 
+def test_registered_ops_reject_strided_or_misshaped_buffers(dev, K):
+    """The registered ops pass raw pointers to the C ABI, so they check their own buffers: a transposed state, a
+    strided pool, a wrong-dtype slot index or a mis-shaped snapshot buffer raises ValueError before any launch, and
+    the buffers are left untouched."""
+    say("registered ops validate buffers")
+    B, T = 3, 4
+    x = to_dev(operands(B, T, H8, seed=71), dev)
+    st = torch.randn(B, H8, 64, 64, device=dev)
+    st_t = st.transpose(2, 3)  # same shape, not contiguous
+    before = st.clone()
+    nk = torch.tensor([1, 2, 4], device=dev)
+    with pytest.raises(ValueError, match="state"):
+        torch.ops.rwkv_next_amd.wkv7_replay_(*x, st_t, nk, H8, 64)
+    with pytest.raises(ValueError, match="state"):
+        torch.ops.rwkv_next_amd.wkv7_replay_(*x, st[:2], nk, H8, 64)
+    with pytest.raises(ValueError, match="n_keep"):
+        torch.ops.rwkv_next_amd.wkv7_replay_(*x, st, nk.to(torch.int32), H8, 64)
+    pool = torch.randn(8, H8, 64, 64, device=dev)
+    slots = torch.tensor([5, 1, 2], device=dev)
+    common = (H8, 64, None, None, None, True, True)
+    with pytest.raises(ValueError, match="pool"):
+        torch.ops.rwkv_next_amd.wkv7_pool_(*x, pool.transpose(2, 3), slots, *common, None, None, T, 0, -1)
+    with pytest.raises(ValueError, match="slots"):
+        torch.ops.rwkv_next_amd.wkv7_pool_(*x, pool, slots.to(torch.int32), *common, None, None, T, 0, -1)
+    snaps = torch.zeros(B, T, H8, 64, 64, device=dev).transpose(3, 4)
+    with pytest.raises(ValueError, match="snapshots"):
+        torch.ops.rwkv_next_amd.wkv7_pool_(*x, pool, slots, H8, 64, None, None, None, False, True, snaps, None, T,
+                                           0, -1)
+    torch.cuda.synchronize()
+    assert torch.equal(st, before)
+
+
 @pytest.mark.parametrize("B,T,use_s0", [(3, 1, True), (2, 4, True), (2, 300, False), (1, 300, True)])
 def test_reference_cases_compiled(dev, K, B, T, use_s0):
     """tools/test_wkv7.py:50-54: every dense case also through torch.compile(lambda *x: wkv7(*x, s0, H, K))."""
