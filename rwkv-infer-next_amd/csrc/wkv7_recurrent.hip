@@ -242,6 +242,163 @@ __global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_kernel(const Param
     }
 }
 
+// One decode token on a half-pair unit's state S (rows 8 i + g, columns col0 + 4 c .. + 3) and its output, u the unit
+// index; dvec is the wave's LDS slab (decay, a, b, k, r, 64 floats each).  The same instruction sequence as the
+// token step written out in wkv7_decode_kernel (kept inline there: its register allocation at eight units per wave
+// is tuned), so both decode kernels produce the same bits; a GPU test compares them.
+__device__ __forceinline__ void decode_token(const Params& p, const HalfIn& x, f4 (&S)[8], uint64_t u, int col0, int g,
+                             int c, int slot, float* dvec, uint32_t nwaves) {
+    float* const avec = dvec + HS;
+    float* const bvec = dvec + 2 * HS;
+    float* const kvec = dvec + 3 * HS;
+    float* const rvec = dvec + 4 * HS;
+    const HalfIn& cur = x;
+    dvec[slot] = decay(bf16_to_f32(cur.w));
+    avec[slot] = bf16_to_f32(cur.a);
+    bvec[slot] = bf16_to_f32(cur.b);
+    kvec[slot] = bf16_to_f32(cur.k);
+    rvec[slot] = bf16_to_f32(cur.r);
+    float vj[4];
+    bf16x2_to_f32(cur.v.x, vj[0], vj[1]);
+    bf16x2_to_f32(cur.v.y, vj[2], vj[3]);
+    wave_lds_sync();
+    // sa[q] = sum_k a_k S[k][q] over the old state (wkv7.py:75)
+    float sa[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2) {
+        const f4 av = *reinterpret_cast<const f4*>(avec + 8 * g + 4 * i2);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) sa[q] = fmaf(av[ii], S[4 * i2 + ii][q], sa[q]);
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) sa[q] = butterfly8(sa[q]);
+    // S[k][q] = d_k S[k][q] + b_k sa[q] + k_k v_q;  y[q] = sum_k r_k S[k][q] (updated state, wkv7.py:75-77)
+    float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i2 = 0; i2 < 2; ++i2) {
+        const f4 dv = *reinterpret_cast<const f4*>(dvec + 8 * g + 4 * i2);
+        const f4 bv = *reinterpret_cast<const f4*>(bvec + 8 * g + 4 * i2);
+        const f4 kv = *reinterpret_cast<const f4*>(kvec + 8 * g + 4 * i2);
+        const f4 rv = *reinterpret_cast<const f4*>(rvec + 8 * g + 4 * i2);
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+            const int i = 4 * i2 + ii;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                S[i][q] = fmaf(dv[ii], S[i][q], fmaf(bv[ii], sa[q], kv[ii] * vj[q]));
+                y[q] = fmaf(rv[ii], S[i][q], y[q]);
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) y[q] = butterfly8(y[q]);
+    if (p.o && g == 0) {
+        const uint32_t pr = (uint32_t)(u >> 1);
+        const int n = (int)(pr / (uint32_t)p.H), h = (int)(pr % (uint32_t)p.H);
+        uint2 pk;
+        pk.x = pack_bf16x2(y[0], y[1]);
+        pk.y = pack_bf16x2(y[2], y[3]);
+        uniform_ptr(reinterpret_cast<uint2*>(p.o + (int64_t)n * p.o_tok_stride + (int64_t)h * HS +
+                                             col0))[c] = pk;
+    }
+    wave_lds_sync();  // this unit's LDS reads precede the next unit's writes
+}
+
+// Wave-uniform loads through the constant address space compile to scalar loads (s_load), which put a unit's slot
+// index into the SGPRs that address its state without a vector load and a readlane.  The caller's index arrays are
+// not written during the launch.
+template <typename T>
+__device__ __forceinline__ T scalar_load(const T* ptr) {
+    return *(const __attribute__((address_space(4))) T*)(ptr);
+}
+// One byte by a scalar load of the aligned dword that holds it (an aligned dword never crosses a page, so it is
+// mapped wherever the byte is).
+__device__ __forceinline__ int scalar_load_u8(const uint8_t* ptr) {
+    const uintptr_t a = reinterpret_cast<uintptr_t>(ptr);
+    const uint32_t w = scalar_load(reinterpret_cast<const uint32_t*>(a & ~(uintptr_t)3));
+    return (int)((w >> (8 * (a & 3))) & 0xffu);
+}
+
+// The decode kernel for launches with few units per wave (G <= kDecodeScalarMaxUnits: small B * H, e.g. one
+// tensor-parallel rank's heads), where the launch is latency-bound: each unit's row metadata (n_keep, fresh, the
+// two slot indices) comes by scalar loads issued before the token loads, so the state loads start one vector round
+// trip earlier.  Same layout and arithmetic as wkv7_decode_kernel.  (For many units per wave the vector gather of
+// wkv7_decode_kernel is faster: 2 G scalar loads and their SGPRs cost more than one vector round trip.)
+constexpr int kDecodeScalarMaxUnits = 4;
+
+template <int G>
+__global__ __launch_bounds__(64 * kWaves, 1) void wkv7_decode_small_kernel(const Params p) {
+    __shared__ __attribute__((aligned(16))) float slab[kWaves][5 * HS];  // decay, a, b, k, r (permuted)
+    const int lane = threadIdx.x & 63;
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 3, c = lane & 7;
+    const uint64_t nunits = 2ull * (uint64_t)p.num_seqs * (uint64_t)p.H;
+    const uint32_t nwaves = gridDim.x * kWaves;
+    float* const dvec = slab[wv];
+    const int slot = slab_slot(lane);
+    const int rowoff = g * HS + 4 * c;
+
+    for (uint64_t base = blockIdx.x * kWaves + wv; base < nunits; base += (uint64_t)G * nwaves) {
+        HalfIn x[G];
+        int col0[G], hd[G], fr[G];
+        int64_t nk[G], hi[G], ti[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const uint64_t u = base + (uint64_t)j * nwaves;
+            const uint32_t pr = (uint32_t)((u < nunits ? u : 0) >> 1);
+            const int n = (int)(pr / (uint32_t)p.H), h = (int)(pr % (uint32_t)p.H);
+            hd[j] = h;
+            nk[j] = p.n_keep ? scalar_load(p.n_keep + n) : 1;
+            fr[j] = p.fresh ? scalar_load_u8(p.fresh + n) : 0;
+            hi[j] = p.h0_idx ? scalar_load(p.h0_idx + n) : n;
+            ti[j] = p.ht_idx ? scalar_load(p.ht_idx + n) : n;
+            col0[j] = 32 * (int)(u & 1);
+            const int64_t off = (int64_t)n * p.in_tok_stride + (int64_t)h * HS;
+            x[j].w = uniform_ptr(p.w + off)[lane];
+            x[j].a = uniform_ptr(p.a + off)[lane];
+            x[j].b = uniform_ptr(p.b + off)[lane];
+            x[j].k = uniform_ptr(p.k + off)[lane];
+            x[j].r = uniform_ptr(p.r + off)[lane];
+            x[j].v = uniform_ptr(reinterpret_cast<const uint2*>(p.v + off + col0[j]))[c];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        f4 S[G][8];
+        int len[G];
+        __amdgpu_buffer_rsrc_t dst[G];
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            const bool valid = base + (uint64_t)j * nwaves < nunits;
+            len[j] = valid && nk[j] >= 1 ? 1 : 0;
+            const int64_t s = (valid && p.h0 && !fr[j] && hi[j] >= 0 && hi[j] < p.h0_rows)
+                                  ? (hi[j] * p.H + hd[j]) * (int64_t)HS2 : -1;
+            const int64_t d = (valid && p.ht && ti[j] >= 0 && ti[j] < p.ht_rows) ? (ti[j] * p.H + hd[j]) * (int64_t)HS2
+                                                                               : -1;
+            const bool mine = valid && (p.rec_max_len < 0 || len[j] <= p.rec_max_len);
+            const __amdgpu_buffer_rsrc_t src = state_rsrc(s >= 0 ? p.h0 + s : nullptr, mine && s >= 0);
+            dst[j] = state_rsrc(d >= 0 ? p.ht + d : nullptr, mine && d >= 0);
+            if (!mine) len[j] = -1;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                S[j][i] = __builtin_bit_cast(
+                    f4, __builtin_amdgcn_raw_buffer_load_b128(
+                            src, (int)((rowoff + 8 * i * HS + col0[j]) * sizeof(float)), 0, kCachePolicyNT));
+        }
+#pragma unroll
+        for (int j = 0; j < G; ++j) {
+            if (len[j] == 1) decode_token(p, x[j], S[j], base + (uint64_t)j * nwaves, col0[j], g, c, slot, dvec, nwaves);
+            if (len[j] < 0) continue;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, S[j][i]), dst[j],
+                                                       (int)((rowoff + 8 * i * HS + col0[j]) * sizeof(float)), 0,
+                                                       kCachePolicyNT);
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
@@ -256,6 +413,15 @@ hipError_t launch_recurrent(const Params& p, hipStream_t stream) {
         const int64_t waves = std::min<int64_t>(units, simds);
         const int G = (int)std::min<int64_t>((units + waves - 1) / waves, kDecodeMaxUnits);
         const dim3 grid((unsigned)((waves + kWaves - 1) / kWaves)), block(64 * kWaves);
+        if (G <= kDecodeScalarMaxUnits) {
+            switch (G) {
+                case 1: hipLaunchKernelGGL(wkv7_decode_small_kernel<1>, grid, block, 0, stream, p); break;
+                case 2: hipLaunchKernelGGL(wkv7_decode_small_kernel<2>, grid, block, 0, stream, p); break;
+                case 3: hipLaunchKernelGGL(wkv7_decode_small_kernel<3>, grid, block, 0, stream, p); break;
+                default: hipLaunchKernelGGL(wkv7_decode_small_kernel<4>, grid, block, 0, stream, p); break;
+            }
+            return hipGetLastError();
+        }
         switch (G) {
             case 1: hipLaunchKernelGGL(wkv7_decode_kernel<1>, grid, block, 0, stream, p); break;
             case 2: hipLaunchKernelGGL(wkv7_decode_kernel<2>, grid, block, 0, stream, p); break;

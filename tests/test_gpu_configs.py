@@ -199,13 +199,15 @@ def test_config4_verify_snapshots_rollback(dev, K):
     assert eo <= Y_TOL and es <= S_TOL
 
 
-def test_config4_snapshots_equal_decode_steps(dev, K):
+@pytest.mark.parametrize("H", [64, 8])
+def test_config4_snapshots_equal_decode_steps(dev, K, H):
     """Rollback bit-identity does not depend on which kernel re-runs the accepted tokens: the verify's snapshot
     after token t (token-serial kernel) equals, bit for bit, the state after t + 1 dense single-token wkv7_pool_ calls
-    (the decode kernel), and each decode step's output equals the verify's output of that token.  B = 64, H = 64."""
+    (a decode kernel), and each decode step's output equals the verify's output of that token.  B = 64: H = 64 runs
+    the decode kernel with eight units per wave, H = 8 the small-launch decode kernel (scalar index loads)."""
     import rwkv_next_amd.synth as synth
-    say("config 4: snapshots vs decode steps")
-    B, T, H = 64, 5, 64
+    say("config 4: snapshots vs decode steps", H)
+    B, T = 64, 5
     ops = operands(B, T, H, seed=1014)
     pool0 = synth.state_np((B, H, 64, 64), seed=1114)
     slots = torch.arange(B, device=dev)
