@@ -13,9 +13,10 @@
  * with the RAW w (the decay is computed in fp32 inside the kernels).  Head size K = V = 64.
  *
  * Plain C: no HIP, CUDA or torch types.  Pointers are device pointers; `stream` is a hipStream_t passed as
- * void*.  No function allocates device memory or synchronises the host, and the only global state is a per-device
- * cache of the compute-unit count, so every call is reentrant and can be recorded into a hipGraph (scratch memory
- * comes from the caller's workspace).
+ * void*.  No function allocates device memory or synchronises the host, and every call is reentrant and can be
+ * recorded into a hipGraph (scratch memory comes from the caller's workspace).  Global state: a per-device cache of
+ * the compute-unit count, and the static device scratch array of wkv7_run_noalloc (WKV7_NOALLOC_SCRATCH_BYTES on
+ * every GPU the library is loaded on, from module load to process exit) with a per-device cache of its address.
  */
 #ifndef RWKV_NEXT_AMD_WKV7_H
 #define RWKV_NEXT_AMD_WKV7_H
@@ -66,12 +67,16 @@ extern "C" {
 #define WKV7_CHUNK_W_MAX 1.0f
 
 /* Algorithm selection (wkv7_args.algo). */
-#define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens, chunked otherwise; a
-                                * ragged call whose rows are short enough runs as one chain-kernel dispatch */
+#define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens; longer dense rows the
+                                * segmented kernel (the chunked one for calls of fewer than 8 x CUs 32-token
+                                * chunk-heads); a ragged call runs its short rows token-serial and its long rows
+                                * segmented (two dispatches), or as one chain-kernel dispatch when no row is longer
+                                * than twice the average chunk work per CU */
 #define WKV7_ALGO_RECURRENT 1  /* token-serial kernel for every row */
 #define WKV7_ALGO_CHUNKED 2    /* chunked MFMA prefill for every row */
-#define WKV7_ALGO_SEGMENTED 4  /* every row through the segmented chunked kernel (32-token chunks, rows cut into
-                                * segments, one dispatch; needs a workspace) */
+#define WKV7_ALGO_SEGMENTED 4  /* the segmented chunked kernel (32-token chunks, rows cut into segments, one
+                                * dispatch; needs a workspace): every row, or with rec_max_len >= 0 the rows longer
+                                * than it, the others token-serial (two dispatches) */
 #define WKV7_ALGO_CHAIN 3      /* one dispatch: rows of at most rec_max_len tokens token-serial, longer rows chunked with
                                 * each (row, head) chain walked by one workgroup (no workspace; num_seqs <= 512) */
 
@@ -101,7 +106,11 @@ typedef struct wkv7_args {
     const int64_t *n_keep;        /* NULL, or per sequence: run only the first min(len, n_keep[n]) tokens */
     float *snapshots;             /* NULL, or [num_seqs][T][H][64][64]: state after each token (recurrent) */
 
-    void *workspace;              /* device scratch for the chunked path (see wkv7_workspace_size) */
+    void *workspace;              /* device scratch of the chunked paths (see wkv7_workspace_size), 256-byte aligned.
+                                   * Its first WKV7_SEG_FLAG_BYTES hold the segmented kernel's hand-off flags: they
+                                   * must be zero before the workspace's first call, and every call that completes
+                                   * leaves them zero (WKV7_STATUS_SEGMENT_WAIT aside), so a workspace serves any
+                                   * number of calls in stream order without clearing */
     size_t workspace_bytes;
 
     int32_t num_seqs;             /* N: B when dense, cu_seqlens entries - 1 when ragged */
@@ -116,6 +125,8 @@ typedef struct wkv7_args {
 } wkv7_args;
 
 /* Size of the device scratch array behind wkv7_run_noalloc (per GPU, held from module load to process exit). */
+/* Bytes at the start of a workspace reserved for the segmented kernel's hand-off flags (zero between calls). */
+#define WKV7_SEG_FLAG_BYTES (256u << 10)
 #define WKV7_NOALLOC_SCRATCH_BYTES (128u << 20)
 
 /* Bytes of device workspace `wkv7_run` needs for these arguments (0 when only the token-serial kernel runs).
@@ -132,10 +143,10 @@ int wkv7_workspace_size(const wkv7_args *args, size_t *bytes);
  * Asynchronous; returns after launching. */
 int wkv7_run(const wkv7_args *args, void *stream);
 
-/* wkv7_run without a caller-provided workspace, for callers that cannot allocate device memory (code under HIP
- * graph capture that must not allocate, tight serving loops, harnesses that forbid hipMalloc).  No counterpart in
- * the reference (its launcher allocates through the torch caching allocator, wkv7.py:93, 119, 135).  args->workspace
- * and args->workspace_bytes are ignored: the scratch is a static device array of WKV7_NOALLOC_SCRATCH_BYTES per GPU.
+/* wkv7_run without a caller-provided workspace.  It has no counterpart in the reference; it is for callers that
+ * cannot allocate device memory (code under HIP graph capture that must not allocate, tight serving loops, harnesses
+ * that forbid hipMalloc).  args->workspace and args->workspace_bytes are ignored: the scratch is a static device
+ * array of WKV7_NOALLOC_SCRATCH_BYTES per GPU, whose flag region starts zero and is left zero by every call.
  * A call whose wkv7_workspace_size exceeds that returns WKV7_ERR_SCRATCH_LIMIT before launching anything.  Calls no
  * hipMalloc/hipFree.  All calls on one GPU share its array: calls whose kernels overlap on one device (other streams,
  * other threads) race; calls in stream order on one stream do not. */

@@ -33,8 +33,10 @@ namespace {
 using wkv7::Params;
 
 // AUTO threshold: rows of at most this many tokens run the token-serial kernel.  Below it one wavefront walking
-// the tokens beats the chunked path's fixed cost (a 64-token chunk transition built on MFMA per row).
+// the tokens beats the chunked paths' fixed cost (a chunk transition built on MFMA per row).
 constexpr int kDefaultRecMaxLen = 32;
+// AUTO on dense rows: the segmented kernel from this many 32-token chunk-heads per CU up (measured crossover near 8)
+constexpr int kSegMinChunkHeadsPerCu = 8;
 
 struct Plan {
     bool run_recurrent = false;
@@ -120,17 +122,31 @@ Plan make_plan(const wkv7_args* a) {
     } else if (bound <= thr) {
         pl.run_recurrent = true;
     } else if (!varlen && !a->n_keep) {
-        pl.run_chunked = true;  // every row has exactly T > thr tokens
+        // every row has exactly T > thr tokens: one segmented dispatch, unless the call is too small to fill the
+        // GPU with segments (then the chunked path's wider per-chunk parallelism wins: B = 1, T = 512 is 41 against
+        // 51 us at H = 64, T = 1024 about even)
+        const int64_t chunk_heads = (int64_t)a->num_seqs * ((bound + wkv7::kSegChunk - 1) / wkv7::kSegChunk) * a->H;
+        if (chunk_heads >= (int64_t)kSegMinChunkHeadsPerCu * wkv7::device_cu_count()) pl.run_seg = true;
+        else pl.run_chunked = true;
     } else {
-        pl.run_recurrent = pl.run_chunked = true;  // row lengths are only known on the device: split by length
-        pl.rec_len_rec = thr;
-        pl.rec_len_chunk = thr;
+        // row lengths are only known on the device: rows of at most thr tokens token-serial, the others segmented
+        // (chunked when the segmented kernel's LDS row table cannot hold the call)
+        pl.run_recurrent = true;
+        pl.rec_len_rec = pl.rec_len_chunk = thr;
+        if (a->num_seqs <= wkv7::kSegMaxRows) pl.run_seg = true;
+        else pl.run_chunked = true;
+    }
+    if (pl.run_seg) {
+        pl.sws = wkv7::seg_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen || a->n_keep != nullptr,
+                                     pl.rec_len_chunk, wkv7::device_cu_count());
+        // AUTO falls back to the chunked path when the segmented grid would not fit its hand-off flag region
+        if (a->algo == WKV7_ALGO_AUTO && pl.sws.units > (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t))) {
+            pl.run_seg = false;
+            pl.run_chunked = true;
+        }
     }
     if (pl.run_chunked)
         pl.ws = wkv7::chunk_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen, pl.rec_len_chunk);
-    if (pl.run_seg)
-        pl.sws = wkv7::seg_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen || a->n_keep != nullptr,
-                                     pl.rec_len_chunk, wkv7::device_cu_count());
     return pl;
 }
 

@@ -6,6 +6,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "wkv7.h"
 #include "wkv7_device.h"
 
 namespace wkv7 {
@@ -65,7 +66,7 @@ __host__ __device__ inline int seg_start(int nch, int nseg, int s) {
 }
 // The workspace starts with one int32 hand-off flag per unit (at most kSegFlagRegion / 4 units).  The region must be
 // zero before a workspace's first call; every call that completes leaves it zero.  No other path writes it.
-constexpr size_t kSegFlagRegion = 256 * 1024;
+constexpr size_t kSegFlagRegion = WKV7_SEG_FLAG_BYTES;
 struct SegWorkspace {
     int seg;             // chunks per segment
     int64_t units;       // grid (an upper bound on the call's units)

@@ -87,9 +87,15 @@ def test_workspace_sizing_follows_the_dispatch_rule():
     # (A hi/lo bf16, H^T fp32, Q bf16, O_intra^T bf16: 64 x 64 each)
     n = _lib.workspace_size(base_args(T=100, total_tokens=300))
     assert n >= 3 * 2 * 2 * (2 * 2 + 4 + 2 + 2) * 64 * 64
-    # ragged: bound by total_tokens, plus the chunk table
+    # a dense call of at least 8 x CUs 32-token chunk-heads takes the segmented kernel (256 CUs assumed without a
+    # GPU): B = 1, T = 4096, H = 64 is 4 segments of the row per head (36 + 31 + 31 + 30 chunks), 256 units with a
+    # 32 KB hand-off entry each, a 4 KB Q P record per chunk after the first segment, after the flag region
+    seg = _lib.workspace_size(base_args(num_seqs=1, T=4096, total_tokens=4096, H=64, in_tok_stride=64 * 64,
+                                           o_tok_stride=64 * 64))
+    assert seg == _lib.WKV7_FLAG_REGION_BYTES + 256 * 2 * 64 * 64 * 4 + (128 - 36) * 64 * 4096
+    # ragged: short rows token-serial, long rows segmented (bounded by total_tokens); the flag region leads
     r = _lib.workspace_size(base_args(cu_seqlens=0x10000, T=0, total_tokens=1000))
-    assert r > 0
+    assert r > _lib.WKV7_FLAG_REGION_BYTES
     # a missing workspace is refused before launch
     a = base_args(T=100, total_tokens=300)
     assert _lib.load().wkv7_run(ctypes.byref(a), None) == _lib.WKV7_ERR_WORKSPACE

@@ -92,3 +92,5 @@ def test_status_bits_match_header():
         assert value == getattr(_lib, f"ALGO_{name}")
     w_max = float(re.search(r"#define WKV7_CHUNK_W_MAX ([0-9.]+)f", text).group(1))
     assert w_max == _lib.WKV7_CHUNK_W_MAX
+    flag = re.search(r"#define WKV7_SEG_FLAG_BYTES \((\d+)u << (\d+)\)", text)
+    assert int(flag.group(1)) << int(flag.group(2)) == _lib.WKV7_FLAG_REGION_BYTES
