@@ -70,8 +70,7 @@ extern "C" {
 #define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens; longer dense rows the
                                 * segmented kernel (the chunked one for calls of fewer than 8 x CUs 32-token
                                 * chunk-heads); a ragged call runs its short rows token-serial and its long rows
-                                * segmented (two dispatches), or as one chain-kernel dispatch when no row is longer
-                                * than twice the average chunk work per CU */
+                                * segmented (two dispatches; chunked beyond kSegMaxRows = 4096 rows) */
 #define WKV7_ALGO_RECURRENT 1  /* token-serial kernel for every row */
 #define WKV7_ALGO_CHUNKED 2    /* chunked MFMA prefill for every row */
 #define WKV7_ALGO_SEGMENTED 4  /* the segmented chunked kernel (32-token chunks, rows cut into segments, one

@@ -89,18 +89,6 @@ int validate(const wkv7_args* a) {
     return WKV7_OK;
 }
 
-// AUTO on a ragged call: one chain-kernel dispatch when the longest possible row (the caller's bound, in chunks) is
-// no longer than twice the average chunk work per CU, so that walking each (row, head) chain on one CU does not set
-// the call's length -- e.g. a continuous-batching step of a few prefill rows up to 2048 tokens and many decode rows.
-// Long rows (one 4096-token prefill) keep the two-kernel path, which spreads a row's chunks over all CUs.
-bool chain_fits(const wkv7_args* a, int64_t bound, int thr) {
-    if (a->algo != WKV7_ALGO_AUTO || !a->cu_seqlens || a->snapshots || a->num_seqs > wkv7::kChainMaxSeqs) return false;
-    if (bound <= thr) return false;
-    const int64_t longest = (bound + wkv7::kChunk - 1) / wkv7::kChunk;
-    const int64_t chunk_items = (int64_t)a->H * ((a->total_tokens + wkv7::kChunk - 1) / wkv7::kChunk);
-    return longest * wkv7::device_cu_count() <= 2 * chunk_items;
-}
-
 Plan make_plan(const wkv7_args* a) {
     Plan pl;
     const bool varlen = a->cu_seqlens != nullptr;
@@ -114,7 +102,7 @@ Plan make_plan(const wkv7_args* a) {
             pl.run_recurrent = true;
             pl.rec_len_rec = pl.rec_len_chunk = a->rec_max_len;
         }
-    } else if (a->algo == WKV7_ALGO_CHAIN || chain_fits(a, bound, thr)) {
+    } else if (a->algo == WKV7_ALGO_CHAIN) {
         pl.run_chain = true;
         pl.rec_len_rec = thr;
     } else if (a->algo == WKV7_ALGO_CHUNKED) {

@@ -1,12 +1,14 @@
 // wkv7_noalloc.hip -- wkv7_run_noalloc: wkv7_run for callers that cannot allocate device memory (code under HIP
 // graph capture that must not touch an allocator, tight serving loops, harnesses that forbid hipMalloc).
 //
-// The only scratch memory wkv7_run uses is the chunked path's workspace (the chunk table and the per-(chunk, head)
-// records).  Here it comes from `scratch`, a file-scope device array of WKV7_NOALLOC_SCRATCH_BYTES that every GPU
-// the library runs on holds from module load until the process ends.  Calls needing more are refused with
-// WKV7_ERR_SCRATCH_LIMIT before anything is launched.  The chunked kernels write every workspace byte they read in
-// the same call (the plan kernel fills the chunk table, prep writes every record the scan reads), so nothing has to
-// start at zero and no clearing is needed between calls.
+// The only scratch memory wkv7_run uses is the chunked paths' workspace (hand-off flags, exchange entries, records).
+// Here it comes from `scratch`, a file-scope device array of WKV7_NOALLOC_SCRATCH_BYTES that every GPU the library
+// runs on holds from module load until the process ends.  Calls needing more are refused with
+// WKV7_ERR_SCRATCH_LIMIT before anything is launched.  The segmented kernel's flag region (the first
+// WKV7_SEG_FLAG_BYTES) must be zero before a call: the array starts zeroed and every call that completes leaves it
+// zero; everything else is written before it is read within each call, so no clearing is needed between calls.  (A
+// call that reports WKV7_STATUS_SEGMENT_WAIT -- a bounded hand-off wait that expired -- can leave flags set; later
+// segmented calls through this entry are then unreliable until the process restarts.)
 //
 // All calls on one GPU share that GPU's array: two calls whose kernels overlap on one device (different streams,
 // or different host threads) race on it.  Calls in stream order on one stream are safe.

@@ -43,6 +43,7 @@
 //   An identity operand turns an N fragment into the RL tile of M or of M^T (one exact MFMA per tile).
 // The state S is held as RL tiles (k tile m, column tile j); a state wavefront j holds tiles (0..3, j).
 #include <algorithm>
+#include <cstdint>
 
 #include "wkv7.h"
 #include "wkv7_device.h"
@@ -84,6 +85,8 @@ struct SegSmem {
     int ready[NREC];       // chunk index + 1 of the record a slot holds
     int done[NREC][4];     // per state wavefront: uses of the slot it has finished reading
     int fail;
+    int scan[8];
+    int rows[kSegMaxRows + 1];  // ragged and n_keep calls: first stream chunk of each row
 };
 
 __device__ __forceinline__ f4 z4() { return f4{0.f, 0.f, 0.f, 0.f}; }
@@ -220,113 +223,151 @@ __device__ __forceinline__ bf8 as_bf8(uint4 x) { return __builtin_bit_cast(bf8, 
 __device__ __forceinline__ uint4 as_u4(bf8 x) { return __builtin_bit_cast(uint4, x); }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Units
+// Units.  Each head's owned rows, in row order, form a stream of chunks: a row of L tokens has max(1, ceil(L / 32))
+// of them (an empty row's one chunk holds no token and passes its state through).  A unit (one workgroup) takes one
+// head's stream chunks [c0, c1):
+//   * dense calls (every row T tokens, no n_keep): the segments of one row, seg_start's split;
+//   * ragged and n_keep calls: equal shares of the stream, ceil(chunks / units per head) each (at least
+//     kSegMinChunks), which may cross rows, so that every CU gets the same work whatever the row lengths.
+// The unit's first piece (the chunks of its first row) continues a row an earlier unit started when c0 is inside
+// that row ("P mode": it starts from zeros, carries P, and its outputs are corrected once the row's state at c0 is
+// known); every later row of the unit starts inside it, from the row's initial state.  A row spanning the units
+// k0 < .. < km of a head is handed on through their exchange entries: k0 publishes its true end state, k0+1 .. km-1
+// their local end states and P; unit k reads the entries of k0 .. k-1 (lower workgroup indices: dispatched first).
 // ------------------------------------------------------------------------------------------------------------------
+
+// Rows this launch owns: every row when p.rec_max_len < 0, else rows longer than it (the token-serial kernel takes
+// the others).
+__device__ __forceinline__ bool owns(const Params& p, int L) { return p.rec_max_len < 0 || L > p.rec_max_len; }
+__device__ __forceinline__ int row_chunks(int L) { return L > 0 ? (L + SC - 1) / SC : 1; }
+
+struct Row {   // an owned row: stream chunks [first, first + nch), tokens [bos, bos + L)
+    int n, nch, L;
+    int64_t first, bos;
+};
 
 struct Unit {
     bool ok;
-    int n, h, s, nseg;
-    int64_t bos;
-    int L, nch;       // row length and chunks of the row
-    int c0, c1;       // chunk range of the unit
-    int first;        // chunks of the row's first segment
-    int64_t u;        // unit index (exchange slot); the previous segment's is u - H
-    int64_t qp0;      // Q P slot of the row's chunk `first` (chunks of later segments follow it)
+    bool dense;
+    int h;
+    int64_t k;              // unit index within the head; exchange slot and workgroup index k * H + h
+    int64_t c0, c1;         // stream chunks of the unit
+    int nch, nseg, first;   // dense: chunks per row, segments per row, chunks of a row's first segment
+    int64_t seg;            // ragged: stream chunks per unit
+    int N;                  // ragged: rows of the call (the LDS table's length)
 };
 
-// Rows this launch owns: every row when p.rec_max_len < 0, else rows longer than it (the token-serial kernel takes
-// the others).  An owned row has at least one unit: an empty row's unit passes its initial state to its final state.
-__device__ __forceinline__ bool owns(const Params& p, int L) { return p.rec_max_len < 0 || L > p.rec_max_len; }
-__device__ __forceinline__ int row_chunks(int L) { return (L + SC - 1) / SC; }
-__device__ __forceinline__ int row_units(const Params& p, int L, int seg) {
-    return owns(p, L) ? std::max(1, (row_chunks(L) + seg - 1) / seg) : 0;
+__device__ __forceinline__ Row row_dense(const Params& p, const Unit& U, int64_t c) {
+    Row r;
+    r.n = (int)(c / U.nch);
+    r.nch = U.nch;
+    r.first = (int64_t)r.n * U.nch;
+    r.bos = (int64_t)r.n * p.T;
+    r.L = p.T;
+    return r;
+}
+__device__ __forceinline__ Row row_ragged(const Params& p, const int* rows, int n) {
+    Row r;
+    r.n = n;
+    r.first = rows[n];
+    r.nch = rows[n + 1] - rows[n];
+    seq_extent(p, n, r.bos, r.L);
+    return r;
+}
+// the owned row holding stream chunk c
+__device__ Row row_at(const Params& p, const Unit& U, const int* rows, int64_t c) {
+    if (U.dense) return row_dense(p, U, c);
+    int lo = 0, hi = U.N - 1;  // the last n with rows[n] <= c (then rows[n + 1] > c: row n owns chunks)
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (rows[mid] <= c) lo = mid; else hi = mid - 1;
+    }
+    return row_ragged(p, rows, lo);
+}
+// the owned row after r (called only while r ends before the unit's last chunk, so one exists)
+__device__ Row next_row(const Params& p, const Unit& U, const int* rows, const Row& r) {
+    if (U.dense) return row_dense(p, U, r.first + r.nch);
+    int n = r.n + 1;
+    while (rows[n + 1] == rows[n]) ++n;  // rows without chunks (not owned)
+    return row_ragged(p, rows, n);
+}
+// the units of the head holding row r's first and last chunks
+__device__ __forceinline__ int64_t first_unit(const Unit& U, const Row& r) {
+    return U.dense ? (int64_t)r.n * U.nseg : r.first / U.seg;
+}
+__device__ __forceinline__ int64_t last_unit(const Unit& U, const Row& r) {
+    return U.dense ? (int64_t)r.n * U.nseg + U.nseg - 1 : (r.first + r.nch - 1) / U.seg;
 }
 
-// Row table of ragged / n_keep calls, built in LDS by every workgroup (rows <= kSegMaxRows):
-// tab[n] = units (segments) before row n, tab[kSegMaxRows + 1 + n] = Q P chunks before row n.
-__device__ Unit find_unit(const Params& p, int seg, int64_t blk, int* tab) {
+// Exclusive prefix sum of x over the workgroup's 512 threads (tmp: 8 ints of LDS); *total gets the sum.
+__device__ int block_excl_scan(int x, int* tmp, int* total) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    int incl = x;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const int y = __shfl_up(incl, d);
+        if (lane >= d) incl += y;
+    }
+    if (lane == 63) tmp[wv] = incl;
+    __syncthreads();
+    int off = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+        const int t = tmp[w];
+        off += w < wv ? t : 0;
+        tot += t;
+    }
+    __syncthreads();
+    *total = tot;
+    return off + incl - x;
+}
+
+// The unit of workgroup blk.  Ragged and n_keep calls first build the row table in LDS with every thread:
+// rows[n] = the first stream chunk of row n (rows[N] = the stream's length), N <= kSegMaxRows.
+__device__ Unit find_unit(const Params& p, int seg, int64_t blk, int* rows, int* tmp) {
     Unit U{};
     const int H = p.H;
-    const int64_t k = blk / H;
-    U.h = (int)(blk - k * H);
+    U.k = blk / H;
+    U.h = (int)(blk - U.k * H);
     if (!p.cu && !p.n_keep) {
-        const int L = p.T;
-        const int nseg = row_units(p, L, seg);
-        if (nseg == 0) return U;
-        const int nch = row_chunks(L);
-        const int64_t n = k / nseg;
+        U.dense = true;
+        if (!owns(p, p.T)) return U;
+        U.nch = row_chunks(p.T);
+        U.nseg = std::max(1, (U.nch + seg - 1) / seg);
+        U.first = seg_start(U.nch, U.nseg, 1);
+        const int64_t n = U.k / U.nseg;
         if (n >= p.num_seqs) return U;
-        U.n = (int)n;
-        U.s = (int)(k - n * nseg);
-        U.nseg = nseg;
-        U.L = L;
-        U.nch = nch;
-        U.bos = n * (int64_t)p.T;
-        U.qp0 = n * (int64_t)(nch - seg_start(nch, nseg, 1));
+        const int s = (int)(U.k - n * U.nseg);
+        U.c0 = n * U.nch + seg_start(U.nch, U.nseg, s);
+        U.c1 = n * U.nch + seg_start(U.nch, U.nseg, s + 1);
     } else {
-        const int N = p.num_seqs;
-        int* useg = tab;
-        int* uqp = tab + kSegMaxRows + 1;
-        // per-thread partial sums over a contiguous block of rows, then an exclusive scan over threads
-        int (*part)[512] = reinterpret_cast<int (*)[512]>(tab + 2 * (kSegMaxRows + 1));
-        const int tid = threadIdx.x, nt = blockDim.x;
-        const int per = (N + nt - 1) / nt;
+        const int N = p.num_seqs, tid = threadIdx.x;
+        const int per = (N + 511) / 512;
         const int r0 = min(N, tid * per), r1 = min(N, r0 + per);
-        int a = 0, b = 0;
+        int a = 0;
         for (int n = r0; n < r1; ++n) {
             int64_t bos;
             int L;
             seq_extent(p, n, bos, L);
-            useg[n] = row_units(p, L, seg);
-            uqp[n] = useg[n] ? row_chunks(L) - seg_start(row_chunks(L), useg[n], 1) : 0;
-            a += useg[n];
-            b += uqp[n];
+            rows[n] = owns(p, L) ? row_chunks(L) : 0;
+            a += rows[n];
         }
-        part[0][tid] = a;
-        part[1][tid] = b;
-        __syncthreads();
-        if (tid < 2) {
-            int acc = 0;
-            for (int t = 0; t < nt; ++t) {
-                const int x = part[tid][t];
-                part[tid][t] = acc;
-                acc += x;
-            }
-            if (tid == 0) useg[N] = acc; else uqp[N] = acc;
-        }
-        __syncthreads();
-        a = part[0][tid];
-        b = part[1][tid];
+        int total;
+        int off = block_excl_scan(a, tmp, &total);
         for (int n = r0; n < r1; ++n) {
-            const int x = useg[n], y = uqp[n];
-            useg[n] = a;
-            uqp[n] = b;
-            a += x;
-            b += y;
+            const int x = rows[n];
+            rows[n] = off;
+            off += x;
         }
+        if (tid == 0) rows[N] = total;
         __syncthreads();
-        if (k >= useg[N]) {
-            __syncthreads();
-            return U;
-        }
-        int lo = 0, hi = N - 1;  // last n with useg[n] <= k
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (useg[mid] <= k) lo = mid; else hi = mid - 1;
-        }
-        U.n = lo;
-        U.s = (int)(k - useg[lo]);
-        U.nseg = useg[lo + 1] - useg[lo];
-        U.qp0 = uqp[lo];
-        seq_extent(p, lo, U.bos, U.L);
-        U.nch = row_chunks(U.L);
-        __syncthreads();  // the table lives in the ring
+        U.N = N;
+        const int64_t per_head = std::max<int64_t>(1, (int64_t)gridDim.x / H);
+        U.seg = std::max<int64_t>(kSegMinChunks, (total + per_head - 1) / per_head);
+        U.c0 = U.k * U.seg;
+        U.c1 = std::min<int64_t>(U.c0 + U.seg, total);
     }
-    U.ok = true;
-    U.u = blk;
-    U.c0 = seg_start(U.nch, U.nseg, U.s);
-    U.c1 = seg_start(U.nch, U.nseg, U.s + 1);
-    U.first = seg_start(U.nch, U.nseg, 1);
+    U.ok = U.c0 < U.c1;
     return U;
 }
 
@@ -340,6 +381,10 @@ struct Raw {
 
 __device__ __forceinline__ void load_raw(Raw& x, const Params& p, int64_t tok0, int Lc, int h, int lane) {
     const int i = lane & 15, q = lane >> 4;
+    if (Lc <= 0) {  // an empty row's chunk: no token to read (every row of the record is masked anyway)
+        x = Raw{};
+        return;
+    }
 #pragma unroll
     for (int tau = 0; tau < 2; ++tau) {
         const int t = 16 * tau + i;
@@ -683,34 +728,45 @@ __device__ __forceinline__ void store_y(const Params& p, int64_t tok0, int Lc, i
 
 }  // namespace
 
-// xbuf: one 32 KB entry per unit (its local end state, then its P^T, RL tiles); flags: one per unit, set to the number
-// of later segments of the row that read the entry and counted down by them.
+// xbuf: 32 KB exchange entries (a local end state, then its P^T, RL tiles): entry b for workgroup b's published row,
+// and for ragged calls entry gridDim.x + b, where workgroup b parks its first row's local end state and P when that
+// row ends inside it.  flags: one per workgroup, set to the number of later units that read its entry and counted
+// down by them.  seg: dense calls' chunks per segment.
 __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, int32_t* __restrict__ flags,
                                                        float* __restrict__ xbuf, char* __restrict__ qpbuf) {
     __shared__ SegSmem sm;
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, q = lane >> 4;
-    const Unit U = find_unit(p, seg, (int64_t)blockIdx.x, reinterpret_cast<int*>(&sm.ring[0][0]));
+    const Unit U = find_unit(p, seg, (int64_t)blockIdx.x, sm.rows, sm.scan);
     if (!U.ok) return;
     const int H = p.H, h = U.h;
+    const int64_t uid = blockIdx.x;
     if (tid < NREC) sm.ready[tid] = 0;
     if (tid < NREC * 4) (&sm.done[0][0])[tid] = 0;
     if (tid == 0) sm.fail = 0;
     __syncthreads();
-    const int nloc = U.c1 - U.c0;  // chunks of this unit
-    // Q P slot of local chunk cl (segments after the first): the row's chunks c >= U.first are numbered from U.qp0
-    auto qp_slot = [&](int cl) -> uint4* {
-        const int64_t slot = U.qp0 + (int64_t)(U.c0 + cl - U.first);
+    const int nloc = (int)(U.c1 - U.c0);  // chunks of this unit
+    const Row A = row_at(p, U, sm.rows, U.c0);  // the unit's first row
+    const bool pmodeA = U.c0 > A.first;       // ... continued from an earlier unit
+    // Q P record of stream chunk c of the first row (P mode only): dense calls number a row's chunks after its
+    // first segment, ragged calls the stream's chunks
+    auto qp_slot = [&](int64_t c) -> uint4* {
+        const int64_t slot = U.dense ? (int64_t)A.n * (U.nch - U.first) + (c - A.first - U.first) : c;
         return reinterpret_cast<uint4*>(qpbuf + (slot * H + h) * (int64_t)(4 * 1024));
     };
+    // exchange entry e: its local end state [m][j][lane], then (P mode) its P^T [j][m][lane]
+    auto xs_of = [&](int64_t e) { return reinterpret_cast<f4*>(xbuf + e * (int64_t)(2 * HS2)); };
 
     f4 S[4], P[4];  // state wavefronts: column tile j of S and of P
     if (wv < 4) {
         // ---------------- prep wavefronts: chunks cl = wv, wv + 4, ..
+        Row r = A;
         for (int cl = wv; cl < nloc; cl += 4) {
-            const int ci = U.c0 + cl;
-            const int64_t tok0 = U.bos + (int64_t)ci * SC;
-            const int Lc = min(SC, U.L - ci * SC);
+            const int64_t c = U.c0 + cl;
+            while (c >= r.first + r.nch) r = next_row(p, U, sm.rows, r);
+            const int ci = (int)(c - r.first);
+            const int64_t tok0 = r.bos + (int64_t)ci * SC;
+            const int Lc = (int)std::max<int64_t>(0, std::min<int64_t>(SC, r.L - (int64_t)ci * SC));
             Raw raw;
             load_raw(raw, p, tok0, Lc, h, lane);
             const int slot = cl % NREC;
@@ -721,16 +777,64 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
     } else {
         // ---------------- state wavefronts: columns 16 j .. 16 j + 15
         const int j = wv - 4;
-        const float* src = U.s == 0 ? state_src(p, U.n, h) : nullptr;
+        // a row's initial / final state (true mode): RL tiles (m, j), element (16 m + 4 q + v, 16 j + i), addressed
+        // from one per-lane pointer (precomputed 64-bit element offsets would spill)
+        const int lane_off = 4 * q * HS + 16 * j + i;
+        auto load_state = [&](const Row& rr) {
+            const float* src = state_src(p, rr.n, h);
+            if (src) {
+                const float* s0 = src + lane_off;
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
+                for (int m = 0; m < 4; ++m)
 #pragma unroll
-            for (int v = 0; v < 4; ++v) S[m][v] = src ? src[(16 * m + 4 * q + v) * HS + 16 * j + i] : 0.f;
-            P[m] = (m == j) ? plus_i(z4(), lane) : z4();
+                    for (int v = 0; v < 4; ++v) S[m][v] = s0[(16 * m + v) * HS];
+            } else {
+#pragma unroll
+                for (int m = 0; m < 4; ++m) S[m] = z4();
+            }
+        };
+        auto store_state = [&](const Row& rr) {
+            float* const dst = state_dst(p, rr.n, h);
+            if (dst) {
+                float* const d0 = dst + lane_off;
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) d0[(16 * m + v) * HS] = S[m][v];
+            }
+        };
+        Row r = A;
+        bool pmode = pmodeA;  // P mode: P accumulates and the outputs get corrected at the end
+        if (pmode) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                S[m] = z4();
+                P[m] = (m == j) ? plus_i(z4(), lane) : z4();
+            }
+        } else {
+            load_state(r);
         }
-        const bool acc_p = U.s > 0 && p.o;  // P S_in enters the outputs and the end state
-        const bool acc_pp = U.s > 0;
         for (int cl = 0; cl < nloc; ++cl) {
+            const int64_t c = U.c0 + cl;
+            if (c >= r.first + r.nch) {
+                // row r ends here: a P-mode first row parks its local end state and P^T for the end phase, any
+                // other row stores its final state; the next row starts from its initial state
+                if (pmode) {
+                    f4* const xd = xs_of((int64_t)gridDim.x + uid);
+                    const s4 Id = ident16(lane);
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) {
+                        xstore(xd + (m * 4 + j) * 64 + lane, S[m]);
+                        const T4 x = split_t(P[m]);
+                        xstore(xd + 16 * 64 + (j * 4 + m) * 64 + lane, mma16(x.l, Id, mma16(x.h, Id, z4())));
+                    }
+                } else {
+                    store_state(r);
+                }
+                r = next_row(p, U, sm.rows, r);
+                pmode = false;
+                load_state(r);
+            }
             const int slot = cl % NREC;
             {
                 bool ok = false;
@@ -774,9 +878,9 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             lds_wait_all();
             if (lane == 0) lds_store(&sm.done[slot][j], cl / NREC + 1);
 
-            const int ci = U.c0 + cl;
-            const int64_t tok0 = U.bos + (int64_t)ci * SC;
-            const int Lc = min(SC, U.L - ci * SC);
+            const int ci = (int)(c - r.first);
+            const int64_t tok0 = r.bos + (int64_t)ci * SC;
+            const int Lc = (int)std::max<int64_t>(0, std::min<int64_t>(SC, r.L - (int64_t)ci * SC));
             // X = W M (token tiles 0, 1; columns 16 j ..) for M = S or P
             auto wmul = [&](const T8 (&mo)[2], f4 (&X)[2]) {
 #pragma unroll
@@ -825,16 +929,16 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             }
             qmul(so, X, y);
             if (p.o) store_y(p, tok0, Lc, h, j, lane, y);
-            if (acc_pp) {
+            if (pmode) {
                 T8 po[2];
                 state_ops(P, po);
                 f4 XP[2];
                 wmul(po, XP);
-                if (acc_p) {
+                if (p.o) {
                     // (Q P)^T rows k' in column tile j, for the correction once S_in is known
                     f4 qp[2] = {z4(), z4()};
                     qmul(po, XP, qp);
-                    uint4* const dst = qp_slot(cl);
+                    uint4* const dst = qp_slot(c);
 #pragma unroll
                     for (int tau = 0; tau < 2; ++tau) {
                         // piece [tau][kb = j >> 1], half j & 1
@@ -846,45 +950,63 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             }
             apply(S, X, true);
         }
+        // the last row, if it ends here in true mode: its final state (P mode and rows continuing in later units are
+        // finished in the end phase)
+        if (!pmode && U.c1 == r.first + r.nch) store_state(r);
     }
     __syncthreads();  // every main loop done: the ring is free
-    // ---------------- end phase: all eight wavefronts.  LDS (ring space): local end state, this unit's P^T, S_in.
+    // ---------------- end phase: all eight wavefronts.  LDS (ring space): the first row's local end state and P^T,
+    // then its S_in.  Row A (first) in P mode needs S_in; row Z (last) continuing past the unit is published.
     f4* const Sx = reinterpret_cast<f4*>(sm.ring[0]);  // S_local, [column tile j][k tile m][lane]
     f4* const Ptx = Sx + 16 * 64;                      // P^T, RL tiles [k' tile][k tile][lane]
     f4* const Sin = Ptx + 16 * 64;                     // S_in, [k tile m][column tile j][lane]
-    const bool last = U.s == U.nseg - 1;
-    // exchange entry of a unit: its local end state [m][j][lane], then (segments after the first) its P^T
-    auto xs_of = [&](int64_t u) { return reinterpret_cast<f4*>(xbuf + u * (int64_t)(2 * HS2)); };
+    const Row Z = row_at(p, U, sm.rows, U.c1 - 1);
+    const bool cont = U.c1 < Z.first + Z.nch;  // row Z goes on in later units
+    const bool one_row = A.n == Z.n;           // (then S and P in registers are row A's)
     if (wv >= 4) {
         const int j = wv - 4;
         const s4 Id = ident16(lane);
+        if (pmodeA) {
+            if (one_row) {
 #pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            Sx[(j * 4 + m) * 64 + lane] = S[m];
-            if (U.s > 0) {
-                const T4 x = split_t(P[m]);
-                Ptx[(j * 4 + m) * 64 + lane] = mma16(x.l, Id, mma16(x.h, Id, z4()));  // RL(P^T) tile (j, m)
+                for (int m = 0; m < 4; ++m) {
+                    Sx[(j * 4 + m) * 64 + lane] = S[m];
+                    const T4 x = split_t(P[m]);
+                    Ptx[(j * 4 + m) * 64 + lane] = mma16(x.l, Id, mma16(x.h, Id, z4()));  // RL(P^T) tile (j, m)
+                }
+            } else {  // parked by this wavefront at the row switch
+                vmem_wait_all();
+                const f4* const st = xs_of((int64_t)gridDim.x + uid);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    Sx[(j * 4 + m) * 64 + lane] = xload(st + (m * 4 + j) * 64 + lane);
+                    Ptx[(j * 4 + m) * 64 + lane] = xload(st + 16 * 64 + (j * 4 + m) * 64 + lane);
+                }
             }
         }
-        if (!last) {  // publish for the later segments of the row
-            f4* const xd = xs_of(U.u);
+        if (cont) {  // publish row Z's entry: its end state here, and P^T when that is P-mode row A
+            f4* const xd = xs_of(uid);
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 xstore(xd + (m * 4 + j) * 64 + lane, S[m]);
-                if (U.s > 0) xstore(xd + 16 * 64 + (j * 4 + m) * 64 + lane, Ptx[(j * 4 + m) * 64 + lane]);
+                if (pmodeA && one_row) xstore(xd + 16 * 64 + (j * 4 + m) * 64 + lane, Ptx[(j * 4 + m) * 64 + lane]);
             }
             vmem_wait_all();
         }
     }
     __syncthreads();
-    // every later segment of the row reads this entry once: the flag counts its readers down to zero
-    if (!last && tid == 0)
-        __hip_atomic_store(flags + U.u, U.nseg - 1 - U.s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every later unit holding row Z reads this entry once: the flag counts its readers down to zero
+    if (cont && tid == 0)
+        __hip_atomic_store(flags + uid, (int)(last_unit(U, Z) - U.k), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 
-    if (U.s > 0) {
-        // S_in = S_end(s - 1) by Horner over the earlier segments: X = S_end(0); X <- P_jj X + S_local(jj), jj = 1 ..
-        if (tid < U.s) {
-            int* const f = flags + (U.u - (int64_t)(U.s - tid) * H);
+    if (pmodeA) {
+        // S_in = row A's state at c0, by Horner over the entries of its earlier units k0 .. k - 1: X = S_end(k0);
+        // X <- P X + S_local of each later one
+        const int64_t k0 = first_unit(U, A);
+        const int ns = (int)(U.k - k0);
+        auto entry = [&](int jj) { return xs_of((k0 + jj) * H + h); };
+        if (tid < ns) {
+            int* const f = flags + (k0 + tid) * H + h;
             bool ok = false;
             for (int it = 0; it < kFlagSpinLimit; ++it) {
                 if (__hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) > 0) {
@@ -898,16 +1020,15 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
         __syncthreads();
         if (wv >= 4) {
             const int j = wv - 4;
-            const int64_t u0 = U.u - (int64_t)U.s * H;
             f4 X[4];
 #pragma unroll
-            for (int m = 0; m < 4; ++m) X[m] = xload(xs_of(u0) + (m * 4 + j) * 64 + lane);
+            for (int m = 0; m < 4; ++m) X[m] = xload(entry(0) + (m * 4 + j) * 64 + lane);
             // entries two at a time, both loaded before either is applied (one memory round trip per pair)
-            for (int jj = 1; jj < U.s; jj += 2) {
+            for (int jj = 1; jj < ns; jj += 2) {
                 f4 es[2][4], ep[2][4][4];
 #pragma unroll
                 for (int x = 0; x < 2; ++x) {
-                    const f4* const e = xs_of(u0 + (int64_t)min(jj + x, U.s - 1) * H);
+                    const f4* const e = entry(min(jj + x, ns - 1));
 #pragma unroll
                     for (int m = 0; m < 4; ++m) {
                         es[x][m] = xload(e + (m * 4 + j) * 64 + lane);
@@ -917,7 +1038,7 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
                 }
 #pragma unroll
                 for (int x = 0; x < 2; ++x) {
-                    if (jj + x >= U.s) break;
+                    if (jj + x >= ns) break;
                     T8 xo[2];
                     state_ops(X, xo);
 #pragma unroll
@@ -932,10 +1053,10 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             }
 #pragma unroll
             for (int m = 0; m < 4; ++m) Sin[(m * 4 + j) * 64 + lane] = X[m];
-            if (last) {  // the row's final state S_end = P_s S_in + S_local(s)
+            if (!(cont && one_row)) {  // row A ends in this unit: its final state S_end = P S_in + S_local
                 T8 xo[2];
                 state_ops(X, xo);
-                float* const dst = state_dst(p, U.n, h);
+                float* const dst = state_dst(p, A.n, h);
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     f4 x = Sx[(j * 4 + m) * 64 + lane];
@@ -950,13 +1071,13 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             }
         }
         __syncthreads();
-        // the earlier segments' entries are read: count this unit out of their flags
-        if (tid < U.s)
-            __hip_atomic_fetch_add(flags + (U.u - (int64_t)(U.s - tid) * H), -1, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-        // correction of this segment's outputs: y_c^T += S_in^T (Q_c P_{c-1})^T.  Wavefront w takes the chunks
-        // cl = w, w + 8, .. whole (all four column tiles: one Q P read per chunk, full 128-byte rows of y), RB chunks
-        // per round with their loads issued together
+        // the earlier units' entries are read: count this unit out of their flags
+        if (tid < ns)
+            __hip_atomic_fetch_add(flags + (k0 + tid) * H + h, -1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        // correction of row A's outputs here (its first nA chunks): y_c^T += S_in^T (Q_c P_{c-1})^T.  Wavefront w
+        // takes the chunks cl = w, w + 8, .. whole (all four column tiles: one Q P read per chunk, full 128-byte rows
+        // of y), RB chunks per round with their loads issued together
+        const int nA = (int)(std::min<int64_t>(U.c1, A.first + A.nch) - U.c0);
         if (p.o) {
             bf8 sh[4][2];  // S_in hi, [column tile j][k block]
 #pragma unroll
@@ -965,18 +1086,20 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
                 for (int kb = 0; kb < 2; ++kb)
                     sh[j][kb] = cat(hi_t(Sin[((2 * kb) * 4 + j) * 64 + lane]), hi_t(Sin[((2 * kb + 1) * 4 + j) * 64 + lane]));
             constexpr int RB = 4;
-            for (int cl0 = wv; cl0 < nloc; cl0 += 8 * RB) {
+            for (int cl0 = wv; cl0 < nA; cl0 += 8 * RB) {
                 uint4 qp[RB][4];
                 uint2 old[RB][4][2];
                 int64_t tok0[RB];
                 int Lc[RB];
 #pragma unroll
                 for (int r = 0; r < RB; ++r) {
-                    const int cl = min(cl0 + 8 * r, nloc - 1);  // a duplicate of the last chunk is not stored
-                    const int ci = U.c0 + cl;
-                    tok0[r] = U.bos + (int64_t)ci * SC;
-                    Lc[r] = (cl0 + 8 * r < nloc) ? min(SC, U.L - ci * SC) : 0;
-                    const uint4* const src = qp_slot(cl);
+                    const int cl = min(cl0 + 8 * r, nA - 1);  // a duplicate of the last chunk is not stored
+                    const int64_t c = U.c0 + cl;
+                    const int ci = (int)(c - A.first);
+                    tok0[r] = A.bos + (int64_t)ci * SC;
+                    Lc[r] = (cl0 + 8 * r < nA) ? (int)std::max<int64_t>(0, std::min<int64_t>(SC, A.L - (int64_t)ci * SC))
+                                               : 0;
+                    const uint4* const src = qp_slot(c);
 #pragma unroll
                     for (int x = 0; x < 4; ++x) qp[r][x] = src[x * 64 + lane];
 #pragma unroll
@@ -1008,18 +1131,6 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
                 }
             }
         }
-    } else if (last && wv >= 4) {
-        // a single-segment row: the local end state is the final state
-        const int j = wv - 4;
-        float* const dst = state_dst(p, U.n, h);
-        if (dst) {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                const f4 x = S[m];
-#pragma unroll
-                for (int v = 0; v < 4; ++v) dst[(16 * m + 4 * q + v) * HS + 16 * j + i] = x[v];
-            }
-        }
     }
     if (tid == 0 && sm.fail && p.status)
         __hip_atomic_fetch_or(p.status, WKV7_STATUS_SEGMENT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1028,35 +1139,33 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
 SegWorkspace seg_workspace(int num_seqs, int H, int64_t total_tokens, int64_t max_len_bound, bool varlen,
                            int rec_max_len, int cus) {
     SegWorkspace ws{};
-    // rows the launch owns: all of them, or those longer than rec_max_len
-    const int64_t long_rows = rec_max_len < 0 ? num_seqs
-                                              : std::min<int64_t>(num_seqs, total_tokens / ((int64_t)rec_max_len + 1));
-    int64_t chunks;
+    int64_t entries, qp_chunks;
     if (!varlen) {
-        chunks = (int64_t)num_seqs * ((max_len_bound + SC - 1) / SC);
-    } else {
-        chunks = std::min<int64_t>((int64_t)num_seqs * ((max_len_bound + SC - 1) / SC),
-                                   (total_tokens + SC - 1) / SC + long_rows);
-    }
-    ws.seg = (int)std::max<int64_t>(kSegMinChunks, (chunks * H + cus - 1) / std::max(1, cus));
-    int64_t units;
-    if (!varlen) {
-        const int64_t nch = (max_len_bound + SC - 1) / SC;
-        units = (int64_t)num_seqs * std::max<int64_t>(1, (nch + ws.seg - 1) / ws.seg);
-    } else {
-        units = (chunks + ws.seg - 1) / ws.seg + long_rows;
-    }
-    ws.units = units * H;
-    // Q P slots: chunks after a row's first segment (for ragged calls, bounded by the chunks of all owned rows)
-    int64_t qp_chunks = chunks;
-    if (!varlen) {
-        const int nch = (int)((max_len_bound + SC - 1) / SC);
-        const int nseg = (int)std::max<int64_t>(1, (nch + ws.seg - 1) / ws.seg);
+        // dense: each row cut into segments, about one unit per CU over the call
+        const int nch = (int)std::max<int64_t>(1, (max_len_bound + SC - 1) / SC);
+        const int64_t chunks = (int64_t)num_seqs * nch;
+        ws.seg = (int)std::max<int64_t>(kSegMinChunks, (chunks * H + cus - 1) / std::max(1, cus));
+        const int nseg = std::max(1, (nch + ws.seg - 1) / ws.seg);
+        ws.units = (int64_t)num_seqs * nseg * H;
+        entries = ws.units;  // a dense unit never crosses a row: nothing to park
         qp_chunks = (int64_t)num_seqs * (nch - seg_start(nch, nseg, 1));
+    } else {
+        // ragged / n_keep: CUs / H units per head share each head's chunk stream; the stream has ceil(L / 32) chunks
+        // per owned row (1 for an empty one), at most ceil(total / 32) + the owned rows
+        const int64_t long_rows = rec_max_len < 0 ? num_seqs
+                                                  : std::min<int64_t>(num_seqs, total_tokens / ((int64_t)rec_max_len + 1));
+        const int64_t chunks = std::min<int64_t>((int64_t)num_seqs * std::max<int64_t>(1, (max_len_bound + SC - 1) / SC),
+                                                 (total_tokens + SC - 1) / SC + long_rows);
+        ws.seg = 0;  // the kernel sizes the shares from the stream's length
+        ws.units = std::max(1, cus / std::max(1, H)) * (int64_t)H;
+        if (chunks > 0x7fffffff) ws.units = INT64_MAX;  // stream offsets are int32 in LDS: refused by the callers
+        entries = 2 * ws.units;  // published, and parked
+        qp_chunks = chunks;
     }
+    if (ws.units == INT64_MAX) return ws;
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     ws.flag_bytes = al(sizeof(int32_t) * (size_t)ws.units);
-    ws.x_bytes = al((size_t)ws.units * 2 * HS2 * sizeof(float));  // local end state + P^T per unit
+    ws.x_bytes = al((size_t)entries * 2 * HS2 * sizeof(float));  // local end state + P^T per entry
     ws.qp_bytes = al((size_t)qp_chunks * H * 4096);
     ws.total_bytes = kSegFlagRegion + ws.x_bytes + ws.qp_bytes;
     return ws;

@@ -1,8 +1,9 @@
 """GPU parity of the segmented chunked prefill (algo ALGO_SEGMENTED, rwkv-infer-next_amd/csrc/wkv7_seg.hip) in the
 cases its design adds to the reference's single varlen launch (rwkv_next/kernels/wkv7.py:89-104, 126-138): rows cut
 into several segments whose end states are handed over between workgroups (with and without an initial state), chunk
-edges, ragged slot-pool calls with fresh rows and n_keep, calls without outputs, repeated calls on one workspace (the
-hand-off flags must come back to zero) and replays of a captured HIP graph.  Tolerances as everywhere: y <= 2e-2 and
+edges, ragged slot-pool calls with fresh rows and n_keep (units that start inside one row, run whole rows and hand
+their last row on), calls without outputs, repeated calls on one workspace (the hand-off flags must come back to zero)
+and replays of a captured HIP graph.  Tolerances as everywhere: y <= 2e-2 and
 final state <= 1e-4 (max-relative) against the fp64 recurrence on the same bf16-rounded inputs."""
 import numpy as np
 import pytest
@@ -148,3 +149,64 @@ def test_graph_replays_match_eager(dev, K):
         assert torch.equal(o_g, o_e) and torch.equal(S_g, S_e), f"replay {rep}"
         K.wkv7(*x, s0, H, 64, algo=SEG)  # eager work on the same stream between replays
         torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("rec_max_len", [-1, 32])
+def test_ragged_units_cross_many_rows(dev, K, rec_max_len):
+    """H = 64 gives four units per head, each an equal share of the head's chunk stream, so a unit starts inside one
+    row (P mode), finishes it, runs several whole rows (final states stored mid-loop) and hands its last row on.
+    Empty and one-token rows sit between long ones.  rec_max_len = 32 sends the rows of at most 32 tokens to the
+    token-serial kernel (two dispatches); -1 runs every row, empty ones included, through the segmented kernel."""
+    from oracle import rel_max, wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H, S_slots = 64, 48
+    rng = np.random.default_rng(17)
+    lens = [int(x) for x in rng.integers(1, 400, size=24)] + [0, 1, 31, 32, 33, 1100, 0, 2, 700, 64]
+    lens = [lens[i] for i in rng.permutation(len(lens))]
+    say("seg ragged cross rows", rec_max_len, len(lens), sum(lens))
+    total = sum(lens)
+    ops = operands(1, total, H, seed=4242)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool0 = synth.state_np((S_slots, H, 64, 64), seed=4243)
+    slots = rng.permutation(S_slots)[:len(lens)].astype(np.int64)
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(ops), pool0, cu_seqlens=cu, state_idx=slots)
+    pool = torch.from_numpy(pool0).to(dev)
+    status = K.new_status(dev)
+    o = K.wkv7_pool_(*to_dev(ops, dev), pool, torch.from_numpy(slots).to(dev), H, 64,
+                     cu_seqlens=torch.from_numpy(cu).to(dev), max_len=max(lens), algo=SEG, rec_max_len=rec_max_len,
+                     status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    eo = rel_max(as_np(o).reshape(o_ref.shape), o_ref)
+    es = rel_max(as_np(pool), pool_ref)
+    say(f"y max-rel {eo:.3e}  state max-rel {es:.3e}")
+    assert eo <= Y_TOL and es <= S_TOL
+    untouched = np.setdiff1d(np.arange(S_slots), slots)
+    assert np.array_equal(as_np(pool)[untouched], pool0[untouched])
+
+
+def test_ragged_equal_rows_on_unit_edges_and_auto(dev, K):
+    """Four 2048-token rows at H = 64: the four units of a head take one row each (no hand-off at all).  The same
+    batch through AUTO (short rows token-serial, long rows segmented) gives the same bits."""
+    from oracle import rel_max, wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H, lens = 64, [2048] * 4
+    say("seg ragged equal rows")
+    total = sum(lens)
+    ops = operands(1, total, H, seed=515)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool0 = synth.state_np((8, H, 64, 64), seed=516)
+    slots = np.array([6, 1, 3, 0], np.int64)
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(ops), pool0, cu_seqlens=cu, state_idx=slots)
+    outs = []
+    for algo in (SEG, 0):
+        pool = torch.from_numpy(pool0).to(dev)
+        o = K.wkv7_pool_(*to_dev(ops, dev), pool, torch.from_numpy(slots).to(dev), H, 64,
+                         cu_seqlens=torch.from_numpy(cu).to(dev), max_len=2048, algo=algo)
+        torch.cuda.synchronize()
+        outs.append((o, pool))
+    eo = rel_max(as_np(outs[0][0]).reshape(o_ref.shape), o_ref)
+    es = rel_max(as_np(outs[0][1]), pool_ref)
+    say(f"y max-rel {eo:.3e}  state max-rel {es:.3e}")
+    assert eo <= Y_TOL and es <= S_TOL
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
