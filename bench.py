@@ -9,12 +9,14 @@ value = algorithmic bytes / time: 33 664 B per (slot, head) per layer (16 KB sta
 768 B operands + 128 B output).
 
 Secondary (same line): the same decode step at configuration 1's H = 40 (pool [128, 40, 64, 64] x 32 layers,
-"decode_cfg1"), chunked prefill B = 1, T = 4096, H = 64 (tok/s and fraction of its roofline), the
-speculative verify with snapshots (config 4), the mixed continuous-batching step in a HIP graph (config 3), the
+"decode_cfg1"), chunked prefill B = 1, T = 4096, H = 64 (tok/s and fraction of its roofline; AUTO runs the
+segmented kernel), the drop-in varlen prefill call on a 4-row 2048-token chunk, the speculative verify with
+snapshots (config 4), the mixed continuous-batching step in a HIP graph (config 3), the
 fused time-mix prologue/epilogue at the prefill shape, the W6A16 weight GEMM at K = 4096, N = 16384, and the CPU
 baseline (the oracle's fp32 loop on the host cores).
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu] [--only decode|prefill|verify|mixed|timemix|int6]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 5] [--skip-cpu]
+                    [--only decode|prefill|varlen|verify|mixed|timemix|int6|tp]
 """
 import argparse
 import json
@@ -33,10 +35,11 @@ BF16_PEAK_TFLOPS = 2516.6
 DECODE_BYTES_PER_PAIR = 16384 + 16384 + 6 * 64 * 2 + 64 * 2       # 33 664
 PREFILL_BYTES_PER_HEAD_TOKEN = 6 * 64 * 2 + 64 * 2                 # 896 (+ 32 KB state per (sequence, head))
 COPY_CALIB_BYTES = 1 << 30
-C = 64
+C = 32
 N = 64
-# Chunked (WY) form at chunk C, per (chunk, head): the state path (Grams alpha/beta, the triangular solve, W, G, A,
-# F, H) and the output path (rho, sigma, Q, E, O_intra).  Together 18 C N + 8 N^2 + 2/3 C^2 per head-token.
+# Chunked form at the segmented kernel's chunk C = 32, per (chunk, head): the state path (Grams alpha/beta, the
+# triangular inverse, W, U0, the state update) and the output path (rho, sigma, R0 and the outputs).  Together
+# 18 C N + 8 N^2 + 2/3 C^2 per head-token.
 PREFILL_STATE_FLOPS_PER_CHUNK = 10 * C * C * N + 6 * C * N * N + (2 * C ** 3) // 3
 PREFILL_OUTPUT_FLOPS_PER_CHUNK = 8 * C * C * N + 2 * C * N * N
 PREFILL_FLOPS_PER_HEAD_TOKEN = (PREFILL_STATE_FLOPS_PER_CHUNK + PREFILL_OUTPUT_FLOPS_PER_CHUNK) / C
@@ -138,8 +141,8 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
     t_mfma = (STATE_PATH_BF16_PASSES * f_state + f_out) / (BF16_PEAK_TFLOPS * 1e12)
     t_roof = max(t_hbm, t_mfma)
     # The baseline's own compute roofline prices the (fp32-accurate) state path at the fp32 MFMA rate and the output
-    # path at the bf16 rate (about 118 us here); reported beside the stricter one above, which prices the state path
-    # as the three bf16 passes these kernels run.
+    # path at the bf16 rate (about 79 us at C = 32; 118 us at the chunked kernels' C = 64); reported beside the
+    # stricter one above, which prices the state path as the three bf16 passes these kernels run.
     t_fp32_state = f_state / (FP32_PEAK_TFLOPS * 1e12) + f_out / (BF16_PEAK_TFLOPS * 1e12)
     t_roof_fp32_state = max(t_hbm, t_fp32_state)
     return {"ms": ms, "ms_eager": ms_eager, "timing": "ms: HIP graph replay per call; ms_eager: eager calls",
@@ -150,6 +153,24 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
                          "frac_fp32_state_path": t_roof_fp32_state / (ms * 1e-3),
                          "algorithmic_bytes": bytes_, "flops_state_path": f_state, "flops_output_path": f_out},
             "recurrence_equiv_TFLOPs": 9 * 64 * 64 * T * H / (ms * 1e-3) / 1e12}
+
+
+def varlen_bench(torch, kernels, synth, dev, steps, warmup):
+    """The drop-in varlen prefill call kernels.wkv7(..., cu_seqlens=cu) (rwkv_next/kernels/wkv7.py:126-138) on one
+    2048-token prefill chunk of the engine (rwkv_next/engine.py:218-228) split over 4 rows, H = 64, from zero states,
+    final states returned.  AUTO runs it as two dispatches (the token-serial kernel for rows of at most 32 tokens,
+    here none, and the segmented kernel).  Timed as HIP graph replays."""
+    H, lens = 64, [700, 512, 600, 236]
+    total = sum(lens)
+    cu = torch.tensor([0, 700, 1212, 1812, 2048], dtype=torch.int32, device=dev)
+    ops = synth.operands_torch((1, total, H, 64), seed=1005, device=dev)
+    x = [ops[n].reshape(1, total, H * 64).contiguous() for n in synth.OPERAND_NAMES]
+    us = graph_us(torch, [lambda: kernels.wkv7(*x, None, H, 64, cu_seqlens=cu)], steps, warmup)
+    nbytes = PREFILL_BYTES_PER_HEAD_TOKEN * total * H + len(lens) * 16384 * H  # no initial states read
+    t_roof_us = nbytes / (HBM_PEAK_GBS * 1e3)
+    return {"us": us, "timing": "HIP graph replay per call", "rows": lens, "tokens": total, "H": H,
+            "tok_s": total / (us * 1e-6), "algorithmic_bytes": nbytes, "t_roof_us": t_roof_us,
+            "frac": t_roof_us / us}
 
 
 def mixed_bench(torch, kernels, synth, dev, steps, warmup):
@@ -445,7 +466,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "verify", "mixed", "timemix", "int6", "tp"], default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "varlen", "verify", "mixed", "timemix", "int6", "tp"],
+                    default=None)
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain device copy of 1 GiB (reference dispatch for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -489,6 +511,9 @@ def main():
         res["prefill"] = prefill_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
         log("configuration 0 on the GPU")
         res["cfg0_gpu"] = cfg0_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
+    if args.only in (None, "varlen"):
+        log("varlen prefill chunk (drop-in wkv7 with cu_seqlens)")
+        res["varlen"] = varlen_bench(torch, kernels, synth, dev, max(5, args.steps // 5), args.warmup)
     if args.only in (None, "verify"):
         log("verify")
         res["verify"] = verify_bench(torch, kernels, synth, dev, args.steps, args.warmup)
@@ -537,6 +562,8 @@ def main():
         out["cfg0_gpu"] = res["cfg0_gpu"]
     if "tp_share_H8" in res:
         out["tp_share_H8"] = res["tp_share_H8"]
+    if "varlen" in res:
+        out["varlen"] = res["varlen"]
     if "verify" in res:
         out["verify"] = res["verify"]
     if "mixed" in res:

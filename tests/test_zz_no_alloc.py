@@ -56,7 +56,8 @@ def run_both(lib, dev, x, H, N, T, total, h0=None, cu=None, algo=0):
             rc = lib.wkv7_run_noalloc(ctypes.byref(a), ctypes.c_void_p(stream))
         else:
             nbytes = _lib.workspace_size(a)
-            ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+            # zeroed: the first WKV7_SEG_FLAG_BYTES are the segmented kernel's hand-off flags
+            ws = torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=dev)
             a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
             rc = lib.wkv7_run(ctypes.byref(a), ctypes.c_void_p(stream))
         assert rc == 0, _lib.strerror(rc)
@@ -67,13 +68,16 @@ def run_both(lib, dev, x, H, N, T, total, h0=None, cu=None, algo=0):
     assert not torch.isnan(o1.float()).any() and not torch.isnan(s1).any()
 
 
-def test_two_chunked_calls_in_a_row_second_smaller(dev, lib):
+@pytest.mark.parametrize("algo,sizes", [(2, ((2, 300, 1), (1, 100, 2))), (4, ((1, 3000, 1), (2, 700, 2)))])
+def test_two_chunked_calls_in_a_row_second_smaller(dev, lib, algo, sizes):
+    """The two-kernel chunked path (algo 2) and the segmented kernel (algo 4: rows cut into several segments that
+    hand their states on through flags in the scratch's first 256 KB, which every call must leave zero)."""
     H = 8
-    for B, T, seed in ((2, 300, 1), (1, 100, 2)):
-        say("noalloc chunked", B, T)
+    for B, T, seed in sizes:
+        say("noalloc chunked", algo, B, T)
         x = to_dev(operands(B, T, H, seed=seed), dev)
         h0 = torch.from_numpy((0.3 * np.random.default_rng(seed).standard_normal((B, H, 64, 64))).astype(np.float32)).to(dev)
-        run_both(lib, dev, x, H, B, T, B * T, h0=h0, algo=2)
+        run_both(lib, dev, x, H, B, T, B * T, h0=h0, algo=algo)
 
 
 def test_ragged_and_decode_calls(dev, lib):
