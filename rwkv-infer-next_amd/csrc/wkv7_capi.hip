@@ -175,9 +175,20 @@ Params to_params(const wkv7_args* a) {
 // caller passes a status pointer (so calls without one keep their single dispatch and pay nothing).  It checks
 // exactly what the kernels skip: an h0 slot outside [0, h0_rows) on a row that reads it (not fresh), an ht slot
 // outside [0, ht_rows), cu_seqlens entries that are not non-decreasing within [0, total_tokens], a negative n_keep;
-// and, when the call runs the chunked or chain kernels, every w against WKV7_CHUNK_W_MAX (16 bytes per thread).
+// and, when the call runs the chunked, segmented or chain kernels, w against WKV7_CHUNK_W_MAX (16 bytes per thread)
+// on the tokens those kernels run: rows longer than chunk_thr (every row when chunk_thr < 0), within n_keep.
+__device__ __forceinline__ int row_of_token(const wkv7::Params& p, int64_t t) {
+    if (!p.cu) return (int)(t / (p.T > 0 ? p.T : 1));
+    int lo = 0, hi = p.num_seqs - 1;  // the last row n with cu[n] <= t
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (p.cu[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return lo;
+}
+
 __global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, int32_t* __restrict__ status,
-                                                          bool check_w) {
+                                                          bool check_w, int chunk_thr) {
     int bits = 0;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x, nthr = (int64_t)gridDim.x * blockDim.x;
     for (int64_t n = tid; n < p.num_seqs; n += nthr) {
@@ -197,8 +208,16 @@ __global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, 
     }
     if (check_w) {
         const int64_t per_tok = (int64_t)p.H * (wkv7::HS / 8);  // 16-byte pieces of one token's w
+        const bool all_rows = chunk_thr < 0 && !p.n_keep;
         for (int64_t i = tid; i < p.total_tokens * per_tok; i += nthr) {
             const int64_t t = i / per_tok, j = (i - t * per_tok) * 8;
+            if (!all_rows) {  // only tokens a chunked kernel runs
+                const int n = row_of_token(p, t);
+                int64_t bos;
+                int L;
+                wkv7::seq_extent(p, n, bos, L);
+                if (L <= chunk_thr || t - bos >= L) continue;
+            }
             const uint4 x = *reinterpret_cast<const uint4*>(p.w + t * p.in_tok_stride + j);
             const uint32_t wd[4] = {x.x, x.y, x.z, x.w};
 #pragma unroll
@@ -309,11 +328,14 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     Params p = to_params(args);
     if (args->status) {
         const bool check_w = pl.run_chunked || pl.run_chain || pl.run_seg;
+        // the rows the chunked kernels run: those longer than the token-serial threshold of a split plan
+        const int chunk_thr = pl.run_chain ? pl.rec_len_rec : (pl.run_recurrent ? pl.rec_len_chunk : -1);
         const int64_t work = std::max<int64_t>(args->num_seqs, check_w ? args->total_tokens * args->H * 8 : 0);
         int blocks = (int)std::min<int64_t>((work + 255) / 256, 1024);
         // the slot-clash comparison (up to 1024 x 1024 slot pairs) is spread over at least 16 workgroups
         if (args->ht && args->num_seqs >= 2 && args->num_seqs <= WKV7_STATUS_CLASH_MAX_SEQS) blocks = std::max(blocks, 16);
-        hipLaunchKernelGGL(wkv7_status_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, args->status, check_w);
+        hipLaunchKernelGGL(wkv7_status_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p, args->status, check_w,
+                           chunk_thr);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);
     }

@@ -330,3 +330,39 @@ def test_status_word_reports_w_outside_the_chunked_range(dev, K):
     npo[1] = as_np(w_hi).reshape(npo[1].shape).astype(npo[1].dtype)
     o_ref, S_ref, _ = wkv7_ref(*npo, pool0[[3, 0]])
     check(o, o_ref, as_np(pool)[[3, 0]], S_ref)
+
+
+def test_status_w_check_covers_only_chunked_rows(dev, K):
+    """In a ragged AUTO call, rows of at most 32 tokens run token-serial (any w); only the longer rows, within
+    n_keep, are checked against WKV7_CHUNK_W_MAX.  w = 1.25 in a short row, or past a long row's n_keep, leaves the
+    word zero and every result exact; the same w inside a long row sets WKV7_STATUS_DECAY."""
+    from oracle import wkv7_ref
+    import rwkv_next_amd.synth as synth
+    from rwkv_next_amd import _lib
+    lens = [40, 7, 100, 1]
+    n_keep = np.array([40, 7, 60, 1], np.int64)
+    say("status word, w check on chunked rows only", lens)
+    total = sum(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    ops = operands(1, total, H8, seed=75)
+    pool0 = synth.state_np((6, H8, 64, 64), seed=76)
+    slots = np.array([4, 1, 5, 0], np.int64)
+    x = to_dev(ops, dev)
+    args = dict(cu_seqlens=torch.from_numpy(cu).to(dev), n_keep=torch.from_numpy(n_keep).to(dev), max_len=100)
+    for tok, expect in ((40 + 3, 0), (47 + 80, 0), (47 + 10, _lib.WKV7_STATUS_DECAY)):
+        w_hi = x[1].clone()
+        w_hi[0, tok, 5] = 1.25  # head 5 of: row 1 (7 tokens), past row 2's n_keep, inside row 2's kept tokens
+        xs = [x[0], w_hi] + list(x[2:])
+        status = K.new_status(dev)
+        pool = torch.from_numpy(pool0).to(dev)
+        o = K.wkv7_pool_(*xs, pool, torch.from_numpy(slots).to(dev), H8, 64, status=status, **args)
+        torch.cuda.synchronize()
+        assert int(status.item()) == expect, (tok, int(status.item()))
+        if expect == 0:
+            npo = np_list(ops)
+            npo[1] = as_np(w_hi).reshape(npo[1].shape).astype(npo[1].dtype)
+            o_ref, pool_ref, _ = wkv7_ref(*npo, pool0, cu_seqlens=cu, state_idx=slots, n_keep=n_keep)
+            keep = np.zeros(total, bool)
+            for i in range(len(lens)):
+                keep[cu[i]:cu[i] + min(lens[i], n_keep[i])] = True
+            check(as_np(o).reshape(o_ref.shape)[:, keep], o_ref[:, keep], as_np(pool), pool_ref)

@@ -107,3 +107,45 @@ def test_too_large_is_refused_before_launch(dev, lib):
     assert rc == _lib.WKV7_ERR_SCRATCH_LIMIT
     torch.cuda.synchronize()
     assert bool((o == 7.0).all())
+
+
+def test_noalloc_call_captured_in_a_graph(dev, lib):
+    """For code under HIP graph capture: after one eager wkv7_run_noalloc call on the device (which looks up the
+    scratch array's device address), a captured call replays bit-equal to the eager wkv7_run result, three times with
+    eager work between the replays.  The segmented kernel, so the replays also use the scratch's hand-off flags."""
+    from rwkv_next_amd import _lib
+    H, B, T = 8, 1, 1500
+    say("noalloc under graph capture", B, T)
+    x = to_dev(operands(B, T, H, seed=9), dev)
+    h0 = torch.from_numpy((0.3 * np.random.default_rng(10).standard_normal((B, H, 64, 64))).astype(np.float32)).to(dev)
+    # eager reference through wkv7_run with a zeroed workspace
+    o_ref = torch.full_like(x[3], float("nan"))
+    s_ref = torch.full((B, H, 64, 64), float("nan"), device=dev)
+    a = make_args(x, H, B, T, B * T, o_ref, h0, s_ref, None, 4)
+    nbytes = _lib.workspace_size(a)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+    a.workspace, a.workspace_bytes = ws.data_ptr(), nbytes
+    assert lib.wkv7_run(ctypes.byref(a), ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)) == 0
+    torch.cuda.synchronize()
+    o = torch.full_like(x[3], float("nan"))
+    ht = torch.full((B, H, 64, 64), float("nan"), device=dev)
+    g_args = make_args(x, H, B, T, B * T, o, h0, ht, None, 4)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # the eager call before capture
+        assert lib.wkv7_run_noalloc(ctypes.byref(g_args), ctypes.c_void_p(side.cuda_stream)) == 0
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = lib.wkv7_run_noalloc(ctypes.byref(g_args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    assert rc == 0
+    for rep in range(3):
+        o.fill_(float("nan"))
+        ht.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(o, o_ref) and torch.equal(ht, s_ref), f"replay {rep}"
+        # eager work on the device between replays (another noalloc call on the same scratch)
+        assert lib.wkv7_run_noalloc(ctypes.byref(g_args), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)) == 0
+        torch.cuda.synchronize()
