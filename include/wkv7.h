@@ -50,8 +50,9 @@ extern "C" {
 #define WKV7_STATUS_HT_SLOT 2   /* an ht index outside [0, ht_rows): that final state was not stored */
 #define WKV7_STATUS_SEQLENS 4   /* cu_seqlens entries not non-decreasing within [0, total_tokens]: extents clamped */
 #define WKV7_STATUS_NKEEP 8     /* a negative n_keep entry: treated as 0 */
-#define WKV7_STATUS_DECAY 16    /* the call runs the chunked or chain kernels and some w exceeds WKV7_CHUNK_W_MAX:
-                                 * the chunked rows' results are not finite; run such calls with WKV7_ALGO_RECURRENT */
+#define WKV7_STATUS_DECAY 16    /* some w of a token that the chunked, segmented or chain kernels run (rows longer
+                                 * than the token-serial threshold, within n_keep) exceeds WKV7_CHUNK_W_MAX: those
+                                 * rows' results are not finite; run such calls with WKV7_ALGO_RECURRENT */
 #define WKV7_STATUS_SLOT_CLASH 32  /* (calls of at most WKV7_STATUS_CLASH_MAX_SEQS sequences) two sequences store their
                                     * final states to the same ht slot, or, with h0 and ht one pool, a sequence stores
                                     * to a slot another sequence reads its initial state from: the result depends on
