@@ -43,6 +43,7 @@ struct Plan {
     bool run_chunked = false;
     bool run_chain = false;
     bool run_seg = false;
+    bool seg_short = false;  // the segmented launch also runs the short rows (no token-serial launch)
     int rec_len_rec = -1;    // Params.rec_max_len of the token-serial launch (-1: all rows)
     int rec_len_chunk = -1;  // Params.rec_max_len of the chunked launch (-1: all rows)
     wkv7::ChunkWorkspace ws{};
@@ -98,9 +99,9 @@ Plan make_plan(const wkv7_args* a) {
         pl.run_recurrent = true;
     } else if (a->algo == WKV7_ALGO_SEGMENTED) {
         pl.run_seg = true;
-        if (a->rec_max_len >= 0) {  // rows of at most rec_max_len tokens go to the token-serial kernel
-            pl.run_recurrent = true;
-            pl.rec_len_rec = pl.rec_len_chunk = a->rec_max_len;
+        if (a->rec_max_len >= 0) {  // rows of at most rec_max_len tokens run token-serial in the same launch
+            pl.seg_short = true;
+            pl.rec_len_chunk = a->rec_max_len;
         }
     } else if (a->algo == WKV7_ALGO_CHAIN) {
         pl.run_chain = true;
@@ -117,12 +118,15 @@ Plan make_plan(const wkv7_args* a) {
         if (chunk_heads >= (int64_t)kSegMinChunkHeadsPerCu * wkv7::device_cu_count()) pl.run_seg = true;
         else pl.run_chunked = true;
     } else {
-        // row lengths are only known on the device: rows of at most thr tokens token-serial, the others segmented
-        // (chunked when the segmented kernel's LDS row table cannot hold the call)
-        pl.run_recurrent = true;
+        // row lengths are only known on the device: rows of at most thr tokens token-serial, the others segmented,
+        // both in the segmented launch (chunked beside a token-serial launch when the segmented kernel's LDS row
+        // table cannot hold the call)
         pl.rec_len_rec = pl.rec_len_chunk = thr;
-        if (a->num_seqs <= wkv7::kSegMaxRows) pl.run_seg = true;
-        else pl.run_chunked = true;
+        if (a->num_seqs <= wkv7::kSegMaxRows) {
+            pl.run_seg = pl.seg_short = true;
+        } else {
+            pl.run_recurrent = pl.run_chunked = true;
+        }
     }
     if (pl.run_seg) {
         pl.sws = wkv7::seg_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen || a->n_keep != nullptr,
@@ -131,6 +135,8 @@ Plan make_plan(const wkv7_args* a) {
         if (a->algo == WKV7_ALGO_AUTO && pl.sws.units > (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t))) {
             pl.run_seg = false;
             pl.run_chunked = true;
+            if (pl.seg_short) pl.run_recurrent = true;
+            pl.seg_short = false;
         }
     }
     if (pl.run_chunked)
@@ -329,7 +335,7 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     if (args->status) {
         const bool check_w = pl.run_chunked || pl.run_chain || pl.run_seg;
         // the rows the chunked kernels run: those longer than the token-serial threshold of a split plan
-        const int chunk_thr = pl.run_chain ? pl.rec_len_rec : (pl.run_recurrent ? pl.rec_len_chunk : -1);
+        const int chunk_thr = pl.run_chain ? pl.rec_len_rec : pl.rec_len_chunk;
         const int64_t work = std::max<int64_t>(args->num_seqs, check_w ? args->total_tokens * args->H * 8 : 0);
         int blocks = (int)std::min<int64_t>((work + 255) / 256, 1024);
         // the slot-clash comparison (up to 1024 x 1024 slot pairs) is spread over at least 16 workgroups
@@ -356,7 +362,7 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     }
     if (pl.run_seg) {
         p.rec_max_len = pl.rec_len_chunk;
-        const hipError_t e = wkv7::launch_seg(p, pl.sws, args->workspace, s);
+        const hipError_t e = wkv7::launch_seg(p, pl.sws, args->workspace, pl.seg_short, s);
         if (e != hipSuccess) return static_cast<int>(e);
     }
     return WKV7_OK;

@@ -74,6 +74,8 @@ struct SegWorkspace {
 };
 SegWorkspace seg_workspace(int num_seqs, int H, int64_t total_tokens, int64_t max_len_bound, bool varlen,
                            int rec_max_len, int cus);
-hipError_t launch_seg(const Params& p, const SegWorkspace& ws, void* workspace, hipStream_t stream);
+// short_rows: the launch also runs the rows of at most p.rec_max_len tokens (token-serial, after each workgroup's
+// own chunks), so a ragged call needs no second dispatch.
+hipError_t launch_seg(const Params& p, const SegWorkspace& ws, void* workspace, bool short_rows, hipStream_t stream);
 
 }  // namespace wkv7

@@ -48,6 +48,7 @@
 #include "wkv7.h"
 #include "wkv7_device.h"
 #include "wkv7_launch.h"
+#include "wkv7_token.h"
 
 namespace wkv7 {
 
@@ -728,17 +729,11 @@ __device__ __forceinline__ void store_y(const Params& p, int64_t tok0, int Lc, i
 
 }  // namespace
 
-// xbuf: 32 KB exchange entries (a local end state, then its P^T, RL tiles): entry b for workgroup b's published row,
-// and for ragged calls entry gridDim.x + b, where workgroup b parks its first row's local end state and P when that
-// row ends inside it.  flags: one per workgroup, set to the number of later units that read its entry and counted
-// down by them.  seg: dense calls' chunks per segment.
-__global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, int32_t* __restrict__ flags,
-                                                       float* __restrict__ xbuf, char* __restrict__ qpbuf) {
-    __shared__ SegSmem sm;
+// One unit: its chunks' main loop (prep and state wavefronts) and the end phase (hand-off, correction).
+__device__ __forceinline__ void run_unit(const Params& p, const Unit& U, int32_t* __restrict__ flags,
+                                         float* __restrict__ xbuf, char* __restrict__ qpbuf, SegSmem& sm) {
     const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int i = lane & 15, q = lane >> 4;
-    const Unit U = find_unit(p, seg, (int64_t)blockIdx.x, sm.rows, sm.scan);
-    if (!U.ok) return;
     const int H = p.H, h = U.h;
     const int64_t uid = blockIdx.x;
     if (tid < NREC) sm.ready[tid] = 0;
@@ -1132,6 +1127,64 @@ __global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, 
             }
         }
     }
+}
+
+// Short rows (p.rec_max_len >= 0: rows of at most that many tokens, which no unit owns), token-serial with the
+// recurrent kernel's per-pair code (wkv7_token.h), after the workgroup's own unit: every workgroup builds the list of
+// short rows in the freed ring, and its wavefronts take the (row, head) pairs blockIdx * 8 + wave, + 8 * gridDim, ..
+__device__ __forceinline__ void run_short_rows(const Params& p, SegSmem& sm) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    __syncthreads();  // the ring is free
+    int* const list = reinterpret_cast<int*>(sm.ring[0]);                          // <= kSegMaxRows rows
+    float* const slab = reinterpret_cast<float*>(sm.ring[1]) + wv * 5 * HS;       // per wavefront: d, a, b, k, r
+    const int N = p.num_seqs;
+    const int per = (N + 511) / 512;
+    const int r0 = min(N, tid * per), r1 = min(N, r0 + per);
+    int cnt = 0;
+    for (int n = r0; n < r1; ++n) {
+        int64_t bos;
+        int L;
+        seq_extent(p, n, bos, L);
+        cnt += owns(p, L) ? 0 : 1;
+    }
+    int total;
+    int off = block_excl_scan(cnt, sm.scan, &total);
+    for (int n = r0; n < r1; ++n) {
+        int64_t bos;
+        int L;
+        seq_extent(p, n, bos, L);
+        if (!owns(p, L)) list[off++] = n;
+    }
+    __syncthreads();
+    const int g = lane >> 3, c = lane & 7;
+    const int64_t npairs = (int64_t)total * p.H, nwaves = (int64_t)gridDim.x * 8;
+    f4 S[16];
+    for (int64_t pa = (int64_t)blockIdx.x * 8 + wv; pa < npairs; pa += nwaves) {
+        const int64_t k = pa / p.H;
+        Pair pr;
+        pr.n = list[k];
+        pr.h = (int)(pa - k * p.H);
+        seq_extent(p, pr.n, pr.bos, pr.L);
+        pr.run = true;
+        TokenIn x{};
+        prefetch_pair(p, pr, lane, g, c, S, x);
+        run_pair(p, pr, lane, g, c, S, x, slab);
+    }
+}
+
+// xbuf: 32 KB exchange entries (a local end state, then its P^T, RL tiles): entry b for workgroup b's published row,
+// and for ragged calls entry gridDim.x + b, where workgroup b parks its first row's local end state and P when that
+// row ends inside it.  flags: one per workgroup, set to the number of later units that read its entry and counted
+// down by them.  seg: dense calls' chunks per segment.
+__global__ __launch_bounds__(512) void wkv7_seg_kernel(const Params p, int seg, int32_t* __restrict__ flags,
+                                                       float* __restrict__ xbuf, char* __restrict__ qpbuf,
+                                                       bool short_rows) {
+    __shared__ SegSmem sm;
+    const int tid = threadIdx.x;
+    if (tid == 0) sm.fail = 0;
+    const Unit U = find_unit(p, seg, (int64_t)blockIdx.x, sm.rows, sm.scan);
+    if (U.ok) run_unit(p, U, flags, xbuf, qpbuf, sm);
+    if (short_rows) run_short_rows(p, sm);
     if (tid == 0 && sm.fail && p.status)
         __hip_atomic_fetch_or(p.status, WKV7_STATUS_SEGMENT_WAIT, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1171,13 +1224,14 @@ SegWorkspace seg_workspace(int num_seqs, int H, int64_t total_tokens, int64_t ma
     return ws;
 }
 
-hipError_t launch_seg(const Params& p, const SegWorkspace& ws, void* workspace, hipStream_t stream) {
+hipError_t launch_seg(const Params& p, const SegWorkspace& ws, void* workspace, bool short_rows, hipStream_t stream) {
     if (p.num_seqs == 0 || ws.units == 0) return hipSuccess;
     char* base = static_cast<char*>(workspace);
     int32_t* flags = reinterpret_cast<int32_t*>(base);
     float* xbuf = reinterpret_cast<float*>(base + kSegFlagRegion);
     char* qp = base + kSegFlagRegion + ws.x_bytes;
-    hipLaunchKernelGGL(wkv7_seg_kernel, dim3((unsigned)ws.units), dim3(512), 0, stream, p, ws.seg, flags, xbuf, qp);
+    hipLaunchKernelGGL(wkv7_seg_kernel, dim3((unsigned)ws.units), dim3(512), 0, stream, p, ws.seg, flags, xbuf, qp,
+                       short_rows);
     return hipGetLastError();
 }
 
