@@ -34,19 +34,31 @@ def stream_workspace(cache: dict, device, nbytes: int, zero_bytes: int):
     """The workspace of the current stream on `device` from `cache`, at least `nbytes` long, whose first `zero_bytes`
     are zero in stream order when the call that requested it runs.
 
-    A workspace created eagerly is zero-filled there.  One created during a HIP graph capture is zero-filled by a
-    node of that graph only, so until an eager call has zeroed it in stream order, every further capture that uses
-    it starts with a fill of its zero region (a graph may be replayed before the one that created the buffer).
-    A larger request replaces the buffer; the old one is kept alive, since a captured graph may still address it."""
+    Only that leading region is ever cleared.  A workspace created eagerly is cleared there.  A capture on a stream
+    without a workspace first takes over a large-enough one that another stream of the device has cleared eagerly
+    (torch synchronises the device before a capture begins, so the clear is complete; that stream gets a new one at
+    its next call), so a graph captured after an eager warm-up records no clearing.  Otherwise the new workspace is
+    cleared by a node of that graph, and until an eager call has cleared it in stream order, every further capture
+    that uses it starts with a clear of its leading region (a graph may be replayed before the one that created the
+    buffer).  A larger request replaces the buffer; the old one is kept alive, since a captured graph may still
+    address it."""
     idx = device.index if device.index is not None else torch.cuda.current_device()
     stream = torch.cuda.current_stream(idx).cuda_stream
     capturing = torch.cuda.is_current_stream_capturing()
     key = (idx, stream)
     entry = cache.get(key)
+    if entry is None and capturing:
+        for other, e in list(cache.items()):
+            if other[0] == idx and e[1] and e[0].numel() >= nbytes:
+                entry = cache.pop(other)
+                entry[2] = capture_id(stream)
+                cache[key] = entry
+                break
     if entry is None or entry[0].numel() < nbytes:
         if entry is not None:
             _RETIRED.append(entry[0])
-        ws = torch.zeros(max(nbytes, 2 * zero_bytes), dtype=torch.uint8, device=torch.device("cuda", idx))
+        ws = torch.empty(max(nbytes, 2 * zero_bytes), dtype=torch.uint8, device=torch.device("cuda", idx))
+        ws[:zero_bytes].zero_()
         entry = [ws, not capturing, capture_id(stream) if capturing else None]
         cache[key] = entry
     if not entry[1]:
