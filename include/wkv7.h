@@ -68,15 +68,15 @@ extern "C" {
 #define WKV7_CHUNK_W_MAX 1.0f
 
 /* Algorithm selection (wkv7_args.algo). */
-#define WKV7_ALGO_AUTO 0       /* token-serial kernel for rows of at most rec_max_len tokens; longer dense rows the
-                                * segmented kernel (the chunked one for calls of fewer than 8 x CUs 32-token
-                                * chunk-heads); a ragged call runs its short rows token-serial and its long rows
-                                * segmented (two dispatches; chunked beyond kSegMaxRows = 4096 rows) */
+#define WKV7_ALGO_AUTO 0       /* dense rows of at most rec_max_len tokens token-serial, longer ones on the segmented
+                                * kernel (the chunked one for calls of fewer than 8 x CUs 32-token chunk-heads); a
+                                * ragged call in one segmented dispatch, its short rows token-serial in the
+                                * kernel's tail (beyond 4096 rows: token-serial + two-kernel chunked) */
 #define WKV7_ALGO_RECURRENT 1  /* token-serial kernel for every row */
 #define WKV7_ALGO_CHUNKED 2    /* chunked MFMA prefill for every row */
 #define WKV7_ALGO_SEGMENTED 4  /* the segmented chunked kernel (32-token chunks, rows cut into segments, one
                                 * dispatch; needs a workspace): every row, or with rec_max_len >= 0 the rows longer
-                                * than it, the others token-serial (two dispatches) */
+                                * than it, the others token-serially in the same launch */
 #define WKV7_ALGO_CHAIN 3      /* one dispatch: rows of at most rec_max_len tokens token-serial, longer rows chunked with
                                 * each (row, head) chain walked by one workgroup (no workspace; num_seqs <= 512) */
 
