@@ -90,6 +90,12 @@ int validate(const wkv7_args* a) {
     return WKV7_OK;
 }
 
+// The segmented launch holds one hand-off flag per unit in the workspace's flag region and addresses output rows with
+// 32-bit offsets.
+bool seg_fits(const Plan& pl, const wkv7_args* a) {
+    return pl.sws.units <= (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t)) && a->o_tok_stride <= wkv7::kSegMaxTokStride;
+}
+
 Plan make_plan(const wkv7_args* a) {
     Plan pl;
     const bool varlen = a->cu_seqlens != nullptr;
@@ -131,8 +137,8 @@ Plan make_plan(const wkv7_args* a) {
     if (pl.run_seg) {
         pl.sws = wkv7::seg_workspace(a->num_seqs, a->H, a->total_tokens, bound, varlen || a->n_keep != nullptr,
                                      pl.rec_len_chunk, wkv7::device_cu_count());
-        // AUTO falls back to the chunked path when the segmented grid would not fit its hand-off flag region
-        if (a->algo == WKV7_ALGO_AUTO && pl.sws.units > (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t))) {
+        // AUTO falls back to the chunked path when the segmented launch cannot take the call
+        if (a->algo == WKV7_ALGO_AUTO && !seg_fits(pl, a)) {
             pl.run_seg = false;
             pl.run_chunked = true;
             if (pl.seg_short) pl.run_recurrent = true;
@@ -313,7 +319,7 @@ int wkv7_workspace_size(const wkv7_args* args, size_t* bytes) {
     const int rc = validate(args);
     if (rc != WKV7_OK) return rc;
     const Plan pl = make_plan(args);
-    if (pl.run_seg && pl.sws.units > (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t))) return WKV7_ERR_SHAPE;
+    if (pl.run_seg && !seg_fits(pl, args)) return WKV7_ERR_SHAPE;
     *bytes = workspace_bytes(pl);
     return WKV7_OK;
 }
@@ -323,7 +329,7 @@ int wkv7_run(const wkv7_args* args, void* stream) {
     const int rc = validate(args);
     if (rc != WKV7_OK) return rc;
     const Plan pl = make_plan(args);
-    if (pl.run_seg && pl.sws.units > (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t))) return WKV7_ERR_SHAPE;
+    if (pl.run_seg && !seg_fits(pl, args)) return WKV7_ERR_SHAPE;
     const size_t need = workspace_bytes(pl);
     if (need > 0) {
         if (!args->workspace || args->workspace_bytes < need) return WKV7_ERR_WORKSPACE;

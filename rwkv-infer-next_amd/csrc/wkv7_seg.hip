@@ -56,6 +56,7 @@ namespace {
 
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef short s4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
 
 constexpr int SC = kSegChunk;          // 32 tokens per chunk
 constexpr int NREC = 3;                // LDS ring slots
@@ -713,17 +714,27 @@ __device__ __forceinline__ void state_ops(const f4 (&S)[4], T8 (&o)[2]) {
     for (int kb = 0; kb < 2; ++kb) o[kb] = cat(split_t(S[2 * kb]), split_t(S[2 * kb + 1]));
 }
 
+// y^T tiles (column tile j, token tiles 0, 1) of a chunk's first Lc tokens as bf16, through a raw buffer that covers
+// exactly those tokens' rows (head h, columns 16 j ..): the stores of rows t >= Lc fall outside it and are dropped,
+// and so are all of them without an output (an empty range), so no branch splits the caller's code.  Offsets are
+// 32-bit: the launch requires o_tok_stride <= kSegMaxTokStride.
 __device__ __forceinline__ void store_y(const Params& p, int64_t tok0, int Lc, int h, int j, int lane, const f4 (&y)[2]) {
     const int i = lane & 15, q = lane >> 4;
+    const int stride2 = (int)p.o_tok_stride * 2;
+    const uint64_t base = p.o ? (uint64_t)(p.o + tok0 * p.o_tok_stride + (int64_t)h * HS + 16 * j) : 0;
+    const int bytes = (p.o && Lc > 0) ? (Lc - 1) * stride2 + 32 : 0;
+    // readfirstlane returns int: each half goes through uint32_t, so that the low one is not sign-extended
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+    const __amdgpu_buffer_rsrc_t rs =
+        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
+                                          __builtin_amdgcn_readfirstlane(bytes), 0x00020000 /* raw 32-bit buffer */);
 #pragma unroll
     for (int tau = 0; tau < 2; ++tau) {
-        const int t = 16 * tau + i;
-        if (t < Lc) {
-            uint2 pk;
-            pk.x = pack_bf16x2(y[tau][0], y[tau][1]);
-            pk.y = pack_bf16x2(y[tau][2], y[tau][3]);
-            *reinterpret_cast<uint2*>(p.o + (tok0 + t) * p.o_tok_stride + (int64_t)h * HS + 16 * j + 4 * q) = pk;
-        }
+        uint2 pk;
+        pk.x = pack_bf16x2(y[tau][0], y[tau][1]);
+        pk.y = pack_bf16x2(y[tau][2], y[tau][3]);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u2v, pk), rs, (16 * tau + i) * stride2 + 8 * q, 0, 0);
     }
 }
 
@@ -799,37 +810,12 @@ __device__ __forceinline__ void run_unit(const Params& p, const Unit& U, int32_t
             }
         };
         Row r = A;
-        bool pmode = pmodeA;  // P mode: P accumulates and the outputs get corrected at the end
-        if (pmode) {
-#pragma unroll
-            for (int m = 0; m < 4; ++m) {
-                S[m] = z4();
-                P[m] = (m == j) ? plus_i(z4(), lane) : z4();
-            }
-        } else {
-            load_state(r);
-        }
-        for (int cl = 0; cl < nloc; ++cl) {
+        // chunk cl of row r.  PM: P mode (S starts at zero, P = A_c .. A_1 accumulates, (Q P)^T goes out for the
+        // output correction).  After the record wait the step is one basic block (the output stores are masked by
+        // their buffer range, not by branches), so the S and P chains of a P-mode chunk schedule together.
+        auto chunk = [&](auto pm, const int cl) {
+            constexpr bool PM = decltype(pm)::value;
             const int64_t c = U.c0 + cl;
-            if (c >= r.first + r.nch) {
-                // row r ends here: a P-mode first row parks its local end state and P^T for the end phase, any
-                // other row stores its final state; the next row starts from its initial state
-                if (pmode) {
-                    f4* const xd = xs_of((int64_t)gridDim.x + uid);
-                    const s4 Id = ident16(lane);
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        xstore(xd + (m * 4 + j) * 64 + lane, S[m]);
-                        const T4 x = split_t(P[m]);
-                        xstore(xd + 16 * 64 + (j * 4 + m) * 64 + lane, mma16(x.l, Id, mma16(x.h, Id, z4())));
-                    }
-                } else {
-                    store_state(r);
-                }
-                r = next_row(p, U, sm.rows, r);
-                pmode = false;
-                load_state(r);
-            }
             const int slot = cl % NREC;
             {
                 bool ok = false;
@@ -923,31 +909,62 @@ __device__ __forceinline__ void run_unit(const Params& p, const Unit& U, int32_t
                 y[1] = mma32(vp, as_bf8(sig[1]), y[1]);
             }
             qmul(so, X, y);
-            if (p.o) store_y(p, tok0, Lc, h, j, lane, y);
-            if (pmode) {
+            store_y(p, tok0, Lc, h, j, lane, y);
+            if constexpr (PM) {
                 T8 po[2];
                 state_ops(P, po);
                 f4 XP[2];
                 wmul(po, XP);
-                if (p.o) {
-                    // (Q P)^T rows k' in column tile j, for the correction once S_in is known
-                    f4 qp[2] = {z4(), z4()};
-                    qmul(po, XP, qp);
-                    uint4* const dst = qp_slot(c);
+                // (Q P)^T rows k' in column tile j, for the correction once S_in is known
+                f4 qp[2] = {z4(), z4()};
+                qmul(po, XP, qp);
+                uint4* const dst = qp_slot(c);
 #pragma unroll
-                    for (int tau = 0; tau < 2; ++tau) {
-                        // piece [tau][kb = j >> 1], half j & 1
-                        uint2* d2 = reinterpret_cast<uint2*>(dst + (tau * 2 + (j >> 1)) * 64 + lane) + (j & 1);
-                        *d2 = __builtin_bit_cast(uint2, hi_t(qp[tau]));
-                    }
+                for (int tau = 0; tau < 2; ++tau) {
+                    // piece [tau][kb = j >> 1], half j & 1
+                    uint2* d2 = reinterpret_cast<uint2*>(dst + (tau * 2 + (j >> 1)) * 64 + lane) + (j & 1);
+                    *d2 = __builtin_bit_cast(uint2, hi_t(qp[tau]));
                 }
                 apply(P, XP, false);
             }
             apply(S, X, true);
+        };
+        int cl = 0;
+        if (pmodeA) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                S[m] = z4();
+                P[m] = (m == j) ? plus_i(z4(), lane) : z4();
+            }
+            const int nA = (int)(std::min<int64_t>(U.c1, A.first + A.nch) - U.c0);
+            for (; cl < nA; ++cl) chunk(std::true_type{}, cl);
+            if (nA < nloc) {
+                // row A ends here: park its local end state and P^T for the end phase
+                f4* const xd = xs_of((int64_t)gridDim.x + uid);
+                const s4 Id = ident16(lane);
+#pragma unroll
+                for (int m = 0; m < 4; ++m) {
+                    xstore(xd + (m * 4 + j) * 64 + lane, S[m]);
+                    const T4 x = split_t(P[m]);
+                    xstore(xd + 16 * 64 + (j * 4 + m) * 64 + lane, mma16(x.l, Id, mma16(x.h, Id, z4())));
+                }
+                r = next_row(p, U, sm.rows, r);
+                load_state(r);
+            }
+        } else {
+            load_state(r);
+        }
+        for (; cl < nloc; ++cl) {
+            if (U.c0 + cl >= r.first + r.nch) {  // row r ends here: its final state; the next starts from its initial
+                store_state(r);
+                r = next_row(p, U, sm.rows, r);
+                load_state(r);
+            }
+            chunk(std::false_type{}, cl);
         }
         // the last row, if it ends here in true mode: its final state (P mode and rows continuing in later units are
         // finished in the end phase)
-        if (!pmode && U.c1 == r.first + r.nch) store_state(r);
+        if (U.c1 == r.first + r.nch && !(pmodeA && r.n == A.n)) store_state(r);
     }
     __syncthreads();  // every main loop done: the ring is free
     // ---------------- end phase: all eight wavefronts.  LDS (ring space): the first row's local end state and P^T,
