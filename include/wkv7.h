@@ -77,7 +77,7 @@ extern "C" {
 #define WKV7_ALGO_SEGMENTED 4  /* the segmented chunked kernel (32-token chunks, rows cut into segments, one
                                 * dispatch; needs a workspace): every row, or with rec_max_len >= 0 the rows longer
                                 * than it, the others token-serially in the same launch.  WKV7_ERR_SHAPE when
-                                * o_tok_stride > 2^24 or the grid needs more flags than the flag region holds (AUTO
+                                * a token stride exceeds 2^24 or the grid needs more flags than the flag region holds (AUTO
                                 * then takes the chunked path) */
 #define WKV7_ALGO_CHAIN 3      /* one dispatch: rows of at most rec_max_len tokens token-serial, longer rows chunked with
                                 * each (row, head) chain walked by one workgroup (no workspace; num_seqs <= 512) */

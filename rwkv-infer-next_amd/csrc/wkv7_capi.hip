@@ -90,10 +90,11 @@ int validate(const wkv7_args* a) {
     return WKV7_OK;
 }
 
-// The segmented launch holds one hand-off flag per unit in the workspace's flag region and addresses output rows with
-// 32-bit offsets.
+// The segmented launch holds one hand-off flag per unit in the workspace's flag region and addresses a chunk's operand
+// and output rows with 32-bit offsets.
 bool seg_fits(const Plan& pl, const wkv7_args* a) {
-    return pl.sws.units <= (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t)) && a->o_tok_stride <= wkv7::kSegMaxTokStride;
+    return pl.sws.units <= (int64_t)(wkv7::kSegFlagRegion / sizeof(int32_t)) &&
+           a->in_tok_stride <= wkv7::kSegMaxTokStride && a->o_tok_stride <= wkv7::kSegMaxTokStride;
 }
 
 Plan make_plan(const wkv7_args* a) {

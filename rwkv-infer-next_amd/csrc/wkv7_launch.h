@@ -53,7 +53,8 @@ hipError_t launch_chunked(const Params& p, const ChunkWorkspace& ws, void* works
 constexpr int kSegChunk = 32;
 constexpr int kSegMaxRows = 4096;
 constexpr int kSegMinChunks = 8;
-// The kernel addresses a chunk's output rows with 32-bit byte offsets: o_tok_stride at most this many elements.
+// The kernel addresses a chunk's operand and output rows with 32-bit byte offsets: in_tok_stride and o_tok_stride at
+// most this many elements.
 constexpr int64_t kSegMaxTokStride = int64_t(1) << 24;
 // First chunk of segment s.  Segments after the first also carry the map from the row's initial state and finish
 // with a correction pass, so the first segment takes a longer share, round(7 nch / (6 nseg + 1)) chunks (the measured

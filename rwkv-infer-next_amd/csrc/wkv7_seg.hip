@@ -83,7 +83,7 @@ constexpr int REC_BYTES = REC_G + 256;         // 45312
 
 struct SegSmem {
     char ring[NREC][REC_BYTES];
-    float fac[4][3][HS];   // per prep wavefront: 2^m, 2^{c-m}, 2^c per channel of its current chunk
+    float fac[4][4][HS];   // per prep wavefront: 2^m, 2^{c-m}, 2^c, 2^{-m} per channel of its current chunk
     int ready[NREC];       // chunk index + 1 of the record a slot holds
     int done[NREC][4];     // per state wavefront: uses of the slot it has finished reading
     int fail;
@@ -183,13 +183,19 @@ __device__ __forceinline__ float dpp(float x) {
 __device__ __forceinline__ float bitsel(uint32_t mask, float a, float b) {
     return __uint_as_float((__float_as_uint(a) & mask) | (__float_as_uint(b) & ~mask));
 }
-// inclusive prefix sum over the 16 lanes of each row (Hillis-Steele on row_shr; lanes before the start read 0)
-__device__ __forceinline__ float row_scan16(float x) {
-    x = x + dpp<0x111, true>(x);
-    x = x + dpp<0x112, true>(x);
-    x = x + dpp<0x114, true>(x);
-    x = x + dpp<0x118, true>(x);
-    return x;
+// inclusive prefix sums over the 16 lanes of each row of N values (Hillis-Steele on row_shr; lanes before the start
+// read 0), in lockstep: each step runs over all N values, so the dependent adds of one value are N instructions apart
+// (no DPP read-after-write waits, N chains in flight)
+template <int N>
+__device__ __forceinline__ void row_scan16(float* x) {
+#pragma unroll
+    for (int n = 0; n < N; ++n) x[n] = x[n] + dpp<0x111, true>(x[n]);
+#pragma unroll
+    for (int n = 0; n < N; ++n) x[n] = x[n] + dpp<0x112, true>(x[n]);
+#pragma unroll
+    for (int n = 0; n < N; ++n) x[n] = x[n] + dpp<0x114, true>(x[n]);
+#pragma unroll
+    for (int n = 0; n < N; ++n) x[n] = x[n] + dpp<0x118, true>(x[n]);
 }
 __device__ __forceinline__ float bcast15(float x) { return dpp<0x15F, false>(x); }  // row_newbcast:15
 __device__ __forceinline__ float shr1(float x) { return dpp<0x111, true>(x); }
@@ -381,25 +387,37 @@ struct Raw {
     uint4 w[2][2], a[2][2], b[2][2], k[2][2], r[2][2], v[2][2];  // N layout [token tile][channel block]
 };
 
+// A wave-uniform raw buffer over [base, base + bytes) for the chunk operand loads and output stores: accesses past
+// `bytes` read zeros and drop their writes.  readfirstlane returns int: each half goes through uint32_t, so that the
+// low one is not sign-extended.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(uint64_t base, int bytes) {
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
+    return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
+                                             __builtin_amdgcn_readfirstlane(bytes), 0x00020000 /* raw 32-bit buffer */);
+}
+
+// The chunk's operands, token rows 16 tau + i, head h, channels 32 kb + 8 q ..: each through a buffer that ends after
+// the chunk's last valid token, so rows t >= Lc (and every row of an empty row's chunk) read zeros.  Offsets are
+// 32-bit: the launch requires in_tok_stride <= kSegMaxTokStride.
 __device__ __forceinline__ void load_raw(Raw& x, const Params& p, int64_t tok0, int Lc, int h, int lane) {
     const int i = lane & 15, q = lane >> 4;
-    if (Lc <= 0) {  // an empty row's chunk: no token to read (every row of the record is masked anyway)
-        x = Raw{};
-        return;
-    }
+    const int64_t e0 = tok0 * p.in_tok_stride + (int64_t)h * HS;
+    const int bytes = Lc > 0 ? (Lc - 1) * (int)p.in_tok_stride * 2 + HS * 2 : 0;
+    const __amdgpu_buffer_rsrc_t rw = buf_rsrc((uint64_t)(p.w + e0), bytes), ra = buf_rsrc((uint64_t)(p.a + e0), bytes),
+                                 rb = buf_rsrc((uint64_t)(p.b + e0), bytes), rk = buf_rsrc((uint64_t)(p.k + e0), bytes),
+                                 rr = buf_rsrc((uint64_t)(p.r + e0), bytes), rv = buf_rsrc((uint64_t)(p.v + e0), bytes);
 #pragma unroll
     for (int tau = 0; tau < 2; ++tau) {
-        const int t = 16 * tau + i;
-        const int64_t tok = tok0 + (t < Lc ? t : 0);  // rows past the chunk read its first token and are zeroed
-        const int64_t off = tok * p.in_tok_stride + (int64_t)h * HS + 8 * q;
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb) {
-            x.w[tau][kb] = *reinterpret_cast<const uint4*>(p.w + off + 32 * kb);
-            x.a[tau][kb] = *reinterpret_cast<const uint4*>(p.a + off + 32 * kb);
-            x.b[tau][kb] = *reinterpret_cast<const uint4*>(p.b + off + 32 * kb);
-            x.k[tau][kb] = *reinterpret_cast<const uint4*>(p.k + off + 32 * kb);
-            x.r[tau][kb] = *reinterpret_cast<const uint4*>(p.r + off + 32 * kb);
-            x.v[tau][kb] = *reinterpret_cast<const uint4*>(p.v + off + 32 * kb);
+            const int off = ((16 * tau + i) * (int)p.in_tok_stride + 8 * q + 32 * kb) * 2;
+            x.w[tau][kb] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rw, off, 0, 0));
+            x.a[tau][kb] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+            x.b[tau][kb] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rb, off, 0, 0));
+            x.k[tau][kb] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+            x.r[tau][kb] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0));
+            x.v[tau][kb] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
         }
     }
 }
@@ -451,10 +469,11 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float lam = -__builtin_amdgcn_exp2f(w8[e] * kL2E) * kL2E;
-                g[tau][kb][e] = row_scan16(valid ? lam : 0.f);
+                g[tau][kb][e] = valid ? lam : 0.f;
             }
         }
     }
+    row_scan16<32>(&g[0][0][0]);
     float m[2][8], c[2][8];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
@@ -464,17 +483,26 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
             g[1][kb][e] += m[kb][e];
             c[kb][e] = bcast15(g[1][kb][e]);
         }
-    // per-channel factors for the products' row/column scalings (lanes i == 0 hold every channel once)
+    // per-channel factors for the products' row/column scalings: the lanes i == 0, which hold every channel's m and c
+    // once, park them in fac[0] and fac[1]; lane l then turns channel l's into 2^m, 2^{c-m}, 2^c and 2^{-m} (four
+    // quarter-rate exponentials a lane instead of 48 on every lane, most of them masked off)
     if (i == 0) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int ch = 32 * kb + 8 * q + e;
-                fac[0][ch] = __builtin_amdgcn_exp2f(m[kb][e]);
-                fac[1][ch] = __builtin_amdgcn_exp2f(c[kb][e] - m[kb][e]);
-                fac[2][ch] = __builtin_amdgcn_exp2f(c[kb][e]);
+            for (int h4 = 0; h4 < 2; ++h4) {
+                const int ch = 32 * kb + 8 * q + 4 * h4;
+                *reinterpret_cast<f4*>(&fac[0][ch]) = f4{m[kb][4 * h4], m[kb][4 * h4 + 1], m[kb][4 * h4 + 2], m[kb][4 * h4 + 3]};
+                *reinterpret_cast<f4*>(&fac[1][ch]) = f4{c[kb][4 * h4], c[kb][4 * h4 + 1], c[kb][4 * h4 + 2], c[kb][4 * h4 + 3]};
             }
+    }
+    wave_lds_sync();
+    {
+        const float ml = fac[0][lane], cl = fac[1][lane];
+        fac[0][lane] = __builtin_amdgcn_exp2f(ml);
+        fac[1][lane] = __builtin_amdgcn_exp2f(cl - ml);
+        fac[2][lane] = __builtin_amdgcn_exp2f(cl);
+        fac[3][lane] = __builtin_amdgcn_exp2f(-ml);
     }
     wave_lds_sync();
 
@@ -482,16 +510,23 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
     bf8 Ah[2][2], Al[2][2], Bh[2][2], Bl[2][2], Kh[2][2], Kl[2][2], Rh[2][2], Vn[2][2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-        float fr0[8];
+        float fr0[8], fm[8];  // (tau = 1) token 15's 2^{g-m}; 2^{-m} of the lane's 8 channels
+        {
+            const f4 f0 = *reinterpret_cast<const f4*>(&fac[3][32 * kb + 8 * q]);
+            const f4 f1 = *reinterpret_cast<const f4*>(&fac[3][32 * kb + 8 * q + 4]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                fm[v] = f0[v];
+                fm[4 + v] = f1[v];
+            }
+        }
 #pragma unroll
         for (int tau = 0; tau < 2; ++tau) {
-            const uint32_t vm = (16 * tau + i < Lc) ? 0xffffffffu : 0u;
-            auto msk = [vm](uint4 x) { return make_uint4(x.x & vm, x.y & vm, x.z & vm, x.w & vm); };
-            float a8[8], b8[8], k8[8], r8[8];
-            unpack8(msk(raw.a[tau][kb]), a8);
-            unpack8(msk(raw.b[tau][kb]), b8);
-            unpack8(msk(raw.k[tau][kb]), k8);
-            unpack8(msk(raw.r[tau][kb]), r8);
+            float a8[8], b8[8], k8[8], r8[8];  // zero past the chunk's valid tokens (load_raw)
+            unpack8(raw.a[tau][kb], a8);
+            unpack8(raw.b[tau][kb], b8);
+            unpack8(raw.k[tau][kb], k8);
+            unpack8(raw.r[tau][kb], r8);
             float fa[8], fr[8], fb[8];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
@@ -499,7 +534,7 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
                 fr[e] = __builtin_amdgcn_exp2f(d);
                 fb[e] = __builtin_amdgcn_exp2f(-d);
                 const float prev = shr1(fr[e]);  // token t - 1 of the row (lane 0 reads 0)
-                const float first = tau == 0 ? __builtin_amdgcn_exp2f(-m[kb][e]) : bcast15(fr0[e]);
+                const float first = tau == 0 ? fm[e] : bcast15(fr0[e]);
                 fa[e] = bitsel(i == 0 ? 0xffffffffu : 0u, first, prev);
             }
             if (tau == 0)
@@ -518,7 +553,7 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
 #pragma unroll
             for (int e = 0; e < 8; ++e) x8[e] = r8[e] * fr[e];
             Rh[tau][kb] = hi8(x8);
-            Vn[tau][kb] = as_bf8(msk(raw.v[tau][kb]));
+            Vn[tau][kb] = as_bf8(raw.v[tau][kb]);
         }
     }
 
@@ -723,12 +758,7 @@ __device__ __forceinline__ void store_y(const Params& p, int64_t tok0, int Lc, i
     const int stride2 = (int)p.o_tok_stride * 2;
     const uint64_t base = p.o ? (uint64_t)(p.o + tok0 * p.o_tok_stride + (int64_t)h * HS + 16 * j) : 0;
     const int bytes = (p.o && Lc > 0) ? (Lc - 1) * stride2 + 32 : 0;
-    // readfirstlane returns int: each half goes through uint32_t, so that the low one is not sign-extended
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)base);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(base >> 32));
-    const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(((uint64_t)hi << 32) | lo), 0,
-                                          __builtin_amdgcn_readfirstlane(bytes), 0x00020000 /* raw 32-bit buffer */);
+    const __amdgpu_buffer_rsrc_t rs = buf_rsrc(base, bytes);
 #pragma unroll
     for (int tau = 0; tau < 2; ++tau) {
         uint2 pk;

@@ -93,14 +93,16 @@ def test_workspace_sizing_follows_the_dispatch_rule():
     seg = _lib.workspace_size(base_args(num_seqs=1, T=4096, total_tokens=4096, H=64, in_tok_stride=64 * 64,
                                            o_tok_stride=64 * 64))
     assert seg == _lib.WKV7_FLAG_REGION_BYTES + 256 * 2 * 64 * 64 * 4 + (128 - 36) * 64 * 4096
-    # the segmented kernel addresses a chunk's output rows with 32-bit offsets: beyond 2^24 elements per output
-    # token AUTO takes the chunked path (32 KB records of 16 chunks, no P records) and SEGMENTED is refused
-    wide = dict(num_seqs=1, T=4096, total_tokens=4096, H=64, in_tok_stride=64 * 64, o_tok_stride=(1 << 24) + 8)
-    assert _lib.workspace_size(base_args(**wide)) != seg
-    assert _lib.workspace_size(base_args(**dict(wide, o_tok_stride=1 << 24))) == seg
-    with pytest.raises(_lib.Wkv7Error) as e:
-        _lib.workspace_size(base_args(algo=_lib.ALGO_SEGMENTED, **wide))
-    assert e.value.code == _lib.WKV7_ERR_SHAPE
+    # the segmented kernel addresses a chunk's operand and output rows with 32-bit offsets: beyond 2^24 elements per
+    # token AUTO takes the chunked path (another workspace) and SEGMENTED is refused
+    dense = dict(num_seqs=1, T=4096, total_tokens=4096, H=64, in_tok_stride=64 * 64, o_tok_stride=64 * 64)
+    for field in ("in_tok_stride", "o_tok_stride"):
+        wide = dict(dense, **{field: (1 << 24) + 8})
+        assert _lib.workspace_size(base_args(**wide)) != seg
+        assert _lib.workspace_size(base_args(**dict(wide, **{field: 1 << 24}))) == seg
+        with pytest.raises(_lib.Wkv7Error) as e:
+            _lib.workspace_size(base_args(algo=_lib.ALGO_SEGMENTED, **wide))
+        assert e.value.code == _lib.WKV7_ERR_SHAPE
     # ragged: short rows token-serial, long rows segmented (bounded by total_tokens); the flag region leads
     r = _lib.workspace_size(base_args(cu_seqlens=0x10000, T=0, total_tokens=1000))
     assert r > _lib.WKV7_FLAG_REGION_BYTES
