@@ -48,7 +48,8 @@ extern "C" {
  * (rwkv_next/model.py:366-396: index_select / index_copy_ / pool views). */
 #define WKV7_STATUS_H0_SLOT 1   /* an h0 index outside [0, h0_rows): that sequence started from a zero state */
 #define WKV7_STATUS_HT_SLOT 2   /* an ht index outside [0, ht_rows): that final state was not stored */
-#define WKV7_STATUS_SEQLENS 4   /* cu_seqlens entries not non-decreasing within [0, total_tokens]: extents clamped */
+#define WKV7_STATUS_SEQLENS 4   /* cu_seqlens entries not non-decreasing within [0, total_tokens], or a row longer
+                                 * than the bound T > 0: extents clamped (such a row is cut to its first T tokens) */
 #define WKV7_STATUS_NKEEP 8     /* a negative n_keep entry: treated as 0 */
 #define WKV7_STATUS_DECAY 16    /* some w of a token that the chunked, segmented or chain kernels run (rows longer
                                  * than the token-serial threshold, within n_keep) exceeds WKV7_CHUNK_W_MAX: those
@@ -106,7 +107,8 @@ typedef struct wkv7_args {
     /* sequences -- wkv7.py:46-54 */
     const int32_t *cu_seqlens;    /* NULL: dense, sequence n = tokens [n*T, (n+1)*T); else [num_seqs + 1] */
     const int64_t *n_keep;        /* NULL, or per sequence: run only the first min(len, n_keep[n]) tokens */
-    float *snapshots;             /* NULL, or [num_seqs][T][H][64][64]: state after each token (recurrent) */
+    float *snapshots;             /* NULL, or [num_seqs][T][H][64][64]: state after each token t < len of each row
+                                   * (the others untouched; ragged calls need T >= 1), recurrent kernel */
 
     void *workspace;              /* device scratch of the chunked paths (see wkv7_workspace_size), 256-byte aligned.
                                    * Its first WKV7_SEG_FLAG_BYTES hold the segmented kernel's hand-off flags: they
@@ -117,7 +119,8 @@ typedef struct wkv7_args {
 
     int32_t num_seqs;             /* N: B when dense, cu_seqlens entries - 1 when ragged */
     int32_t T;                    /* dense: tokens per sequence.  Ragged: an upper bound on any row's length
-                                   * (0 = total_tokens); the snapshot time stride in both cases */
+                                   * (0 = total_tokens; a longer row is cut to T tokens, see WKV7_STATUS_SEQLENS);
+                                   * the snapshot time stride in both cases */
     int64_t total_tokens;         /* operand rows: N*T dense, the packed length when ragged */
     int32_t H;                    /* heads */
     int32_t head_size;            /* must be 64 */

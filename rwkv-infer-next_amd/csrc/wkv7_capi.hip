@@ -187,7 +187,8 @@ Params to_params(const wkv7_args* a) {
 // The optional status word: one pass over the call's sequences, launched before the recurrence only when the
 // caller passes a status pointer (so calls without one keep their single dispatch and pay nothing).  It checks
 // exactly what the kernels skip: an h0 slot outside [0, h0_rows) on a row that reads it (not fresh), an ht slot
-// outside [0, ht_rows), cu_seqlens entries that are not non-decreasing within [0, total_tokens], a negative n_keep;
+// outside [0, ht_rows), cu_seqlens entries that are not non-decreasing within [0, total_tokens] or span more than
+// the length bound T, a negative n_keep;
 // and, when the call runs the chunked, segmented or chain kernels, w against WKV7_CHUNK_W_MAX (16 bytes per thread)
 // on the tokens those kernels run: rows longer than chunk_thr (every row when chunk_thr < 0), within n_keep.
 __device__ __forceinline__ int row_of_token(const wkv7::Params& p, int64_t t) {
@@ -215,7 +216,7 @@ __global__ __launch_bounds__(256) void wkv7_status_kernel(const wkv7::Params p, 
         }
         if (p.cu) {
             const int64_t b = p.cu[n], e = p.cu[n + 1];
-            if (b < 0 || e < b || e > p.total_tokens) bits |= WKV7_STATUS_SEQLENS;
+            if (b < 0 || e < b || e > p.total_tokens || (p.T > 0 && e - b > p.T)) bits |= WKV7_STATUS_SEQLENS;
         }
         if (p.n_keep && p.n_keep[n] < 0) bits |= WKV7_STATUS_NKEEP;
     }

@@ -121,10 +121,12 @@ struct Params {
 // Extent of sequence n (rwkv_next/kernels/wkv7.py:46-54).
 __device__ __forceinline__ void seq_extent(const Params& p, int n, int64_t& bos, int& len) {
     if (p.cu) {
-        // clamped to [0, total_tokens] so that a malformed cu_seqlens cannot index past the operands
+        // clamped to [0, total_tokens] so that a malformed cu_seqlens cannot index past the operands, and to the
+        // caller's length bound T when one is given (it sizes the workspaces and the snapshot rows)
         int64_t s = p.cu[n], e = p.cu[n + 1];
         s = s < 0 ? 0 : (s > p.total_tokens ? p.total_tokens : s);
         e = e < s ? s : (e > p.total_tokens ? p.total_tokens : e);
+        if (p.T > 0 && e - s > p.T) e = s + p.T;
         bos = s;
         len = (int)(e - s);
     } else {

@@ -267,7 +267,7 @@ def wkv7_pool_op(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tenso
     if fresh is not None:
         _require(fresh, "fresh", torch.uint8, (N,))
     if snapshots is not None:
-        _require(snapshots, "snapshots", torch.float32, (N, T, H, K, K))
+        _require(snapshots, "snapshots", torch.float32, (N, Tn, H, K, K))
     if status is not None:
         _require(status, "status", torch.int32, (None,))
         if status.numel() < 1:
@@ -295,9 +295,11 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
     (1, sumT, H*K) with cu_seqlens (N+1,) int32.  fresh (N,) bool: start those rows from zeros (the reference
     zeroes them first, model.py:382-383).  n_keep (N,) int64: run only the first n_keep[n] tokens.
     final=False reads the pool without writing it (speculative verify, model.py:475-496).
-    snapshots: optional (N, T, H, K, K) fp32 receiving the state after every token (dense only); rolling back to
-    an accepted prefix of n tokens is `restore_snapshots_(pool, slots, snapshots, n)`.
-    max_len: ragged calls may pass an upper bound on any row's length (sizes the workspace; 0 = sumT).
+    snapshots: optional (N, T, H, K, K) fp32 receiving the state after every token (ragged calls: (N, max_len, H,
+    K, K), row n's entries t < its length written, the rest untouched); rolling back to an accepted prefix of n
+    tokens is `restore_snapshots_(pool, slots, snapshots, n)`.  Snapshot calls run the token-serial kernel.
+    max_len: ragged calls may pass an upper bound on any row's length (sizes the workspace and the snapshot rows;
+    0 = sumT); a longer row is cut to its first max_len tokens and reported through status (WKV7_STATUS_SEQLENS).
     status: optional int32 device tensor (one element, see new_status): a check launched ahead of the recurrence
     ORs WKV7_STATUS_* bits into it when a slot index lies outside the pool, cu_seqlens is malformed or an n_keep
     entry is negative (the kernels skip such reads and writes and go on), when a call that runs the chunked
@@ -329,11 +331,12 @@ def wkv7_pool_(r, w, k, v, a, b, pool, slots, H, K, *, cu_seqlens=None, n_keep=N
         fr = torch.as_tensor(fresh, device=dev)
         fr = (fr if fr.dtype == torch.uint8 else fr.to(torch.uint8)).contiguous()
     if snapshots is not None:
-        if cu is not None:
-            raise ValueError("snapshots are supported for dense (N, T) calls only")
+        if cu is not None and max_len < 1:
+            raise ValueError("ragged calls with snapshots need max_len >= 1 (the snapshot rows' length)")
+        Ts = T if cu is None else int(max_len)
         if snapshots.dtype != torch.float32 or not snapshots.is_contiguous() or \
-                tuple(snapshots.shape) != (N, T, H, K, K):
-            raise ValueError(f"snapshots must be a contiguous float32 ({N}, {T}, {H}, {K}, {K}) tensor")
+                tuple(snapshots.shape) != (N, Ts, H, K, K):
+            raise ValueError(f"snapshots must be a contiguous float32 ({N}, {Ts}, {H}, {K}, {K}) tensor")
     if status is not None and (status.dtype != torch.int32 or status.numel() < 1 or status.device != dev):
         raise ValueError("status must be an int32 tensor of at least one element on the operands' device")
     o = wkv7_pool_op(r, w, k, v, a, b, pool, sl, H, K, cu, nk, fr, final, store_o, snapshots, status,

@@ -321,6 +321,86 @@ def test_snapshots_are_bit_identical_to_a_rerun(dev, K):
     assert torch.equal(o_verify, o_plain)
 
 
+def test_ragged_snapshots_and_rollback(dev, K):
+    """A ragged verify (rows of 0..5 tokens packed with cu_seqlens) with per-token snapshots (N, max_len, H, 64, 64):
+    row n's entries t < its length hold the state after token t (the oracle within tolerance, and bit for bit a dense
+    verify of that row alone), the entries past its length are untouched, and restoring n accepted tokens equals a
+    ragged re-run of the first n tokens bit for bit."""
+    from oracle import rel_max, wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H, Tm = 4, 5
+    lens = [5, 1, 0, 3, 5, 2]
+    N = len(lens)
+    say("ragged snapshots", lens)
+    seqs = [operands(1, L, H, seed=600 + i) for i, L in enumerate(lens)]
+    cat = {n: np.concatenate([s[n] for s in seqs], axis=1) for n in seqs[0]}
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool0 = synth.state_np((10, H, 64, 64), seed=601)
+    slots = np.array([7, 2, 9, 0, 4, 5], np.int64)
+    _, _, snap_ref = wkv7_ref(*np_list(cat), pool0, cu_seqlens=cu, state_idx=slots, snapshots=True)
+    x, sl, cu_d = to_dev(cat, dev), torch.from_numpy(slots).to(dev), torch.from_numpy(cu).to(dev)
+    pool = torch.from_numpy(pool0).to(dev)
+    snaps = torch.full((N, Tm, H, 64, 64), -7.0, device=dev)
+    status = K.new_status(dev)
+    K.wkv7_pool_(*x, pool, sl, H, 64, cu_seqlens=cu_d, final=False, snapshots=snaps, max_len=Tm, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    assert torch.equal(pool.cpu(), torch.from_numpy(pool0))  # final=False: the pool is only read
+    got = as_np(snaps)
+    for n, L in enumerate(lens):
+        assert np.all(got[n, L:] == -7.0), n
+        if L == 0:
+            continue
+        es = rel_max(got[n, :L], snap_ref[n, :L])
+        say(f"row {n}: snapshot max-rel {es:.3e}")
+        assert es <= S_TOL
+        alone = torch.empty(1, L, H, 64, 64, device=dev)
+        K.wkv7_pool_(*to_dev(seqs[n], dev), torch.from_numpy(pool0).to(dev), sl[n:n + 1], H, 64, final=False,
+                     snapshots=alone)
+        torch.cuda.synchronize()
+        assert torch.equal(snaps[n, :L], alone[0]), n
+    n_acc = torch.tensor([5, 1, 0, 2, 0, 1], device=dev)
+    K.restore_snapshots_(pool, sl, snaps, n_acc)
+    rerun = torch.from_numpy(pool0).to(dev)
+    K.wkv7_pool_(*x, rerun, sl, H, 64, cu_seqlens=cu_d, n_keep=n_acc, store_o=False, max_len=Tm)
+    torch.cuda.synchronize()
+    assert torch.equal(pool, rerun)
+    with pytest.raises(ValueError, match="max_len"):
+        K.wkv7_pool_(*x, pool, sl, H, 64, cu_seqlens=cu_d, final=False, snapshots=snaps)
+
+
+@pytest.mark.parametrize("algo", [0, 1, 2, 3, 4])
+def test_ragged_rows_longer_than_max_len_are_cut(dev, K, algo):
+    """max_len bounds a ragged call's rows (it sizes the chunked and segmented workspaces): a longer row runs on its
+    first max_len tokens only, on every path, and the status word reports it."""
+    from rwkv_next_amd import _lib
+    from oracle import rel_max, wkv7_ref
+    import rwkv_next_amd.synth as synth
+    H, max_len = 4, 96
+    lens = [300, 40, 0, 129, 7, 96]
+    say("rows cut to max_len", algo, lens, max_len)
+    seqs = [operands(1, L, H, seed=700 + i) for i, L in enumerate(lens)]
+    cat = {n: np.concatenate([s[n] for s in seqs], axis=1) for n in seqs[0]}
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    pool0 = synth.state_np((8, H, 64, 64), seed=701)
+    slots = np.array([3, 6, 0, 1, 7, 4], np.int64)
+    kept = np.minimum(lens, max_len)
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(cat), pool0, cu_seqlens=cu, state_idx=slots, n_keep=kept)
+    pool = torch.from_numpy(pool0).to(dev)
+    status = K.new_status(dev)
+    o = K.wkv7_pool_(*to_dev(cat, dev), pool, torch.from_numpy(slots).to(dev), H, 64,
+                     cu_seqlens=torch.from_numpy(cu).to(dev), max_len=max_len, algo=algo, status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == _lib.WKV7_STATUS_SEQLENS
+    keep = np.zeros(sum(lens), bool)
+    for i in range(len(lens)):
+        keep[cu[i]:cu[i] + kept[i]] = True
+    eo = rel_max(as_np(o).reshape(o_ref.shape)[:, keep], o_ref[:, keep])
+    es = rel_max(as_np(pool), pool_ref)
+    say(f"y max-rel {eo:.3e}  state max-rel {es:.3e}")
+    assert eo <= Y_TOL and es <= S_TOL
+
+
 def test_check_distinct_slots(dev, K):
     with pytest.raises(ValueError):
         K.check_distinct_slots(torch.tensor([1, 2, 1], device=dev), 4)
