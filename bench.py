@@ -158,8 +158,8 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
 def varlen_bench(torch, kernels, synth, dev, steps, warmup):
     """The drop-in varlen prefill call kernels.wkv7(..., cu_seqlens=cu) (rwkv_next/kernels/wkv7.py:126-138) on one
     2048-token prefill chunk of the engine (rwkv_next/engine.py:218-228) split over 4 rows, H = 64, from zero states,
-    final states returned.  AUTO runs it as two dispatches (the token-serial kernel for rows of at most 32 tokens,
-    here none, and the segmented kernel).  Timed as HIP graph replays."""
+    final states returned.  AUTO runs it as one segmented dispatch (rows of at most 32 tokens, here none, would run
+    token-serially in the same launch).  Timed as HIP graph replays."""
     H, lens = 64, [700, 512, 600, 236]
     total = sum(lens)
     cu = torch.tensor([0, 700, 1212, 1812, 2048], dtype=torch.int32, device=dev)
