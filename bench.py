@@ -118,21 +118,30 @@ def cfg0_bench(torch, kernels, synth, dev, steps, warmup):
     return out
 
 
-def prefill_bench(torch, kernels, synth, dev, steps, warmup):
+def prefill_bench(torch, kernels, synth, dev, steps, warmup, copies=4):
+    """Config 2 (B = 1, T = 4096, H = 64, zero initial state, final state returned).  ms: one call per HIP graph
+    replay, the same operands each time (201 MB, which the 256 MB Infinity Cache largely keeps between replays, as it
+    keeps a layer's operands between the kernel that writes them and this one); ms_eager: those calls launched
+    eagerly.  ms_layers_cold: `copies` layer calls, each on its own operands (none cached), in one graph, per call.
+    (A graph replay ends with a fixed ~6-9 us on these boxes, which the one-call figure carries in full.)"""
     T, H = 4096, 64
-    ops = synth.operands_torch((1, T, H, 64), seed=1002, device=dev)
-    x = [ops[n].reshape(1, T, H * 64).contiguous() for n in synth.OPERAND_NAMES]
+    xs = []
+    for i in range(copies):
+        ops = synth.operands_torch((1, T, H, 64), seed=1002 + 17 * i, device=dev)
+        xs.append([ops[n].reshape(1, T, H * 64).contiguous() for n in synth.OPERAND_NAMES])
+    fns = [lambda x=x: kernels.wkv7(*x, None, H, 64) for x in xs]
     for _ in range(warmup):
-        kernels.wkv7(*x, None, H, 64)
+        fns[0]()
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(steps):
-        kernels.wkv7(*x, None, H, 64)
+        fns[0]()
     e1.record()
     torch.cuda.synchronize()
     ms_eager = e0.elapsed_time(e1) / steps
-    ms = graph_us(torch, [lambda: kernels.wkv7(*x, None, H, 64)], steps, warmup) * 1e-3
+    ms = graph_us(torch, fns[:1], steps, warmup) * 1e-3
+    ms_cold = graph_us(torch, fns, steps, warmup) * 1e-3
     chunks = T // C
     bytes_ = PREFILL_BYTES_PER_HEAD_TOKEN * T * H + 2 * 16384 * H
     t_hbm = bytes_ / (HBM_PEAK_GBS * 1e9)
@@ -145,7 +154,9 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
     # stricter one above, which prices the state path as the three bf16 passes these kernels run.
     t_fp32_state = f_state / (FP32_PEAK_TFLOPS * 1e12) + f_out / (BF16_PEAK_TFLOPS * 1e12)
     t_roof_fp32_state = max(t_hbm, t_fp32_state)
-    return {"ms": ms, "ms_eager": ms_eager, "timing": "ms: HIP graph replay per call; ms_eager: eager calls",
+    return {"ms": ms, "ms_eager": ms_eager, "ms_layers_cold": ms_cold, "copies": copies,
+            "timing": "ms: one call per HIP graph replay; ms_eager: eager calls; ms_layers_cold: per call, `copies` "
+                      "layer calls on their own operands per replay",
             "tok_s": T / (ms * 1e-3), "head_tok_s": T * H / (ms * 1e-3),
             "roofline": {"bound": "hbm" if t_hbm >= t_mfma else "mfma", "t_roof_us": t_roof * 1e6,
                          "t_hbm_us": t_hbm * 1e6, "t_mfma_us": t_mfma * 1e6, "frac": t_roof / (ms * 1e-3),
@@ -155,27 +166,35 @@ def prefill_bench(torch, kernels, synth, dev, steps, warmup):
             "recurrence_equiv_TFLOPs": 9 * 64 * 64 * T * H / (ms * 1e-3) / 1e12}
 
 
-def varlen_bench(torch, kernels, synth, dev, steps, warmup):
+def varlen_bench(torch, kernels, synth, dev, steps, warmup, copies=4):
     """The drop-in varlen prefill call kernels.wkv7(..., cu_seqlens=cu) (rwkv_next/kernels/wkv7.py:126-138) on one
     2048-token prefill chunk of the engine (rwkv_next/engine.py:218-228) split over 4 rows, H = 64, from zero states,
     final states returned.  AUTO runs it as one segmented dispatch (rows of at most 32 tokens, here none, would run
-    token-serially in the same launch).  Timed as HIP graph replays."""
+    token-serially in the same launch).  us: one call per HIP graph replay; us_layers_cold: `copies` layer calls,
+    each on its own operands, per replay, per call."""
     H, lens = 64, [700, 512, 600, 236]
     total = sum(lens)
     cu = torch.tensor([0, 700, 1212, 1812, 2048], dtype=torch.int32, device=dev)
-    ops = synth.operands_torch((1, total, H, 64), seed=1005, device=dev)
-    x = [ops[n].reshape(1, total, H * 64).contiguous() for n in synth.OPERAND_NAMES]
-    us = graph_us(torch, [lambda: kernels.wkv7(*x, None, H, 64, cu_seqlens=cu)], steps, warmup)
+    xs = []
+    for i in range(copies):
+        ops = synth.operands_torch((1, total, H, 64), seed=1005 + 17 * i, device=dev)
+        xs.append([ops[n].reshape(1, total, H * 64).contiguous() for n in synth.OPERAND_NAMES])
+    fns = [lambda x=x: kernels.wkv7(*x, None, H, 64, cu_seqlens=cu) for x in xs]
+    us = graph_us(torch, fns[:1], steps, warmup)
+    us_cold = graph_us(torch, fns, steps, warmup)
     nbytes = PREFILL_BYTES_PER_HEAD_TOKEN * total * H + len(lens) * 16384 * H  # no initial states read
     t_roof_us = nbytes / (HBM_PEAK_GBS * 1e3)
-    return {"us": us, "timing": "HIP graph replay per call", "rows": lens, "tokens": total, "H": H,
+    return {"us": us, "us_layers_cold": us_cold, "copies": copies,
+            "timing": "us: one call per HIP graph replay; us_layers_cold: per call, `copies` layer calls per replay",
+            "rows": lens, "tokens": total, "H": H,
             "tok_s": total / (us * 1e-6), "algorithmic_bytes": nbytes, "t_roof_us": t_roof_us,
             "frac": t_roof_us / us}
 
 
-def mixed_bench(torch, kernels, synth, dev, steps, warmup):
+def mixed_bench(torch, kernels, synth, dev, steps, warmup, copies=4):
     """Config 3: one continuous-batching step over a 256-slot pool, H = 64: 8 prefill rows of U[1, 2048] tokens and
-    120 decode rows, packed varlen, random distinct slots, captured in one HIP graph and replayed."""
+    120 decode rows, packed varlen, random distinct slots.  ms: the step captured in one HIP graph and replayed;
+    ms_layers_cold: `copies` layers' steps (each its own pool and operands) per replay, per step."""
     import numpy as np
     H, S = 64, 256
     rng = np.random.default_rng(1003)
@@ -184,34 +203,22 @@ def mixed_bench(torch, kernels, synth, dev, steps, warmup):
     total = int(sum(lens))
     cu = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=dev)
     slots = torch.from_numpy(rng.permutation(S)[:len(lens)].astype(np.int64)).to(dev)
-    ops = synth.operands_torch((1, total, H, 64), seed=1003, device=dev)
-    x = [ops[n].reshape(1, total, H * 64).contiguous() for n in synth.OPERAND_NAMES]
-    pool = 0.1 * torch.randn(S, H, 64, 64, device=dev)
-    stream = torch.cuda.Stream()
-    stream.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(stream):
-        kernels.wkv7_pool_(*x, pool, slots, H, 64, cu_seqlens=cu, max_len=2048)
-    torch.cuda.current_stream().wait_stream(stream)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        kernels.wkv7_pool_(*x, pool, slots, H, 64, cu_seqlens=cu, max_len=2048)
-    torch.cuda.synchronize()
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
-        graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+    layers = []
+    for i in range(copies):
+        ops = synth.operands_torch((1, total, H, 64), seed=1003 + 17 * i, device=dev)
+        x = [ops[n].reshape(1, total, H * 64).contiguous() for n in synth.OPERAND_NAMES]
+        layers.append((x, 0.1 * torch.randn(S, H, 64, 64, device=dev)))
+    fns = [lambda x=x, pool=pool: kernels.wkv7_pool_(*x, pool, slots, H, 64, cu_seqlens=cu, max_len=2048)
+           for x, pool in layers]
+    ms = graph_us(torch, fns[:1], steps, warmup) * 1e-3
+    ms_cold = graph_us(torch, fns, steps, warmup) * 1e-3
     # HBM roofline: every (row, head) reads and writes its 16 KB state once, and every head-token moves 896 B of
     # operands and output
     nbytes = H * (len(lens) * 2 * 64 * 64 * 4 + total * 896)
     t_roof_us = nbytes / (HBM_PEAK_GBS * 1e3)
-    return {"ms": ms, "tokens": total, "tok_s": total / (ms * 1e-3), "prefill_lens": sorted(v for v in lens if v > 1),
+    return {"ms": ms, "ms_layers_cold": ms_cold, "copies": copies,
+            "timing": "ms: one step per HIP graph replay; ms_layers_cold: per step, `copies` layers per replay",
+            "tokens": total, "tok_s": total / (ms * 1e-3), "prefill_lens": sorted(v for v in lens if v > 1),
             "algorithmic_bytes": nbytes, "t_roof_us": t_roof_us, "frac": t_roof_us / (ms * 1e3)}
 
 
