@@ -15,8 +15,8 @@
  * Plain C: no HIP, CUDA or torch types.  Pointers are device pointers; `stream` is a hipStream_t passed as
  * void*.  No function allocates device memory or synchronises the host, and every call is reentrant and can be
  * recorded into a hipGraph (scratch memory comes from the caller's workspace).  Global state: a per-device cache of
- * the compute-unit count, and the static device scratch array of wkv7_run_noalloc (WKV7_NOALLOC_SCRATCH_BYTES on
- * every GPU the library is loaded on, from module load to process exit) with a per-device cache of its address.
+ * the compute-unit count.  (The allocation-free variant of wkv7_run, with its static device scratch array, is a
+ * separate library: include/wkv7_noalloc.h.)
  */
 #ifndef RWKV_NEXT_AMD_WKV7_H
 #define RWKV_NEXT_AMD_WKV7_H
@@ -38,7 +38,7 @@ extern "C" {
 #define WKV7_ERR_ALIGN (-3)      /* operand/state pointers not 16-byte aligned, or strides not multiples of 8 */
 #define WKV7_ERR_WORKSPACE (-4)  /* workspace missing or smaller than wkv7_workspace_size() */
 #define WKV7_ERR_ARG (-5)        /* inconsistent arguments (snapshots on the chunked path, bad algo, ...) */
-#define WKV7_ERR_SCRATCH_LIMIT (-6) /* wkv7_run_noalloc: the call needs more than WKV7_NOALLOC_SCRATCH_BYTES */
+#define WKV7_ERR_SCRATCH_LIMIT (-6) /* wkv7_run_noalloc (wkv7_noalloc.h): the call needs more than its scratch */
 
 /* Bits of the optional device status word (wkv7_args.status).  The recurrence kernels never follow an index outside
  * its buffer: they go on as documented for each case below, so every kernel exits normally.  When status is set,
@@ -129,10 +129,8 @@ typedef struct wkv7_args {
     int32_t *status;              /* NULL, or one device int32 that receives WKV7_STATUS_* bits (see above) */
 } wkv7_args;
 
-/* Size of the device scratch array behind wkv7_run_noalloc (per GPU, held from module load to process exit). */
 /* Bytes at the start of a workspace reserved for the segmented kernel's hand-off flags (zero between calls). */
 #define WKV7_SEG_FLAG_BYTES (256u << 10)
-#define WKV7_NOALLOC_SCRATCH_BYTES (128u << 20)
 
 /* Bytes of device workspace `wkv7_run` needs for these arguments (0 when only the token-serial kernel runs).
  * Depends only on host-side sizes and flags, never on device data.  No reference counterpart: the reference's
@@ -147,17 +145,6 @@ int wkv7_workspace_size(const wkv7_args *args, size_t *bytes);
  * 485 verify with final=False) when h0/ht address the slot pool through h0_idx/ht_idx.
  * Asynchronous; returns after launching. */
 int wkv7_run(const wkv7_args *args, void *stream);
-
-/* wkv7_run without a caller-provided workspace.  It has no counterpart in the reference; it is for callers that
- * cannot allocate device memory (code under HIP graph capture that must not allocate, tight serving loops, harnesses
- * that forbid hipMalloc).  args->workspace and args->workspace_bytes are ignored: the scratch is a static device
- * array of WKV7_NOALLOC_SCRATCH_BYTES per GPU, whose flag region starts zero and is left zero by every call.  The
- * first call on a device looks up the array's device address (hipGetSymbolAddress): make one eager call on a device
- * before capturing calls into a HIP graph there.
- * A call whose wkv7_workspace_size exceeds that returns WKV7_ERR_SCRATCH_LIMIT before launching anything.  Calls no
- * hipMalloc/hipFree.  All calls on one GPU share its array: calls whose kernels overlap on one device (other streams,
- * other threads) race; calls in stream order on one stream do not. */
-int wkv7_run_noalloc(const wkv7_args *args, void *stream);
 
 /*
  * Slot-pool maintenance on a pool of `layers` consecutive fp32 [rows][H][64][64] arrays (a model's per-layer state

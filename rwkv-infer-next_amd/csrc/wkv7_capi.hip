@@ -311,7 +311,7 @@ const char* wkv7_strerror(int code) {
         case WKV7_ERR_ALIGN: return "pointers must be 16-byte aligned and token strides multiples of 8 elements";
         case WKV7_ERR_WORKSPACE: return "workspace missing or smaller than wkv7_workspace_size()";
         case WKV7_ERR_ARG: return "inconsistent arguments";
-        case WKV7_ERR_SCRATCH_LIMIT: return "the call needs more scratch than WKV7_NOALLOC_SCRATCH_BYTES";
+        case WKV7_ERR_SCRATCH_LIMIT: return "the call needs more scratch than wkv7_run_noalloc holds";
         default: return code > 0 ? hipGetErrorString(static_cast<hipError_t>(code)) : "unknown error";
     }
 }

@@ -3,8 +3,10 @@
 //
 // The only scratch memory wkv7_run uses is the chunked paths' workspace (hand-off flags, exchange entries, records).
 // Here it comes from `scratch`, a file-scope device array of WKV7_NOALLOC_SCRATCH_BYTES that every GPU the library
-// runs on holds from module load until the process ends.  Calls needing more are refused with
-// WKV7_ERR_SCRATCH_LIMIT before anything is launched.  The segmented kernel's flag region (the first
+// runs on holds from module load until the process ends.  It is built as its own library, librwkv7_noalloc.so, on
+// top of librwkv7_hip.so (it calls only wkv7_workspace_size and wkv7_run), so processes that never load it hold no
+// such array.  Calls needing more are refused with WKV7_ERR_SCRATCH_LIMIT before anything is launched.  The
+// segmented kernel's flag region (the first
 // WKV7_SEG_FLAG_BYTES) must be zero before a call: the array starts zeroed and every call that completes leaves it
 // zero; everything else is written before it is read within each call, so no clearing is needed between calls.  (A
 // call that reports WKV7_STATUS_SEGMENT_WAIT -- a bounded hand-off wait that expired -- can leave flags set; later
@@ -17,7 +19,7 @@
 
 #include <atomic>
 
-#include "wkv7.h"
+#include "wkv7_noalloc.h"
 
 namespace {
 

@@ -1,4 +1,5 @@
-"""ctypes binding of librwkv7_hip.so (the C ABI declared in include/wkv7.h and include/w6a16.h).
+"""ctypes binding of librwkv7_hip.so (the C ABI declared in include/wkv7.h and include/w6a16.h) and of
+librwkv7_noalloc.so (include/wkv7_noalloc.h, loaded only on request by load_noalloc).
 
 The library must have been built (rwkv_next_amd._build / __graft_entry__.build()).  There is no fallback: if the
 shared object is missing or does not match this binding, importing the kernels raises.
@@ -8,7 +9,7 @@ from __future__ import annotations
 import ctypes
 import os
 
-from ._build import LIB_PATH
+from ._build import LIB_PATH, NOALLOC_LIB_PATH
 
 WKV7_ABI_VERSION = 2
 WKV7_OK = 0
@@ -18,7 +19,8 @@ WKV7_ERR_ALIGN = -3
 WKV7_ERR_WORKSPACE = -4
 WKV7_ERR_ARG = -5
 WKV7_ERR_SCRATCH_LIMIT = -6
-WKV7_NOALLOC_SCRATCH_BYTES = 128 << 20
+WKV7_NOALLOC_SCRATCH_BYTES = 128 << 20  # include/wkv7_noalloc.h
+NOALLOC_EXPORTED = ("wkv7_run_noalloc",)
 
 WKV7_STATUS_H0_SLOT = 1
 WKV7_STATUS_HT_SLOT = 2
@@ -38,7 +40,7 @@ ALGO_SEGMENTED = 4
 WKV7_FLAG_REGION_BYTES = 256 << 10  # leading workspace region of hand-off flags (zero between calls)
 
 EXPORTED = ("wkv7_run", "wkv7_workspace_size", "wkv7_strerror", "wkv7_abi_version", "wkv7_args_size",
-            "wkv7_args_layout", "wkv7_run_noalloc",
+            "wkv7_args_layout",
             "wkv7_pool_reset", "wkv7_pool_move", "wkv7_snapshot_restore", "wkv7_timemix_prologue",
             "wkv7_timemix_epilogue")
 W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split", "w6a16_plan_split_packed",
@@ -119,6 +121,7 @@ class Wkv7Error(RuntimeError):
 
 
 _lib = None
+_noalloc = None
 
 
 def load(path: str = LIB_PATH):
@@ -136,8 +139,6 @@ def load(path: str = LIB_PATH):
     lib = ctypes.CDLL(path)
     lib.wkv7_run.restype = ctypes.c_int
     lib.wkv7_run.argtypes = [ctypes.POINTER(Wkv7Args), _vp]
-    lib.wkv7_run_noalloc.restype = ctypes.c_int
-    lib.wkv7_run_noalloc.argtypes = [ctypes.POINTER(Wkv7Args), _vp]
     lib.wkv7_workspace_size.restype = ctypes.c_int
     lib.wkv7_workspace_size.argtypes = [ctypes.POINTER(Wkv7Args), ctypes.POINTER(ctypes.c_size_t)]
     lib.wkv7_strerror.restype = ctypes.c_char_p
@@ -184,6 +185,22 @@ def load(path: str = LIB_PATH):
     if lib.w6a16_args_size() != ctypes.sizeof(W6a16Args):
         raise ImportError(f"{path}: sizeof(w6a16_args) {lib.w6a16_args_size()} != binding {ctypes.sizeof(W6a16Args)}")
     _lib = lib
+    return lib
+
+
+def load_noalloc(path: str = NOALLOC_LIB_PATH):
+    """Load librwkv7_noalloc.so (wkv7_run_noalloc, include/wkv7_noalloc.h), after librwkv7_hip.so, which it links
+    and shares with this process.  Loading it makes every GPU the process uses hold its static scratch array."""
+    global _noalloc
+    if _noalloc is not None:
+        return _noalloc
+    load()
+    if not os.path.exists(path):
+        raise ImportError(f"{path} is missing: build it with `python -m rwkv_next_amd._build`")
+    lib = ctypes.CDLL(path)
+    lib.wkv7_run_noalloc.restype = ctypes.c_int
+    lib.wkv7_run_noalloc.argtypes = [ctypes.POINTER(Wkv7Args), _vp]
+    _noalloc = lib
     return lib
 
 

@@ -12,10 +12,11 @@ from conftest import REPO
 from rwkv_next_amd import _lib
 
 HEADER = os.path.join(REPO, "include", "wkv7.h")
+NOALLOC_HEADER = os.path.join(REPO, "include", "wkv7_noalloc.h")
 
 
-def declared_functions():
-    text = open(HEADER).read()
+def declared_functions(header=HEADER):
+    text = open(header).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"^[A-Za-z_][\w \*]*?\b(wkv7_\w+)\s*\(", text, flags=re.M)))
 
@@ -26,6 +27,31 @@ def test_library_exports_every_declared_function():
     assert set(names) == set(_lib.EXPORTED), names
     for n in names:
         assert hasattr(lib, n), n
+
+
+def dynamic_symbols(path):
+    """Names the shared object defines in its dynamic symbol table (nm -D --defined-only)."""
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def test_noalloc_library_is_separate():
+    """wkv7_run_noalloc and its static scratch array live in librwkv7_noalloc.so, which links librwkv7_hip.so: the
+    main library neither defines the entry nor carries the array, so loading it alone holds no scratch."""
+    names = declared_functions(NOALLOC_HEADER)
+    assert set(names) == set(_lib.NOALLOC_EXPORTED), names
+    main_syms, na_syms = dynamic_symbols(_lib.LIB_PATH), dynamic_symbols(_lib.NOALLOC_LIB_PATH)
+    assert "wkv7_run_noalloc" not in main_syms
+    assert set(_lib.NOALLOC_EXPORTED) <= na_syms
+    assert "wkv7_run" not in na_syms  # resolved from librwkv7_hip.so at load time
+    lib = _lib.load_noalloc()
+    for n in names:
+        assert hasattr(lib, n), n
+    # the array's host-side shadow symbol exists in the no-alloc library only
+    import subprocess
+    syms = lambda p: subprocess.run(["nm", p], capture_output=True, text=True, check=True).stdout
+    assert "7scratchE" in syms(_lib.NOALLOC_LIB_PATH) and "7scratchE" not in syms(_lib.LIB_PATH)
 
 
 def test_abi_version_and_struct_layout():

@@ -1,8 +1,10 @@
-"""wkv7_run_noalloc (the allocation-free variant of wkv7_run, include/wkv7.h) through the C ABI: two chunked calls
+"""wkv7_run_noalloc (the allocation-free variant of wkv7_run, include/wkv7_noalloc.h, in librwkv7_noalloc.so) through
+the C ABI: two chunked calls
 in a row (the second smaller), a ragged call and a decode call, each bit-identical to wkv7_run with a
 caller-allocated workspace on the same inputs; a call that needs more than WKV7_NOALLOC_SCRATCH_BYTES is refused
 before anything is launched."""
 import ctypes
+import types
 
 import numpy as np
 import pytest
@@ -22,8 +24,10 @@ def dev():
 
 @pytest.fixture(scope="module")
 def lib():
+    """wkv7_run from librwkv7_hip.so and wkv7_run_noalloc from librwkv7_noalloc.so (which links the former)."""
     from rwkv_next_amd import _lib
-    return _lib.load()
+    main, noalloc = _lib.load(), _lib.load_noalloc()
+    return types.SimpleNamespace(wkv7_run=main.wkv7_run, wkv7_run_noalloc=noalloc.wkv7_run_noalloc)
 
 
 def make_args(x, H, N, T, total, o, h0=None, ht=None, cu=None, algo=0):
