@@ -10,7 +10,7 @@
  *   scales fp16  [B'][K/group_k][N]
  * with u = q + 32 in [0, 63] the stored code of q in [-32, 31] and w = scale * q.
  *
- * C[b][m][n] = sum_k A[b][m][k] * w[b][k][n], A bf16 row-major (k contiguous), fp32 accumulation.
+ * C[b][m][n] = sum_k A[b][m][k] * w[b][k][n], A bf16 or fp16 row-major (k contiguous), fp32 accumulation.
  * Return codes are the WKV7_* codes of wkv7.h.
  */
 #ifndef RWKV_NEXT_AMD_W6A16_H
@@ -26,20 +26,25 @@ extern "C" {
 #endif
 
 #define W6A16_OUT_BF16 0
+#define W6A16_OUT_F16 1
 #define W6A16_OUT_F32 2
+
+/* Activation types of w6a16_args.a_dtype (the reference takes a.dtype, int6_gemm.py:144-147, 253-287) */
+#define W6A16_IN_BF16 0
+#define W6A16_IN_F16 1
 
 /* Weight formats of w6a16_args.format */
 #define W6A16_FORMAT_PLANES 0   /* the reference's planes: lo, hi, scales as above */
 #define W6A16_FORMAT_PACKED 1   /* w6a16_pack's layout: lo = packed weight, scales = packed scales, hi unused */
 
 typedef struct w6a16_args {
-    const uint16_t *a;                 /* bf16 activations [B][M][K] */
+    const uint16_t *a;                 /* activations [B][M][K], bf16 or fp16 (a_dtype) */
     int64_t a_batch_stride, a_row_stride;          /* elements; row stride >= K, multiples of 8 */
     const uint8_t *lo, *hi;            /* weight planes; batch strides 0 to share one weight across the batch */
     int64_t lo_batch_stride, hi_batch_stride;      /* bytes */
     const uint16_t *scales;            /* fp16, 4-byte aligned */
     int64_t scales_batch_stride;       /* elements */
-    void *out;                         /* [B][M][N] bf16 or fp32 (out_dtype) */
+    void *out;                         /* [B][M][N] bf16, fp16 or fp32 (out_dtype) */
     int64_t out_batch_stride, out_row_stride;      /* elements */
     void *workspace;                   /* split_k > 1 or M > 32: w6a16_workspace_size bytes, 256-byte aligned */
     size_t workspace_bytes;
@@ -47,8 +52,9 @@ typedef struct w6a16_args {
                                           M > 32: B <= 65535 */
     int32_t group_k;                   /* % 64 == 0, divides K */
     int32_t split_k;                   /* 1 .. 256: K is cut into split_k ranges of 64-row chunks */
-    int32_t out_dtype;                 /* W6A16_OUT_BF16 or W6A16_OUT_F32 */
+    int32_t out_dtype;                 /* W6A16_OUT_BF16, W6A16_OUT_F16 or W6A16_OUT_F32 */
     int32_t format;                    /* W6A16_FORMAT_PLANES or W6A16_FORMAT_PACKED */
+    int32_t a_dtype;                   /* W6A16_IN_BF16 (0) or W6A16_IN_F16 */
 } w6a16_args;
 
 /* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
@@ -79,7 +85,7 @@ int w6a16_plan_split_packed(int32_t B, int32_t M, int32_t N, int32_t K);
 /* C = A @ dequant(W) on `stream` (hipStream_t).  Replaces `_impl` + `_w6a16` (int6_gemm.py:253-287, 156-215). */
 int w6a16_matmul(const w6a16_args *args, void *stream);
 
-/* w[b][k][n] = scale * q ([B][K][N], batch stride in elements) as bf16 (W6A16_OUT_BF16) or fp32 (W6A16_OUT_F32):
+/* w[b][k][n] = scale * q ([B][K][N], batch stride in elements) as bf16, fp16 or fp32 (W6A16_OUT_*):
  * the large-M path, where a library GEMM on the dequantised weight wins.  Replaces dequantize_int6
  * (int6_gemm.py:115-131) on the device.  N % 16 == 0; all pointers 16-byte aligned. */
 int w6a16_dequantize(const uint8_t *lo, const uint8_t *hi, const uint16_t *scales, void *w, int32_t B, int32_t K,

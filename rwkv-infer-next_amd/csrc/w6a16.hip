@@ -81,6 +81,38 @@ __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_c
 
 __device__ __forceinline__ f4 mfma(bf8 a, bf8 b, f4 c) { return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0); }
 
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+
+// Activation element types.  The 6-bit code u becomes an exact MFMA operand 2^e + u with no conversion instruction
+// (the code byte beside a constant high byte), and one MFMA pair per chunk against the constant -(2^e + 32) takes the
+// offset out again: 2^e + u - (2^e + 32) = q exactly.  bf16 (the model's activations): 128 + u, high bytes 0x43,
+// offset 160.  fp16 (the reference op casts its codes to a.dtype, rwkv_next/kernels/int6_gemm.py:144-147): 1024 + u,
+// high bytes 0x64, offset 1056; the products stay exact in the fp32 accumulators.
+struct ActBF16 {
+    static constexpr uint32_t kCodeHi = 0x43434343u;
+    static constexpr uint32_t kBias = 0xC320C320u;  // (-160, -160)
+    static constexpr uint32_t kOnes = 0x3F803F80u;  // (1, 1)
+    static constexpr float kOffset = 160.f;
+    __device__ static f4 mma(u4 a, u4 b, f4 c) { return mfma(__builtin_bit_cast(bf8, a), __builtin_bit_cast(bf8, b), c); }
+    __device__ static float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, a), __builtin_bit_cast(bf2, b), c, false);
+    }
+};
+struct ActF16 {
+    static constexpr uint32_t kCodeHi = 0x64646464u;
+    static constexpr uint32_t kBias = 0xE420E420u;  // (-1056, -1056)
+    static constexpr uint32_t kOnes = 0x3C003C00u;  // (1, 1)
+    static constexpr float kOffset = 1056.f;
+    __device__ static f4 mma(u4 a, u4 b, f4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+    }
+    __device__ static float dot2(uint32_t a, uint32_t b, float c) {
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+    }
+};
+
 // Orders LDS traffic between the lanes of one wavefront (its LDS instructions execute in issue order).
 __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -88,10 +120,11 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// 4 codes u (one per byte) -> 4 bf16 values 128 + u as two dwords.
-__device__ __forceinline__ void codes_to_bf16(uint32_t u, uint32_t& lo2, uint32_t& hi2) {
-    lo2 = __builtin_amdgcn_perm(0x43434343u, u, 0x04010400u);  // bytes: u0, 0x43, u1, 0x43
-    hi2 = __builtin_amdgcn_perm(0x43434343u, u, 0x04030402u);  // bytes: u2, 0x43, u3, 0x43
+// 4 codes u (one per byte) -> 4 operand values 2^e + u as two dwords.
+template <class A>
+__device__ __forceinline__ void codes_to_op(uint32_t u, uint32_t& lo2, uint32_t& hi2) {
+    lo2 = __builtin_amdgcn_perm(A::kCodeHi, u, 0x04010400u);  // bytes: u0, hi, u1, hi
+    hi2 = __builtin_amdgcn_perm(A::kCodeHi, u, 0x04030402u);  // bytes: u2, hi, u3, hi
 }
 
 __device__ __forceinline__ void store8(__bf16* dst, const float (&v)[8]) {
@@ -103,9 +136,30 @@ __device__ __forceinline__ void store8(__bf16* dst, const float (&v)[8]) {
     *reinterpret_cast<u4*>(dst) = u4{o[0], o[1], o[2], o[3]};
 }
 
+__device__ __forceinline__ void store8(_Float16* dst, const float (&v)[8]) {
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        o[e] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e]) |
+               (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)v[2 * e + 1]) << 16;
+    *reinterpret_cast<u4*>(dst) = u4{o[0], o[1], o[2], o[3]};
+}
+
 __device__ __forceinline__ void store8(float* dst, const float (&v)[8]) {
     *reinterpret_cast<f4*>(dst) = f4{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f4*>(dst + 4) = f4{v[4], v[5], v[6], v[7]};
+}
+
+// Output element o of the call as its out_dtype, in kernels instantiated apart for fp16 outputs (F16) and for bf16 /
+// fp32 ones.
+template <bool F16>
+__device__ __forceinline__ void put_out(const Args& p, int64_t o, float v) {
+    if constexpr (F16)
+        reinterpret_cast<_Float16*>(p.out)[o] = (_Float16)v;
+    else if (p.out_dtype == W6A16_OUT_F32)
+        reinterpret_cast<float*>(p.out)[o] = v;
+    else
+        reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)v;
 }
 
 // Device-coherent accesses to the split-K partials: relaxed atomics at agent scope, which the compiler emits as
@@ -155,7 +209,7 @@ __device__ __forceinline__ void load_stage(const Args& p, int b, int m0, int n0,
 }
 
 // Contract one chunk into acc: stage it in the wave's LDS buffer, read it back transposed, dequantise, MFMA.
-template <int MT>
+template <class A, int MT>
 __device__ __forceinline__ void process_stage(const Stage<MT>& s, uint8_t* buf, f4 (&acc)[MT][kTiles]) {
     const int lane = threadIdx.x & 63, q = lane >> 4, i = lane & 15;
     const int seg = lane & 7, rr = lane >> 3;
@@ -168,12 +222,12 @@ __device__ __forceinline__ void process_stage(const Stage<MT>& s, uint8_t* buf, 
     }
     *reinterpret_cast<uint32_t*>(buf + kScaleOff + 4 * lane) = s.sc;
     wave_lds_sync();
-    const bf8 bias = __builtin_bit_cast(bf8, u4{0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u});  // -160
+    const u4 bias = u4{A::kBias, A::kBias, A::kBias, A::kBias};  // -(2^e + 32)
     f4 corr[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), bias, f4{0.f, 0.f, 0.f, 0.f});
-        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), bias, corr[mt]);
+        corr[mt] = A::mma(s.a[mt][0], bias, f4{0.f, 0.f, 0.f, 0.f});
+        corr[mt] = A::mma(s.a[mt][1], bias, corr[mt]);
     }
     const int sel = 2 * (q >> 1);  // hi-plane field of rows 8 q .. (first half); the second half's is 4 bits up
     const int r = lane & 15;
@@ -197,23 +251,23 @@ __device__ __forceinline__ void process_stage(const Stage<MT>& s, uint8_t* buf, 
             const uint32_t L = (uint32_t)lov[d], Hs = (uint32_t)hiv[d] >> sel;
             const uint32_t u0 = (L & 0x0F0F0F0Fu) | ((Hs & 0x03030303u) << 4);          // rows 8 q + e
             const uint32_t u1 = ((L >> 4) & 0x0F0F0F0Fu) | (Hs & 0x30303030u);          // rows 32 + 8 q + e
-            codes_to_bf16(u0, o0[2 * d], o0[2 * d + 1]);
-            codes_to_bf16(u1, o1[2 * d], o1[2 * d + 1]);
+            codes_to_op<A>(u0, o0[2 * d], o0[2 * d + 1]);
+            codes_to_op<A>(u1, o1[2 * d], o1[2 * d + 1]);
         }
-        const bf8 w0 = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
-        const bf8 w1 = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+        const u4 w0 = u4{o0[0], o0[1], o0[2], o0[3]};
+        const u4 w1 = u4{o1[0], o1[1], o1[2], o1[3]};
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            f4 tc = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), w0, corr[mt]);
-            tc = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), w1, tc);
+            f4 tc = A::mma(s.a[mt][0], w0, corr[mt]);
+            tc = A::mma(s.a[mt][1], w1, tc);
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[mt][t][v] += tc[v] * sv;
         }
     }
 }
 
-template <int MT>
-__device__ __forceinline__ void store_tile(const Args& p, int b, int m0, int n0, const f4 (&acc)[MT][kTiles]) {
+template <int MT, bool F16>
+__device__ __forceinline__ void store_tile_as(const Args& p, int b, int m0, int n0, const f4 (&acc)[MT][kTiles]) {
     const int lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
     // lane (i, q) holds C[m0 + 16 mt + 4 q + v][n0 + 16 t + i]
 #pragma unroll
@@ -225,20 +279,23 @@ __device__ __forceinline__ void store_tile(const Args& p, int b, int m0, int n0,
             for (int v = 0; v < 4; ++v) {
                 const int m = m0 + 16 * mt + 4 * q + v;
                 if (n >= p.N || m >= p.M) continue;
-                const int64_t o = (int64_t)b * p.so_b + (int64_t)m * p.so_m + n;
-                if (p.out_dtype == W6A16_OUT_F32)
-                    reinterpret_cast<float*>(p.out)[o] = acc[mt][t][v];
-                else
-                    reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)acc[mt][t][v];
+                put_out<F16>(p, (int64_t)b * p.so_b + (int64_t)m * p.so_m + n, acc[mt][t][v]);
             }
         }
+}
+template <int MT>
+__device__ __forceinline__ void store_tile(const Args& p, int b, int m0, int n0, const f4 (&acc)[MT][kTiles]) {
+    if (p.out_dtype == W6A16_OUT_F16)
+        store_tile_as<MT, true>(p, b, m0, n0, acc);
+    else
+        store_tile_as<MT, false>(p, b, m0, n0, acc);
 }
 
 // Split-K reduction of rows r0 .. r0 + R - 1 (those below `rows`) of a tile whose partials lie at `part`: lane l sums
 // columns 2 l, 2 l + 1 split by split in order 0, 1, ... and stores the result.  The loads of R rows x 8 splits are
 // issued together (each batch waits about one memory latency); rows past `rows` and splits past split_k re-read
 // valid entries whose values are not used.
-template <int R>
+template <int R, bool F16>
 __device__ __forceinline__ void reduce_rows(const Args& p, const float* part, int tile_floats, int r0, int rows,
                                             int b, int m0, int n0) {
     const int lane = threadIdx.x & 63;
@@ -271,13 +328,8 @@ __device__ __forceinline__ void reduce_rows(const Args& p, const float* part, in
     for (int j = 0; j < R; ++j) {
         if (r0 + j >= rows || n >= p.N) continue;
         const int64_t o = ob + (int64_t)(m0 + r0 + j) * p.so_m + n;
-        if (p.out_dtype == W6A16_OUT_F32) {
-            reinterpret_cast<float*>(p.out)[o] = s[j].x;
-            reinterpret_cast<float*>(p.out)[o + 1] = s[j].y;
-        } else {
-            reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)s[j].x;
-            reinterpret_cast<__bf16*>(p.out)[o + 1] = (__bf16)s[j].y;
-        }
+        put_out<F16>(p, o, s[j].x);
+        put_out<F16>(p, o + 1, s[j].y);
     }
 }
 
@@ -309,10 +361,19 @@ __device__ __forceinline__ void reduce_tile(const Args& p, int64_t tile, int b, 
     constexpr int kTileFloats = 16 * MT * kTileN;
     const float* const part = p.part + tile * p.split_k * kTileFloats;
     const int rows = min(16 * MT, p.M - m0);
-    if (rows == 1)
-        reduce_rows<1>(p, part, kTileFloats, 0, 1, b, m0, n0);
-    else
-        for (int r0 = 0; r0 < rows; r0 += 4) reduce_rows<4>(p, part, kTileFloats, r0, rows, b, m0, n0);
+    const bool f16 = p.out_dtype == W6A16_OUT_F16;
+    if (rows == 1) {
+        if (f16)
+            reduce_rows<1, true>(p, part, kTileFloats, 0, 1, b, m0, n0);
+        else
+            reduce_rows<1, false>(p, part, kTileFloats, 0, 1, b, m0, n0);
+    } else {
+        for (int r0 = 0; r0 < rows; r0 += 4)
+            if (f16)
+                reduce_rows<4, true>(p, part, kTileFloats, r0, rows, b, m0, n0);
+            else
+                reduce_rows<4, false>(p, part, kTileFloats, r0, rows, b, m0, n0);
+    }
     if (lane == 0) __hip_atomic_store(p.cnt + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
@@ -356,14 +417,14 @@ __device__ __forceinline__ void load_pstage(const Args& p, int b, int m0, int st
     s.sc = *reinterpret_cast<const u4*>(p.sc + (int64_t)b * p.ss_b + ((int64_t)strip * groups + g) * kTileN + 8 * i);
 }
 
-template <int MT>
+template <class A, int MT>
 __device__ __forceinline__ void process_pstage(const PStage<MT>& s, f4 (&acc)[MT][kTiles]) {
-    const bf8 bias = __builtin_bit_cast(bf8, u4{0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u});  // -160
+    const u4 bias = u4{A::kBias, A::kBias, A::kBias, A::kBias};  // -(2^e + 32)
     f4 corr[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), bias, f4{0.f, 0.f, 0.f, 0.f});
-        corr[mt] = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), bias, corr[mt]);
+        corr[mt] = A::mma(s.a[mt][0], bias, f4{0.f, 0.f, 0.f, 0.f});
+        corr[mt] = A::mma(s.a[mt][1], bias, corr[mt]);
     }
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
@@ -374,17 +435,17 @@ __device__ __forceinline__ void process_pstage(const PStage<MT>& s, f4 (&acc)[MT
         const uint32_t u1a = ((L0 >> 4) & 0x0F0F0F0Fu) | ((Hd & 0x0C0C0C0Cu) << 2);  // rows 32 + 8 q + 0..3
         const uint32_t u1b = ((L1 >> 4) & 0x0F0F0F0Fu) | ((Hd >> 2) & 0x30303030u);  // rows 32 + 8 q + 4..7
         uint32_t o0[4], o1[4];
-        codes_to_bf16(u0a, o0[0], o0[1]);
-        codes_to_bf16(u0b, o0[2], o0[3]);
-        codes_to_bf16(u1a, o1[0], o1[1]);
-        codes_to_bf16(u1b, o1[2], o1[3]);
-        const bf8 w0 = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
-        const bf8 w1 = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+        codes_to_op<A>(u0a, o0[0], o0[1]);
+        codes_to_op<A>(u0b, o0[2], o0[3]);
+        codes_to_op<A>(u1a, o1[0], o1[1]);
+        codes_to_op<A>(u1b, o1[2], o1[3]);
+        const u4 w0 = u4{o0[0], o0[1], o0[2], o0[3]};
+        const u4 w1 = u4{o1[0], o1[1], o1[2], o1[3]};
         const float sv = h2f((uint16_t)(s.sc[t >> 1] >> (16 * (t & 1))));
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-            f4 tc = mfma(__builtin_bit_cast(bf8, s.a[mt][0]), w0, corr[mt]);
-            tc = mfma(__builtin_bit_cast(bf8, s.a[mt][1]), w1, tc);
+            f4 tc = A::mma(s.a[mt][0], w0, corr[mt]);
+            tc = A::mma(s.a[mt][1], w1, tc);
 #pragma unroll
             for (int v = 0; v < 4; ++v) acc[mt][t][v] += tc[v] * sv;
         }
@@ -392,7 +453,7 @@ __device__ __forceinline__ void process_pstage(const PStage<MT>& s, f4 (&acc)[MT
 }
 
 // Narrow kernel (M <= 32), both weight formats: a workgroup of four wavefronts, one per 128-column strip.
-template <int MT, int D, bool PACKED>
+template <class A, int MT, int D, bool PACKED>
 __global__ __launch_bounds__(64 * kStrips) void w6a16_kernel(const Args p) {
     constexpr int kStage = PACKED ? 16 : kStrips * kBuf;  // planes: each wavefront's staging buffer
     __shared__ __attribute__((aligned(16))) uint8_t lds[kStage];
@@ -427,8 +488,8 @@ __global__ __launch_bounds__(64 * kStrips) void w6a16_kernel(const Args p) {
             else load_stage<MT>(p, b, m0, n0, c, x);
         };
         auto work = [&](const S& x) {
-            if constexpr (PACKED) process_pstage<MT>(x, acc);
-            else process_stage<MT>(x, buf, acc);
+            if constexpr (PACKED) process_pstage<A, MT>(x, acc);
+            else process_stage<A, MT>(x, buf, acc);
         };
 #pragma unroll
         for (int j = 0; j < D; ++j) load(min(c0 + j, c1 - 1), st[j]);
@@ -516,10 +577,11 @@ __device__ __forceinline__ void load_phalf(const Args& p, int b, int m0, int str
                                            4 * h);
 }
 
+template <class A>
 __device__ __forceinline__ void process_phalf(const PHalf& s, f4 (&acc)[1][4]) {
-    const bf8 bias = __builtin_bit_cast(bf8, u4{0xC320C320u, 0xC320C320u, 0xC320C320u, 0xC320C320u});  // -160
-    f4 corr = mfma(__builtin_bit_cast(bf8, s.a[0]), bias, f4{0.f, 0.f, 0.f, 0.f});
-    corr = mfma(__builtin_bit_cast(bf8, s.a[1]), bias, corr);
+    const u4 bias = u4{A::kBias, A::kBias, A::kBias, A::kBias};  // -(2^e + 32)
+    f4 corr = A::mma(s.a[0], bias, f4{0.f, 0.f, 0.f, 0.f});
+    corr = A::mma(s.a[1], bias, corr);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         const uint32_t L0 = s.w[t >> 1][2 * (t & 1)], L1 = s.w[t >> 1][2 * (t & 1) + 1];
@@ -529,15 +591,15 @@ __device__ __forceinline__ void process_phalf(const PHalf& s, f4 (&acc)[1][4]) {
         const uint32_t u1a = ((L0 >> 4) & 0x0F0F0F0Fu) | ((Hd & 0x0C0C0C0Cu) << 2);
         const uint32_t u1b = ((L1 >> 4) & 0x0F0F0F0Fu) | ((Hd >> 2) & 0x30303030u);
         uint32_t o0[4], o1[4];
-        codes_to_bf16(u0a, o0[0], o0[1]);
-        codes_to_bf16(u0b, o0[2], o0[3]);
-        codes_to_bf16(u1a, o1[0], o1[1]);
-        codes_to_bf16(u1b, o1[2], o1[3]);
-        const bf8 w0 = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
-        const bf8 w1 = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+        codes_to_op<A>(u0a, o0[0], o0[1]);
+        codes_to_op<A>(u0b, o0[2], o0[3]);
+        codes_to_op<A>(u1a, o1[0], o1[1]);
+        codes_to_op<A>(u1b, o1[2], o1[3]);
+        const u4 w0 = u4{o0[0], o0[1], o0[2], o0[3]};
+        const u4 w1 = u4{o1[0], o1[1], o1[2], o1[3]};
         const float sv = h2f((uint16_t)((t >> 1 ? s.sc.y : s.sc.x) >> (16 * (t & 1))));
-        f4 tc = mfma(__builtin_bit_cast(bf8, s.a[0]), w0, corr);
-        tc = mfma(__builtin_bit_cast(bf8, s.a[1]), w1, tc);
+        f4 tc = A::mma(s.a[0], w0, corr);
+        tc = A::mma(s.a[1], w1, tc);
 #pragma unroll
         for (int v = 0; v < 4; ++v) acc[0][t][v] += tc[v] * sv;
     }
@@ -553,7 +615,20 @@ constexpr int kGemvMaxSplit = 8;
 constexpr int kGemvPart = kGemvMaxSplit * 16 * kTileN * 4;  // fp32 partial tiles [split][16 rows][128 columns]
 constexpr int kGemvLds = kGemvMaxSplit * kBuf > kGemvPart ? kGemvMaxSplit * kBuf : kGemvPart;
 
-template <int D, bool PACKED, int NT>
+// The gemv epilogue: output element (r, col) of the tile is the sum of the ks wavefront partials in `part`.
+template <int NC, bool F16>
+__device__ __forceinline__ void gemv_sum_store(const Args& p, const float* part, int rows, int ks, int b, int m0,
+                                               int n0) {
+    for (int e = threadIdx.x; e < rows * NC; e += blockDim.x) {
+        const int r = e / NC, col = e % NC, n = n0 + col;
+        float sum = 0.f;
+        for (int w = 0; w < ks; ++w) sum += part[(w * 16 + r) * NC + col];
+        if (n >= p.N) continue;
+        put_out<F16>(p, (int64_t)b * p.so_b + (int64_t)(m0 + r) * p.so_m + n, sum);
+    }
+}
+
+template <class A, int D, bool PACKED, int NT>
 __global__ __launch_bounds__(64 * kGemvMaxSplit) void w6a16_gemv_kernel(const Args p) {
     static_assert(NT == kTiles || (NT == 4 && PACKED), "half strips: packed layout only");
     constexpr int MT = 1, NC = 16 * NT;  // NC: columns per workgroup
@@ -581,9 +656,9 @@ __global__ __launch_bounds__(64 * kGemvMaxSplit) void w6a16_gemv_kernel(const Ar
             else load_stage<MT>(p, b, m0, n0, c, x);
         };
         auto work = [&](const S& x) {
-            if constexpr (PACKED && NT == 4) process_phalf(x, acc);
-            else if constexpr (PACKED) process_pstage<MT>(x, acc);
-            else process_stage<MT>(x, buf, acc);
+            if constexpr (PACKED && NT == 4) process_phalf<A>(x, acc);
+            else if constexpr (PACKED) process_pstage<A, MT>(x, acc);
+            else process_stage<A, MT>(x, buf, acc);
         };
 #pragma unroll
         for (int j = 0; j < D; ++j) load(min(c0 + j, c1 - 1), st[j]);
@@ -621,17 +696,10 @@ __global__ __launch_bounds__(64 * kGemvMaxSplit) void w6a16_gemv_kernel(const Ar
     }
     __syncthreads();
     const int rows = min(16, p.M - m0), ks = p.split_k;
-    for (int e = threadIdx.x; e < rows * NC; e += blockDim.x) {
-        const int r = e / NC, col = e % NC, n = n0 + col;
-        float sum = 0.f;
-        for (int w = 0; w < ks; ++w) sum += part[(w * 16 + r) * NC + col];
-        if (n >= p.N) continue;
-        const int64_t o = (int64_t)b * p.so_b + (int64_t)(m0 + r) * p.so_m + n;
-        if (p.out_dtype == W6A16_OUT_F32)
-            reinterpret_cast<float*>(p.out)[o] = sum;
-        else
-            reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)sum;
-    }
+    if (p.out_dtype == W6A16_OUT_F16)
+        gemv_sum_store<NC, true>(p, part, rows, ks, b, m0, n0);
+    else
+        gemv_sum_store<NC, false>(p, part, rows, ks, b, m0, n0);
 }
 
 // ---------------------------------------------------------------------------------------------------------------
@@ -655,7 +723,6 @@ __global__ __launch_bounds__(64 * kGemvMaxSplit) void w6a16_gemv_kernel(const Ar
 // Split-K (when used): one partial tile per (tile, split) in the accumulators' register layout, one release per
 // workgroup; the last split adds the others to its own registers in split order.
 constexpr int kCachePolicySC1 = 16;  // buffer instructions' cache-policy bit sc1: device-scope write-through
-constexpr int kRowSumBias = -160;    // 128 + u - 160 = q
 constexpr int kPlaneBytes = kBuf;    // planes: the chunk's 48 plane rows and 128 scales, as in the narrow kernel
 
 template <int MTW>
@@ -669,24 +736,24 @@ __device__ __forceinline__ int a_slot(int r, int j) { return 8 * r + (j ^ ((r >>
 
 using wkv7::unroll;  // f(integral_constant<0>), .., f(integral_constant<N - 1>)
 
-typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
-
-// (1, 1) as a bf16 pair held in a register (an empty asm keeps the compiler from folding the pair into an inline
-// constant, which the packed bf16 dot product would read differently).
-__device__ __forceinline__ bf2 ones_bf16x2() {
-    uint32_t bits = 0x3F803F80u;
+// (1, 1) as an activation pair held in a register (an empty asm keeps the compiler from folding the pair into an
+// inline constant, which the packed dot product would read differently).
+template <class A>
+__device__ __forceinline__ uint32_t ones_x2() {
+    uint32_t bits = A::kOnes;
     asm("" : "+v"(bits));
-    return __builtin_bit_cast(bf2, bits);
+    return bits;
 }
 
-__device__ __forceinline__ float sum8_bf16(const u4 v, bf2 one) {
+template <class A>
+__device__ __forceinline__ float sum8(const u4 v, uint32_t one) {
     float x = 0.f;
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
         // the element is copied out first: bit-casting a vector element in place (v[d]) compiled to a read of
         // element 0 for every d
         const uint32_t word = v[d];
-        x = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2, word), one, x, false);
+        x = A::dot2(word, one, x);
     }
     return x;
 }
@@ -696,9 +763,10 @@ __device__ __forceinline__ float dpp_add(float x) {  // x + x of the lane DPP co
     return x + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
 }
 
-// Row sums of A per chain of 64 CG k: rsum[b][chain][m] = -160 sum A[b][m][chain 64 CG .. + 64 CG - 1], zero for
+// Row sums of A per chain of 64 CG k: rsum[b][chain][m] = -(2^e + 32) sum A[b][m][chain 64 CG .. + 64 CG - 1], zero for
 // rows M <= m < mpad.  One wavefront per (row, 512-element segment of K; 8 bf16 per lane, coalesced); the 8 CG lanes
 // of a chain add their sums with DPP in a fixed order.
+template <class A>
 __global__ __launch_bounds__(256) void w6a16_rowsum_kernel(const Args p) {
     const int lane = threadIdx.x & 63;
     const int m = blockIdx.x * 4 + (threadIdx.x >> 6), k = blockIdx.y * 512 + 8 * lane, b = blockIdx.z;
@@ -706,13 +774,13 @@ __global__ __launch_bounds__(256) void w6a16_rowsum_kernel(const Args p) {
     const int lanes_per_chain = 8 * p.chain_k / 64;  // 8 or 16
     const uint16_t* const row = p.a + (int64_t)b * p.sa_b + (int64_t)min(m, p.M - 1) * p.sa_m;
     // K is a multiple of 64 CG: a chain's lanes are all inside K or all past it
-    float x = (m < p.M && k < p.K) ? sum8_bf16(*reinterpret_cast<const u4*>(row + k), ones_bf16x2()) : 0.f;
+    float x = (m < p.M && k < p.K) ? sum8<A>(*reinterpret_cast<const u4*>(row + k), ones_x2<A>()) : 0.f;
     x = dpp_add<0xB1>(x);   // lanes ^ 1
     x = dpp_add<0x4E>(x);   // lanes ^ 2: each lane holds its quad's sum
     x = dpp_add<0x141>(x);  // half-row mirror: lane 7 - l of the 8-lane group, in the other quad
     if (lanes_per_chain == 16) x = dpp_add<0x140>(x);  // row mirror: lane 15 - l, in the other half
     if ((lane & (lanes_per_chain - 1)) == 0 && k < p.K)
-        p.rsum[((int64_t)b * p.nchains + k / p.chain_k) * p.mpad + m] = (float)kRowSumBias * x;
+        p.rsum[((int64_t)b * p.nchains + k / p.chain_k) * p.mpad + m] = -A::kOffset * x;
 }
 
 // The chunk schedule of one workgroup: its split's range of chains, cut into KP contiguous parts.
@@ -871,8 +939,8 @@ __device__ __forceinline__ f4 fma4(const f4 x, float s, const f4 a) {
 
 // Dequantise the wavefront's two column tiles of one chunk into B operands w0 (rows 0..31 of the chunk) and w1
 // (rows 32..63), and their scales.
-template <int MTW, bool PACKED>
-__device__ __forceinline__ void wide_dequant(const uint8_t* ps, const WideW& w, bf8 (&w0)[2], bf8 (&w1)[2],
+template <class A, int MTW, bool PACKED>
+__device__ __forceinline__ void wide_dequant(const uint8_t* ps, const WideW& w, u4 (&w0)[2], u4 (&w1)[2],
                                              float (&sv)[2]) {
     const int lane = threadIdx.x & 63, cp = (threadIdx.x >> 6) & 3;
     const int i = lane & 15, q = lane >> 4;
@@ -886,12 +954,12 @@ __device__ __forceinline__ void wide_dequant(const uint8_t* ps, const WideW& w, 
             const uint32_t u1a = ((L0 >> 4) & 0x0F0F0F0Fu) | ((Hd & 0x0C0C0C0Cu) << 2);  // rows 32 + 8 q + 0..3
             const uint32_t u1b = ((L1 >> 4) & 0x0F0F0F0Fu) | ((Hd >> 2) & 0x30303030u);  // rows 32 + 8 q + 4..7
             uint32_t o0[4], o1[4];
-            codes_to_bf16(u0a, o0[0], o0[1]);
-            codes_to_bf16(u0b, o0[2], o0[3]);
-            codes_to_bf16(u1a, o1[0], o1[1]);
-            codes_to_bf16(u1b, o1[2], o1[3]);
-            w0[tt] = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
-            w1[tt] = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+            codes_to_op<A>(u0a, o0[0], o0[1]);
+            codes_to_op<A>(u0b, o0[2], o0[3]);
+            codes_to_op<A>(u1a, o1[0], o1[1]);
+            codes_to_op<A>(u1b, o1[2], o1[3]);
+            w0[tt] = u4{o0[0], o0[1], o0[2], o0[3]};
+            w1[tt] = u4{o1[0], o1[1], o1[2], o1[3]};
             sv[tt] = h2f((uint16_t)(w.sc >> (16 * tt)));
         }
     } else {
@@ -916,11 +984,11 @@ __device__ __forceinline__ void wide_dequant(const uint8_t* ps, const WideW& w, 
                 const uint32_t L = (uint32_t)lo_t[tt][d], Hs = (uint32_t)hi_t[tt][d] >> sel;
                 const uint32_t u0 = (L & 0x0F0F0F0Fu) | ((Hs & 0x03030303u) << 4);   // rows 8 q + e
                 const uint32_t u1 = ((L >> 4) & 0x0F0F0F0Fu) | (Hs & 0x30303030u);   // rows 32 + 8 q + e
-                codes_to_bf16(u0, o0[2 * d], o0[2 * d + 1]);
-                codes_to_bf16(u1, o1[2 * d], o1[2 * d + 1]);
+                codes_to_op<A>(u0, o0[2 * d], o0[2 * d + 1]);
+                codes_to_op<A>(u1, o1[2 * d], o1[2 * d + 1]);
             }
-            w0[tt] = __builtin_bit_cast(bf8, u4{o0[0], o0[1], o0[2], o0[3]});
-            w1[tt] = __builtin_bit_cast(bf8, u4{o1[0], o1[1], o1[2], o1[3]});
+            w0[tt] = u4{o0[0], o0[1], o0[2], o0[3]};
+            w1[tt] = u4{o1[0], o1[1], o1[2], o1[3]};
             sv[tt] = h2f(sh[tt]);
         }
     }
@@ -931,26 +999,26 @@ __device__ __forceinline__ void wide_dequant(const uint8_t* ps, const WideW& w, 
 // ahead of the work that hides them (the first batch ahead of the dequantisation, each further batch ahead of the
 // previous batch's MFMAs), with scheduling barriers keeping that order: left to itself the compiler reused a few
 // operand registers and waited on the LDS once per M tile.
-template <int MTW, bool PACKED, bool FIRST, bool LAST>
+template <class A, int MTW, bool PACKED, bool FIRST, bool LAST>
 __device__ __forceinline__ void wide_compute(const uint8_t* ps, const WideW& w, f4 (&tc)[MTW][2], f4 (&acc)[MTW][2]) {
     constexpr int MB = MTW < 4 ? MTW : 4;  // M tiles per batch of LDS reads
     const int lane = threadIdx.x & 63;
     const int i = lane & 15, q = lane >> 4;
     const float* const rsum = reinterpret_cast<const float*>(ps + part_a_bytes<MTW>());
-    bf8 a0[MB], a1[MB], w0[2], w1[2];
+    u4 a0[MB], a1[MB], w0[2], w1[2];
     f4 nc[MB];
     float sv[2];
     auto read = [&](int mb) __attribute__((always_inline)) {
 #pragma unroll
         for (int k = 0; k < MB; ++k) {
             const int mt = mb + k;
-            a0[k] = *reinterpret_cast<const bf8*>(ps + 16 * a_slot(16 * mt + i, q));
-            a1[k] = *reinterpret_cast<const bf8*>(ps + 16 * a_slot(16 * mt + i, 4 + q));
+            a0[k] = *reinterpret_cast<const u4*>(ps + 16 * a_slot(16 * mt + i, q));
+            a1[k] = *reinterpret_cast<const u4*>(ps + 16 * a_slot(16 * mt + i, 4 + q));
             if constexpr (FIRST) nc[k] = *reinterpret_cast<const f4*>(rsum + 16 * mt + 4 * q);  // rows 16 mt + 4 q + v
         }
     };
     read(0);
-    wide_dequant<MTW, PACKED>(ps, w, w0, w1, sv);
+    wide_dequant<A, MTW, PACKED>(ps, w, w0, w1, sv);
 #pragma unroll
     for (int mb = 0; mb < MTW; mb += MB) {
         __builtin_amdgcn_sched_barrier(0);
@@ -958,8 +1026,8 @@ __device__ __forceinline__ void wide_compute(const uint8_t* ps, const WideW& w, 
         for (int k = 0; k < MB; ++k)
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                const f4 c = mfma(a0[k], w0[tt], FIRST ? nc[k] : tc[mb + k][tt]);
-                tc[mb + k][tt] = mfma(a1[k], w1[tt], c);
+                const f4 c = A::mma(a0[k], w0[tt], FIRST ? nc[k] : tc[mb + k][tt]);
+                tc[mb + k][tt] = A::mma(a1[k], w1[tt], c);
             }
         if (mb + MB < MTW) read(mb + MB);
     }
@@ -972,8 +1040,8 @@ __device__ __forceinline__ void wide_compute(const uint8_t* ps, const WideW& w, 
 }
 
 // lane (i, q) of wavefront cp holds C[m0 + 16 mt + 4 q + v][n0 + 16 (2 cp + tt) + i]
-template <int MTW>
-__device__ __forceinline__ void wide_store(const Args& p, int b, int m0, int n0, const f4 (&acc)[MTW][2]) {
+template <int MTW, bool F16>
+__device__ __forceinline__ void wide_store_as(const Args& p, int b, int m0, int n0, const f4 (&acc)[MTW][2]) {
     const int lane = threadIdx.x & 63, cp = (threadIdx.x >> 6) & 3;
     const int i = lane & 15, q = lane >> 4;
 #pragma unroll
@@ -985,16 +1053,19 @@ __device__ __forceinline__ void wide_store(const Args& p, int b, int m0, int n0,
             for (int v = 0; v < 4; ++v) {
                 const int m = m0 + 16 * mt + 4 * q + v;
                 if (n >= p.N || m >= p.M) continue;
-                const int64_t o = (int64_t)b * p.so_b + (int64_t)m * p.so_m + n;
-                if (p.out_dtype == W6A16_OUT_F32)
-                    reinterpret_cast<float*>(p.out)[o] = acc[mt][tt][v];
-                else
-                    reinterpret_cast<__bf16*>(p.out)[o] = (__bf16)acc[mt][tt][v];
+                put_out<F16>(p, (int64_t)b * p.so_b + (int64_t)m * p.so_m + n, acc[mt][tt][v]);
             }
         }
 }
+template <int MTW>
+__device__ __forceinline__ void wide_store(const Args& p, int b, int m0, int n0, const f4 (&acc)[MTW][2]) {
+    if (p.out_dtype == W6A16_OUT_F16)
+        wide_store_as<MTW, true>(p, b, m0, n0, acc);
+    else
+        wide_store_as<MTW, false>(p, b, m0, n0, acc);
+}
 
-template <int MTW, int KP, int CG, int D, int NL, bool PACKED>
+template <class A, int MTW, int KP, int CG, int D, int NL, bool PACKED>
 __global__ __launch_bounds__(256 * KP) void w6a16_wide_kernel(const Args p) {
     constexpr int PB = part_bytes<MTW, PACKED>(), kStage = KP * PB;
     constexpr int kRed = (KP - 1) * 4 * MTW * 2 * 64 * 16;  // K-part partials in LDS
@@ -1055,7 +1126,7 @@ __global__ __launch_bounds__(256 * KP) void w6a16_wide_kernel(const Args p) {
             constexpr int j = decltype(J)::value;
             const int s = base + j;
             const uint8_t* const ps = lds + (j & 1) * kStage + kp * PB;
-            if (s < mine_n) wide_compute<MTW, PACKED, j % CG == 0, j % CG == CG - 1>(ps, ws[j], tc, acc);
+            if (s < mine_n) wide_compute<A, MTW, PACKED, j % CG == 0, j % CG == CG - 1>(ps, ws[j], tc, acc);
             if constexpr (PACKED) wide_load_w(p, src, S.chunk(src.kp, s + D), ws[j]);
             wide_store_lds<MTW, KP, PACKED>(ls[(j + 1) % NL], lds + ((j + 1) & 1) * kStage);
             wide_load_lds<MTW, KP, PACKED>(p, S, src, s + 1 + NL, ls[(j + 1) % NL]);
@@ -1367,7 +1438,9 @@ int validate(const w6a16_args* a) {
     if (a->B < 1 || a->M < 0 || a->N < 1 || a->K < 64 || a->K % 64 || a->N % 16) return WKV7_ERR_SHAPE;
     if (a->group_k < 64 || a->group_k % 64 || a->K % a->group_k) return WKV7_ERR_SHAPE;
     if (a->split_k < 1 || a->split_k > 256) return WKV7_ERR_ARG;
-    if (a->out_dtype != W6A16_OUT_BF16 && a->out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
+    if (a->out_dtype != W6A16_OUT_BF16 && a->out_dtype != W6A16_OUT_F16 && a->out_dtype != W6A16_OUT_F32)
+        return WKV7_ERR_ARG;
+    if (a->a_dtype != W6A16_IN_BF16 && a->a_dtype != W6A16_IN_F16) return WKV7_ERR_ARG;
     if (a->M == 0) return WKV7_OK;
     if (a->format != W6A16_FORMAT_PLANES && a->format != W6A16_FORMAT_PACKED) return WKV7_ERR_ARG;
     const bool packed = a->format == W6A16_FORMAT_PACKED;
@@ -1391,46 +1464,63 @@ int validate(const w6a16_args* a) {
     return WKV7_OK;
 }
 
-template <int D, int DH>
+template <class A, int D, int DH>
 void launch_gemv(const Args& p, const Layout& l, bool packed, hipStream_t s) {
     const dim3 block(64 * p.split_k);
     if (packed && l.gemv_half)
-        hipLaunchKernelGGL((w6a16_gemv_kernel<DH, true, 4>), dim3(2 * l.n_strips, 1, p.B * l.m_groups), block, 0, s,
+        hipLaunchKernelGGL((w6a16_gemv_kernel<A, DH, true, 4>), dim3(2 * l.n_strips, 1, p.B * l.m_groups), block, 0, s,
                            p);
     else if (packed)
-        hipLaunchKernelGGL((w6a16_gemv_kernel<D, true, kTiles>), dim3(l.n_strips, 1, p.B * l.m_groups), block, 0, s,
+        hipLaunchKernelGGL((w6a16_gemv_kernel<A, D, true, kTiles>), dim3(l.n_strips, 1, p.B * l.m_groups), block, 0, s,
                            p);
     else
-        hipLaunchKernelGGL((w6a16_gemv_kernel<D, false, kTiles>), dim3(l.n_strips, 1, p.B * l.m_groups), block, 0, s,
+        hipLaunchKernelGGL((w6a16_gemv_kernel<A, D, false, kTiles>), dim3(l.n_strips, 1, p.B * l.m_groups), block, 0, s,
                            p);
 }
 
-template <int MT, int D>
+template <class A, int MT, int D>
 void launch(const Args& p, const Layout& l, bool packed, hipStream_t s) {
     const dim3 grid((l.n_strips + kStrips - 1) / kStrips, p.split_k, p.B * l.m_groups);
     if (packed)
-        hipLaunchKernelGGL((w6a16_kernel<MT, D, true>), grid, dim3(64 * kStrips), 0, s, p);
+        hipLaunchKernelGGL((w6a16_kernel<A, MT, D, true>), grid, dim3(64 * kStrips), 0, s, p);
     else
-        hipLaunchKernelGGL((w6a16_kernel<MT, D, false>), grid, dim3(64 * kStrips), 0, s, p);
+        hipLaunchKernelGGL((w6a16_kernel<A, MT, D, false>), grid, dim3(64 * kStrips), 0, s, p);
 }
 
-template <int MTW, int KP, int CG>
+template <class A, int MTW, int KP, int CG>
 void launch_wide(const Args& p, const Layout& l, bool packed, hipStream_t s) {
     constexpr int D = 4, NL = 4;  // packed weights D steps ahead; NL register stages of the LDS ring
-    hipLaunchKernelGGL(w6a16_rowsum_kernel, dim3(l.mpad / 4, (p.K + 511) / 512, p.B), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(w6a16_rowsum_kernel<A>, dim3(l.mpad / 4, (p.K + 511) / 512, p.B), dim3(256), 0, s, p);
     const dim3 grid(8 * l.m_groups * ((l.n_strips + 7) / 8), p.split_k, p.B);
     if (packed)
-        hipLaunchKernelGGL((w6a16_wide_kernel<MTW, KP, CG, D, NL, true>), grid, dim3(256 * KP), 0, s, p);
+        hipLaunchKernelGGL((w6a16_wide_kernel<A, MTW, KP, CG, D, NL, true>), grid, dim3(256 * KP), 0, s, p);
     else
-        hipLaunchKernelGGL((w6a16_wide_kernel<MTW, KP, CG, D, NL, false>), grid, dim3(256 * KP), 0, s, p);
+        hipLaunchKernelGGL((w6a16_wide_kernel<A, MTW, KP, CG, D, NL, false>), grid, dim3(256 * KP), 0, s, p);
 }
 
-template <int MTW, int KP>
+template <class A, int MTW, int KP>
 void launch_wide_cg(const Args& p, const Layout& l, bool packed, hipStream_t s) {
     if (l.cg == 2)
-        launch_wide<MTW, KP, 2>(p, l, packed, s);
+        launch_wide<A, MTW, KP, 2>(p, l, packed, s);
     else
-        launch_wide<MTW, KP, 1>(p, l, packed, s);
+        launch_wide<A, MTW, KP, 1>(p, l, packed, s);
+}
+
+// The kernel for the call's shape and layout, with activations of type A.
+template <class A>
+void launch_matmul(const Args& p, const Layout& l, bool packed, hipStream_t s) {
+    if (l.gemv && l.gemv_half && p.split_k <= 4)  // half strips, split <= 4: three chunks in flight
+        launch_gemv<A, 2, 3>(p, l, packed, s);
+    else if (l.gemv)
+        launch_gemv<A, 2, 2>(p, l, packed, s);
+    else if (!l.wide)
+        launch<A, 1, 2>(p, l, packed, s);
+    else if (l.mt == 2)
+        launch_wide_cg<A, 2, 2>(p, l, packed, s);
+    else if (l.kp == 2)
+        launch_wide_cg<A, 4, 2>(p, l, packed, s);
+    else
+        launch_wide_cg<A, 4, 1>(p, l, packed, s);
 }
 
 }  // namespace
@@ -1540,18 +1630,10 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
     }
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const bool packed = a->format == W6A16_FORMAT_PACKED;
-    if (l.gemv && l.gemv_half && p.split_k <= 4)  // half strips, split <= 4: three chunks in flight
-        w6::launch_gemv<2, 3>(p, l, packed, s);
-    else if (l.gemv)
-        w6::launch_gemv<2, 2>(p, l, packed, s);
-    else if (!l.wide)
-        w6::launch<1, 2>(p, l, packed, s);
-    else if (l.mt == 2)
-        w6::launch_wide_cg<2, 2>(p, l, packed, s);
-    else if (l.kp == 2)
-        w6::launch_wide_cg<4, 2>(p, l, packed, s);
+    if (a->a_dtype == W6A16_IN_F16)
+        w6::launch_matmul<w6::ActF16>(p, l, packed, s);
     else
-        w6::launch_wide_cg<4, 1>(p, l, packed, s);
+        w6::launch_matmul<w6::ActBF16>(p, l, packed, s);
     return static_cast<int>(hipGetLastError());
 }
 
@@ -1560,7 +1642,7 @@ int w6a16_dequantize_packed(const void* packed, const uint16_t* packed_scales, v
     if (!packed || !packed_scales || !w) return WKV7_ERR_NULL;
     if (B < 1 || N < 16 || N % 16 || K < 64 || K % 64 || group_k < 64 || group_k % 64 || K % group_k)
         return WKV7_ERR_SHAPE;
-    if (out_dtype != W6A16_OUT_BF16 && out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
+    if (out_dtype != W6A16_OUT_BF16 && out_dtype != W6A16_OUT_F16 && out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
     if (!w6::aligned16(packed) || !w6::aligned16(packed_scales)) return WKV7_ERR_ALIGN;
     if (B > 65535) return WKV7_ERR_SHAPE;
     const int strips = (N + w6::kTileN - 1) / w6::kTileN;
@@ -1571,6 +1653,9 @@ int w6a16_dequantize_packed(const void* packed, const uint16_t* packed_scales, v
     if (out_dtype == W6A16_OUT_F32)
         hipLaunchKernelGGL(w6::w6a16_dequant_packed_kernel<float>, grid, dim3(256), 0, s, pk, packed_scales,
                            static_cast<float*>(w), K, N, group_k, strips, w_batch_stride);
+    else if (out_dtype == W6A16_OUT_F16)
+        hipLaunchKernelGGL(w6::w6a16_dequant_packed_kernel<_Float16>, grid, dim3(256), 0, s, pk, packed_scales,
+                           static_cast<_Float16*>(w), K, N, group_k, strips, w_batch_stride);
     else
         hipLaunchKernelGGL(w6::w6a16_dequant_packed_kernel<__bf16>, grid, dim3(256), 0, s, pk, packed_scales,
                            static_cast<__bf16*>(w), K, N, group_k, strips, w_batch_stride);
@@ -1612,7 +1697,7 @@ int w6a16_dequantize(const uint8_t* lo, const uint8_t* hi, const uint16_t* scale
     if (!lo || !hi || !scales || !w) return WKV7_ERR_NULL;
     if (B < 1 || N < 16 || N % 16 || K < 64 || K % 64 || group_k < 64 || group_k % 64 || K % group_k)
         return WKV7_ERR_SHAPE;
-    if (out_dtype != W6A16_OUT_BF16 && out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
+    if (out_dtype != W6A16_OUT_BF16 && out_dtype != W6A16_OUT_F16 && out_dtype != W6A16_OUT_F32) return WKV7_ERR_ARG;
     if (!w6::aligned16(lo) || !w6::aligned16(hi) || !w6::aligned16(scales) || !w6::aligned16(w) ||
         lo_batch_stride % 16 || hi_batch_stride % 16 || scales_batch_stride % 8 || w_batch_stride % 8)
         return WKV7_ERR_ALIGN;
@@ -1622,6 +1707,10 @@ int w6a16_dequantize(const uint8_t* lo, const uint8_t* hi, const uint16_t* scale
     if (out_dtype == W6A16_OUT_F32)
         hipLaunchKernelGGL(w6::w6a16_dequant_kernel<float>, grid, dim3(256), 0, s, lo, hi, scales,
                            static_cast<float*>(w), K, N, group_k, lo_batch_stride, hi_batch_stride,
+                           scales_batch_stride, w_batch_stride);
+    else if (out_dtype == W6A16_OUT_F16)
+        hipLaunchKernelGGL(w6::w6a16_dequant_kernel<_Float16>, grid, dim3(256), 0, s, lo, hi, scales,
+                           static_cast<_Float16*>(w), K, N, group_k, lo_batch_stride, hi_batch_stride,
                            scales_batch_stride, w_batch_stride);
     else
         hipLaunchKernelGGL(w6::w6a16_dequant_kernel<__bf16>, grid, dim3(256), 0, s, lo, hi, scales,

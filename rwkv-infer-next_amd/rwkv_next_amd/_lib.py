@@ -49,7 +49,10 @@ W6A16_EXPORTED = ("w6a16_args_size", "w6a16_workspace_size", "w6a16_plan_split",
 W6A16_FORMAT_PLANES = 0
 W6A16_FORMAT_PACKED = 1
 W6A16_OUT_BF16 = 0
+W6A16_OUT_F16 = 1
 W6A16_OUT_F32 = 2
+W6A16_IN_BF16 = 0
+W6A16_IN_F16 = 1
 MAX_MOVES = 1024
 
 _vp = ctypes.c_void_p
@@ -110,7 +113,7 @@ class W6a16Args(ctypes.Structure):
         ("workspace", _vp), ("workspace_bytes", ctypes.c_size_t),
         ("B", ctypes.c_int32), ("M", ctypes.c_int32), ("N", ctypes.c_int32), ("K", ctypes.c_int32),
         ("group_k", ctypes.c_int32), ("split_k", ctypes.c_int32), ("out_dtype", ctypes.c_int32),
-        ("format", ctypes.c_int32),
+        ("format", ctypes.c_int32), ("a_dtype", ctypes.c_int32),
     ]
 
 

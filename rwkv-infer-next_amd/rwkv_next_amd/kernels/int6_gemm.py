@@ -21,10 +21,11 @@ fp16 scale, w ~ s q; the code u = q + 32 is split into bit planes per 64-row chu
 Compute: one MFMA kernel for every M up to MAX_M (the reference's reduction form for M = 1 has no counterpart:
 an MFMA with M padded to 16 rows costs the CDNA4 matrix core less than a VALU reduction costs the vector units, and
 the weight bytes, not the arithmetic, bound both).  `use_dot` is accepted for the reference's signature and does
-not change the computation.  Above MAX_M the weight is dequantised once to bf16 and the product goes to the
-library GEMM (hipBLASLt through torch.matmul), which is compute-bound there.
+not change the computation.  Above MAX_M the weight is dequantised once to the activations' type and the product
+goes to the library GEMM (hipBLASLt through torch.matmul), which is compute-bound there.
 
-Activations are bf16; the result is bf16 (fp32 accumulation).  Every call runs on the current stream, no host sync.
+Activations are bf16 (the model's) or fp16 (the reference op takes any a.dtype its dot accepts); the result is
+a.dtype, or out_dtype (fp32 accumulation).  Every call runs on the current stream, no host sync.
 """
 from __future__ import annotations
 
@@ -124,20 +125,24 @@ def _group_k(group_k, K, n_groups):
     return g
 
 
+_OUT_CODES = {torch.bfloat16: _lib.W6A16_OUT_BF16, torch.float16: _lib.W6A16_OUT_F16,
+              torch.float32: _lib.W6A16_OUT_F32}
+_IN_CODES = {torch.bfloat16: _lib.W6A16_IN_BF16, torch.float16: _lib.W6A16_IN_F16}
+
+
 @torch.no_grad()
 def dequantize_int6(lo, hi, sc, group_k, dtype=torch.float32):
-    """w = s q, (K, N) or (B, K, N) in `dtype` (bfloat16 or float32; float32 is exact), on the device."""
+    """w = s q, (K, N) or (B, K, N) in `dtype` (bfloat16, float16 or float32; float32 is exact), on the device."""
     squeeze = lo.dim() == 2
     L, H, S, Bq, K, N = _weights3(lo, hi, sc)
     g = _group_k(group_k, K, S.shape[1])
-    if dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"dequantize_int6 writes bfloat16 or float32 (got {dtype})")
+    if dtype not in _OUT_CODES:
+        raise TypeError(f"dequantize_int6 writes bfloat16, float16 or float32 (got {dtype})")
     w = torch.empty((Bq, K, N), dtype=dtype, device=L.device)
     with torch.cuda.device(L.device):
         _lib.check(_lib.load().w6a16_dequantize(
             L.data_ptr(), H.data_ptr(), S.data_ptr(), w.data_ptr(), Bq, K, N, g, L.stride(0), H.stride(0),
-            S.stride(0), w.stride(0), _lib.W6A16_OUT_F32 if dtype == torch.float32 else _lib.W6A16_OUT_BF16,
-            torch.cuda.current_stream(L.device).cuda_stream))
+            S.stride(0), w.stride(0), _OUT_CODES[dtype], torch.cuda.current_stream(L.device).cuda_stream))
     return w[0] if squeeze else w
 
 
@@ -198,16 +203,15 @@ def prepack_int6(lo, hi, s, group_k) -> Int6Packed:
 
 @torch.no_grad()
 def dequantize_int6_packed(pk: Int6Packed, dtype=torch.float32):
-    """dequantize_int6 for a packed weight: (K, N) or (B, K, N) in bfloat16 or float32."""
-    if dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"dequantize_int6_packed writes bfloat16 or float32 (got {dtype})")
+    """dequantize_int6 for a packed weight: (K, N) or (B, K, N) in bfloat16, float16 or float32."""
+    if dtype not in _OUT_CODES:
+        raise TypeError(f"dequantize_int6_packed writes bfloat16, float16 or float32 (got {dtype})")
     Bq = pk.weight.shape[0]
     w = torch.empty((Bq, pk.K, pk.N), dtype=dtype, device=pk.weight.device)
     with torch.cuda.device(w.device):
         _lib.check(_lib.load().w6a16_dequantize_packed(
             pk.weight.data_ptr(), pk.scales.data_ptr(), w.data_ptr(), Bq, pk.K, pk.N, pk.group_k, w.stride(0),
-            _lib.W6A16_OUT_F32 if dtype == torch.float32 else _lib.W6A16_OUT_BF16,
-            torch.cuda.current_stream(w.device).cuda_stream))
+            _OUT_CODES[dtype], torch.cuda.current_stream(w.device).cuda_stream))
     return w if pk.batches else w[0]
 
 
@@ -236,17 +240,17 @@ def _packed(pk: Int6Packed) -> _W:
               pk.N, pk.group_k)
 
 
-def _dequant(w: _W):
+def _dequant(w: _W, dtype):
     if w.fmt == _lib.W6A16_FORMAT_PACKED:
-        return dequantize_int6_packed(Int6Packed(w.w0, w.sc, w.Bq, w.K, w.N, w.g), dtype=torch.bfloat16)
-    return dequantize_int6(w.w0, w.w1, w.sc, w.g, dtype=torch.bfloat16)
+        return dequantize_int6_packed(Int6Packed(w.w0, w.sc, w.Bq, w.K, w.N, w.g), dtype=dtype)
+    return dequantize_int6(w.w0, w.w1, w.sc, w.g, dtype=dtype)
 
 
 def _impl(a, w: _W, split_k, out_dtype=None):
     batched = a.dim() == 3
     A = a if batched else a.unsqueeze(0)
-    if A.dtype != torch.bfloat16:
-        raise TypeError(f"int6_matmul takes bfloat16 activations (got {A.dtype})")
+    if A.dtype not in _IN_CODES:
+        raise TypeError(f"int6_matmul takes bfloat16 or float16 activations (got {A.dtype})")
     if A.device.type != "cuda":
         raise ValueError(f"a must be on a GPU (got {A.device})")
     B, M, Ka = A.shape
@@ -256,10 +260,10 @@ def _impl(a, w: _W, split_k, out_dtype=None):
     if Bq not in (1, B):
         raise ValueError(f"weight batch {Bq} does not match activation batch {B}")
     odt = A.dtype if out_dtype is None else out_dtype
-    if odt not in (torch.float32, torch.bfloat16):
-        raise TypeError(f"int6_matmul writes bfloat16 or float32 (got {odt})")
-    if M > MAX_M:  # prefill: compute-bound, dequantise once and use the library GEMM
-        wd = _dequant(w)
+    if odt not in _OUT_CODES:
+        raise TypeError(f"int6_matmul writes bfloat16, float16 or float32 (got {odt})")
+    if M > MAX_M:  # prefill: compute-bound, dequantise once (to the activations' type) and use the library GEMM
+        wd = _dequant(w, A.dtype)
         if wd.dim() == 2:
             wd = wd.unsqueeze(0)
         C = torch.matmul(A, wd[0] if Bq == 1 else wd)
@@ -282,7 +286,8 @@ def _impl(a, w: _W, split_k, out_dtype=None):
     args.out, args.out_batch_stride, args.out_row_stride = out.data_ptr(), out.stride(0), out.stride(1)
     args.B, args.M, args.N, args.K, args.group_k = B, M, N, K, w.g
     args.split_k = max(1, int(split_k))
-    args.out_dtype = _lib.W6A16_OUT_F32 if odt == torch.float32 else _lib.W6A16_OUT_BF16
+    args.out_dtype = _OUT_CODES[odt]
+    args.a_dtype = _IN_CODES[A.dtype]
     lib = _lib.load()
     n = ctypes.c_size_t(0)
     _lib.check(lib.w6a16_workspace_size(args, ctypes.byref(n)))
@@ -304,8 +309,8 @@ def _workspace(device, nbytes):
 
 
 def int6_matmul(a, lo, hi=None, s=None, group_k=None, split_k=None, use_dot=None, *, out_dtype=None):
-    """a (M, K) | (B, M, K) bf16 @ dequant(int6 weight (K, N) | (B, K, N)) -> (M, N) | (B, M, N) in a.dtype (or
-    out_dtype: bfloat16 / float32).  The weight is the planes (lo, hi, s, group_k) or an Int6Packed passed as `lo`
+    """a (M, K) | (B, M, K) bf16 or fp16 @ dequant(int6 weight (K, N) | (B, K, N)) -> (M, N) | (B, M, N) in a.dtype
+    (or out_dtype: bfloat16 / float16 / float32), as the reference casts the codes to a.dtype.  The weight is the planes (lo, hi, s, group_k) or an Int6Packed passed as `lo`
     (hi, s, group_k then unused).  A single weight (K, N) is shared by every batch row.  Eager entry point; the
     model-facing functional ops are int6_matmul_op and int6_matmul_packed_op."""
     packed = isinstance(lo, Int6Packed)

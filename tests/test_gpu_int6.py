@@ -5,7 +5,11 @@ Tolerances (stated per test):
   * the W6A16 kernel, fp32 result: |C - C_ref| <= 2e-5 (|a| @ |w|) element-wise (fp32 accumulation of exact
     bf16 x int6 products, scaled per 64-row chunk);
   * bf16 result: that plus one bf16 rounding, 2^-8 |C_ref|;
-  * the dequantise-then-library-GEMM path (M > MAX_M): 8e-3 (|a| @ |w|) (the weight is rounded to bf16 first).
+  * the dequantise-then-library-GEMM path (M > MAX_M): 8e-3 (|a| @ |w|) (the weight is rounded to bf16 first);
+  * fp16 activations (the reference casts its codes to a.dtype): the kernels' fp32 result within 3e-4 (|a| @ |w|)
+    (exact fp16 x int6 products; the offset 1024 + u, taken out once per chunk, leaves about 2^-24 x 1056 of the
+    row's |a| sum per fp32 accumulation), fp16 outputs one fp16 rounding (2^-11 |C_ref|) more; the GEMM path 2e-3
+    (|a| @ |w|) (the weight rounded to fp16 first).
 """
 import numpy as np
 import pytest
@@ -20,6 +24,8 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
 KERNEL_TOL = 2e-5
 GEMM_TOL = 8e-3
+F16_KERNEL_TOL = 3e-4
+F16_GEMM_TOL = 2e-3
 
 
 def _weights(rng, Bq, K, N, g):
@@ -44,13 +50,14 @@ def _split(split, B, M, N, K):
     return split if split is not None else I6.plan_int6(M, N, K, B, torch.device(DEV))[0]
 
 
-def _check(C, a_bf, lo, hi, sc, g, tol, bf16_out=False, shared=False):
+def _check(C, a_bf, lo, hi, sc, g, tol, bf16_out=False, shared=False, f16_out=False):
     a64 = a_bf.float().numpy().astype(np.float64)
     L, H, S = (lo[0], hi[0], sc[0]) if shared else (lo, hi, sc)
     ref = R.int6_matmul_ref(a64, L, H, S, g)
     bound = R.abs_bound(a64, L, H, S, g)
     got = C.float().cpu().numpy().astype(np.float64)
-    lim = tol * bound + (2.0 ** -8 * np.abs(ref) if bf16_out else 0.0) + 1e-30
+    lim = tol * bound + (2.0 ** -8 * np.abs(ref) if bf16_out else 0.0) + (2.0 ** -11 * np.abs(ref) if f16_out else 0.0)
+    lim = lim + 1e-30
     err = np.abs(got - ref)
     worst = np.unravel_index(np.argmax(err / lim), err.shape)
     assert (err <= lim).all(), f"worst at {worst}: got {got[worst]}, ref {ref[worst]}, limit {lim[worst]}"
@@ -262,7 +269,53 @@ def test_split_k_is_deterministic_and_consistent():
         _check(C[None], a, lo, hi, sc, g, KERNEL_TOL)
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,M,N,K,g,split,packed", [
+    (1, 1, 4096, 4096, 128, None, False),   # GEMV, split-K across workgroups or in the workgroup
+    (1, 1, 4096, 4096, 128, None, True),    # packed: half strips
+    (1, 5, 144, 256, 256, 3, False),        # narrow kernel, uneven split ranges, N past the last full strip
+    (1, 16, 2048, 1024, 64, None, True),
+    (2, 48, 272, 512, 128, None, False),    # wide kernel (row-sum pre-pass), batched weights
+    (1, 150, 640, 1024, 256, 2, True),      # wide kernel, split-K
+])
+def test_fp16_activations(B, M, N, K, g, split, packed):
+    """fp16 activations, as the reference takes them (its dot casts the codes to a.dtype, int6_gemm.py:144-147): the
+    result is fp16 by default (a.dtype) or fp32; every kernel form is checked against the oracle on the same fp16
+    values, and planes and packed weights give the same bits."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    say("int6_matmul fp16", dict(B=B, M=M, N=N, K=K, g=g, split=split, packed=packed))
+    rng = np.random.default_rng(700 + M + N + K)
+    lo, hi, sc = _weights(rng, B, K, N, g)
+    a = torch.from_numpy(rng.standard_normal((B, M, K)).astype(np.float32)).to(torch.float16)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    split = _split(split, B, M, N, K)
+    w = I6.prepack_int6(Ld, Hd, Sd, g) if packed else None
+    call = (lambda **kw: I6.int6_matmul(a.to(DEV), w, split_k=split, **kw)) if packed else \
+        (lambda **kw: I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, **kw))
+    C = call(out_dtype=torch.float32)
+    Ch = call()
+    Cp = I6.int6_matmul(a.to(DEV), Ld, Hd, Sd, g, split_k=split, out_dtype=torch.float32) if packed else C
+    torch.cuda.synchronize()
+    assert C.dtype == torch.float32 and Ch.dtype == torch.float16 and Ch.shape == (B, M, N)
+    assert torch.equal(C, Cp)
+    _check(C, a, lo, hi, sc, g, F16_KERNEL_TOL)
+    _check(Ch, a, lo, hi, sc, g, F16_KERNEL_TOL, f16_out=True)
+
+
+def test_fp16_large_m_dequantises_to_fp16():
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    M, N, K, g = I6.MAX_M + 44, 512, 1024, 128
+    say("int6_matmul fp16 large M", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(17)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    a = torch.from_numpy(rng.standard_normal((1, M, K)).astype(np.float32)).to(torch.float16)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    C = I6.int6_matmul(a[0].to(DEV), Ld, Hd, Sd, g)
+    torch.cuda.synchronize()
+    assert C.shape == (M, N) and C.dtype == torch.float16
+    _check(C[None], a, lo, hi, sc, g, F16_GEMM_TOL, f16_out=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_dequantize_is_exact(dtype):
     from rwkv_next_amd.kernels import int6_gemm as I6
     K, N, g = 512, 272, 128

@@ -240,7 +240,8 @@ def base_args(**kw):
     ("out_row_stride", 128, _lib.WKV7_ERR_SHAPE),     # < N
     ("split_k", 0, _lib.WKV7_ERR_ARG),
     ("split_k", 257, _lib.WKV7_ERR_ARG),
-    ("out_dtype", 1, _lib.WKV7_ERR_ARG),
+    ("out_dtype", 3, _lib.WKV7_ERR_ARG),
+    ("a_dtype", 2, _lib.WKV7_ERR_ARG),
     ("lo", None, _lib.WKV7_ERR_NULL),
     ("out", None, _lib.WKV7_ERR_NULL),
     ("a", 0x10008, _lib.WKV7_ERR_ALIGN),
