@@ -333,9 +333,10 @@ def timemix_bench(torch, kernels, dev, steps, warmup):
 def int6_bench(torch, kernels, dev, steps, warmup):
     """W6A16 GEMM/GEMV (rwkv_next/kernels/int6_gemm.py) at the reference's quoted shape K = 4096, N = 16384
     (int6_gemm.py:224-226), group_k = 128, for decode-sized M (the W6A16 kernel, on the reference's planes and on the
-    packed layout of prepack_int6) and M = 4096 (dequantise, then the library GEMM).  Eight weight sets (8 x 51 MB) are cycled so the 256 MB Infinity Cache cannot hold them: every
-    call streams its weight from HBM, as a model's consecutive layers do.  Each M is one HIP graph of 8 calls.
-    Beside it: torch.matmul on the same shape with a bf16 weight (hipBLASLt), cycled the same way."""
+    packed layout of prepack_int6) and M = 4096 (dequantise, then the library GEMM).  Eight weight sets (8 x 51 MB)
+    are cycled so the 256 MB Infinity Cache cannot hold them: every call streams its weight from HBM, as a model's
+    consecutive layers do.  Each M is one HIP graph of 8 calls.  Beside it: torch.matmul on the same shape with a
+    bf16 weight (hipBLASLt), cycled the same way, and the W6A16 kernels again with fp16 activations at four M."""
     from rwkv_next_amd.kernels import int6_gemm as I6
     K, N, G, SETS = 4096, 16384, 128, 8
     gen = torch.Generator(device=dev).manual_seed(1006)
@@ -388,6 +389,17 @@ def int6_bench(torch, kernels, dev, steps, warmup):
         log(f"int6 M={M} ({path}, split {sk}): {us:.2f} us ({rows[-1]['GBps']:.0f} GB/s), "
             f"packed (split {sk_pk}) {us_pk:.2f} us "
             f"({rows[-1]['packed_GBps']:.0f} GB/s), bf16 matmul {us_bf:.2f} us")
+    # fp16 activations (the reference's kernel takes either dtype; the output has A's dtype), same weights
+    f16_rows = []
+    for M in (1, 16, 64, 256):
+        a = torch.randn(M, K, device=dev, generator=gen).to(torch.float16)
+        sk, ud = I6.plan_int6(M, N, K, 1, dev)
+        us = graph_time(lambda: [I6.int6_matmul_op(a, lo[i], hi[i], sc[i], G, sk, ud) for i in range(SETS)], steps)
+        sk_pk = I6.plan_int6_packed(M, N, K, 1, dev)
+        us_pk = graph_time(lambda: [I6.int6_matmul_packed_op(a, pk[i].weight, pk[i].scales, 0, K, N, G, sk_pk)
+                                    for i in range(SETS)], steps)
+        f16_rows.append({"M": M, "us": us, "packed_us": us_pk})
+        log(f"int6 fp16 activations M={M}: {us:.2f} us, packed {us_pk:.2f} us")
     # prefill-sized M: dequantise once, then the library GEMM
     M = 4096
     a = torch.randn(M, K, device=dev, generator=gen).to(torch.bfloat16)
@@ -396,7 +408,7 @@ def int6_bench(torch, kernels, dev, steps, warmup):
     rows.append({"M": M, "path": "dequantize + library GEMM", "us": us, "TFLOPs": 2 * M * K * N / (us * 1e-6) / 1e12,
                  "bf16_matmul_us": us_bf, "speedup_vs_bf16": us_bf / us})
     log(f"int6 M={M}: {us:.1f} us, bf16 matmul {us_bf:.1f} us")
-    return {"K": K, "N": N, "group_k": G, "weight_bytes": weight_bytes, "rows": rows,
+    return {"K": K, "N": N, "group_k": G, "weight_bytes": weight_bytes, "rows": rows, "fp16_rows": f16_rows,
             "reference_quoted_ms": {"M=128": 0.24, "M=4096": 5.9}}
 
 
