@@ -60,7 +60,8 @@ typedef struct w6a16_args {
 /* sizeof(w6a16_args) as compiled into the library (bindings check their struct layout against it). */
 size_t w6a16_args_size(void);
 
-/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1 and M <= 32, and for M <= 32 with split_k 2..8 where the
+/* Bytes of workspace `w6a16_matmul` needs (0 for split_k == 1 and M <= 32, for W6A16_FORMAT_PACKED with M > 256 (the
+ * large-M kernel), and for M <= 32 with split_k 2..8 where the
  * in-workgroup split-K kernel runs: always for W6A16_FORMAT_PACKED, and for the planes when B * ceil(M / 16) *
  * ceil(N / 128) reaches the device's CU count; that kernel sums its split_k partial tiles in LDS): a fixed 1 MiB region of u32 arrival
  * counters (one per output tile; a call with more than 262144 tiles is refused with WKV7_ERR_SHAPE), then fp32
@@ -82,7 +83,9 @@ int w6a16_plan_split(int32_t B, int32_t M, int32_t N, int32_t K);
  * only at the same split_k. */
 int w6a16_plan_split_packed(int32_t B, int32_t M, int32_t N, int32_t K);
 
-/* C = A @ dequant(W) on `stream` (hipStream_t).  Replaces `_impl` + `_w6a16` (int6_gemm.py:253-287, 156-215). */
+/* C = A @ dequant(W) on `stream` (hipStream_t).  Replaces `_impl` + `_w6a16` (int6_gemm.py:253-287, 156-215).
+ * W6A16_FORMAT_PACKED with M > 256 runs the large-M kernel: A times the weight dequantised to A's type (s q rounded
+ * once, the values w6a16_dequantize writes), fp32 accumulation, no workspace; split_k is not used there. */
 int w6a16_matmul(const w6a16_args *args, void *stream);
 
 /* w[b][k][n] = scale * q ([B][K][N], batch stride in elements) as bf16, fp16 or fp32 (W6A16_OUT_*):

@@ -75,6 +75,7 @@ struct Args {
     float* rsum;    // wide kernel: row-sum bias per chain of 64 CG k, [batch][chain][mpad]
     int32_t B, M, N, K, group_k, split_k, out_dtype, m_groups, n_strips, chunks_per_split;
     int32_t mpad, chain_k, nchains, chains_per_split;  // wide kernel
+    int32_t out_vec;  // large-M kernel: the output takes 8-byte (16-byte for fp32) stores of 4 adjacent columns
 };
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
@@ -1372,6 +1373,225 @@ __global__ __launch_bounds__(256) void w6a16_dequant_kernel(const uint8_t* lo, c
     }
 }
 
+// ---------------------------------------------------------------------------------------------------------------
+// Large-M kernel (M > kBigMinM, prefill-sized M, packed weights): C = A W~ with W~ = s q rounded to A's type -- the
+// values w6a16_dequantize writes, so the result is that of dequantising and multiplying, in one kernel with no
+// workspace.  A workgroup of eight wavefronts (two per SIMD) computes a 256 x 256 tile of C.  Per 64-row chunk of K it
+// stages A's 256 x 64 slice and W~'s 64 x 256 slice (dequantised once per workgroup and stored transposed: LDS row n
+// holds the 64 k of column n) in LDS, double-buffered with one barrier per chunk.  Wavefront (wm, wn) multiplies a
+// 128 x 64 eighth: 32 MFMA tiles, 128 fp32 accumulators a lane, in 16 blocks (k half, 16-row tile) whose A operand is
+// read one block ahead.  In the MFMAs' shadow, a quarter of the next chunk's weight share (loaded one chunk earlier)
+// is dequantised and stored after every fourth block, A's next chunk (loaded at the chunk's start) is stored at its
+// end, and the weight bytes of the chunk after that are loaded; scheduler fences keep this order.  The MFMA's A
+// operand is a W~^T tile (rows n), its B operand an A^T tile (columns m), so lane (i, q) of tile (mt, nt) ends
+// holding C[m0 + 16 mt + i][n0 + 16 nt + 4 q .. + 3]: four adjacent outputs, stored together.
+constexpr int kBigTile = 256;                  // rows of A and columns of W per workgroup
+constexpr int kBigStage = 2 * kBigTile * 128;  // bytes per stage: A rows, then W~^T rows, 64 elements each
+
+// 16-byte piece p (k = 8 p .. 8 p + 7) of LDS row r (128-byte rows): piece slots XOR-swizzled by (r >> 1) & 7, so the
+// 16 rows of one operand read (one p) fall in 16 different 16-byte bank groups.
+__device__ __forceinline__ int big_slot(int r, int p) { return r * 128 + 16 * (p ^ ((r >> 1) & 7)); }
+
+// Two values as a pair of A's element type (round to nearest even).
+template <class A>
+__device__ __forceinline__ uint32_t pack_act(float x, float y) {
+    if constexpr (std::is_same_v<A, ActF16>)
+        return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)x) |
+               (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)y) << 16;
+    else
+        return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)x) | (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)y)
+                                                                      << 16;
+}
+
+// s (u - 32) of the four codes u in the bytes of `u`, as A's type: the fp32 product of an 11-bit scale and a 6-bit
+// integer is exact, so the one rounding is the conversion (the dequantisation kernel's values, bit for bit).
+template <class A>
+__device__ __forceinline__ void dequant4(uint32_t u, float s, float s32, uint32_t& d0, uint32_t& d1) {
+    const float v0 = __builtin_fmaf((float)(u & 0xFF), s, s32), v1 = __builtin_fmaf((float)((u >> 8) & 0xFF), s, s32);
+    const float v2 = __builtin_fmaf((float)((u >> 16) & 0xFF), s, s32), v3 = __builtin_fmaf((float)(u >> 24), s, s32);
+    d0 = pack_act<A>(v0, v1);
+    d1 = pack_act<A>(v2, v3);
+}
+
+// One chunk's global bytes, per thread: A rows (t >> 3) + 64 j, piece t & 7 (BigA), and the packed weight's share of
+// wavefront w (BigW: strip w >> 2 of the tile, tiles 2 (w & 3) and 2 (w & 3) + 1 -- their lo dwords, one 16-byte lane
+// load of the block, their two hi dwords and their two scales).
+struct BigA {
+    u4 a[4];
+};
+struct BigW {
+    u4 w;
+    uint2 h;
+    uint32_t sc;
+};
+
+__device__ __forceinline__ void big_load_a(const Args& p, int b, int m0, int c, BigA& g) {
+    const int t = threadIdx.x;
+    const uint16_t* const ab = p.a + (int64_t)b * p.sa_b + 64 * c + 8 * (t & 7);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int m = min(m0 + (t >> 3) + 64 * j, p.M - 1);
+        g.a[j] = *reinterpret_cast<const u4*>(ab + (int64_t)m * p.sa_m);
+    }
+}
+
+__device__ __forceinline__ void big_load_w(const Args& p, int b, int n0, int c, BigW& g) {
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, w4 = wv & 3;
+    const int nchunks = p.K / 64, groups = p.K / p.group_k;
+    const int strip = min(n0 / kTileN + (wv >> 2), p.n_strips - 1);
+    const uint8_t* const blk = p.lo + (int64_t)b * p.sl_b + ((int64_t)strip * nchunks + c) * kPackBytes + 16 * lane;
+    g.w = *reinterpret_cast<const u4*>(blk + 1024 * w4);                                 // R[4 w4 .. 4 w4 + 3]
+    g.h = *reinterpret_cast<const uint2*>(blk + 1024 * (4 + (w4 >> 1)) + 8 * (w4 & 1));  // R[16 + 2 w4], R[17 + 2 w4]
+    const int grp = (c * 64) / p.group_k;
+    g.sc = *reinterpret_cast<const uint32_t*>(p.sc + (int64_t)b * p.ss_b +
+                                              ((int64_t)strip * groups + grp) * kTileN + 8 * i + 2 * w4);
+}
+
+__device__ __forceinline__ void big_store_a(uint8_t* stage, const BigA& g) {
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u4*>(stage + big_slot((t >> 3) + 64 * j, t & 7)) = g.a[j];
+}
+
+// Piece e (0..3) of the wavefront's weight share, dequantised into the stage: tile t = 2 (w & 3) + (e >> 1), rows
+// 8 q .. + 7 (e even) or 32 + 8 q .. + 7 (e odd) of column 128 (w >> 2) + 16 t + i.
+template <class A>
+__device__ __forceinline__ void big_store_w(uint8_t* stage, const BigW& g, int e) {
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4, w4 = wv & 3;
+    const int tt = e >> 1;
+    const uint32_t L0 = g.w[2 * tt], L1 = g.w[2 * tt + 1], Hd = tt ? g.h.y : g.h.x;
+    uint32_t ua, ub;
+    if (e & 1) {
+        ua = ((L0 >> 4) & 0x0F0F0F0Fu) | ((Hd & 0x0C0C0C0Cu) << 2);  // rows 32 + 8 q + 0..3
+        ub = ((L1 >> 4) & 0x0F0F0F0Fu) | ((Hd >> 2) & 0x30303030u);  // rows 32 + 8 q + 4..7
+    } else {
+        ua = (L0 & 0x0F0F0F0Fu) | ((Hd & 0x03030303u) << 4);  // rows 8 q + 0..3
+        ub = (L1 & 0x0F0F0F0Fu) | (Hd & 0x30303030u);         // rows 8 q + 4..7
+    }
+    const float s = h2f((uint16_t)(g.sc >> (16 * tt))), s32 = -32.f * s;
+    uint32_t d[4];
+    dequant4<A>(ua, s, s32, d[0], d[1]);
+    dequant4<A>(ub, s, s32, d[2], d[3]);
+    const int r = kBigTile + 128 * (wv >> 2) + 16 * (2 * w4 + tt) + i;
+    *reinterpret_cast<u4*>(stage + big_slot(r, (e & 1) * 4 + q)) = u4{d[0], d[1], d[2], d[3]};
+}
+
+// Tile index -> (M tile, N tile).  Workgroup x runs on XCD x % 8; when the tiles divide evenly, XCD x takes the x-th
+// eighth of the tiles in bands of 8 N tiles, M tile by M tile, so the workgroups resident on one XCD at a time share
+// A's rows and W's columns in that XCD's L2.
+__device__ __forceinline__ void big_tile(int tiles_m, int tiles_n, int& tm, int& tn) {
+    const int T = tiles_m * tiles_n, x = blockIdx.x;
+    const int L = (T % 8 == 0) ? (x % 8) * (T / 8) + x / 8 : x;
+    constexpr int kBand = 8;
+    const int band = L / (tiles_m * kBand), idx = L - band * tiles_m * kBand;
+    const int width = min(kBand, tiles_n - band * kBand);
+    tm = idx / width;
+    tn = band * kBand + idx % width;
+}
+
+// The wavefront's 128 x 64 outputs, lane row m0 + 16 mt, columns n0 + 16 nt .. + 3: ES = 4 (fp32) or 2 (bf16 / fp16,
+// out_dtype) bytes an element in one vector store, or (VEC false) element by element as out_dtype.
+template <int ES, bool VEC>
+__device__ __forceinline__ void big_store_out(const Args& p, int b, int m0, int n0, const f4 (&acc)[8][4]) {
+    const bool f16 = p.out_dtype == W6A16_OUT_F16;
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt) {
+        const int m = m0 + 16 * mt;
+        if (m >= p.M) continue;
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) {
+            const int n = n0 + 16 * nt;
+            if (n >= p.N) continue;
+            const int64_t o = (int64_t)b * p.so_b + (int64_t)m * p.so_m + n;
+            const f4 v = acc[mt][nt];
+            if constexpr (VEC && ES == 4) {
+                *reinterpret_cast<f4*>(reinterpret_cast<float*>(p.out) + o) = v;
+            } else if constexpr (VEC) {
+                *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(p.out) + o) =
+                    f16 ? uint2{pack_act<ActF16>(v[0], v[1]), pack_act<ActF16>(v[2], v[3])}
+                        : uint2{pack_act<ActBF16>(v[0], v[1]), pack_act<ActBF16>(v[2], v[3])};
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (p.out_dtype == W6A16_OUT_F32)
+                        reinterpret_cast<float*>(p.out)[o + e] = v[e];
+                    else if (f16)
+                        reinterpret_cast<_Float16*>(p.out)[o + e] = (_Float16)v[e];
+                    else
+                        reinterpret_cast<__bf16*>(p.out)[o + e] = (__bf16)v[e];
+                }
+            }
+        }
+    }
+}
+
+template <class A>
+__global__ __launch_bounds__(512, 1) void w6a16_big_kernel(const Args p) {
+    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBigStage];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int wm = wv & 1, wn = wv >> 1;  // rows 128 wm .., columns 64 wn ..
+    const int tiles_m = (p.M + kBigTile - 1) / kBigTile, tiles_n = (p.N + kBigTile - 1) / kBigTile;
+    int tm, tn;
+    big_tile(tiles_m, tiles_n, tm, tn);
+    const int b = blockIdx.z, m0 = tm * kBigTile, n0 = tn * kBigTile;
+    const int nch = p.K / 64;
+    f4 acc[8][4];
+#pragma unroll
+    for (int mt = 0; mt < 8; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+    BigW w0, w1;
+    BigA ga;
+    big_load_a(p, b, m0, 0, ga);
+    big_load_w(p, b, n0, 0, w0);
+    big_load_w(p, b, n0, min(1, nch - 1), w1);
+    big_store_a(lds, ga);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) big_store_w<A>(lds, w0, e);
+    __syncthreads();
+    // chunk c: its stage is c & 1; ws holds chunk c + 1's weight bytes, wl receives chunk c + 2's
+    auto step = [&](int c, const BigW& ws, BigW& wl) {
+        uint8_t* const cur = lds + (c & 1) * kBigStage;
+        uint8_t* const nxt = lds + ((c & 1) ^ 1) * kBigStage;
+        big_load_a(p, b, m0, min(c + 1, nch - 1), ga);  // the last steps reload the last chunk (stored unused)
+        big_load_w(p, b, n0, min(c + 2, nch - 1), wl);
+        u4 wo[4], ao[2];
+        ao[0] = *reinterpret_cast<const u4*>(cur + big_slot(128 * wm + i, q));
+#pragma unroll
+        for (int blk = 0; blk < 16; ++blk) {
+            const int kh = blk >> 3, mt = blk & 7;
+            if (mt == 0) {
+#pragma unroll
+                for (int nt = 0; nt < 4; ++nt)
+                    wo[nt] = *reinterpret_cast<const u4*>(cur + kBigTile * 128 +
+                                                          big_slot(64 * wn + 16 * nt + i, 4 * kh + q));
+            }
+            if (blk + 1 < 16) {
+                const int kn = (blk + 1) >> 3, mn = (blk + 1) & 7;
+                ao[(blk + 1) & 1] = *reinterpret_cast<const u4*>(cur + big_slot(128 * wm + 16 * mn + i, 4 * kn + q));
+            }
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = A::mma(wo[nt], ao[blk & 1], acc[mt][nt]);
+            if ((blk & 3) == 3) big_store_w<A>(nxt, ws, blk >> 2);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        big_store_a(nxt, ga);
+        __syncthreads();
+    };
+    for (int c = 0; c < nch; c += 2) {
+        step(c, w1, w0);
+        if (c + 1 < nch) step(c + 1, w0, w1);
+    }
+    // lane (i, q) of tile (mt, nt): C[m0 + 128 wm + 16 mt + i][n0 + 64 wn + 16 nt + 4 q .. + 3] (N % 16 == 0: the
+    // four columns are all inside or all outside)
+    if (p.out_vec && p.out_dtype == W6A16_OUT_F32)
+        big_store_out<4, true>(p, b, m0 + 128 * wm + i, n0 + 64 * wn + 4 * q, acc);
+    else if (p.out_vec)
+        big_store_out<2, true>(p, b, m0 + 128 * wm + i, n0 + 64 * wn + 4 * q, acc);
+    else
+        big_store_out<0, false>(p, b, m0 + 128 * wm + i, n0 + 64 * wn + 4 * q, acc);
+}
+
 int cu_count() { return wkv7::device_cu_count(); }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -1393,7 +1613,12 @@ WideCfg wide_cfg(int M) {
     return {4, 1};
 }
 
+// Large-M kernel: M above this, packed weights (no workspace, no split-K).
+constexpr int kBigMinM = 256;
+bool big_rows(const w6a16_args* a) { return a->M > kBigMinM && a->format == W6A16_FORMAT_PACKED; }
+
 struct Layout {
+    bool big;                    // the large-M kernel
     bool wide, gemv, gemv_half;  // gemv: the in-workgroup split-K kernel (no workspace); gemv_half: per half strip
     int mt, kp, cg, m_groups, n_strips, mpad, nchains;
     size_t tiles, counter_bytes, partial_bytes, rsum_offset, rsum_bytes;
@@ -1401,8 +1626,10 @@ struct Layout {
 
 Layout layout(const w6a16_args* a) {
     Layout l{};
-    l.wide = wide_rows(a->M);
+    l.big = big_rows(a);
+    l.wide = !l.big && wide_rows(a->M);
     l.n_strips = (a->N + kTileN - 1) / kTileN;
+    if (l.big) return l;  // no workspace
     if (l.wide) {
         const WideCfg c = wide_cfg(a->M);
         l.mt = c.mtw;
@@ -1454,6 +1681,10 @@ int validate(const w6a16_args* a) {
         return WKV7_ERR_ALIGN;
     if (a->a_row_stride < a->K || a->out_row_stride < a->N) return WKV7_ERR_SHAPE;
     const Layout l = layout(a);
+    if (l.big) {  // grid (tiles, 1, B)
+        const int64_t tiles = (int64_t)((a->M + kBigTile - 1) / kBigTile) * ((a->N + kBigTile - 1) / kBigTile);
+        return (a->B > 65535 || tiles > 0x7FFFFFFF) ? WKV7_ERR_SHAPE : WKV7_OK;
+    }
     if ((int64_t)a->B * (l.wide ? 1 : l.m_groups) > 65535) return WKV7_ERR_SHAPE;  // grid z: batch (x M groups)
     if (l.wide && (int64_t)l.m_groups * ((l.n_strips + 7) / 8) * 8 > 0x7FFFFFFF) return WKV7_ERR_SHAPE;
     if (a->split_k > 1 && l.tiles * 4 > kCounterRegion) return WKV7_ERR_SHAPE;  // more tiles than counters (0: gemv)
@@ -1509,7 +1740,10 @@ void launch_wide_cg(const Args& p, const Layout& l, bool packed, hipStream_t s) 
 // The kernel for the call's shape and layout, with activations of type A.
 template <class A>
 void launch_matmul(const Args& p, const Layout& l, bool packed, hipStream_t s) {
-    if (l.gemv && l.gemv_half && p.split_k <= 4)  // half strips, split <= 4: three chunks in flight
+    if (l.big) {
+        const int tiles = ((p.M + kBigTile - 1) / kBigTile) * ((p.N + kBigTile - 1) / kBigTile);
+        hipLaunchKernelGGL(w6a16_big_kernel<A>, dim3(tiles, 1, p.B), dim3(512), 0, s, p);
+    } else if (l.gemv && l.gemv_half && p.split_k <= 4)  // half strips, split <= 4: three chunks in flight
         launch_gemv<A, 2, 3>(p, l, packed, s);
     else if (l.gemv)
         launch_gemv<A, 2, 2>(p, l, packed, s);
@@ -1532,7 +1766,8 @@ size_t w6a16_args_size(void) { return sizeof(w6a16_args); }
 
 int w6a16_workspace_size(const w6a16_args* a, size_t* bytes) {
     if (!a || !bytes) return WKV7_ERR_NULL;
-    if (a->M <= 0 || a->B < 1 || a->N < 1 || a->K < 64 || a->group_k < 64 || (a->split_k <= 1 && !w6::wide_rows(a->M))) {
+    if (a->M <= 0 || a->B < 1 || a->N < 1 || a->K < 64 || a->group_k < 64 ||
+        (a->split_k <= 1 && !w6::wide_rows(a->M)) || w6::big_rows(a)) {
         *bytes = 0;
         return WKV7_OK;
     }
@@ -1628,6 +1863,7 @@ int w6a16_matmul(const w6a16_args* a, void* stream) {
         p.nchains = l.nchains;
         p.chains_per_split = (l.nchains + a->split_k - 1) / a->split_k;
     }
+    p.out_vec = w6::aligned16(a->out) && a->out_row_stride % 8 == 0 && a->out_batch_stride % 8 == 0;
     const hipStream_t s = static_cast<hipStream_t>(stream);
     const bool packed = a->format == W6A16_FORMAT_PACKED;
     if (a->a_dtype == W6A16_IN_F16)

@@ -22,7 +22,10 @@ Compute: one MFMA kernel for every M up to MAX_M (the reference's reduction form
 an MFMA with M padded to 16 rows costs the CDNA4 matrix core less than a VALU reduction costs the vector units, and
 the weight bytes, not the arithmetic, bound both).  `use_dot` is accepted for the reference's signature and does
 not change the computation.  Above MAX_M the weight is dequantised once to the activations' type and the product
-goes to the library GEMM (hipBLASLt through torch.matmul), which is compute-bound there.
+goes to the library GEMM (hipBLASLt through torch.matmul), which is compute-bound there.  The C ABI has its own kernel
+for that range (packed weights, M > 256: dequantisation in LDS fused with the product, the same values); at K = 4096,
+N = 16384 it is level with dequantise + hipBLASLt at M = 1024 and slower from M = 2048 (585 against 465 us at
+M = 4096), so MAX_M (env RWKV_INT6_MAX_M) keeps the library GEMM by default.
 
 Activations are bf16 (the model's) or fp16 (the reference op takes any a.dtype its dot accepts); the result is
 a.dtype, or out_dtype (fp32 accumulation).  Every call runs on the current stream, no host sync.

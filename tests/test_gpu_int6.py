@@ -11,6 +11,8 @@ Tolerances (stated per test):
     row's |a| sum per fp32 accumulation), fp16 outputs one fp16 rounding (2^-11 |C_ref|) more; the GEMM path 2e-3
     (|a| @ |w|) (the weight rounded to fp16 first).
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
@@ -469,6 +471,81 @@ def test_kernel_beyond_128_rows(monkeypatch, packed):
         C = I6.int6_matmul(a.to(DEV), *w, split_k=split, out_dtype=torch.float32)
         torch.cuda.synchronize()
         _check(C, a, lo, hi, sc, g, KERNEL_TOL)
+
+
+def _dequant_as(lo, hi, sc, g, dtype):
+    """s q rounded to `dtype` (what w6a16_dequantize writes), as float64."""
+    w = torch.from_numpy(R.dequantize_ref(lo, hi, sc, g).astype(np.float32)).to(dtype)
+    return w.double().numpy()
+
+
+@pytest.mark.parametrize("B,M,N,K,g,adt,shared", [
+    (1, 257, 272, 192, 64, torch.bfloat16, False),    # a second M tile of one row; a last N tile of 16 columns
+    (2, 300, 512, 512, 128, torch.bfloat16, False),   # batched weights
+    (3, 300, 400, 256, 128, torch.bfloat16, True),    # one weight for the batch; N not a multiple of 128
+    (1, 520, 1024, 1024, 128, torch.float16, False),  # fp16 activations
+    (1, 2304, 768, 256, 256, torch.bfloat16, False),  # 9 x 3 tiles: the XCD-banded tile order
+])
+def test_large_m_kernel(monkeypatch, B, M, N, K, g, adt, shared):
+    """M > 256 on packed weights runs the large-M kernel (the weight dequantised in LDS to A's type, then the
+    product): its result is A times the dequantised weight (the values w6a16_dequantize writes) with fp32
+    accumulation, |C - C_ref| <= 2e-5 (|a| @ |w~|), plus one rounding of the output type."""
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    monkeypatch.setattr(I6, "MAX_M", 1 << 20)
+    say("int6_matmul large-M kernel", dict(B=B, M=M, N=N, K=K, g=g, adt=str(adt), shared=shared))
+    rng = np.random.default_rng(900 + M + N + K)
+    Bq = 1 if shared else B
+    lo, hi, sc = _weights(rng, Bq, K, N, g)
+    a = torch.from_numpy(rng.standard_normal((B, M, K)).astype(np.float32)).to(adt)
+    Ld, Hd, Sd = _dev(lo, hi, sc)
+    pk = I6.prepack_int6(Ld[0], Hd[0], Sd[0], g) if shared else I6.prepack_int6(Ld, Hd, Sd, g)
+    a_dev = a.to(DEV)
+    C = I6.int6_matmul(a_dev, pk, out_dtype=torch.float32)
+    Co = I6.int6_matmul(a_dev, pk)
+    torch.cuda.synchronize()
+    assert C.shape == (B, M, N) and Co.dtype == adt
+    w = _dequant_as(lo, hi, sc, g, adt)
+    a64 = a.double().numpy()
+    wb = [w[0 if shared else bi] for bi in range(B)]
+    ref = np.stack([a64[bi] @ wb[bi] for bi in range(B)])
+    bound = np.stack([np.abs(a64[bi]) @ np.abs(wb[bi]) for bi in range(B)]) + 1e-30
+    got = C.cpu().double().numpy()
+    err = np.abs(got - ref)
+    assert (err <= 2e-5 * bound).all(), f"max err / bound {(err / bound).max():.3g}"
+    rnd = 2.0 ** -8 if adt == torch.bfloat16 else 2.0 ** -11
+    got_o = Co.cpu().double().numpy()
+    assert (np.abs(got_o - ref) <= 2e-5 * bound + rnd * np.abs(ref)).all()
+
+
+def test_large_m_kernel_unaligned_output(monkeypatch):
+    """An output whose rows are not 16-byte aligned takes element stores; the result equals the aligned call's."""
+    from rwkv_next_amd import _lib
+    from rwkv_next_amd.kernels import int6_gemm as I6
+    monkeypatch.setattr(I6, "MAX_M", 1 << 20)
+    M, N, K, g = 300, 272, 256, 128
+    say("int6 large-M kernel, strided output", dict(M=M, N=N, K=K))
+    rng = np.random.default_rng(933)
+    lo, hi, sc = _weights(rng, 1, K, N, g)
+    a = _act(rng, 1, M, K)[0].to(DEV)
+    Ld, Hd, Sd = _dev(lo[0], hi[0], sc[0])
+    pk = I6.prepack_int6(Ld, Hd, Sd, g)
+    C = I6.int6_matmul(a, pk)
+    big = torch.full((M, N + 3), 7.0, dtype=torch.bfloat16, device=DEV)
+    out = big[:, 1:N + 1]  # rows N + 3 elements apart, first element 2 bytes past a 16-byte boundary
+    args = _lib.W6a16Args()
+    args.a, args.a_batch_stride, args.a_row_stride = a.data_ptr(), 0, a.stride(0)
+    args.format, args.lo, args.scales = _lib.W6A16_FORMAT_PACKED, pk.weight.data_ptr(), pk.scales.data_ptr()
+    args.out, args.out_batch_stride, args.out_row_stride = out.data_ptr(), 0, out.stride(0)
+    args.B, args.M, args.N, args.K, args.group_k, args.split_k = 1, M, N, K, g, 1
+    args.out_dtype, args.a_dtype = _lib.W6A16_OUT_BF16, _lib.W6A16_IN_BF16
+    lib = _lib.load()
+    nb = ctypes.c_size_t(0)
+    _lib.check(lib.w6a16_workspace_size(args, ctypes.byref(nb)))
+    assert nb.value == 0  # the large-M kernel takes no workspace
+    _lib.check(lib.w6a16_matmul(args, torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert torch.equal(out, C)
+    assert (big[:, 0] == 7).all() and (big[:, N + 1:] == 7).all()
 
 
 def test_workspace_shared_across_shapes():
