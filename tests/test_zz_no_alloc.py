@@ -1,6 +1,7 @@
 """wkv7_run_noalloc (the allocation-free variant of wkv7_run, include/wkv7_noalloc.h, in librwkv7_noalloc.so) through
 the C ABI: two chunked calls
-in a row (the second smaller), a ragged call and a decode call, each bit-identical to wkv7_run with a
+in a row (the second smaller), a ragged call, a decode call and the headline prefill (configuration 2), each
+bit-identical to wkv7_run with a
 caller-allocated workspace on the same inputs; a call that needs more than WKV7_NOALLOC_SCRATCH_BYTES is refused
 before anything is launched."""
 import ctypes
@@ -97,6 +98,18 @@ def test_ragged_and_decode_calls(dev, lib):
     x = to_dev(operands(16, 1, H, seed=5), dev)
     h0 = torch.from_numpy((0.3 * np.random.default_rng(6).standard_normal((16, H, 64, 64))).astype(np.float32)).to(dev)
     run_both(lib, dev, x, H, 16, 1, 16, h0=h0)
+
+
+def test_headline_prefill_fits(dev, lib):
+    """Configuration 2 (B = 1, T = 4096, H = 64), AUTO: the segmented kernel's workspace (hand-off flags and entries,
+    the later segments' Q P records: about 33 MB) fits the scratch, and the result equals wkv7_run's."""
+    from rwkv_next_amd import _lib
+    H, B, T = 64, 1, 4096
+    say("noalloc configuration 2", B, T, H)
+    x = to_dev(operands(B, T, H, seed=12), dev)
+    a = make_args(x, H, B, T, B * T, torch.empty_like(x[3]))
+    assert 0 < _lib.workspace_size(a) <= _lib.WKV7_NOALLOC_SCRATCH_BYTES
+    run_both(lib, dev, x, H, B, T, B * T)
 
 
 def test_too_large_is_refused_before_launch(dev, lib):
