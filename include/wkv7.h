@@ -34,7 +34,7 @@ extern "C" {
  * of a failed launch (the reference surfaces Triton/GPU errors as Python exceptions, engine.py:486-495). */
 #define WKV7_OK 0
 #define WKV7_ERR_NULL (-1)       /* a required pointer is NULL */
-#define WKV7_ERR_SHAPE (-2)      /* head_size != 64, H < 1, negative sizes, T too large */
+#define WKV7_ERR_SHAPE (-2)      /* head_size outside 1..256, H < 1, negative sizes, T too large */
 #define WKV7_ERR_ALIGN (-3)      /* operand/state pointers not 16-byte aligned, or strides not multiples of 8 */
 #define WKV7_ERR_WORKSPACE (-4)  /* workspace missing or smaller than wkv7_workspace_size() */
 #define WKV7_ERR_ARG (-5)        /* inconsistent arguments (snapshots on the chunked path, bad algo, ...) */
@@ -107,7 +107,7 @@ typedef struct wkv7_args {
     /* sequences -- wkv7.py:46-54 */
     const int32_t *cu_seqlens;    /* NULL: dense, sequence n = tokens [n*T, (n+1)*T); else [num_seqs + 1] */
     const int64_t *n_keep;        /* NULL, or per sequence: run only the first min(len, n_keep[n]) tokens */
-    float *snapshots;             /* NULL, or [num_seqs][T][H][64][64]: state after each token t < len of each row
+    float *snapshots;             /* NULL, or [num_seqs][T][H][K][K]: state after each token t < len of each row
                                    * (the others untouched; ragged calls need T >= 1), recurrent kernel */
 
     void *workspace;              /* device scratch of the chunked paths (see wkv7_workspace_size), 256-byte aligned.
@@ -123,7 +123,11 @@ typedef struct wkv7_args {
                                    * the snapshot time stride in both cases */
     int64_t total_tokens;         /* operand rows: N*T dense, the packed length when ragged */
     int32_t H;                    /* heads */
-    int32_t head_size;            /* must be 64 */
+    int32_t head_size;            /* K == V: 64 (every RWKV-7 model) runs the kernels above; any other 1..256 (the
+                                   * reference pads K to a power of two and masks, wkv7.py:55-59, 96) runs one
+                                   * generic token-serial kernel on every row, no workspace, algo AUTO or RECURRENT
+                                   * (others: WKV7_ERR_ARG); states and snapshots are then [..][K][K], operand rows
+                                   * [token][H][K] (2-byte aligned; states 4-byte aligned) */
     int32_t algo;                 /* WKV7_ALGO_* */
     int32_t rec_max_len;          /* AUTO: rows of at most this many tokens run token-serial; -1 = default */
     int32_t *status;              /* NULL, or one device int32 that receives WKV7_STATUS_* bits (see above) */

@@ -15,7 +15,8 @@
 //   tools/test_wkv7.py:13-23         fp64 loop, sums over the k axis
 //
 // Layouts are the reference's: operands r, w, k, v, a, b are [tokens][H][K] (token stride H*K), passed here as
-// float32 holding the bf16-rounded values; states are [seq][H][K][V] with V contiguous (K == V <= 64).
+// float32 holding the bf16-rounded values; states are [seq][H][K][V] with V contiguous (K == V <= 256: the reference
+// takes any head size, padding it to a power of two with masks, wkv7.py:55-59, 96).
 //
 // Two precisions: wkv7_oracle_f64 (the parity reference) and wkv7_oracle_f32 (the timed CPU baseline and the
 // fp32-vs-fp64 calibration of the tolerances).  Both parallelise over (sequence, head) pairs with OpenMP; the
@@ -28,13 +29,14 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <vector>
 #ifdef _OPENMP
 #include <omp.h>
 #endif
 
 namespace {
 
-constexpr int KMAX = 64;
+constexpr int KMAX = 256;
 
 // Sequence extents, rwkv_next/kernels/wkv7.py:46-54.
 inline void seq_extent(int n, int T, const int32_t* cu, const int64_t* nkeep, int64_t* bos, int64_t* len) {
@@ -67,7 +69,8 @@ int run(const float* r, const float* w, const float* k, const float* v, const fl
         int64_t bos, L;
         seq_extent(n, T, cu, nkeep, &bos, &L);
         const int64_t slot = state_idx ? state_idx[n] : n;
-        Real S[KMAX * KMAX], sa[KMAX], dd[KMAX];
+        std::vector<Real> Sv(KK), sav(K), ddv(K);  // per pair on the heap (K up to 256)
+        Real *S = Sv.data(), *sa = sav.data(), *dd = ddv.data();
         if (h0) {
             const float* s0 = h0 + (slot * H + h) * KK;
             for (int64_t i = 0; i < KK; ++i) S[i] = (Real)s0[i];
@@ -116,7 +119,7 @@ extern "C" {
 // All pointers are host pointers.  o, ht, snap are nullable outputs; h0 is a nullable fp32 initial-state array
 // indexed by state_idx[n] (a pool slot) when state_idx is given, else by n; ht is indexed the same way.
 // snap is [num_seqs][T][H][K][K]: the state after each token (rows past a sequence's length are not written).
-// Returns 0, or -1 for invalid sizes (K > 64).
+// Returns 0, or -1 for invalid sizes (K > 256).
 int wkv7_oracle_f64(const float* r, const float* w, const float* k, const float* v, const float* a, const float* b,
                     double* o, const float* h0, const int64_t* state_idx, double* ht, const int32_t* cu,
                     const int64_t* nkeep, double* snap, int num_seqs, int T, int H, int K, int nthreads) {

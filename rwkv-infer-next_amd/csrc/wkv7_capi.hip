@@ -39,6 +39,7 @@ constexpr int kDefaultRecMaxLen = 32;
 constexpr int kSegMinChunkHeadsPerCu = 8;
 
 struct Plan {
+    bool run_generic = false;  // head size other than 64
     bool run_recurrent = false;
     bool run_chunked = false;
     bool run_chain = false;
@@ -52,10 +53,41 @@ struct Plan {
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
+// Head sizes other than 64: the generic token-serial kernel, with scalar accesses (2-byte operands, 4-byte states).
+int validate_generic(const wkv7_args* a) {
+    if (a->algo != WKV7_ALGO_AUTO && a->algo != WKV7_ALGO_RECURRENT) return WKV7_ERR_ARG;  // K = 64 forms only
+    if ((int64_t)a->num_seqs * a->H > ((int64_t)1 << 31)) return WKV7_ERR_SHAPE;
+    if (!a->cu_seqlens && (int64_t)a->num_seqs * a->T > a->total_tokens) return WKV7_ERR_SHAPE;
+    if (a->T > (1 << 30) || a->total_tokens > ((int64_t)1 << 40)) return WKV7_ERR_SHAPE;
+    const int64_t K = a->head_size;
+    if (a->num_seqs > 0 && a->total_tokens > 0) {
+        const uint16_t* ops[6] = {a->r, a->w, a->k, a->v, a->a, a->b};
+        for (const uint16_t* p : ops) {
+            if (!p) return WKV7_ERR_NULL;
+            if (!aligned(p, 2)) return WKV7_ERR_ALIGN;
+        }
+        if (a->in_tok_stride < a->H * K) return WKV7_ERR_ALIGN;
+        if (a->o && (!aligned(a->o, 2) || a->o_tok_stride < a->H * K)) return WKV7_ERR_ALIGN;
+    }
+    // grid: one wavefront per (sequence, head, 16 state columns), four per workgroup
+    if (((int64_t)a->num_seqs * a->H * ((K + 15) / 16) + 3) / 4 > 0x7FFFFFFF) return WKV7_ERR_SHAPE;
+    if ((a->h0 && !aligned(a->h0, 4)) || (a->ht && !aligned(a->ht, 4))) return WKV7_ERR_ALIGN;
+    if (a->h0_idx && !a->h0) return WKV7_ERR_ARG;
+    if (a->ht_idx && !a->ht) return WKV7_ERR_ARG;
+    if ((a->h0 && a->h0_rows < 0) || (a->ht && a->ht_rows < 0)) return WKV7_ERR_SHAPE;
+    if (a->rec_max_len < -1) return WKV7_ERR_ARG;
+    if (a->snapshots) {
+        if (!aligned(a->snapshots, 4)) return WKV7_ERR_ALIGN;
+        if (a->T < 1) return WKV7_ERR_ARG;
+    }
+    return WKV7_OK;
+}
+
 int validate(const wkv7_args* a) {
-    if (a->head_size != wkv7::HS) return WKV7_ERR_SHAPE;
+    if (a->head_size < 1 || a->head_size > wkv7::kGenericMaxK) return WKV7_ERR_SHAPE;
     if (a->H < 1 || a->num_seqs < 0 || a->T < 0 || a->total_tokens < 0) return WKV7_ERR_SHAPE;
     if (a->algo < WKV7_ALGO_AUTO || a->algo > WKV7_ALGO_SEGMENTED) return WKV7_ERR_ARG;
+    if (a->head_size != wkv7::HS) return validate_generic(a);
     if (a->algo == WKV7_ALGO_SEGMENTED && a->snapshots) return WKV7_ERR_ARG;
     if (a->algo == WKV7_ALGO_SEGMENTED && (a->cu_seqlens || a->n_keep) && a->num_seqs > wkv7::kSegMaxRows)
         return WKV7_ERR_ARG;
@@ -99,6 +131,10 @@ bool seg_fits(const Plan& pl, const wkv7_args* a) {
 
 Plan make_plan(const wkv7_args* a) {
     Plan pl;
+    if (a->head_size != wkv7::HS) {
+        pl.run_generic = true;
+        return pl;
+    }
     const bool varlen = a->cu_seqlens != nullptr;
     const int64_t bound = varlen ? (a->T > 0 ? a->T : a->total_tokens) : a->T;
     const int thr = a->rec_max_len >= 0 ? a->rec_max_len : kDefaultRecMaxLen;
@@ -181,6 +217,7 @@ Params to_params(const wkv7_args* a) {
     p.H = a->H;
     p.rec_max_len = -1;
     p.status = a->status;
+    p.K = a->head_size;
     return p;
 }
 
@@ -307,7 +344,7 @@ const char* wkv7_strerror(int code) {
     switch (code) {
         case WKV7_OK: return "ok";
         case WKV7_ERR_NULL: return "a required pointer is NULL";
-        case WKV7_ERR_SHAPE: return "invalid sizes (head_size must be 64, H >= 1, counts non-negative)";
+        case WKV7_ERR_SHAPE: return "invalid sizes (1 <= head_size <= 256, H >= 1, counts non-negative)";
         case WKV7_ERR_ALIGN: return "pointers must be 16-byte aligned and token strides multiples of 8 elements";
         case WKV7_ERR_WORKSPACE: return "workspace missing or smaller than wkv7_workspace_size()";
         case WKV7_ERR_ARG: return "inconsistent arguments";
@@ -352,6 +389,10 @@ int wkv7_run(const wkv7_args* args, void* stream) {
                            chunk_thr);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return static_cast<int>(e);
+    }
+    if (pl.run_generic) {
+        const hipError_t e = wkv7::launch_generic(p, s);
+        return e == hipSuccess ? WKV7_OK : static_cast<int>(e);
     }
     if (pl.run_chain) {
         p.rec_max_len = pl.rec_len_rec;

@@ -116,6 +116,7 @@ struct Params {
     int32_t H;
     int32_t rec_max_len;            // chunked launches: rows this short run the recurrent path instead
     int32_t* status;                // nullable device status word (WKV7_STATUS_* bits)
+    int32_t K;                      // head size: 64 for every kernel but the generic one (wkv7_generic.hip)
 };
 
 // Extent of sequence n (rwkv_next/kernels/wkv7.py:46-54).

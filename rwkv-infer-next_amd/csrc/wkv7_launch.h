@@ -81,4 +81,9 @@ SegWorkspace seg_workspace(int num_seqs, int H, int64_t total_tokens, int64_t ma
 // own chunks), so a ragged call needs no second dispatch.
 hipError_t launch_seg(const Params& p, const SegWorkspace& ws, void* workspace, bool short_rows, hipStream_t stream);
 
+// Head sizes other than 64 (1 <= p.K <= kGenericMaxK): the token-serial recurrence on every row, no workspace.
+constexpr int kGenericMaxK = 256;
+int64_t generic_grid(const Params& p);  // workgroups of the launch
+hipError_t launch_generic(const Params& p, hipStream_t stream);
+
 }  // namespace wkv7

@@ -23,8 +23,8 @@ LIB_NAME = "librwkv7_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 BUILD_DIR = os.path.join(PROJECT_DIR, "_build")
 
-SOURCES = ("wkv7_recurrent.hip", "wkv7_chunked.hip", "wkv7_seg.hip", "wkv7_pool.hip", "wkv7_timemix.hip", "w6a16.hip",
-           "wkv7_capi.hip")
+SOURCES = ("wkv7_recurrent.hip", "wkv7_chunked.hip", "wkv7_seg.hip", "wkv7_generic.hip", "wkv7_pool.hip",
+           "wkv7_timemix.hip", "w6a16.hip", "wkv7_capi.hip")
 NOALLOC_SOURCE = "wkv7_noalloc.hip"
 NOALLOC_LIB_PATH = os.path.join(PKG_DIR, "librwkv7_noalloc.so")
 HEADERS = ("wkv7_device.h", "wkv7_launch.h", "wkv7_token.h")

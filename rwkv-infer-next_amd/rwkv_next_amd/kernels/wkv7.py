@@ -16,7 +16,9 @@ The in-place entries are registered torch ops too (rwkv_next_amd::wkv7_pool_, rw
 their mutated arguments declared and fake implementations), so a torch.compile'd caller such as the reference's
 part_att (model.py:334-342) traces through them without a graph break.
 
-Layouts: r, w, k, v, a, b (B, T, H*K) bf16 (w RAW); states (N, H, K, K) fp32; o like v.  K must be 64.
+Layouts: r, w, k, v, a, b (B, T, H*K) bf16 (w RAW); states (N, H, K, K) fp32; o like v.  Head size K: 64 (every
+RWKV-7 model) runs the specialised kernels; any other 1 <= K <= 256 (the reference pads K to a power of two and masks,
+wkv7.py:55-59, 96) runs a generic token-serial kernel with the same features, and algo AUTO or RECURRENT.
 All work runs in HIP kernels on the current stream; nothing here synchronises, so every entry point can be
 captured in a CUDA/HIP graph.  There is no CPU or PyTorch fallback.
 """
@@ -37,7 +39,8 @@ def reset_workspaces() -> None:
     """Drop the cached per-stream workspaces (the next call creates a zeroed one)."""
     _WORKSPACES.clear()
 
-HEAD_SIZE = 64
+HEAD_SIZE = 64      # every RWKV-7 model's head size: the specialised kernels
+MAX_HEAD_SIZE = 256  # other head sizes run the generic token-serial kernel
 OPERANDS = ("r", "w", "k", "v", "a", "b")
 
 
@@ -46,8 +49,8 @@ def _ptr(t: Optional[torch.Tensor]):
 
 
 def _prep_operands(r, w, k, v, a, b, H, K):
-    if K != HEAD_SIZE:
-        raise ValueError(f"head size K={K} is not supported (the kernels are built for K = {HEAD_SIZE})")
+    if not 1 <= K <= MAX_HEAD_SIZE:
+        raise ValueError(f"head size K={K} is not supported (1 <= K <= {MAX_HEAD_SIZE})")
     ops = [r, w, k, v, a, b]
     shape = r.shape
     for name, t in zip(OPERANDS, ops):
@@ -83,16 +86,16 @@ def _state_arg(state, rows_expected, H, K, name="state"):
     return state.contiguous()
 
 
-def _launch(ops, *, H, num_seqs, T, total, o=None, h0=None, h0_idx=None, h0_rows=0, ht=None, ht_idx=None,
-            ht_rows=0, fresh=None, cu=None, n_keep=None, snap=None, algo=_lib.ALGO_AUTO, rec_max_len=-1,
+def _launch(ops, *, H, K=HEAD_SIZE, num_seqs, T, total, o=None, h0=None, h0_idx=None, h0_rows=0, ht=None,
+            ht_idx=None, ht_rows=0, fresh=None, cu=None, n_keep=None, snap=None, algo=_lib.ALGO_AUTO, rec_max_len=-1,
             status=None):
     dev = ops[0].device
     args = _lib.Wkv7Args()
     for name, t in zip(OPERANDS, ops):
         setattr(args, name, t.data_ptr())
-    args.in_tok_stride = H * HEAD_SIZE
+    args.in_tok_stride = H * K
     args.o = _ptr(o)
-    args.o_tok_stride = H * HEAD_SIZE
+    args.o_tok_stride = H * K
     args.h0, args.h0_idx, args.h0_rows = _ptr(h0), _ptr(h0_idx), h0_rows
     args.ht, args.ht_idx, args.ht_rows = _ptr(ht), _ptr(ht_idx), ht_rows
     args.fresh = _ptr(fresh)
@@ -100,7 +103,7 @@ def _launch(ops, *, H, num_seqs, T, total, o=None, h0=None, h0_idx=None, h0_rows
     args.n_keep = _ptr(n_keep)
     args.snapshots = _ptr(snap)
     args.num_seqs, args.T, args.total_tokens = num_seqs, T, total
-    args.H, args.head_size, args.algo, args.rec_max_len = H, HEAD_SIZE, algo, rec_max_len
+    args.H, args.head_size, args.algo, args.rec_max_len = H, K, algo, rec_max_len
     args.status = _ptr(status)
     nbytes = _lib.workspace_size(args)
     ws = None
@@ -131,7 +134,7 @@ def _fwd_impl(r, w, k, v, a, b, h0, H: int, K: int, final: bool, algo: int = _li
     o = torch.empty_like(ops[3])
     ht = torch.empty(B, H, K, K, device=r.device, dtype=torch.float32) if final else r.new_empty(0,
                                                                                               dtype=torch.float32)
-    _launch(ops, H=H, num_seqs=B, T=T, total=B * T, o=o, h0=h0, h0_rows=B, ht=ht if final else None, ht_rows=B,
+    _launch(ops, H=H, K=K, num_seqs=B, T=T, total=B * T, o=o, h0=h0, h0_rows=B, ht=ht if final else None, ht_rows=B,
             algo=algo)
     return o, ht
 
@@ -199,7 +202,7 @@ def wkv7(r, w, k, v, a, b, state, H, K, cu_seqlens=None, final=True, *, algo: in
     h0 = _state_arg(state, N, H, K, "state")
     o = torch.empty_like(ops[3])
     ht = torch.empty(N, H, K, K, device=r.device, dtype=torch.float32) if final else None
-    _launch(ops, H=H, num_seqs=N, T=0, total=T, o=o, h0=h0, h0_rows=N, ht=ht, ht_rows=N, cu=cu, algo=algo)
+    _launch(ops, H=H, K=K, num_seqs=N, T=0, total=T, o=o, h0=h0, h0_rows=N, ht=ht, ht_rows=N, cu=cu, algo=algo)
     return o, ht
 
 
@@ -222,7 +225,7 @@ def wkv7_replay_(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tenso
     ops, B, T = _prep_operands(r, w, k, v, a, b, H, K)
     _require(state, "state", torch.float32, (B, H, K, K))
     _require(n_keep, "n_keep", torch.int64, (B,))
-    _launch(ops, H=H, num_seqs=B, T=T, total=B * T, h0=state, h0_rows=B, ht=state, ht_rows=B, n_keep=n_keep,
+    _launch(ops, H=H, K=K, num_seqs=B, T=T, total=B * T, h0=state, h0_rows=B, ht=state, ht_rows=B, n_keep=n_keep,
             algo=_lib.ALGO_RECURRENT)
 
 
@@ -273,7 +276,7 @@ def wkv7_pool_op(r: Tensor, w: Tensor, k: Tensor, v: Tensor, a: Tensor, b: Tenso
         if status.numel() < 1:
             raise ValueError("status must hold at least one int32")
     o = torch.empty_like(ops[3]) if store_o else ops[3].new_empty(0)
-    _launch(ops, H=H, num_seqs=N, T=Tn, total=total, o=o if store_o else None, h0=pool, h0_idx=slots,
+    _launch(ops, H=H, K=K, num_seqs=N, T=Tn, total=total, o=o if store_o else None, h0=pool, h0_idx=slots,
             h0_rows=pool.shape[0], ht=pool if final else None, ht_idx=slots if final else None,
             ht_rows=pool.shape[0], fresh=fresh, cu=cu_seqlens, n_keep=n_keep, snap=snapshots, algo=algo,
             rec_max_len=rec_max_len, status=status)
@@ -425,8 +428,8 @@ class StatePool:
     place; reset and move run as HIP kernels on the current stream (graph-capturable, no host sync)."""
 
     def __init__(self, layers: int, slots: int, H: int, device, N: int = HEAD_SIZE):
-        if N != HEAD_SIZE:
-            raise ValueError(f"head size {N} is not supported (K = {HEAD_SIZE})")
+        if N != HEAD_SIZE:  # the slot reset / move / restore kernels are built for the model's 64 x 64 states
+            raise ValueError(f"head size {N} is not supported by the state pool (N = {HEAD_SIZE})")
         self.L, self.S, self.H = int(layers), int(slots), int(H)
         self.device = torch.device(device)
         self.wkv = torch.zeros(self.L, self.S, self.H, N, N, device=self.device, dtype=torch.float32)

@@ -75,7 +75,8 @@ def base_args(**kw):
 
 
 @pytest.mark.parametrize("field,value,code", [
-    ("head_size", 63, _lib.WKV7_ERR_SHAPE),
+    ("head_size", 257, _lib.WKV7_ERR_SHAPE),            # 1..256: 64 and the generic kernel's other sizes
+    ("head_size", 0, _lib.WKV7_ERR_SHAPE),
     ("H", 0, _lib.WKV7_ERR_SHAPE),
     ("num_seqs", -1, _lib.WKV7_ERR_SHAPE),
     ("total_tokens", 14, _lib.WKV7_ERR_SHAPE),        # dense rows need num_seqs * T operand rows
@@ -95,6 +96,25 @@ def test_validation_rejects_before_launch(field, value, code):
     assert lib.wkv7_workspace_size(ctypes.byref(a), ctypes.byref(n)) == code
     assert lib.wkv7_run(ctypes.byref(a), None) == code
     assert _lib.strerror(code) not in ("", "unknown error")
+
+
+@pytest.mark.parametrize("K,kw,code", [
+    (32, dict(algo=_lib.ALGO_CHUNKED), _lib.WKV7_ERR_ARG),     # the chunked, chain and segmented forms are K = 64
+    (32, dict(algo=_lib.ALGO_SEGMENTED), _lib.WKV7_ERR_ARG),
+    (100, dict(), _lib.WKV7_ERR_ALIGN),                        # in_tok_stride 128 < H * K = 200
+    (100, dict(in_tok_stride=200, o_tok_stride=199), _lib.WKV7_ERR_ALIGN),
+    (24, dict(w=0x10001), _lib.WKV7_ERR_ALIGN),                # bf16 operands need 2-byte alignment
+    (24, dict(h0=0x10002, h0_rows=3), _lib.WKV7_ERR_ALIGN),    # fp32 states 4-byte
+])
+def test_other_head_sizes_validate(K, kw, code):
+    """Head sizes other than 64 run the generic token-serial kernel (no workspace) with scalar accesses."""
+    a = base_args(head_size=K, **kw)
+    n = ctypes.c_size_t(0)
+    lib = _lib.load()
+    assert lib.wkv7_workspace_size(ctypes.byref(a), ctypes.byref(n)) == code
+    assert lib.wkv7_run(ctypes.byref(a), None) == code
+    ok = base_args(head_size=24, T=4000, total_tokens=12000)   # long rows: still no workspace at K != 64
+    assert lib.wkv7_workspace_size(ctypes.byref(ok), ctypes.byref(n)) == 0 and n.value == 0
 
 
 def test_snapshots_force_the_token_serial_kernel():

@@ -118,10 +118,12 @@ def test_low_rank_term_orientation_is_b_times_aTS():
     assert rel_max(S[0, 0], exp) < 1e-14
 
 
-def test_matches_explicit_transition_matrices():
-    """S_t = (diag(d_t) + b_t a_t^T) S_{t-1} + k_t v_t^T and y_t = S_t^T r_t, evaluated with dense K x K matrices."""
+@pytest.mark.parametrize("K", [16, 3, 48, 128])
+def test_matches_explicit_transition_matrices(K):
+    """S_t = (diag(d_t) + b_t a_t^T) S_{t-1} + k_t v_t^T and y_t = S_t^T r_t, evaluated with dense K x K matrices
+    (head sizes other than 64 as well: the reference takes any K)."""
     rng = np.random.default_rng(6)
-    B, T, H, K = 2, 7, 2, 16
+    B, T, H = 2, 7, 2
     r, w, k, v, a, b = model_like(rng, B, T, H, K)
     s0 = rnd(rng, B, H, K, K, scale=0.3)
     o, S, _ = wkv7_ref(r, w, k, v, a, b, s0)
@@ -136,9 +138,10 @@ def test_matches_explicit_transition_matrices():
             assert rel_max(S[bb, h], St) < 1e-12
 
 
-def test_cpp_matches_independent_numpy_transcription():
+@pytest.mark.parametrize("K", [64, 1, 24, 128, 256])
+def test_cpp_matches_independent_numpy_transcription(K):
     rng = np.random.default_rng(7)
-    B, T, H, K = 2, 13, 3, 64
+    B, T, H = 2, 13, 3
     ins = model_like(rng, B, T, H, K)
     s0 = rnd(rng, B, H, K, K, scale=0.3)
     o1, S1, _ = wkv7_ref(*ins, s0)
@@ -291,6 +294,6 @@ def test_metrics():
 
 
 def test_oracle_rejects_bad_head_size():
-    z = np.zeros((1, 1, 1, 65), np.float32)
+    z = np.zeros((1, 1, 1, 257), np.float32)
     with pytest.raises(ValueError):
         wkv7_ref(z, z, z, z, z, z)
