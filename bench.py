@@ -424,7 +424,9 @@ def cpu_baseline(synth):
     """The oracle's fp32 loop (a restatement of rwkv_next/kernels/wkv7.py:65-77) on the host cores, on a bounded
     sample of the decode workload: B = 64 sequences of a 128-slot pool, H = 64, T = 1, one pool, repeated for
     about 10 s with every usable thread (at most 16) and about 4 s with one thread.  Beside it, configuration 0 in
-    full (B = 1, T = 512, H = 12, fp32, zero initial state) with all threads and with one."""
+    full (B = 1, T = 512, H = 12, fp32, zero initial state) with all threads and with one, and configurations 2-4 at
+    their full shapes (the same lengths, slots and snapshot layout as the GPU legs) with all threads, configuration 2
+    also with one."""
     import numpy as np
 
     import oracle
@@ -461,6 +463,43 @@ def cpu_baseline(synth):
         return best
 
     ms_all, ms_one = cfg0_ms(threads), cfg0_ms(1)
+
+    def best_ms(fn, reps=2):
+        best = None
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            fn()
+            t = (time.perf_counter() - t0) * 1e3
+            best = t if best is None else min(best, t)
+        return best
+
+    # configuration 2: B = 1, T = 4096, H = 64, zero initial state
+    c2 = synth.operands_np((1, 4096, 64, 64), seed=1002)
+    c2_ins = [c2[nm] for nm in synth.OPERAND_NAMES]
+    c2_all = best_ms(lambda: oracle.wkv7_ref(*c2_ins, None, precision="f32", threads=threads))
+    c2_one = best_ms(lambda: oracle.wkv7_ref(*c2_ins, None, precision="f32", threads=1), reps=1)
+    del c2, c2_ins
+    # configuration 3: the mixed step (bench.py's mixed_bench lengths and slots), 256-slot pool
+    rng = np.random.default_rng(1003)
+    lens = [int(v) for v in rng.integers(1, 2049, size=8)] + [1] * 120
+    lens = [lens[i] for i in rng.permutation(len(lens))]
+    total3 = int(sum(lens))
+    cu3 = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    slots3 = rng.permutation(256)[:len(lens)].astype(np.int64)
+    c3 = synth.operands_np((1, total3, 64, 64), seed=1003)
+    c3_ins = [c3[nm] for nm in synth.OPERAND_NAMES]
+    pool3 = synth.state_np((256, 64, 64, 64), seed=1013)
+    c3_all = best_ms(lambda: oracle.wkv7_ref(*c3_ins, pool3, cu_seqlens=cu3, state_idx=slots3, precision="f32",
+                                             threads=threads))
+    del c3, c3_ins, pool3
+    # configuration 4: B = 64 rows of a 128-slot pool, T = 5, H = 64, per-token snapshots
+    c4 = synth.operands_np((64, 5, 64, 64), seed=1004)
+    c4_ins = [c4[nm] for nm in synth.OPERAND_NAMES]
+    pool4 = synth.state_np((128, 64, 64, 64), seed=1014)
+    slots4 = np.random.default_rng(1004).permutation(128)[:64].astype(np.int64)
+    c4_all = best_ms(lambda: oracle.wkv7_ref(*c4_ins, pool4, state_idx=slots4, snapshots=True, precision="f32",
+                                             threads=threads))
+    del c4, c4_ins, pool4
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
@@ -473,7 +512,13 @@ def cpu_baseline(synth):
             "affinity": affinity, "value_1thread": gbs1, "sample_1thread": f"{n1} steps in {dt1:.1f} s",
             "cfg0": {"shape": "B=1 T=512 H=12 fp32, zero initial state", "ms_all_threads": ms_all,
                      "ms_1thread": ms_one, "tok_s_all_threads": 512 / (ms_all * 1e-3),
-                     "tok_s_1thread": 512 / (ms_one * 1e-3)}}
+                     "tok_s_1thread": 512 / (ms_one * 1e-3)},
+            "cfg2": {"shape": "B=1 T=4096 H=64, zero initial state (full)", "ms_all_threads": c2_all,
+                     "ms_1thread": c2_one, "tok_s_all_threads": 4096 / (c2_all * 1e-3)},
+            "cfg3": {"shape": f"mixed step: 8 prefill rows + 120 decode rows, {total3} tokens, H=64, 256-slot pool "
+                              "(full)", "ms_all_threads": c3_all, "tok_s_all_threads": total3 / (c3_all * 1e-3)},
+            "cfg4": {"shape": "B=64 T=5 H=64 of a 128-slot pool, per-token snapshots (full)",
+                     "ms_all_threads": c4_all}}
 
 
 def decode_traffic():
