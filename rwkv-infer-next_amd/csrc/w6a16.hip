@@ -1425,26 +1425,46 @@ struct BigW {
     uint32_t sc;
 };
 
-__device__ __forceinline__ void big_load_a(const Args& p, int b, int m0, int c, BigA& g) {
-    const int t = threadIdx.x;
-    const uint16_t* const ab = p.a + (int64_t)b * p.sa_b + 64 * c + 8 * (t & 7);
+// Where a thread's loads go, fixed for the call: raw buffers over A's batch slice, the packed weight's and its scales
+// (wave-uniform descriptors), the lane's 32-bit offsets, and the wavefront's strip offsets; per chunk only a scalar
+// offset changes.  (With 64-bit per-lane addresses the compiler placed the next chunk's address registers where the
+// previous chunk's weight bytes were still arriving and waited for those loads first.)
+struct BigSrc {
+    __amdgpu_buffer_rsrc_t ra, rw, rs;
+    int va[4];        // A rows (t >> 3) + 64 j of the tile, piece t & 7 (+ 128 bytes per chunk)
+    int vw, vh, vs;   // the lane's offsets into a weight block (lo dwords, hi dwords) and a scale block
+    int sw, ss;       // the wavefront's strip: byte offsets of its first weight block and first scale block
+};
+
+__device__ __forceinline__ BigSrc big_src(const Args& p, int b, int m0, int n0) {
+    BigSrc d;
+    const int t = threadIdx.x, wv = t >> 6, lane = t & 63, i = lane & 15, w4 = wv & 3;
+    const int nchunks = p.K / 64, groups = p.K / p.group_k;
+    d.ra = rsrc((uint64_t)(p.a + (int64_t)b * p.sa_b), ((int64_t)(p.M - 1) * p.sa_m + p.K) * 2);
+    d.rw = rsrc((uint64_t)(p.lo + (int64_t)b * p.sl_b), (int64_t)p.n_strips * nchunks * kPackBytes);
+    d.rs = rsrc((uint64_t)(p.sc + (int64_t)b * p.ss_b), (int64_t)p.n_strips * groups * kTileN * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int m = min(m0 + (t >> 3) + 64 * j, p.M - 1);
-        g.a[j] = *reinterpret_cast<const u4*>(ab + (int64_t)m * p.sa_m);
-    }
+    for (int j = 0; j < 4; ++j) d.va[j] = min(m0 + (t >> 3) + 64 * j, p.M - 1) * (int)p.sa_m * 2 + 16 * (t & 7);
+    const int strip = min(n0 / kTileN + (wv >> 2), p.n_strips - 1);
+    d.vw = 1024 * w4 + 16 * lane;                                  // R[4 w4 .. 4 w4 + 3]
+    d.vh = 1024 * (4 + (w4 >> 1)) + 8 * (w4 & 1) + 16 * lane;     // R[16 + 2 w4], R[17 + 2 w4]
+    d.vs = (8 * i + 2 * w4) * 2;
+    d.sw = strip * nchunks * kPackBytes;
+    d.ss = strip * groups * kTileN * 2;
+    return d;
 }
 
-__device__ __forceinline__ void big_load_w(const Args& p, int b, int n0, int c, BigW& g) {
-    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, w4 = wv & 3;
-    const int nchunks = p.K / 64, groups = p.K / p.group_k;
-    const int strip = min(n0 / kTileN + (wv >> 2), p.n_strips - 1);
-    const uint8_t* const blk = p.lo + (int64_t)b * p.sl_b + ((int64_t)strip * nchunks + c) * kPackBytes + 16 * lane;
-    g.w = *reinterpret_cast<const u4*>(blk + 1024 * w4);                                 // R[4 w4 .. 4 w4 + 3]
-    g.h = *reinterpret_cast<const uint2*>(blk + 1024 * (4 + (w4 >> 1)) + 8 * (w4 & 1));  // R[16 + 2 w4], R[17 + 2 w4]
-    const int grp = (c * 64) / p.group_k;
-    g.sc = *reinterpret_cast<const uint32_t*>(p.sc + (int64_t)b * p.ss_b +
-                                              ((int64_t)strip * groups + grp) * kTileN + 8 * i + 2 * w4);
+__device__ __forceinline__ void big_load_a(const BigSrc& d, int c, BigA& g) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        g.a[j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(d.ra, d.va[j], soff(128 * c), 0));
+}
+
+__device__ __forceinline__ void big_load_w(const Args& p, const BigSrc& d, int c, BigW& g) {
+    const int blk = soff(d.sw + c * kPackBytes);
+    g.w = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(d.rw, d.vw, blk, 0));
+    g.h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(d.rw, d.vh, blk, 0));
+    g.sc = __builtin_amdgcn_raw_buffer_load_b32(d.rs, d.vs, soff(d.ss + ((c * 64) / p.group_k) * kTileN * 2), 0);
 }
 
 __device__ __forceinline__ void big_store_a(uint8_t* stage, const BigA& g) {
@@ -1540,11 +1560,12 @@ __global__ __launch_bounds__(512, 1) void w6a16_big_kernel(const Args p) {
     for (int mt = 0; mt < 8; ++mt)
 #pragma unroll
         for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
+    const BigSrc src = big_src(p, b, m0, n0);
     BigW w0, w1;
     BigA ga;
-    big_load_a(p, b, m0, 0, ga);
-    big_load_w(p, b, n0, 0, w0);
-    big_load_w(p, b, n0, min(1, nch - 1), w1);
+    big_load_a(src, 0, ga);
+    big_load_w(p, src, 0, w0);
+    big_load_w(p, src, min(1, nch - 1), w1);
     big_store_a(lds, ga);
 #pragma unroll
     for (int e = 0; e < 4; ++e) big_store_w<A>(lds, w0, e);
@@ -1553,8 +1574,8 @@ __global__ __launch_bounds__(512, 1) void w6a16_big_kernel(const Args p) {
     auto step = [&](int c, const BigW& ws, BigW& wl) {
         uint8_t* const cur = lds + (c & 1) * kBigStage;
         uint8_t* const nxt = lds + ((c & 1) ^ 1) * kBigStage;
-        big_load_a(p, b, m0, min(c + 1, nch - 1), ga);  // the last steps reload the last chunk (stored unused)
-        big_load_w(p, b, n0, min(c + 2, nch - 1), wl);
+        big_load_a(src, min(c + 1, nch - 1), ga);  // the last steps reload the last chunk (stored unused)
+        big_load_w(p, src, min(c + 2, nch - 1), wl);
         u4 wo[4], ao[2];
         ao[0] = *reinterpret_cast<const u4*>(cur + big_slot(128 * wm + i, q));
 #pragma unroll
@@ -1615,7 +1636,13 @@ WideCfg wide_cfg(int M) {
 
 // Large-M kernel: M above this, packed weights (no workspace, no split-K).
 constexpr int kBigMinM = 256;
-bool big_rows(const w6a16_args* a) { return a->M > kBigMinM && a->format == W6A16_FORMAT_PACKED; }
+// (its loads go through raw buffers: A's batch slice and the packed weight's below 2 GB)
+bool big_rows(const w6a16_args* a) {
+    if (a->M <= kBigMinM || a->format != W6A16_FORMAT_PACKED || a->K < 64) return false;
+    const int64_t a_bytes = ((int64_t)(a->M - 1) * a->a_row_stride + a->K) * 2;
+    const int64_t w_bytes = (int64_t)((a->N + kTileN - 1) / kTileN) * (a->K / 64) * kPackBytes;
+    return a_bytes < 0x7FFFFFFF && w_bytes < 0x7FFFFFFF;
+}
 
 struct Layout {
     bool big;                    // the large-M kernel
