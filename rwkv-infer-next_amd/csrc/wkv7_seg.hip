@@ -65,21 +65,23 @@ constexpr int kSpinLimit = 1 << 22;    // LDS ring waits (s_sleep 1 each: a few 
 constexpr int kFlagSpinLimit = 1 << 20;  // segment hand-off waits (s_sleep 8 each)
 
 // Record of one chunk in the LDS ring (byte offsets).  Pieces are lane-contiguous 16-byte words.
-// The chunk transition is kept in factored form (Bt = Bp diag(2^{c-m}), Kt = Kp diag(2^{c-m}), W = W' diag(2^m),
-// R0 = Rh diag(2^m)): the state wavefronts apply
-//   U = W S + U0,   S <- Gamma S + Bt^T U + Kt^T V,   y^T = S^T R0^T + U^T rho^T + V^T sigma^T
+// The chunk transition is kept in factored form (W = W' diag(2^m), R0 = Rh diag(2^m), and Bp, Kp with their row
+// factor 2^{c-m} kept apart): the state wavefronts apply
+//   U = W S + U0,   S <- Gamma S + diag(2^{c-m}) (Bp^T U + Kp^T V),   y^T = S^T R0^T + U^T rho^T + V^T sigma^T
 // per 16-column tile, which costs them about as many MFMAs as a dense A S + H would and saves the prep wavefront
-// forming A, H and O (its critical path; the state wavefronts have slack).
+// forming A, H and O (its critical path; the state wavefronts have slack).  Bp and Kp go into the record as exact
+// transposes of the prep's own hi/lo splits, so the prep wavefront does not rescale and split them again.
 constexpr int REC_W = 0;                       // W^T hi/lo as 16x16x32 A operands: [token tile][kb][hl][lane]
-constexpr int REC_B = REC_W + 8 * 1024;        // Bt hi/lo as 16x16x32 A operands: [k tile m][hl][lane]
-constexpr int REC_K = REC_B + 8 * 1024;        // Kt hi/lo, same
+constexpr int REC_B = REC_W + 8 * 1024;        // Bp hi/lo as 16x16x32 A operands: [k tile m][hl][lane]
+constexpr int REC_K = REC_B + 8 * 1024;        // Kp hi/lo, same
 constexpr int REC_R = REC_K + 8 * 1024;        // R0^T hi as 16x16x32 B operands: [token tile][kb][lane]
 constexpr int REC_U = REC_R + 4 * 1024;        // U0, RL fp32: [column tile j][token tile][lane]
 constexpr int REC_V = REC_U + 8 * 1024;        // V (exact), RL tiles (0, j), (1, j) stacked: [column tile j][lane]
 constexpr int REC_RHO = REC_V + 4 * 1024;      // rho^T hi: tile (0,0) (low 8 bytes), then tiles (0,1), (1,1) stacked
 constexpr int REC_SIG = REC_RHO + 2 * 1024;    // sigma^T hi, same
 constexpr int REC_G = REC_SIG + 2 * 1024;      // Gamma = 2^c per channel, fp32 [64]
-constexpr int REC_BYTES = REC_G + 256;         // 45312
+constexpr int REC_F = REC_G + 256;             // 2^{c-m} per channel, fp32 [64]
+constexpr int REC_BYTES = REC_F + 256;         // 45568
 
 struct SegSmem {
     char ring[NREC][REC_BYTES];
@@ -614,12 +616,8 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
             T4 acc = split_t(p16x3(split_t(plus_i(LLf, lane)), split_t(plus_i(L2tf, lane)), z4()));
             acc = split_t(p16x3(split_t(plus_i(L4f, lane)), acc, z4()));
             TT[d] = split_t(p16x3(split_t(plus_i(L8f, lane)), acc, z4()));
-            if (d == 0) {  // T00 itself, for the off-diagonal block
-                const f4 L8tf = p16x3(L4, L4t, z4());
-                T4 t0 = split_t(p16x3(split_t(plus_i(LTf, lane)), split_t(plus_i(L2f, lane)), z4()));
-                t0 = split_t(p16x3(split_t(plus_i(L4tf, lane)), t0, z4()));
-                T00 = split_t(p16x3(split_t(plus_i(L8tf, lane)), t0, z4()));
-            }
+            if (d == 0)  // T00 itself, for the off-diagonal block: the transpose of T00^T (hi and lo, exact)
+                T00 = split_t(mma16(TT[0].l, Id, mma16(TT[0].h, Id, z4())));
         }
         const T4 Z = split_t(p16x3(split_t(aT[1]), T00, z4()));  // alpha10 T00
         tt00 = TT[0];
@@ -716,27 +714,18 @@ __device__ __forceinline__ void prep_chunk(const Raw& raw, int Lc, char* rec, fl
             reinterpret_cast<f4*>(rec + REC_G)[lane] = *reinterpret_cast<const f4*>(&fac[2][4 * lane]);
     }
 
-    // ---- 8. per k tile m: Bt = Bp diag(2^{c-m}) and Kt = Kp diag(2^{c-m}) (token-row RL tiles, rescaled and split
-    //         again), stored
-    float cfm[4];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) cfm[m] = fac[1][16 * m + i];
-    auto scaled = [&](const bf8 (&H8)[2][2], const bf8 (&L8)[2][2], int tau, int m) {
-        const bf8 I = (m & 1) ? I1 : I0;
-        f4 x = mma32(L8[tau][m >> 1], I, mma32(H8[tau][m >> 1], I, z4()));  // hi + lo, exact
-#pragma unroll
-        for (int v = 0; v < 4; ++v) x[v] *= cfm[m];
-        return split_t(x);
-    };
+    // ---- 8. per k tile m: Bp and Kp as token-row RL tiles (the transposes of their hi and lo parts, each exact),
+    //         stored with the row factors 2^{c-m}
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
-        const T8 btm = cat(scaled(Bh, Bl, 0, m), scaled(Bh, Bl, 1, m));
-        R[(REC_B / 16) + (m * 2 + 0) * 64 + lane] = as_u4(btm.h);
-        R[(REC_B / 16) + (m * 2 + 1) * 64 + lane] = as_u4(btm.l);
-        const T8 ktm = cat(scaled(Kh, Kl, 0, m), scaled(Kh, Kl, 1, m));
-        R[(REC_K / 16) + (m * 2 + 0) * 64 + lane] = as_u4(ktm.h);
-        R[(REC_K / 16) + (m * 2 + 1) * 64 + lane] = as_u4(ktm.l);
+        const T8 bpm = cat(rl(Bh, Bl, 0, m), rl(Bh, Bl, 1, m));
+        R[(REC_B / 16) + (m * 2 + 0) * 64 + lane] = as_u4(bpm.h);
+        R[(REC_B / 16) + (m * 2 + 1) * 64 + lane] = as_u4(bpm.l);
+        const T8 kpm = cat(rl(Kh, Kl, 0, m), rl(Kh, Kl, 1, m));
+        R[(REC_K / 16) + (m * 2 + 0) * 64 + lane] = as_u4(kpm.h);
+        R[(REC_K / 16) + (m * 2 + 1) * 64 + lane] = as_u4(kpm.l);
     }
+    if (lane < 16) reinterpret_cast<f4*>(rec + REC_F)[lane] = *reinterpret_cast<const f4*>(&fac[1][4 * lane]);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -861,7 +850,7 @@ __device__ __forceinline__ void run_unit(const Params& p, const Unit& U, int32_t
             }
             const uint4* const R = reinterpret_cast<const uint4*>(sm.ring[slot]);
             uint4 rw[2][2][2], rb[4][2], rk[4][2], rr[2][2], rho[2], sig[2], rv;
-            f4 ru[2], gm[4];
+            f4 ru[2], gm[4], cf[4];
 #pragma unroll
             for (int tau = 0; tau < 2; ++tau)
 #pragma unroll
@@ -876,6 +865,7 @@ __device__ __forceinline__ void run_unit(const Params& p, const Unit& U, int32_t
                     rk[m][hl] = R[(REC_K / 16) + (m * 2 + hl) * 64 + lane];
                 }
                 gm[m] = reinterpret_cast<const f4*>(sm.ring[slot] + REC_G)[4 * m + q];  // 2^c of rows 16 m + 4 q + v
+                cf[m] = reinterpret_cast<const f4*>(sm.ring[slot] + REC_F)[4 * m + q];  // 2^{c-m}, same rows
             }
 #pragma unroll
             for (int tau = 0; tau < 2; ++tau) {
@@ -903,16 +893,16 @@ __device__ __forceinline__ void run_unit(const Params& p, const Unit& U, int32_t
                     X[tau] = x;
                 }
             };
-            // M <- Gamma M + Bt^T X (+ Kt^T V for the state)
+            // M <- Gamma M + diag(2^{c-m}) (Bp^T X (+ Kp^T V for the state))
             auto apply = [&](f4 (&M)[4], const f4 (&X)[2], bool state) {
                 const T8 xo = cat(split_t(X[0]), split_t(X[1]));
 #pragma unroll
                 for (int m = 0; m < 4; ++m) {
                     f4 x = z4();
-#pragma unroll
-                    for (int v = 0; v < 4; ++v) x[v] = gm[m][v] * M[m][v];
                     if (state) x = p32x2(T8{as_bf8(rk[m][0]), as_bf8(rk[m][1])}, as_bf8(rv), x);
-                    M[m] = p32x3(T8{as_bf8(rb[m][0]), as_bf8(rb[m][1])}, xo, x);
+                    x = p32x3(T8{as_bf8(rb[m][0]), as_bf8(rb[m][1])}, xo, x);
+#pragma unroll
+                    for (int v = 0; v < 4; ++v) M[m][v] = fmaf(cf[m][v], x[v], gm[m][v] * M[m][v]);
                 }
             };
             // (R0 M + rho X)^T tiles (column tile j, token tile): y^T for M = S, X = U, (Q P)^T for M = P, X = W P
