@@ -92,6 +92,64 @@ def decode_bench(torch, kernels, synth, dev, steps, warmup, H=64):
             "launches_per_step": L, "pairs_per_launch": B * H}
 
 
+def head_size_bench(torch, kernels, synth, dev, steps, warmup, K):
+    """Head sizes other than 64 (the generic token-serial kernel): H = 4096 / K heads, the 7.2B model's width.
+    Decode: B = 64 slots of a 128-slot [128, H, K, K] pool, T = 1, 8 layer pools in one HIP graph; traffic per pair
+    2 K^2 fp32 (state read and written in place) + 7 K bf16 (six operands, y).  Prefill: B = 1, T = 512 dense,
+    state from zeros, eager; traffic 7 K bf16 per head-token + K^2 fp32 per head (the final state)."""
+    H, L, S, B = 4096 // K, 8, 128, 64
+    g = torch.Generator(device=dev).manual_seed(3001 + K)
+    pools = [(0.1 * torch.randn(S, H, K, K, device=dev, generator=g)) for _ in range(L)]
+    ins = []
+    for layer in range(L):
+        ops = synth.operands_torch((B, 1, H, K), seed=4000 + layer, device=dev)
+        ins.append([ops[n].reshape(B, 1, H * K).contiguous() for n in synth.OPERAND_NAMES])
+    slots = torch.randperm(S, device=dev, generator=g)[:B].contiguous()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for layer in range(L):
+            kernels.wkv7_pool_(*ins[layer], pools[layer], slots, H, K)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = [kernels.wkv7_pool_(*ins[layer], pools[layer], slots, H, K) for layer in range(L)]
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us_launch = e0.elapsed_time(e1) * 1e3 / (steps * L)
+    bytes_launch = B * H * (2 * K * K * 4 + 7 * K * 2)
+    del outs, graph, pools
+    T = 512
+    ops = synth.operands_torch((1, T, H, K), seed=4100 + K, device=dev)
+    x = [ops[n].reshape(1, T, H * K).contiguous() for n in synth.OPERAND_NAMES]
+    for _ in range(2):
+        kernels.wkv7(*x, None, H, K)
+    torch.cuda.synchronize()
+    n = max(2, steps // 10)
+    e0.record()
+    for _ in range(n):
+        kernels.wkv7(*x, None, H, K)
+    e1.record()
+    torch.cuda.synchronize()
+    us_pf = e0.elapsed_time(e1) * 1e3 / n
+    pf_bytes = T * H * 7 * K * 2 + H * K * K * 4
+    return {"K": K, "H": H,
+            "decode": {"us_per_launch": us_launch, "bytes_per_launch": bytes_launch,
+                       "GBps": bytes_launch / (us_launch * 1e-6) / 1e9,
+                       "frac_hbm": bytes_launch / (us_launch * 1e-6) / 1e9 / HBM_PEAK_GBS},
+            "prefill_T512": {"us": us_pf, "tok_s": T / (us_pf * 1e-6), "bytes": pf_bytes,
+                             "frac_hbm": pf_bytes / (us_pf * 1e-6) / 1e9 / HBM_PEAK_GBS}}
+
+
 def cfg0_bench(torch, kernels, synth, dev, steps, warmup):
     """Configuration 0's shape on the GPU (B = 1, T = 512, H = 12; bf16 operands, fp32 state from zeros), eager
     calls, for every algorithm -- beside cpu_baseline.cfg0, the oracle's fp32 loop on the host at the same shape."""
@@ -538,8 +596,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--skip-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "varlen", "verify", "mixed", "timemix", "int6", "tp"],
-                    default=None)
+    ap.add_argument("--only", choices=["decode", "prefill", "varlen", "verify", "mixed", "timemix", "int6", "tp",
+                                       "heads"], default=None)
     ap.add_argument("--copy-calib", action="store_true",
                     help="first run a plain device copy of 1 GiB (reference dispatch for rocprofv3 --pmc scaling)")
     args = ap.parse_args()
@@ -595,6 +653,9 @@ def main():
     if args.only in (None, "timemix"):
         log("timemix")
         res["timemix"] = timemix_bench(torch, kernels, dev, max(5, args.steps // 5), args.warmup)
+    if args.only in (None, "heads"):
+        log("head sizes 128 and 32 (generic kernel)")
+        res["head_sizes"] = [head_size_bench(torch, kernels, synth, dev, args.steps, args.warmup, K) for K in (128, 32)]
     if args.only in (None, "int6"):
         log("int6")
         res["int6"] = int6_bench(torch, kernels, dev, args.steps, args.warmup)
@@ -636,6 +697,8 @@ def main():
         out["tp_share_H8"] = res["tp_share_H8"]
     if "varlen" in res:
         out["varlen"] = res["varlen"]
+    if "head_sizes" in res:
+        out["head_sizes"] = res["head_sizes"]
     if "verify" in res:
         out["verify"] = res["verify"]
     if "mixed" in res:
