@@ -210,3 +210,40 @@ def test_ragged_equal_rows_on_unit_edges_and_auto(dev, K):
     say(f"y max-rel {eo:.3e}  state max-rel {es:.3e}")
     assert eo <= Y_TOL and es <= S_TOL
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+@pytest.mark.parametrize("nrows", [4096, 4097])
+def test_ragged_row_table_limit(dev, K, nrows):
+    """The segmented kernel keeps a ragged call's row table in LDS, at most 4096 rows.  4096 rows (mostly short, a
+    few long, H = 2 so that each head's chunk stream is shared by many units) run as one segmented dispatch with the
+    short rows in its tail; 4097 rows make AUTO take the two-kernel chunked path beside a token-serial launch, and an
+    explicit SEGMENTED request is refused before any launch.  Both AUTO calls against the fp64 oracle."""
+    from oracle import wkv7_ref
+    from rwkv_next_amd import _lib
+    import rwkv_next_amd.synth as synth
+    H = 2
+    rng = np.random.default_rng(nrows)
+    lens = rng.integers(0, 48, size=nrows)
+    lens[rng.choice(nrows, size=8, replace=False)] = rng.integers(300, 1500, size=8)
+    lens = [int(x) for x in lens]
+    say("seg row table limit", nrows, sum(lens))
+    total = sum(lens)
+    ops = operands(1, total, H, seed=nrows + 1)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    slots_n = nrows + 16
+    pool0 = synth.state_np((slots_n, H, 64, 64), seed=nrows + 2)
+    slots = rng.permutation(slots_n)[:nrows].astype(np.int64)
+    o_ref, pool_ref, _ = wkv7_ref(*np_list(ops), pool0, cu_seqlens=cu, state_idx=slots)
+    pool = torch.from_numpy(pool0).to(dev)
+    status = K.new_status(dev)
+    dev_ops, dslots, dcu = to_dev(ops, dev), torch.from_numpy(slots).to(dev), torch.from_numpy(cu).to(dev)
+    o = K.wkv7_pool_(*dev_ops, pool, dslots, H, 64, cu_seqlens=dcu, max_len=max(lens), status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    eo, es = errs(o, o_ref, pool, pool_ref)
+    assert eo <= Y_TOL and es <= S_TOL
+    if nrows > 4096:
+        with pytest.raises(_lib.Wkv7Error):
+            K.wkv7_pool_(*dev_ops, torch.from_numpy(pool0).to(dev), dslots, H, 64, cu_seqlens=dcu,
+                         max_len=max(lens), algo=SEG)
+        torch.cuda.synchronize()
