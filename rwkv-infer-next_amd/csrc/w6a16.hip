@@ -1413,12 +1413,9 @@ __device__ __forceinline__ void dequant4(uint32_t u, float s, float s32, uint32_
     d1 = pack_act<A>(v2, v3);
 }
 
-// One chunk's global bytes, per thread: A rows (t >> 3) + 64 j, piece t & 7 (BigA), and the packed weight's share of
-// wavefront w (BigW: strip w >> 2 of the tile, tiles 2 (w & 3) and 2 (w & 3) + 1 -- their lo dwords, one 16-byte lane
-// load of the block, their two hi dwords and their two scales).
-struct BigA {
-    u4 a[4];
-};
+// One chunk's weight bytes, per thread: the packed weight's share of wavefront w (strip w >> 2 of the tile, tiles
+// 2 (w & 3) and 2 (w & 3) + 1 -- their lo dwords, one 16-byte lane load of the block, their two hi dwords and their
+// two scales).  A's rows go from memory straight into LDS (big_copy_a).
 struct BigW {
     u4 w;
     uint2 h;
@@ -1431,7 +1428,8 @@ struct BigW {
 // previous chunk's weight bytes were still arriving and waited for those loads first.)
 struct BigSrc {
     __amdgpu_buffer_rsrc_t ra, rw, rs;
-    int va[4];        // A rows (t >> 3) + 64 j of the tile, piece t & 7 (+ 128 bytes per chunk)
+    int va[4];        // A row 8 w + 64 j + (lane >> 3) of the tile, the piece its LDS slot lane & 7 holds (+ 128
+                      // bytes per chunk)
     int vw, vh, vs;   // the lane's offsets into a weight block (lo dwords, hi dwords) and a scale block
     int sw, ss;       // the wavefront's strip: byte offsets of its first weight block and first scale block
 };
@@ -1444,7 +1442,10 @@ __device__ __forceinline__ BigSrc big_src(const Args& p, int b, int m0, int n0) 
     d.rw = rsrc((uint64_t)(p.lo + (int64_t)b * p.sl_b), (int64_t)p.n_strips * nchunks * kPackBytes);
     d.rs = rsrc((uint64_t)(p.sc + (int64_t)b * p.ss_b), (int64_t)p.n_strips * groups * kTileN * 2);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) d.va[j] = min(m0 + (t >> 3) + 64 * j, p.M - 1) * (int)p.sa_m * 2 + 16 * (t & 7);
+    for (int j = 0; j < 4; ++j) {
+        const int r = 8 * wv + 64 * j + (lane >> 3), piece = (lane & 7) ^ ((r >> 1) & 7);  // big_slot's swizzle
+        d.va[j] = min(m0 + r, p.M - 1) * (int)p.sa_m * 2 + 16 * piece;
+    }
     const int strip = min(n0 / kTileN + (wv >> 2), p.n_strips - 1);
     d.vw = 1024 * w4 + 16 * lane;                                  // R[4 w4 .. 4 w4 + 3]
     d.vh = 1024 * (4 + (w4 >> 1)) + 8 * (w4 & 1) + 16 * lane;     // R[16 + 2 w4], R[17 + 2 w4]
@@ -1454,10 +1455,18 @@ __device__ __forceinline__ BigSrc big_src(const Args& p, int b, int m0, int n0) 
     return d;
 }
 
-__device__ __forceinline__ void big_load_a(const BigSrc& d, int c, BigA& g) {
+__device__ __forceinline__ void vmem_wait() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// A's 256 x 64 slice of chunk c into a stage, straight from memory (buffer_load ... lds): wavefront w's load j fills
+// the stage's 1 KB of rows 8 w + 64 j .. + 7, lane l the 16-byte slot l & 7 of row 8 w + 64 j + (l >> 3), with the
+// piece big_slot places there.  The two stages are separate LDS arrays, so the compiler sees that these writes do
+// not alias the current stage's operand reads and waits for them only at the barrier.
+__device__ __forceinline__ void big_copy_a(const BigSrc& d, int c, uint8_t* stage) {
+    const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int j = 0; j < 4; ++j)
-        g.a[j] = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(d.ra, d.va[j], soff(128 * c), 0));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(d.ra, (__attribute__((address_space(3))) void*)(stage + (8 * wv + 64 * j) * 128),
+                                                 16, d.va[j], soff(128 * c), 0, 0);
 }
 
 __device__ __forceinline__ void big_load_w(const Args& p, const BigSrc& d, int c, BigW& g) {
@@ -1465,12 +1474,6 @@ __device__ __forceinline__ void big_load_w(const Args& p, const BigSrc& d, int c
     g.w = __builtin_bit_cast(u4, __builtin_amdgcn_raw_buffer_load_b128(d.rw, d.vw, blk, 0));
     g.h = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(d.rw, d.vh, blk, 0));
     g.sc = __builtin_amdgcn_raw_buffer_load_b32(d.rs, d.vs, soff(d.ss + ((c * 64) / p.group_k) * kTileN * 2), 0);
-}
-
-__device__ __forceinline__ void big_store_a(uint8_t* stage, const BigA& g) {
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u4*>(stage + big_slot((t >> 3) + 64 * j, t & 7)) = g.a[j];
 }
 
 // Piece e (0..3) of the wavefront's weight share, dequantised into the stage: tile t = 2 (w & 3) + (e >> 1), rows
@@ -1545,9 +1548,51 @@ __device__ __forceinline__ void big_store_out(const Args& p, int b, int m0, int 
     }
 }
 
+// One chunk of the large-M kernel: the MFMAs over stage `cur`; the next chunk's weights dequantised into the other
+// stage's weight rows (`nxt_w`) during the first two MFMA blocks, then A's next chunk copied into its A rows (`nxt_a`,
+// the same stage base: the two touch disjoint bytes).  The stages come in as restrict pointers, so that after
+// inlining their accesses carry alias scopes and the compiler's wait insertion sees that the copies do not alias the
+// operand reads of `cur`; no LDS store follows the copies within the step (the compiler would wait for them before
+// one), so the only wait for them is at the barrier.
+template <class A>
+__device__ __forceinline__ void big_step(const Args& p, const BigSrc& src, int c, int nch,
+                                         const uint8_t* __restrict__ cur, uint8_t* __restrict__ nxt_a,
+                                         uint8_t* __restrict__ nxt_w, const BigW& ws, BigW& wl, f4 (&acc)[8][4]) {
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
+    const int wm = wv & 1, wn = wv >> 1;
+    big_load_w(p, src, min(c + 2, nch - 1), wl);
+    u4 wo[4], ao[2];
+    ao[0] = *reinterpret_cast<const u4*>(cur + big_slot(128 * wm + i, q));
+#pragma unroll
+    for (int blk = 0; blk < 16; ++blk) {
+        const int kh = blk >> 3, mt = blk & 7;
+        if (mt == 0) {
+#pragma unroll
+            for (int nt = 0; nt < 4; ++nt)
+                wo[nt] = *reinterpret_cast<const u4*>(cur + kBigTile * 128 + big_slot(64 * wn + 16 * nt + i, 4 * kh + q));
+        }
+        if (blk + 1 < 16) {
+            const int kn = (blk + 1) >> 3, mn = (blk + 1) & 7;
+            ao[(blk + 1) & 1] = *reinterpret_cast<const u4*>(cur + big_slot(128 * wm + 16 * mn + i, 4 * kn + q));
+        }
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = A::mma(wo[nt], ao[blk & 1], acc[mt][nt]);
+        if (blk < 2) {
+#pragma unroll
+            for (int e = 2 * blk; e < 2 * blk + 2; ++e) big_store_w<A>(nxt_w, ws, e);
+        }
+        if (blk == 1) big_copy_a(src, min(c + 1, nch - 1), nxt_a);  // after the last weight store (the last steps
+                                                                       // copy the last chunk again, unused)
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    vmem_wait();
+    __syncthreads();
+}
+
 template <class A>
 __global__ __launch_bounds__(512, 1) void w6a16_big_kernel(const Args p) {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[2 * kBigStage];
+    __shared__ __attribute__((aligned(16))) uint8_t lds0[kBigStage];
+    __shared__ __attribute__((aligned(16))) uint8_t lds1[kBigStage];
     const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63, i = lane & 15, q = lane >> 4;
     const int wm = wv & 1, wn = wv >> 1;  // rows 128 wm .., columns 64 wn ..
     const int tiles_m = (p.M + kBigTile - 1) / kBigTile, tiles_n = (p.N + kBigTile - 1) / kBigTile;
@@ -1562,46 +1607,24 @@ __global__ __launch_bounds__(512, 1) void w6a16_big_kernel(const Args p) {
         for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = f4{0.f, 0.f, 0.f, 0.f};
     const BigSrc src = big_src(p, b, m0, n0);
     BigW w0, w1;
-    BigA ga;
-    big_load_a(src, 0, ga);
+    big_copy_a(src, 0, lds0);
     big_load_w(p, src, 0, w0);
     big_load_w(p, src, min(1, nch - 1), w1);
-    big_store_a(lds, ga);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) big_store_w<A>(lds, w0, e);
+    for (int e = 0; e < 4; ++e) big_store_w<A>(lds0, w0, e);
+    vmem_wait();  // this wavefront's copies into the stage have landed (the barrier does not wait for them)
     __syncthreads();
-    // chunk c: its stage is c & 1; ws holds chunk c + 1's weight bytes, wl receives chunk c + 2's
-    auto step = [&](int c, const BigW& ws, BigW& wl) {
-        uint8_t* const cur = lds + (c & 1) * kBigStage;
-        uint8_t* const nxt = lds + ((c & 1) ^ 1) * kBigStage;
-        big_load_a(src, min(c + 1, nch - 1), ga);  // the last steps reload the last chunk (stored unused)
-        big_load_w(p, src, min(c + 2, nch - 1), wl);
-        u4 wo[4], ao[2];
-        ao[0] = *reinterpret_cast<const u4*>(cur + big_slot(128 * wm + i, q));
-#pragma unroll
-        for (int blk = 0; blk < 16; ++blk) {
-            const int kh = blk >> 3, mt = blk & 7;
-            if (mt == 0) {
-#pragma unroll
-                for (int nt = 0; nt < 4; ++nt)
-                    wo[nt] = *reinterpret_cast<const u4*>(cur + kBigTile * 128 +
-                                                          big_slot(64 * wn + 16 * nt + i, 4 * kh + q));
-            }
-            if (blk + 1 < 16) {
-                const int kn = (blk + 1) >> 3, mn = (blk + 1) & 7;
-                ao[(blk + 1) & 1] = *reinterpret_cast<const u4*>(cur + big_slot(128 * wm + 16 * mn + i, 4 * kn + q));
-            }
-#pragma unroll
-            for (int nt = 0; nt < 4; ++nt) acc[mt][nt] = A::mma(wo[nt], ao[blk & 1], acc[mt][nt]);
-            if ((blk & 3) == 3) big_store_w<A>(nxt, ws, blk >> 2);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-        big_store_a(nxt, ga);
-        __syncthreads();
+    // chunk c: its stage is c & 1 (lds0 / lds1, fixed per unrolled step); ws holds chunk c + 1's weight bytes, wl
+    // receives chunk c + 2's
+    auto step = [&](auto odd, int c, const BigW& ws, BigW& wl) {
+        if constexpr (decltype(odd)::value)
+            big_step<A>(p, src, c, nch, lds1, lds0, lds0, ws, wl, acc);
+        else
+            big_step<A>(p, src, c, nch, lds0, lds1, lds1, ws, wl, acc);
     };
     for (int c = 0; c < nch; c += 2) {
-        step(c, w1, w0);
-        if (c + 1 < nch) step(c + 1, w0, w1);
+        step(std::false_type{}, c, w1, w0);
+        if (c + 1 < nch) step(std::true_type{}, c + 1, w0, w1);
     }
     // lane (i, q) of tile (mt, nt): C[m0 + 128 wm + 16 mt + i][n0 + 64 wn + 16 nt + 4 q .. + 3] (N % 16 == 0: the
     // four columns are all inside or all outside)
