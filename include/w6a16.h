@@ -89,7 +89,8 @@ int w6a16_plan_split_packed(int32_t B, int32_t M, int32_t N, int32_t K);
 int w6a16_matmul(const w6a16_args *args, void *stream);
 
 /* w[b][k][n] = scale * q ([B][K][N], batch stride in elements) as bf16, fp16 or fp32 (W6A16_OUT_*):
- * the large-M path, where a library GEMM on the dequantised weight wins.  Replaces dequantize_int6
+ * the Python layer's path above M = 256, where a library GEMM on the dequantised weight is faster than the large-M
+ * kernel (measured at K = 4096, N = 16384) except near M = 1024.  Replaces dequantize_int6
  * (int6_gemm.py:115-131) on the device.  N % 16 == 0; all pointers 16-byte aligned. */
 int w6a16_dequantize(const uint8_t *lo, const uint8_t *hi, const uint16_t *scales, void *w, int32_t B, int32_t K,
                      int32_t N, int32_t group_k, int64_t lo_batch_stride, int64_t hi_batch_stride,
