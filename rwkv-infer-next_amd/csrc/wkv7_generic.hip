@@ -18,6 +18,7 @@
 #include "wkv7.h"
 #include "wkv7_device.h"
 #include "wkv7_launch.h"
+#include "wkv7_token.h"
 
 namespace wkv7 {
 
@@ -161,10 +162,124 @@ __global__ __launch_bounds__(64 * kGWaves) void wkv7_generic_kernel(const Params
     }
 }
 
+// Head sizes that are multiples of 32, with 16-byte aligned state buffers: the K = 64 decode kernel's layout
+// (wkv7_token.h) stretched to K rows.  One wavefront per (sequence, head, block of 32 state columns); lane
+// L = 8 g + c holds rows k = g + 8 j (j < K / 8) and columns 32 cb + 4 c .. + 3 as float4s, so every state load or
+// store instruction moves 8 rows x 128 contiguous bytes; the k-side vectors are staged in a per-wave LDS slab
+// (channel k at slot (k & 7) * K / 8 + (k >> 3)); sa and y are per-lane fmaf chains over the lane's rows plus the
+// three-step butterfly over the row groups g.  Operands and outputs keep 2-byte accesses (the generic path's operand
+// alignment).
+constexpr int kVCols = 32;
+
+// (K = 64 never comes here: the specialised kernels serve it)
+inline bool vec_ok(const Params& p) {
+    auto al = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    return p.K % kVCols == 0 && p.K != 64 && p.K <= kGenericMaxK && al(p.h0) && al(p.ht) && al(p.snap);
+}
+
+template <int RPL>
+__global__ __launch_bounds__(64 * kGWaves) void wkv7_generic_vec_kernel(const Params p) {
+    constexpr int K = 8 * RPL;
+    constexpr int NCH = (K + 63) / 64;  // k-side channels staged per lane
+    constexpr int ncb = K / kVCols;
+    __shared__ float slab_all[kGWaves][5 * K];
+    const int wv = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int g = lane >> 3, c = lane & 7;
+    const int64_t unit = (int64_t)blockIdx.x * kGWaves + wv;
+    if (unit >= (int64_t)p.num_seqs * p.H * ncb) return;  // the whole wavefront: no barrier follows
+    const int cb = (int)(unit % ncb);
+    const int64_t pair = unit / ncb;
+    const int n = (int)(pair / p.H), h = (int)(pair % p.H);
+    int64_t bos;
+    int L;
+    seq_extent(p, n, bos, L);
+    const int col0 = cb * kVCols + 4 * c;
+    float* const slab = slab_all[wv];
+    f4 S[RPL];
+    {
+        const float* const src = gsrc(p, n, h);
+#pragma unroll
+        for (int j = 0; j < RPL; ++j)
+            S[j] = src ? *reinterpret_cast<const f4*>(src + (int64_t)(g + 8 * j) * K + col0) : f4{0.f, 0.f, 0.f, 0.f};
+    }
+    GTok<NCH> cur{}, nxt{};
+    float vc[4] = {0.f, 0.f, 0.f, 0.f}, vn[4] = {0.f, 0.f, 0.f, 0.f};
+    auto vload = [&](int64_t tok, float (&v)[4]) {
+        const uint16_t* const vp = p.v + tok * p.in_tok_stride + (int64_t)h * K + col0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = bf16_to_f32(vp[e]);
+    };
+    if (L > 0) {
+        gload(p, bos, h, lane, 0, cur);
+        vload(bos, vc);
+    }
+    const int64_t KK = (int64_t)K * K;
+    for (int t = 0; t < L; ++t) {
+        wave_lds_sync();  // the previous token's slab reads precede these writes
+#pragma unroll
+        for (int m = 0; m < NCH; ++m) {
+            const int ch = lane + 64 * m;
+            if (ch < K) {
+                const int sl = (ch & 7) * RPL + (ch >> 3);
+                slab[sl] = decay(cur.d[m]);
+                slab[K + sl] = cur.a[m];
+                slab[2 * K + sl] = cur.b[m];
+                slab[3 * K + sl] = cur.k[m];
+                slab[4 * K + sl] = cur.r[m];
+            }
+        }
+        if (t + 1 < L) {  // in flight during this token's arithmetic
+            gload(p, bos + t + 1, h, lane, 0, nxt);
+            vload(bos + t + 1, vn);
+        }
+        wave_lds_sync();
+        const float* const dv = slab + g * RPL;
+        // sa = a^T S over the old state, per column (wkv7.py:75)
+        float sa[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < RPL; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) sa[e] = fmaf(dv[K + j], S[j][e], sa[e]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sa[e] = butterfly8(sa[e]);
+        // S = d S + b sa + k v;  y = r^T S over the updated state (wkv7.py:75-77)
+        float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) {
+            const float d = dv[j], b = dv[2 * K + j], k = dv[3 * K + j], r = dv[4 * K + j];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                S[j][e] = fmaf(d, S[j][e], fmaf(b, sa[e], k * vc[e]));
+                y[e] = fmaf(r, S[j][e], y[e]);
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = butterfly8(y[e]);
+        if (p.o && g == 0) {
+            uint16_t* const op = p.o + (bos + t) * p.o_tok_stride + (int64_t)h * K + col0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) op[e] = f32_to_bf16(y[e]);
+        }
+        if (p.snap && t < p.T) {
+            float* const sp = p.snap + (((int64_t)n * p.T + t) * p.H + h) * KK + col0;
+#pragma unroll
+            for (int j = 0; j < RPL; ++j) *reinterpret_cast<f4*>(sp + (int64_t)(g + 8 * j) * K) = S[j];
+        }
+        cur = nxt;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) vc[e] = vn[e];
+    }
+    if (float* const dst = gdst(p, n, h)) {
+#pragma unroll
+        for (int j = 0; j < RPL; ++j) *reinterpret_cast<f4*>(dst + (int64_t)(g + 8 * j) * K + col0) = S[j];
+    }
+}
+
 }  // namespace
 
 int64_t generic_grid(const Params& p) {
-    const int64_t units = (int64_t)p.num_seqs * p.H * ((p.K + kGCols - 1) / kGCols);
+    const int cols = vec_ok(p) ? kVCols : kGCols;
+    const int64_t units = (int64_t)p.num_seqs * p.H * ((p.K + cols - 1) / cols);
     return (units + kGWaves - 1) / kGWaves;
 }
 
@@ -172,6 +287,18 @@ hipError_t launch_generic(const Params& p, hipStream_t stream) {
     const int64_t blocks = generic_grid(p);
     if (blocks == 0) return hipSuccess;
     const dim3 grid((unsigned)blocks), block(64 * kGWaves);
+    if (vec_ok(p)) {
+        switch (p.K) {
+            case 32: hipLaunchKernelGGL(wkv7_generic_vec_kernel<4>, grid, block, 0, stream, p); break;
+            case 96: hipLaunchKernelGGL(wkv7_generic_vec_kernel<12>, grid, block, 0, stream, p); break;
+            case 128: hipLaunchKernelGGL(wkv7_generic_vec_kernel<16>, grid, block, 0, stream, p); break;
+            case 160: hipLaunchKernelGGL(wkv7_generic_vec_kernel<20>, grid, block, 0, stream, p); break;
+            case 192: hipLaunchKernelGGL(wkv7_generic_vec_kernel<24>, grid, block, 0, stream, p); break;
+            case 224: hipLaunchKernelGGL(wkv7_generic_vec_kernel<28>, grid, block, 0, stream, p); break;
+            default: hipLaunchKernelGGL(wkv7_generic_vec_kernel<32>, grid, block, 0, stream, p); break;  // 256
+        }
+        return hipGetLastError();
+    }
     int kp = 4;
     while (kp < p.K) kp *= 2;
     switch (kp) {

@@ -1,5 +1,6 @@
 """Head sizes other than 64 (the reference takes any K, padding it to a power of two with masks,
-rwkv_next/kernels/wkv7.py:55-59, 96): the generic token-serial kernel through every entry point -- the functional
+rwkv_next/kernels/wkv7.py:55-59, 96): the generic token-serial kernels (float4 rows for multiples of 32 with 16-byte
+aligned states -- K = 32, 96, 128, 256 here -- scalar rows otherwise) through every entry point -- the functional
 wkv7 (dense and varlen), the in-place replay (n_keep), and the slot pool with fresh rows and per-token snapshots --
 against the fp64 oracle on the same bf16-rounded inputs.  Tolerances as for K = 64: y max-relative <= 2e-2 (bf16
 output), states max-relative <= 1e-4."""
@@ -79,7 +80,7 @@ def test_replay_in_place(dev, K):
     assert torch.equal(st[0].cpu(), torch.from_numpy(s0[0]))  # n_keep = 0 keeps the state bit for bit
 
 
-@pytest.mark.parametrize("K", [24, 64 + 16])
+@pytest.mark.parametrize("K", [24, 64 + 16, 96])  # 96: the float4 kernel for multiples of 32
 def test_pool_with_fresh_rows_and_snapshots(dev, K):
     """Slots in a pool, one row fresh (starts from zeros), snapshots after every token: each snapshot equals the
     oracle's state after that token, and the pool's untouched slots keep their values."""
